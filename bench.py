@@ -1,0 +1,293 @@
+"""Benchmark of the q4 matmul path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|gemv|moe|gemm|moe_prefill]
+
+Prints ONE JSON line. The headline (`value`) is the q4 decode GEMV of
+a "step" is one decode pass over the dense projections of
+L_LAYERS layers (fused QKV/gate-up 4096->12288 and down 6144->4096, every layer
+its own weights) plus the LM head 4096->151936, at batch M; the step is run for
+M in {1, 2, 4, 6, 8}. value = algorithmic bytes / time over all timed steps of
+the sweep (GB/s). The weight pool (1.26 GB) is ~5x the 256 MB Infinity Cache,
+so each launch streams its weights from HBM. Inputs are resident in HBM when the
+timed region starts.
+
+The other configs are measured too and reported under "workloads": the routed
+MoE decode (config 3), the 4096-token q4 prefill GEMM (config 4) and the grouped
+MoE prefill (config 5).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "v620-inference-engine_amd"))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+L_LAYERS = 24
+BATCHES = (1, 2, 4, 6, 8)
+H, QKV, FFN_DOWN_K, VOCAB = 4096, 12288, 6144, 151936
+
+
+def q4_bytes(N, K):
+    return N * K // 2 + N * (K // 128) * 2 + N * (K // 128) // 2
+
+
+def gen_q4(torch, dev, N, K, zeros=True, lead=(), seed=0):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    G = K // 128
+    W = torch.randint(-2**31, 2**31 - 1, lead + (N, K // 8), generator=g, device=dev, dtype=torch.int32)
+    S = (torch.randn(lead + (N, G), generator=g, device=dev) * 0.02).abs().to(torch.float16)
+    Z = torch.randint(-2**31, 2**31 - 1, lead + (N, (G + 7) // 8), generator=g, device=dev,
+                      dtype=torch.int32) if zeros else None
+    return W, S, Z
+
+
+def gen_x(torch, dev, M, K, seed=1):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+
+
+class Timer:
+    """HIP events on torch's current stream, the stream every qwq4 call launches on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.a = torch.cuda.Event(enable_timing=True)
+        self.b = torch.cuda.Event(enable_timing=True)
+
+    def __enter__(self):
+        self.torch.cuda.synchronize()
+        self.a.record()
+        return self
+
+    def __exit__(self, *exc):
+        self.b.record()
+        self.torch.cuda.synchronize()
+        self.ms = self.a.elapsed_time(self.b)
+
+
+# ---------------------------------------------------------------- config 2
+def bench_gemv(torch, qwq4, dev, steps, warmup):
+    layers = []
+    for l in range(L_LAYERS):
+        layers.append((gen_q4(torch, dev, QKV, H, seed=2 * l), gen_q4(torch, dev, H, FFN_DOWN_K, seed=2 * l + 1)))
+    head = gen_q4(torch, dev, VOCAB, H, seed=999)
+    step_bytes_w = L_LAYERS * (q4_bytes(QKV, H) + q4_bytes(H, FFN_DOWN_K)) + q4_bytes(VOCAB, H)
+    per_m = {}
+    tot_bytes = tot_ms = 0.0
+    for M in BATCHES:
+        x = gen_x(torch, dev, M, FFN_DOWN_K, seed=M)
+        y = torch.empty((M, VOCAB), dtype=torch.bfloat16, device=dev)
+
+        def step():
+            for (wq, wd) in layers:
+                qwq4.gemv(*wq, x, QKV, H, M, y=y, y_bf16=True, xs=x.stride(0), ys=y.stride(0))
+                qwq4.gemv(*wd, x, H, FFN_DOWN_K, M, y=y, y_bf16=True, xs=x.stride(0), ys=y.stride(0))
+            qwq4.gemv(*head, x, VOCAB, H, M, y=y, y_bf16=True, xs=x.stride(0), ys=y.stride(0))
+
+        for _ in range(warmup):
+            step()
+        with Timer(torch) as t:
+            for _ in range(steps):
+                step()
+        act = L_LAYERS * (M * H * 2 + M * QKV * 2 + M * FFN_DOWN_K * 2 + M * H * 2) + M * H * 2 + M * VOCAB * 2
+        b = (step_bytes_w + act) * steps
+        per_m[M] = {"GB_s": b / (t.ms * 1e-3) / 1e9, "ms_per_step": t.ms / steps,
+                    "tokens_s": M * steps / (t.ms * 1e-3)}
+        tot_bytes += b
+        tot_ms += t.ms
+    launches = 2 * L_LAYERS + 1
+    return {
+        "GB_s": tot_bytes / (tot_ms * 1e-3) / 1e9,
+        "ms_per_step": tot_ms / (steps * len(BATCHES)),
+        "per_batch": per_m,
+        "bytes_per_step_weights": step_bytes_w,
+        "launches_per_step": launches,
+        "avg_launch_us": tot_ms * 1e3 / (steps * len(BATCHES) * launches),
+        "avg_bytes_per_launch": tot_bytes / (steps * len(BATCHES) * launches),
+    }
+
+
+# ---------------------------------------------------------------- config 3
+def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
+    E, F, k = 256, 1536, 8
+    gate = gen_q4(torch, dev, F, H, lead=(E,), seed=10)
+    up = gen_q4(torch, dev, F, H, lead=(E,), seed=11)
+    down = gen_q4(torch, dev, H, F, lead=(E,), seed=12)
+    per_expert = q4_bytes(F, H) * 2 + q4_bytes(H, F)
+    out = {}
+    for B in batches:
+        x = gen_x(torch, dev, B, H, seed=100 + B)
+        g = torch.Generator(device=dev)
+        g.manual_seed(200 + B)
+        logits = torch.randn((B, E), generator=g, device=dev)
+        r = qwq4.Route(B, E, k, dev)
+        h = torch.empty((B * k, F), dtype=torch.float16, device=dev)
+        yp = torch.empty((B * k, H), dtype=torch.float32, device=dev)
+        o = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
+
+        def step():
+            qwq4.moe_route(logits, k, out=r)
+            qwq4.moe_experts_gemv(gate, up, down, r, x, h=h, yp=yp)
+            qwq4.moe_combine(yp, r, H, out=o)
+
+        for _ in range(warmup):
+            step()
+        with Timer(torch) as t:
+            for _ in range(steps):
+                step()
+        U = int(r.n_active.item())
+        b = U * per_expert
+        out[B] = {"distinct_experts": U, "GB_s": b * steps / (t.ms * 1e-3) / 1e9, "us_per_step": t.ms * 1e3 / steps,
+                  "tokens_s": B * steps / (t.ms * 1e-3)}
+    return out
+
+
+# ---------------------------------------------------------------- config 4
+def bench_gemm(torch, qwq4, dev, steps, warmup):
+    T = 4096
+    res = {}
+    for (N, K) in ((QKV, H), (H, FFN_DOWN_K)):
+        W = gen_q4(torch, dev, N, K, seed=300 + N)
+        X = gen_x(torch, dev, T, K, seed=301)
+        Y = torch.empty((T, N), dtype=torch.bfloat16, device=dev)
+        ws = torch.empty(qwq4.gemm_workspace_size(T, K), dtype=torch.uint8, device=dev)
+        Yh = torch.empty((T // 2, N), dtype=torch.bfloat16, device=dev)
+        wsh = torch.empty(qwq4.gemm_workspace_size(T // 2, K), dtype=torch.uint8, device=dev)
+        for _ in range(warmup):
+            qwq4.gemm(*W, X, N, K, Y=Y, y_bf16=True, workspace=ws)
+        with Timer(torch) as t:
+            for _ in range(steps):
+                qwq4.gemm(*W, X, N, K, Y=Y, y_bf16=True, workspace=ws)
+        with Timer(torch) as t2:
+            for _ in range(steps):
+                for half in range(2):
+                    qwq4.gemm(*W, X[half * (T // 2):(half + 1) * (T // 2)], N, K, Y=Yh, y_bf16=True, workspace=wsh)
+        flops = 2.0 * T * N * K
+        res[f"{K}x{N}"] = {"TFLOP_s": flops * steps / (t.ms * 1e-3) / 1e12, "us": t.ms * 1e3 / steps,
+                           "TFLOP_s_2x2048": flops * steps / (t2.ms * 1e-3) / 1e12,
+                           "tokens_s": T * steps / (t.ms * 1e-3)}
+    return res
+
+
+# ---------------------------------------------------------------- config 5
+def bench_moe_prefill(torch, qwq4, dev, steps, warmup):
+    E, F, k, T = 256, 1536, 8, 4096
+    gate = gen_q4(torch, dev, F, H, lead=(E,), seed=10)
+    up = gen_q4(torch, dev, F, H, lead=(E,), seed=11)
+    down = gen_q4(torch, dev, H, F, lead=(E,), seed=12)
+    x = gen_x(torch, dev, T, H, seed=400)
+    g = torch.Generator(device=dev)
+    g.manual_seed(401)
+    logits = torch.randn((T, E), generator=g, device=dev) + torch.randn((1, E), generator=g, device=dev) * 0.5
+    tm = qwq4.moe_grouped_tile_m()
+    r = qwq4.Route(T, E, k, dev, tile_m=tm)
+    h = torch.empty((T * k, F), dtype=torch.float16, device=dev)
+    yp = torch.empty((T * k, H), dtype=torch.float32, device=dev)
+    o = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(max(qwq4.moe_grouped_workspace_size(T, k, E, H, F), 1), dtype=torch.uint8, device=dev)
+
+    def step():
+        qwq4.moe_route(logits, k, tile_m=tm, out=r)
+        qwq4.moe_experts_grouped(gate, up, down, r, x, h=h, yp=yp, workspace=ws)
+        qwq4.moe_combine(yp, r, H, out=o)
+
+    for _ in range(warmup):
+        step()
+    with Timer(torch) as t:
+        for _ in range(steps):
+            step()
+    flops = 2.0 * (k * T) * (2 * F * H + H * F)
+    return {"TFLOP_s": flops * steps / (t.ms * 1e-3) / 1e12, "us_per_step": t.ms * 1e3 / steps,
+            "tokens_s": T * steps / (t.ms * 1e-3)}
+
+
+# ------------------------------------------------------------ CPU baseline
+def cpu_baseline(budget_s=12.0):
+    """The C oracle (oracle/q4_oracle.c, the reference's expert_linear scheme) on
+    the host cores: decode step at M=1 on a 2-layer + LM-head sample."""
+    from oracle import oracle as o
+    from qwq4 import synth
+    threads = min(os.cpu_count() or 1, 16)
+    mats = [(QKV, H), (H, FFN_DOWN_K)] * 2 + [(VOCAB, H)]
+    ws = [synth.q4_weights(7, f"cpu{i}", N, K) for i, (N, K) in enumerate(mats)]
+    xs = {K: synth.acts(7, f"cx{K}", 1, K)[1] for K in (H, FFN_DOWN_K)}
+    nbytes = sum(q4_bytes(N, K) for N, K in mats)
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        for (N, K), (W, S, Z) in zip(mats, ws):
+            o.q4_linear(W, S, Z, N, K, xs[K], threads=threads)
+        runs += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": nbytes * runs / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle q4_linear, M=1, 2 layers (4096->12288, 6144->4096) + LM head 4096->151936, "
+                      f"{runs} passes in {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="all")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: --gpus must be 1 (no collectives, "
+                                   "no multi-GPU path)"}))
+        sys.exit(2)
+    import torch
+    import qwq4
+    dev = torch.device("cuda:0")
+    qwq4.lib()
+    wl = a.workload
+    res = {}
+    if wl in ("all", "gemv"):
+        res["gemv"] = bench_gemv(torch, qwq4, dev, a.steps, a.warmup)
+        print(f"# gemv {res['gemv']['GB_s']:.1f} GB/s", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+    if wl in ("all", "moe"):
+        res["moe_decode"] = bench_moe(torch, qwq4, dev, a.steps, a.warmup)
+        print("# moe decode done", file=sys.stderr, flush=True)
+    if wl in ("all", "gemm"):
+        res["prefill_gemm"] = bench_gemm(torch, qwq4, dev, max(2, a.steps // 4), 1)
+        print("# gemm done", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+    if wl in ("all", "moe_prefill"):
+        res["moe_prefill"] = bench_moe_prefill(torch, qwq4, dev, max(2, a.steps // 4), 1)
+        print("# moe prefill done", file=sys.stderr, flush=True)
+    line = {
+        "metric": "q4 GEMV HBM GB/s (% of peak) at batch 1-8; q4 prefill GEMM TFLOP/s (% MFMA)",
+        "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "q4 weights, bf16 x, fp32 acc",
+        "data": "synthetic (seeded): uniform nibbles, |N(0,0.02)| fp16 scales, uniform 4-bit zeros, N(0,1) bf16 x",
+        "config": {"workload": f"decode dense q4 GEMV, {L_LAYERS} layers x (4096->12288, 6144->4096) + LM head "
+                               f"4096->151936, batch 1/2/4/6/8, bf16 out",
+                   "batches": list(BATCHES)},
+    }
+    if "gemv" in res:
+        g = res["gemv"]
+        line["value"] = round(g["GB_s"], 1)
+        line["ms_per_step"] = round(g["ms_per_step"], 4)
+        ach = g["avg_bytes_per_launch"] / (g["avg_launch_us"] * 1e-6) / 1e9
+        line["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel": "q4_gemv_kernel", "avg_launch_us": round(g["avg_launch_us"], 3)}
+    line["workloads"] = res
+    if not a.no_cpu and wl in ("all", "gemv"):
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

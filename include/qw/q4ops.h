@@ -1,0 +1,142 @@
+/* q4ops.h -- C ABI of the MI355X (gfx950) q4 matmul path of qw.
+ *
+ * Drop-in operator layer for the reference engine's quantized matmul roles
+ * (manuelbaez/v620-inference-engine, paths relative to that repository):
+ *   qw_q4_gemv            gpu::gemv_rows            src/kernels/gemv.hpp:13-14
+ *   qw_q4_gemm            gpu::gemm (rocBLAS)       src/kernels/gemm.hpp:14-15
+ *   qw_moe_route          gpu::moe_route_B, and
+ *                         gpu::moe_route_T + moe_scatter_T
+ *                                                   src/kernels/moe.hpp:17-27
+ *   qw_moe_experts_gemv   gpu::moe_experts_P        src/kernels/moe.hpp:35-37
+ *   qw_moe_experts_grouped gpu::moe_experts_T       src/kernels/moe.hpp:29-32
+ *   qw_moe_combine        gpu::moe_combine_B/T      src/kernels/moe.hpp:42-46
+ *   qw_q4_unpack / qw_q4_dequant                    src/ref/ref_model.cpp:108-114
+ *   qw_q4_from_engine_order (inverse of pack_int4_words)
+ *                                                   src/engine/weight_convert.cpp:61-71
+ *
+ * Conventions
+ *   - Every pointer is a device pointer owned by the caller; nothing here
+ *     allocates, frees or synchronises, so all calls are safe under HIP graph
+ *     capture. `stream` is a hipStream_t (NULL = the default stream).
+ *   - Functions return 0 on success and a negative code on error:
+ *       QW_Q4_EINVAL  a bad shape, stride, alignment or null pointer (nothing
+ *                     was launched; qw_q4_last_error() says which);
+ *       QW_Q4_ELAUNCH the HIP launch failed (hipGetLastError).
+ *     Unlike the reference launchers (which return void and ignore launch
+ *     errors, and silently skip an unsupported row count), no unsupported
+ *     case is a silent no-op.
+ *   - Calls on different streams are independent; the library holds no state
+ *     beyond the per-thread error string.
+ *
+ * q4 weight format (the compressed-tensors checkpoint order, docs/MODEL.md:34-37)
+ *   W  uint32 [N][K/8]          element 8c+i of row n in bits 4i..4i+3 of word c
+ *   S  fp16   [N][K/128]        scale per 128-element group along K
+ *   Z  uint32 [N][ceil(G/8)]    4-bit zero of group g in bits 4(g%8) of word
+ *                               g/8 (G = K/128); NULL = zero 8 for every group,
+ *                               the reference's symmetric format
+ *   weight = (q - z) * s, exactly, in fp32.
+ *   K must be a multiple of 128. Activations are bf16 (uint16 bit patterns);
+ *   accumulation is fp32.
+ */
+#ifndef QW_Q4OPS_H
+#define QW_Q4OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QW_Q4_OK 0
+#define QW_Q4_EINVAL (-1)
+#define QW_Q4_ELAUNCH (-2)
+
+/* Version of this ABI (bumped on any signature change). */
+int qw_q4_abi_version(void);
+
+/* Message for the last error returned on this thread ("" if none). */
+const char *qw_q4_last_error(void);
+
+/* Decode GEMV (replaces gpu::gemv_rows, src/kernels/gemv.hpp:13-14):
+ *   y[m*ys + n] (+)= sum_k W[n][k] * x[m*xs + k],   m < M, n < N
+ * x bf16 rows of stride xs (elements, a multiple of 8, x 16-byte aligned);
+ * y fp32 (y_bf16 = 0) or bf16 (y_bf16 = 1, round to nearest even) rows of
+ * stride ys; accumulate != 0 adds to y. 1 <= M <= 32. */
+int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint32_t *Z, const uint16_t *x, int xs, void *y, int ys,
+               int y_bf16, int N, int K, int M, int accumulate, void *stream);
+
+/* Prefill GEMM (replaces gpu::gemm, src/kernels/gemm.hpp:14-15, with q4
+ * weights): Y[t][n] = sum_k X[t][k] * W[n][k], t < T. X bf16 rows of stride
+ * ldx; Y fp32 or bf16 rows of stride ldy. `workspace` (device memory of at
+ * least qw_q4_gemm_workspace_size(T, K) bytes, 256-byte aligned) is scratch
+ * for the activation pre-pass; it holds nothing between calls. */
+size_t qw_q4_gemm_workspace_size(int T, int K);
+int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint32_t *Z, const uint16_t *X, int ldx, int T, void *Y,
+               int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Routing of T tokens over E experts (replaces gpu::moe_route_B for decode
+ * rows and gpu::moe_route_T + moe_scatter_T for prefill, moe.hpp:17-27; math
+ * of ref::Model::moe, src/ref/ref_model.cpp:412-431):
+ *   p = float(exp(l - max l)); top k by (p desc, index asc);
+ *   top_w = float(p / sum of the k selected p, in double)
+ * Outputs (all device int32 unless noted):
+ *   top_e [T][k], top_w [T][k] (fp32), counts [E], offsets [E+1],
+ *   tok_slot [T][k] (slot of each selection), pair_tok [T*k] (token of each
+ *   slot), active [E] (experts with pairs, ascending; first *n_active valid),
+ *   n_active [1].
+ * Slots are deterministic: experts ascending, tokens ascending within one.
+ * tile_m > 0 also writes a tile list for qw_moe_experts_grouped:
+ *   tile_e, tile_m0 [T*k/tile_m + E], n_tiles [1]  (tile_m 0: may be NULL).
+ * Limits: 1 <= k <= min(E, 64), E <= 1024, T <= 8192 for E <= 256 (LDS). */
+int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_t *top_e, float *top_w,
+                 int32_t *counts, int32_t *offsets, int32_t *tok_slot, int32_t *pair_tok, int32_t *active,
+                 int32_t *n_active, int32_t *tile_e, int32_t *tile_m0, int32_t *n_tiles, void *stream);
+
+/* Gathered per-expert GEMVs for decode batches (replaces gpu::moe_experts_P,
+ * moe.hpp:35-37). For every slot p of expert e (from qw_moe_route):
+ *   h[p]  = silu(G_e x[pair_tok[p]]) * (U_e x[pair_tok[p]])     fp16 [T*k][F]
+ *   yp[p] = D_e h[p]                                            fp32 [T*k][H]
+ * gate/up: [E][F][H/8] words, [E][F][H/128] scales, [E][F][ceil(H/1024)] zeros;
+ * down: [E][H][F/8], [E][H][F/128], [E][H][ceil(F/1024)]. x bf16 [T][H].
+ * h is scratch in this library's own element order (each 8-element chunk
+ * permuted); yp is in natural order. 1 <= T <= 32. Each expert's weights are
+ * read once per call however many of the batch's tokens chose it. */
+int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint32_t *gz, const uint32_t *uw,
+                        const uint16_t *us, const uint32_t *uz, const uint32_t *dw, const uint16_t *ds,
+                        const uint32_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
+                        const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int T, int topk,
+                        uint16_t *h, float *yp, void *stream);
+
+/* Grouped per-expert GEMMs for prefill chunks (replaces gpu::moe_experts_T,
+ * moe.hpp:29-32): the same outputs as qw_moe_experts_gemv for any T, over
+ * the (expert, tile) list qw_moe_route writes when called with
+ * tile_m = qw_moe_grouped_tile_m(). workspace: at least
+ * qw_moe_grouped_workspace_size(...) bytes (may be 0), 256-byte aligned. */
+int qw_moe_grouped_tile_m(void);
+size_t qw_moe_grouped_workspace_size(int T, int topk, int E, int H, int F);
+int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint32_t *gz, const uint32_t *uw,
+                           const uint16_t *us, const uint32_t *uz, const uint32_t *dw, const uint16_t *ds,
+                           const uint32_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
+                           const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
+                           int T, int topk, uint16_t *h, float *yp, void *workspace, size_t workspace_bytes,
+                           void *stream);
+
+/* Weighted combine (replaces gpu::moe_combine_B/T, moe.hpp:42-46):
+ *   out[t][j] = shared[t][j] + sum_{i<k} tok_w[t][i] * yp[tok_slot[t][i]][j]
+ * shared fp32 [T][H] or NULL; out fp32 or bf16 (out_bf16). H % 4 == 0. */
+int qw_moe_combine(const float *yp, const int32_t *tok_slot, const float *tok_w, const float *shared, int T, int topk,
+                   int H, void *out, int out_bf16, void *stream);
+
+/* Format surface (bit-exact): nibbles as bytes [N][K]; dequantised fp32
+ * weights [N][K]; reference-engine word order -> checkpoint word order. */
+int qw_q4_unpack(const uint32_t *W, int64_t N, int64_t K, uint8_t *out, void *stream);
+int qw_q4_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, float *out,
+                  void *stream);
+int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QW_Q4OPS_H */

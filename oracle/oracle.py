@@ -1,0 +1,195 @@
+"""numpy/ctypes front end of the CPU oracle (oracle/q4_oracle.c).
+
+Test infrastructure only: imported by tests/, by __graft_entry__.smoke() and by
+bench.py's cpu_baseline leg, as the checker. The product library never loads
+it. Reference citations for each routine are in q4_oracle.c.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C")
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C")
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE, "liboq4.so"], check=True)
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboq4.so")
+        if not os.path.exists(path):
+            build()
+        L = ctypes.CDLL(path)
+        L.o_q4_unpack.argtypes = [_u32p, _i64, _i64, _u8p]
+        L.o_q4_dequant.argtypes = [_u32p, _u16p, _vp, _i64, _i64, _f32p]
+        L.o_q4_linear.argtypes = [_u32p, _u16p, _vp, _i64, _i64, _f32p, _int, _int, _f32p, _int, _int]
+        L.o_q4_linear_f64.argtypes = [_u32p, _u16p, _vp, _i64, _i64, _f32p, _int, _int, _f64p, _int, _int]
+        L.o_pack_engine_order.argtypes = [_u32p, _u32p, _i64]
+        L.o_unpack_engine_order.argtypes = [_u32p, _u32p, _i64]
+        L.o_quantize_g128.argtypes = [_u16p, _i64, _u32p, _u16p]
+        L.o_route.argtypes = [_f32p, _int, _int, _int, _i32p, _f32p]
+        L.o_moe_slots.argtypes = [_i32p, _int, _int, _int, _i32p, _i32p, _i32p, _i32p]
+        L.o_moe.argtypes = [_f32p, _int, _int, _int, _int, _int, _f32p] + [_u32p, _u16p, _vp] * 3 + [_f32p, _vp, _vp, _int]
+        for n in ("o_bf16_to_f32", "o_f16_to_f32"):
+            getattr(L, n).argtypes = [ctypes.c_uint16]
+            getattr(L, n).restype = ctypes.c_float
+        for n in ("o_f32_to_f16", "o_f32_to_bf16"):
+            getattr(L, n).argtypes = [ctypes.c_float]
+            getattr(L, n).restype = ctypes.c_uint16
+        _LIB = L
+    return _LIB
+
+
+def _zp(Z):
+    return None if Z is None else Z.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def nthreads():
+    return os.cpu_count() or 1
+
+
+# ---- numbers (vectorised by looping in C over a numpy array would be nicer;
+# these are exact helpers for small arrays and for golden checks)
+def f16_to_f32(h):
+    h = np.asarray(h, np.uint16)
+    return np.array([lib().o_f16_to_f32(int(v)) for v in h.ravel()], np.float32).reshape(h.shape)
+
+
+def f32_to_f16(x):
+    x = np.asarray(x, np.float32)
+    return np.array([lib().o_f32_to_f16(float(v)) for v in x.ravel()], np.uint16).reshape(x.shape)
+
+
+def f32_to_bf16(x):
+    x = np.asarray(x, np.float32)
+    return np.array([lib().o_f32_to_bf16(float(v)) for v in x.ravel()], np.uint16).reshape(x.shape)
+
+
+def bf16_to_f32(b):
+    b = np.asarray(b, np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+# ---- q4 format
+def q4_unpack(W, N, K):
+    out = np.empty((N, K), np.uint8)
+    lib().o_q4_unpack(_c(W, np.uint32), N, K, out)
+    return out
+
+
+def q4_dequant(W, S, Z, N, K):
+    out = np.empty((N, K), np.float32)
+    W, S = _c(W, np.uint32), _c(S, np.uint16)
+    Z = None if Z is None else _c(Z, np.uint32)
+    lib().o_q4_dequant(W, S, _zp(Z), N, K, out)
+    return out
+
+
+def q4_linear(W, S, Z, N, K, x, threads=None):
+    """y[t][n] = sum_k deq(W)[n][k] x[t][k]; x fp32 [T][K] -> y fp32 [T][N]."""
+    x = _c(x, np.float32).reshape(-1, K)
+    T = x.shape[0]
+    y = np.empty((T, N), np.float32)
+    W, S = _c(W, np.uint32), _c(S, np.uint16)
+    Z = None if Z is None else _c(Z, np.uint32)
+    lib().o_q4_linear(W, S, _zp(Z), N, K, x, T, K, y, N, threads or nthreads())
+    return y
+
+
+def q4_linear_f64(W, S, Z, N, K, x, threads=None):
+    x = _c(x, np.float32).reshape(-1, K)
+    T = x.shape[0]
+    y = np.empty((T, N), np.float64)
+    W, S = _c(W, np.uint32), _c(S, np.uint16)
+    Z = None if Z is None else _c(Z, np.uint32)
+    lib().o_q4_linear_f64(W, S, _zp(Z), N, K, x, T, K, y, N, threads or nthreads())
+    return y
+
+
+def pack_engine_order(words):
+    w = _c(words, np.uint32).ravel()
+    out = np.empty_like(w)
+    lib().o_pack_engine_order(w, out, w.size)
+    return out.reshape(np.shape(words))
+
+
+def unpack_engine_order(words):
+    w = _c(words, np.uint32).ravel()
+    out = np.empty_like(w)
+    lib().o_unpack_engine_order(w, out, w.size)
+    return out.reshape(np.shape(words))
+
+
+def quantize_g128(src_bf16):
+    s = _c(src_bf16, np.uint16).ravel()
+    ng = s.size // 128
+    words = np.empty(ng * 16, np.uint32)
+    scales = np.empty(ng, np.uint16)
+    lib().o_quantize_g128(s, ng, words, scales)
+    return words, scales
+
+
+# ---- routing / MoE
+def route(logits, topk):
+    logits = _c(logits, np.float32)
+    T, E = logits.shape
+    top_e = np.empty((T, topk), np.int32)
+    top_w = np.empty((T, topk), np.float32)
+    lib().o_route(logits, T, E, topk, top_e, top_w)
+    return top_e, top_w
+
+
+def moe_slots(top_e, E):
+    top_e = _c(top_e, np.int32)
+    T, k = top_e.shape
+    counts = np.empty(E, np.int32)
+    offsets = np.empty(E + 1, np.int32)
+    tok_slot = np.empty((T, k), np.int32)
+    pair_tok = np.empty(T * k, np.int32)
+    lib().o_moe_slots(top_e, T, E, k, counts, offsets, tok_slot, pair_tok)
+    return counts, offsets, tok_slot, pair_tok
+
+
+def moe(x, logits, topk, gate, up, down, threads=None, want_parts=False):
+    """gate/up/down: (W, S, Z) with W [E][rows][K/8], S [E][rows][G], Z or None."""
+    x = _c(x, np.float32)
+    logits = _c(logits, np.float32)
+    T, H = x.shape
+    E = logits.shape[1]
+    F = gate[0].shape[1]
+    out = np.empty((T, H), np.float32)
+    h = np.empty((T * topk, F), np.float32) if want_parts else None
+    yp = np.empty((T * topk, H), np.float32) if want_parts else None
+    args = []
+    for W, S, Z in (gate, up, down):
+        args += [_c(W, np.uint32), _c(S, np.uint16), None if Z is None else _c(Z, np.uint32)]
+    keep = args[:]
+    cargs = []
+    for i, a in enumerate(args):
+        cargs.append(_zp(a) if i % 3 == 2 else a)
+    lib().o_moe(x, T, H, F, E, topk, logits, *cargs, out,
+                None if h is None else h.ctypes.data_as(ctypes.c_void_p),
+                None if yp is None else yp.ctypes.data_as(ctypes.c_void_p), threads or nthreads())
+    del keep
+    if want_parts:
+        return out, h, yp
+    return out

@@ -1,0 +1,420 @@
+/*
+ * q4_oracle.c -- CPU restatement of qw's int4 ("q4") matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker that the HIP kernels are
+ * compared against; it is loaded by tests/, by __graft_entry__.smoke() and by
+ * bench.py's cpu_baseline leg, and never by the product library.
+ *
+ * What it restates (reference paths relative to the reference repository):
+ *   - number conversions           src/core/common.hpp:34-99
+ *   - int4 g128 unpack / dequant   src/ref/ref_model.cpp:100-119, docs/MODEL.md:34-37
+ *       generalised with a per-group 4-bit zero point z: w = (q - z) * s.
+ *       With no zero array z == 8, which is the reference's symmetric format.
+ *   - expert_linear (fp32 dot)      src/ref/ref_model.cpp:25-30, 100-119
+ *   - engine nibble order          src/engine/weight_convert.cpp:61-71
+ *   - int4 g128 quantiser          src/engine/weight_convert.cpp:73-90
+ *   - MoE routing and combine      src/ref/ref_model.cpp:406-463
+ *   - slot order                   src/kernels/moe_route.hip:149-160
+ *   - parallel_for chunking        src/core/threadpool.hpp:38-58
+ *
+ * Formats used throughout (the device formats of this build):
+ *   W  uint32 [N][K/8]        element 8c+i of a row at bits 4i of word c
+ *   S  fp16   [N][K/128]      one scale per 128-weight group along K
+ *   Z  uint32 [N][ceil(G/8)]  4-bit zero of group g at bits 4(g%8) of word g/8;
+ *                             NULL means z = 8 for every group
+ *
+ * Parity pinning (what each function is checked against) is listed in the
+ * test files tests/test_oracle*.py; every function here has at least one
+ * check that does not retype its formula.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define QGROUP 128
+
+/* ---------------------------------------------------------------- numbers */
+
+/* src/core/common.hpp:34-39: bf16 is the top half of an fp32. */
+float o_bf16_to_f32(uint16_t v) {
+    uint32_t u = (uint32_t)v << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* src/core/common.hpp:41-65: exact fp16 -> fp32, subnormals renormalised. */
+float o_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu, u;
+    if (exp == 0) {
+        if (man == 0) {
+            u = sign;
+        } else {
+            exp = 127 - 15 + 1;
+            while (!(man & 0x400u)) {
+                man <<= 1;
+                --exp;
+            }
+            man &= 0x3ffu;
+            u = sign | (exp << 23) | (man << 13);
+        }
+    } else if (exp == 31) {
+        u = sign | 0x7f800000u | (man << 13);
+    } else {
+        u = sign | ((exp + 127 - 15) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* src/core/common.hpp:76-97: round-to-nearest-even fp32 -> fp16. */
+uint16_t o_f32_to_f16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    int32_t exp = (int32_t)((u >> 23) & 0xffu) - 127 + 15;
+    uint32_t man = u & 0x7fffffu;
+    if (((u >> 23) & 0xffu) == 0xffu) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u : 0u));
+    if (exp >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (exp <= 0) {
+        if (exp < -10) return (uint16_t)sign;
+        man |= 0x800000u;
+        uint32_t shift = (uint32_t)(14 - exp);
+        uint32_t half = man >> shift, rem = man & ((1u << shift) - 1u), mid = 1u << (shift - 1);
+        if (rem > mid || (rem == mid && (half & 1u))) ++half;
+        return (uint16_t)(sign | half);
+    }
+    uint32_t half = sign | ((uint32_t)exp << 10) | (man >> 13), rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) ++half;
+    return (uint16_t)half;
+}
+
+/* Round-to-nearest-even fp32 -> bf16 (NaN kept quiet). The reference has no
+ * bf16 writer (gfx1030 has no bf16); this is the IEEE rule the outputs use. */
+uint16_t o_f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* ---------------------------------------------------------- q4 format */
+
+static inline int zero_of(const uint32_t *Z, int64_t n, int64_t G, int64_t g) {
+    if (!Z) return 8;
+    const int64_t zw = (G + 7) / 8;
+    return (int)((Z[n * zw + g / 8] >> (4 * (g % 8))) & 0xfu);
+}
+
+/* Nibble values q in [0,15], row-major [N][K]. docs/MODEL.md:34-37. */
+void o_q4_unpack(const uint32_t *W, int64_t N, int64_t K, uint8_t *out) {
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t c = 0; c < K / 8; ++c) {
+            const uint32_t word = W[n * (K / 8) + c];
+            for (int i = 0; i < 8; ++i) out[n * K + c * 8 + i] = (uint8_t)((word >> (4 * i)) & 0xfu);
+        }
+}
+
+/* One dequantised row: row[8c+i] = float(q - z) * f16(s), the line
+ * ref_model.cpp:114 with the scale read as fp16 and z in place of 8. */
+static void dequant_row(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t n, int64_t K, float *row) {
+    const int64_t G = K / QGROUP;
+    const uint32_t *p = W + n * (K / 8);
+    for (int64_t c = 0; c < K / 8; ++c) {
+        const int64_t g = c * 8 / QGROUP;
+        const float sc = o_f16_to_f32(S[n * G + g]);
+        const int z = zero_of(Z, n, G, g);
+        const uint32_t word = p[c];
+        for (int i = 0; i < 8; ++i) row[c * 8 + i] = (float)((int)((word >> (4 * i)) & 0xfu) - z) * sc;
+    }
+}
+
+void o_q4_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, float *out) {
+    for (int64_t n = 0; n < N; ++n) dequant_row(W, S, Z, n, K, out + n * K);
+}
+
+/* ------------------------------------------------------- parallel_for */
+
+/* src/core/threadpool.hpp:38-58: [0,n) split into at most 4*threads chunks of
+ * at least `grain` items, handed out dynamically. */
+typedef void (*range_fn)(void *ctx, int64_t b, int64_t e);
+typedef struct {
+    range_fn fn;
+    void *ctx;
+    int64_t n, chunk, chunks;
+    int64_t next; /* atomic */
+} pf_job;
+
+static void *pf_worker(void *arg) {
+    pf_job *j = (pf_job *)arg;
+    for (;;) {
+        const int64_t c = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
+        if (c >= j->chunks) break;
+        const int64_t b = c * j->chunk, e = b + j->chunk < j->n ? b + j->chunk : j->n;
+        if (b < e) j->fn(j->ctx, b, e);
+    }
+    return NULL;
+}
+
+static void parallel_for(int threads, int64_t n, int64_t grain, range_fn fn, void *ctx) {
+    if (n <= 0) return;
+    if (grain < 1) grain = 1;
+    if (threads < 1) threads = 1;
+    int64_t chunks = (n + grain - 1) / grain;
+    if (chunks > (int64_t)threads * 4) chunks = (int64_t)threads * 4;
+    if (chunks <= 1 || threads == 1) {
+        fn(ctx, 0, n);
+        return;
+    }
+    pf_job j = {fn, ctx, n, (n + chunks - 1) / chunks, chunks, 0};
+    pthread_t *tids = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+    for (int t = 1; t < threads; ++t) pthread_create(&tids[t], NULL, pf_worker, &j);
+    pf_worker(&j);
+    for (int t = 1; t < threads; ++t) pthread_join(tids[t], NULL);
+    free(tids);
+}
+
+/* ------------------------------------------------------- expert_linear */
+
+/* ref_model.cpp:25-30 sums a[i]*b[i] in fp32 under `omp simd reduction`,
+ * whose order is the compiler's. This restatement fixes one such order:
+ * 16 interleaved partial sums, then a pairwise fold. */
+static float dot_f32(const float *a, const float *b, int64_t n) {
+    float part[16] = {0};
+    int64_t i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 16; ++l) part[l] += a[i + l] * b[i + l];
+    for (; i < n; ++i) part[i % 16] += a[i] * b[i];
+    for (int w = 8; w > 0; w >>= 1)
+        for (int l = 0; l < w; ++l) part[l] += part[l + w];
+    return part[0];
+}
+
+typedef struct {
+    const uint32_t *W;
+    const uint16_t *S;
+    const uint32_t *Z;
+    int64_t K;
+    const float *x;
+    int T, ldx;
+    float *y;
+    int ldy;
+    double *yd;
+} lin_ctx;
+
+static void lin_range(void *vc, int64_t b, int64_t e) {
+    lin_ctx *c = (lin_ctx *)vc;
+    float *row = (float *)malloc(sizeof(float) * (size_t)c->K);
+    for (int64_t o = b; o < e; ++o) {
+        dequant_row(c->W, c->S, c->Z, o, c->K, row);
+        for (int t = 0; t < c->T; ++t) c->y[(size_t)t * c->ldy + o] = dot_f32(row, c->x + (size_t)t * c->ldx, c->K);
+    }
+    free(row);
+}
+
+/* y[t][o] = sum_i deq(W)[o][i] * x[t][i], the loop of ref_model.cpp:100-119:
+ * one dequantised row at a time, dotted against every token, rows split by
+ * parallel_for(out, grain 16). */
+void o_q4_linear(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, const float *x, int T,
+                 int ldx, float *y, int ldy, int threads) {
+    lin_ctx c = {W, S, Z, K, x, T, ldx, y, ldy, NULL};
+    parallel_for(threads, N, 16, lin_range, &c);
+}
+
+static void lin_range_f64(void *vc, int64_t b, int64_t e) {
+    lin_ctx *c = (lin_ctx *)vc;
+    float *row = (float *)malloc(sizeof(float) * (size_t)c->K);
+    for (int64_t o = b; o < e; ++o) {
+        dequant_row(c->W, c->S, c->Z, o, c->K, row);
+        for (int t = 0; t < c->T; ++t) {
+            double s = 0.0;
+            const float *xt = c->x + (size_t)t * c->ldx;
+            for (int64_t i = 0; i < c->K; ++i) s += (double)row[i] * (double)xt[i];
+            c->yd[(size_t)t * c->ldy + o] = s;
+        }
+    }
+    free(row);
+}
+
+/* The same product as an fp64 brute-force dot on the exact fp32 weights (the
+ * method of tests/gpu/test_gemv.hip:57-65): a second, independent answer. */
+void o_q4_linear_f64(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, const float *x,
+                     int T, int ldx, double *y, int ldy, int threads) {
+    lin_ctx c = {W, S, Z, K, x, T, ldx, NULL, ldy, y};
+    parallel_for(threads, N, 16, lin_range_f64, &c);
+}
+
+/* ------------------------------------------------ weight conversion */
+
+/* weight_convert.cpp:61-71: checkpoint order (element 8c+i at bits 4i) to the
+ * reference engine's order (even elements in the low half-word, odd ones in
+ * the high half-word). */
+void o_pack_engine_order(const uint32_t *ct, uint32_t *out, int64_t n_words) {
+    for (int64_t i = 0; i < n_words; ++i) {
+        uint32_t w = ct[i], r = 0;
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t nib = (w >> (4 * k)) & 0xfu;
+            const int bit = (k & 1) ? 16 + 4 * (k >> 1) : 4 * (k >> 1);
+            r |= nib << bit;
+        }
+        out[i] = r;
+    }
+}
+
+/* The inverse: reference engine order back to checkpoint order. */
+void o_unpack_engine_order(const uint32_t *eng, uint32_t *out, int64_t n_words) {
+    for (int64_t i = 0; i < n_words; ++i) {
+        uint32_t w = eng[i], r = 0;
+        for (int k = 0; k < 8; ++k) {
+            const int bit = (k & 1) ? 16 + 4 * (k >> 1) : 4 * (k >> 1);
+            r |= ((w >> bit) & 0xfu) << (4 * k);
+        }
+        out[i] = r;
+    }
+}
+
+/* weight_convert.cpp:73-90: symmetric int4 g128 (scale = amax/7 as fp16,
+ * q = clamp(lrint(x/scale), -8, 7) + 8), checkpoint word order. */
+void o_quantize_g128(const uint16_t *src_bf16, int64_t n_groups, uint32_t *words, uint16_t *scales) {
+    for (int64_t g = 0; g < n_groups; ++g) {
+        const uint16_t *x = src_bf16 + g * QGROUP;
+        float amax = 0.f;
+        for (int k = 0; k < QGROUP; ++k) {
+            const float a = fabsf(o_bf16_to_f32(x[k]));
+            amax = a > amax ? a : amax;
+        }
+        const uint16_t sc16 = o_f32_to_f16(amax / 7.f);
+        const float sc = o_f16_to_f32(sc16), inv = sc > 0.f ? 1.f / sc : 0.f;
+        for (int k = 0; k < QGROUP; k += 8) {
+            uint32_t word = 0;
+            for (int j = 0; j < 8; ++j) {
+                long q = lrintf(o_bf16_to_f32(x[k + j]) * inv);
+                q = q < -8 ? -8 : (q > 7 ? 7 : q);
+                word |= (uint32_t)(q + 8) << (4 * j);
+            }
+            words[(g * QGROUP + k) / 8] = word;
+        }
+        scales[g] = sc16;
+    }
+}
+
+/* ------------------------------------------------------------- routing */
+
+/* ref_model.cpp:412-431 for one token: p = exp(l - max) in fp32, the top k by
+ * (p descending, index ascending), weights float(p / sum_top p) with the sum
+ * in double in selection order. */
+void o_route(const float *logits, int T, int E, int topk, int32_t *top_e, float *top_w) {
+    float *pr = (float *)malloc(sizeof(float) * (size_t)E);
+    char *used = (char *)malloc((size_t)E);
+    for (int t = 0; t < T; ++t) {
+        const float *l = logits + (size_t)t * E;
+        float mx = l[0];
+        for (int e = 1; e < E; ++e) mx = l[e] > mx ? l[e] : mx;
+        for (int e = 0; e < E; ++e) pr[e] = expf(l[e] - mx);
+        memset(used, 0, (size_t)E);
+        /* selection sort of the first k: the same order partial_sort yields
+         * under the strict comparator (p desc, index asc). */
+        for (int i = 0; i < topk; ++i) {
+            int best = -1;
+            for (int e = 0; e < E; ++e) {
+                if (used[e]) continue;
+                if (best < 0 || pr[e] > pr[best]) best = e;
+            }
+            used[best] = 1;
+            top_e[(size_t)t * topk + i] = best;
+        }
+        double top = 0.0;
+        for (int i = 0; i < topk; ++i) top += (double)pr[top_e[(size_t)t * topk + i]];
+        for (int i = 0; i < topk; ++i)
+            top_w[(size_t)t * topk + i] = (float)((double)pr[top_e[(size_t)t * topk + i]] / top);
+    }
+    free(used);
+    free(pr);
+}
+
+/* Gather order of ref_model.cpp:411-431 (by_expert[e] filled in ascending
+ * token order) and of moe_route.hip:149-160: experts ascending, pairs of one
+ * expert in (token, k) order. counts[E], offsets[E+1], tok_slot[T*k],
+ * pair_tok[T*k]. */
+void o_moe_slots(const int32_t *top_e, int T, int E, int topk, int32_t *counts, int32_t *offsets, int32_t *tok_slot,
+                 int32_t *pair_tok) {
+    memset(counts, 0, sizeof(int32_t) * (size_t)E);
+    for (int i = 0; i < T * topk; ++i) counts[top_e[i]]++;
+    offsets[0] = 0;
+    for (int e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + counts[e];
+    int32_t *fill = (int32_t *)calloc((size_t)E, sizeof(int32_t));
+    for (int i = 0; i < T * topk; ++i) {
+        const int e = top_e[i];
+        const int slot = offsets[e] + fill[e]++;
+        tok_slot[i] = slot;
+        pair_tok[slot] = i / topk;
+    }
+    free(fill);
+}
+
+static float o_silu(float x) { return x * (1.f / (1.f + expf(-x))); }
+
+/* ref_model.cpp:406-463 without the shared expert (bf16 dense, not on the q4
+ * path): route, then for each expert in ascending order gather its tokens,
+ * g = gate x, u = up x, h = silu(g) u, y = down h, out[t] += w y.
+ * Weights per expert are contiguous: gate/up [E][F][H/8], down [E][H][F/8].
+ * Also returns h [T*k][F] and yp [T*k][H] in slot order when non-NULL. */
+void o_moe(const float *x, int T, int H, int F, int E, int topk, const float *logits, const uint32_t *gw,
+           const uint16_t *gs, const uint32_t *gz, const uint32_t *uw, const uint16_t *us, const uint32_t *uz,
+           const uint32_t *dw, const uint16_t *ds, const uint32_t *dz, float *out, float *h_out, float *yp_out,
+           int threads) {
+    const int P = T * topk;
+    int32_t *top_e = (int32_t *)malloc(sizeof(int32_t) * (size_t)P);
+    float *top_w = (float *)malloc(sizeof(float) * (size_t)P);
+    int32_t *counts = (int32_t *)malloc(sizeof(int32_t) * (size_t)E);
+    int32_t *offsets = (int32_t *)malloc(sizeof(int32_t) * (size_t)(E + 1));
+    int32_t *tok_slot = (int32_t *)malloc(sizeof(int32_t) * (size_t)P);
+    int32_t *pair_tok = (int32_t *)malloc(sizeof(int32_t) * (size_t)P);
+    o_route(logits, T, E, topk, top_e, top_w);
+    o_moe_slots(top_e, T, E, topk, counts, offsets, tok_slot, pair_tok);
+    float *slot_w = (float *)malloc(sizeof(float) * (size_t)P);
+    for (int i = 0; i < P; ++i) slot_w[tok_slot[i]] = top_w[i];
+
+    const int GH = H / QGROUP, GF = F / QGROUP;
+    const int zwH = (GH + 7) / 8, zwF = (GF + 7) / 8;
+    memset(out, 0, sizeof(float) * (size_t)T * (size_t)H);
+    float *xs = (float *)malloc(sizeof(float) * (size_t)T * (size_t)H);
+    float *g = (float *)malloc(sizeof(float) * (size_t)T * (size_t)F);
+    float *u = (float *)malloc(sizeof(float) * (size_t)T * (size_t)F);
+    float *y = (float *)malloc(sizeof(float) * (size_t)T * (size_t)H);
+    for (int e = 0; e < E; ++e) {
+        const int n = counts[e];
+        if (!n) continue;
+        const int base = offsets[e];
+        for (int i = 0; i < n; ++i) memcpy(xs + (size_t)i * H, x + (size_t)pair_tok[base + i] * H, sizeof(float) * (size_t)H);
+        const size_t guw = (size_t)e * F * (H / 8), gus = (size_t)e * F * GH, guz = (size_t)e * F * zwH;
+        o_q4_linear(gw + guw, gs + gus, gz ? gz + guz : NULL, F, H, xs, n, H, g, F, threads);
+        o_q4_linear(uw + guw, us + gus, uz ? uz + guz : NULL, F, H, xs, n, H, u, F, threads);
+        for (size_t i = 0; i < (size_t)n * F; ++i) g[i] = o_silu(g[i]) * u[i];
+        const size_t dww = (size_t)e * H * (F / 8), dss = (size_t)e * H * GF, dzz = (size_t)e * H * zwF;
+        o_q4_linear(dw + dww, ds + dss, dz ? dz + dzz : NULL, H, F, g, n, F, y, H, threads);
+        if (h_out) memcpy(h_out + (size_t)base * F, g, sizeof(float) * (size_t)n * F);
+        if (yp_out) memcpy(yp_out + (size_t)base * H, y, sizeof(float) * (size_t)n * H);
+        for (int i = 0; i < n; ++i) {
+            const float w = slot_w[base + i];
+            float *o = out + (size_t)pair_tok[base + i] * H;
+            for (int j = 0; j < H; ++j) o[j] += w * y[(size_t)i * H + j];
+        }
+    }
+    free(xs);
+    free(g);
+    free(u);
+    free(y);
+    free(slot_w);
+    free(top_e);
+    free(top_w);
+    free(counts);
+    free(offsets);
+    free(tok_slot);
+    free(pair_tok);
+}

@@ -1,0 +1,52 @@
+"""The C-ABI library: loads, exports every declared symbol, rejects bad
+arguments with a message (host-side checks only; no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import qwq4
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qw", "q4ops.h")
+
+
+def declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return set(re.findall(r"\b(qw_\w+)\s*\(", src))
+
+
+def test_exports_every_declared_symbol():
+    L = qwq4.lib()
+    names = declared()
+    assert names == set(qwq4.SYMBOLS)
+    for n in names:
+        assert getattr(L, n) is not None
+
+
+def test_abi_version():
+    assert qwq4.lib().qw_q4_abi_version() == 1
+
+
+@pytest.mark.parametrize("call", [
+    lambda L: L.qw_q4_gemv(None, None, None, None, 4096, None, 4096, 0, 4096, 4096, 1, 0, None),
+    lambda L: L.qw_q4_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(256), 4096,
+                           ctypes.c_void_p(256), 4096, 0, 4096, 4000, 1, 0, None),
+    lambda L: L.qw_q4_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(256), 4096,
+                           ctypes.c_void_p(256), 4096, 0, 4096, 4096, 33, 0, None),
+    lambda L: L.qw_moe_route(ctypes.c_void_p(256), 4, 256, 0, 0, *([ctypes.c_void_p(256)] * 11), None),
+    lambda L: L.qw_moe_combine(None, None, None, None, 1, 8, 4096, None, 1, None),
+    lambda L: L.qw_q4_gemm(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(256), 4096, 4096,
+                           ctypes.c_void_p(256), 4096, 1, 4096, 4096, None, 0, None),
+])
+def test_bad_arguments_are_rejected(call):
+    L = qwq4.lib()
+    assert call(L) == -1
+    assert len(L.qw_q4_last_error()) > 0
+
+
+def test_workspace_sizes():
+    assert qwq4.gemm_workspace_size(4096, 4096) >= 4096 * 4096 * 2
+    assert qwq4.lib().qw_q4_gemm_workspace_size(0, 4096) == 0

@@ -1,0 +1,46 @@
+"""q4 prefill GEMM (qw_q4_gemm) and the grouped expert GEMM against the oracle."""
+import numpy as np
+import pytest
+
+import qwq4
+from qwq4 import synth
+from _gpu_util import TOL, bf16_err_ok, host, rel_err, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("T,N,K", [(1, 256, 512), (200, 384, 1024), (512, 1024, 4096), (333, 4096, 6144)])
+def test_gemm_small_full_check(gpu, oracle, T, N, K):
+    print(f"gemm T={T} N={N} K={K}", flush=True)
+    W, S, Z = synth.q4_weights(51, f"g{N}x{K}", N, K)
+    xb, xf = synth.acts(51, f"x{T}x{K}", T, K)
+    Y = host(qwq4.gemm(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), to_dev(xb, gpu), N, K))
+    assert rel_err(Y, oracle.q4_linear(W, S, Z, N, K, xf)) <= TOL
+
+
+@pytest.mark.parametrize("N,K", [(12288, 4096), (4096, 6144)])
+def test_gemm_prefill_chunk_sampled(gpu, oracle, N, K):
+    """4096-token chunk, bf16 out; checked on sampled tokens and rows (fp64 oracle)."""
+    T = 4096
+    W, S, Z = synth.q4_weights(52, f"p{N}x{K}", N, K)
+    xb, xf = synth.acts(52, f"px{K}", T, K)
+    Y = host(qwq4.gemm(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), to_dev(xb, gpu), N, K, y_bf16=True))
+    r = np.random.default_rng(0)
+    toks = np.sort(r.choice(T, 48, replace=False))
+    rows = np.sort(r.choice(N, 512, replace=False))
+    ref = oracle.q4_linear(W[rows], S[rows], Z[rows], len(rows), K, xf[toks])
+    assert bf16_err_ok(Y[np.ix_(toks, rows)], ref)
+
+
+def test_grouped_matches_oracle_small(gpu, oracle):
+    E, H, F, k, T = 16, 512, 256, 4, 300
+    ex = synth.experts(61, E, H, F)
+    xb, xf = synth.acts(61, "x", T, H)
+    l = synth.router_logits(61, "l", T, E, bias_sigma=0.5)
+    out, h_ref, yp_ref = oracle.moe(xf, l, k, *ex, want_parts=True)
+    dex = [tuple(to_dev(a, gpu) for a in w) for w in ex]
+    r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=qwq4.moe_grouped_tile_m())
+    h, yp = qwq4.moe_experts_grouped(*dex, r, to_dev(xb, gpu))
+    assert rel_err(host(yp), yp_ref) <= TOL
+    o = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
+    assert rel_err(o, out) <= TOL

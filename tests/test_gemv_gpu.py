@@ -1,0 +1,93 @@
+"""q4 GEMV (qw_q4_gemv) against the CPU oracle (decode projections, LM head)."""
+import numpy as np
+import pytest
+
+import qwq4
+from qwq4 import synth
+from _gpu_util import TOL, bf16_err_ok, host, rel_err, to_dev
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(256, 512), (384, 128), (4096, 4096), (12288, 4096), (4096, 6144), (1536, 4096), (4096, 1536)]
+
+
+def _setup(dev, N, K, M, zeros=True, seed=11):
+    W, S, Z = synth.q4_weights(seed, f"w{N}x{K}", N, K, zeros)
+    xb, xf = synth.acts(seed, f"x{M}x{K}", M, K)
+    return (W, S, Z, xb, xf), (to_dev(W, dev), to_dev(S, dev), to_dev(Z, dev), to_dev(xb, dev))
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("M", [1, 2, 4, 6, 8])
+def test_gemv_fp32(gpu, oracle, N, K, M):
+    print(f"gemv N={N} K={K} M={M}", flush=True)
+    (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M)
+    y = host(qwq4.gemv(dW, dS, dZ, dx, N, K, M))
+    r = oracle.q4_linear(W, S, Z, N, K, xf)
+    assert rel_err(y, r) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 8, 16, 17, 32])
+def test_gemv_symmetric_and_wide(gpu, oracle, M):
+    N, K = 1024, 2048
+    (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M, zeros=False)
+    y = host(qwq4.gemv(dW, dS, None, dx, N, K, M))
+    r = oracle.q4_linear(W, S, None, N, K, xf)
+    assert rel_err(y, r) <= TOL
+
+
+def test_gemv_bf16_out_is_rne_of_fp32(gpu, oracle):
+    N, K, M = 4096, 4096, 4
+    (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M)
+    y32 = host(qwq4.gemv(dW, dS, dZ, dx, N, K, M))
+    y16 = qwq4.gemv(dW, dS, dZ, dx, N, K, M, y_bf16=True)
+    bits = host(y16).view(np.uint32) >> 16
+    assert np.array_equal(bits.astype(np.uint16), synth.bf16_bits(y32))
+    assert bf16_err_ok(host(y16), oracle.q4_linear(W, S, Z, N, K, xf))
+
+
+def test_gemv_lm_head(gpu, oracle):
+    N, K, M = 151936, 4096, 2
+    (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M)
+    y = host(qwq4.gemv(dW, dS, dZ, dx, N, K, M, y_bf16=True))
+    r = oracle.q4_linear(W, S, Z, N, K, xf)
+    assert bf16_err_ok(y, r)
+
+
+def test_gemv_rows_independent_bit_exact(gpu):
+    N, K, M = 2048, 4096, 8
+    (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M)
+    y8 = host(qwq4.gemv(dW, dS, dZ, dx, N, K, M))
+    for m in (0, 5, 7):
+        y1 = host(qwq4.gemv(dW, dS, dZ, dx[m:m + 1].contiguous(), N, K, 1))
+        assert np.array_equal(y1[0].view(np.uint32), y8[m].view(np.uint32))
+
+
+def test_gemv_strides_accumulate_and_guard(gpu, oracle):
+    import torch
+    N, K, M = 1000, 1024, 3   # N not a multiple of 16
+    (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M)
+    xs = K + 64
+    xpad = torch.zeros((M, xs), dtype=torch.int16, device=gpu)
+    xpad[:, :K] = dx
+    ys = N + 24
+    y = torch.full((M, ys), 12345.0, device=gpu)
+    y[:, :N] = 1.5
+    qwq4.gemv(dW, dS, dZ, xpad, N, K, M, y=y, accumulate=True, xs=xs, ys=ys)
+    yh = host(y)
+    assert np.all(yh[:, N:] == 12345.0)  # no stray writes past N
+    r = oracle.q4_linear(W, S, Z, N, K, xf) + 1.5
+    assert rel_err(yh[:, :N], r) <= TOL
+
+
+def test_gemv_special_inputs(gpu, oracle):
+    import torch
+    N, K = 512, 1024
+    W, S, Z = synth.q4_weights(12, "sp", N, K)
+    dW, dS, dZ = to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu)
+    x = np.zeros((2, K), np.float32)
+    x[1, 777] = 1.0
+    y = host(qwq4.gemv(dW, dS, dZ, to_dev(synth.bf16_bits(x), gpu), N, K, 2))
+    assert np.all(y[0] == 0)
+    deq = oracle.q4_dequant(W, S, Z, N, K)
+    assert np.array_equal(y[1], deq[:, 777])  # one-hot: a column, exactly

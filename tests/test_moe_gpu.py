@@ -1,0 +1,95 @@
+"""MoE decode path: routing (bit-exact), gathered expert GEMVs, combine."""
+import numpy as np
+import pytest
+
+import qwq4
+from qwq4 import synth
+from _gpu_util import TOL, bf16_err_ok, host, rel_err, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _experts_dev(dev, ex):
+    return [tuple(to_dev(a, dev) for a in w) for w in ex]
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 256, 8), (7, 256, 8), (32, 256, 8), (64, 128, 4), (100, 512, 10),
+                                   (4096, 256, 8)])
+def test_route_bit_exact(gpu, oracle, T, E, k):
+    print(f"route T={T} E={E} k={k}", flush=True)
+    l = synth.router_logits(31, f"l{T}", T, E, bias_sigma=0.5 if T > 64 else 0.0)
+    if T == 7:
+        l[2, :] = 0.0          # all-equal logits: ties to the lower index
+        l[3, [5, 9, 200]] = 9.0
+    r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=32 if T > 64 else 0)
+    te, tw = oracle.route(l, k)
+    assert np.array_equal(host(r.top_e), te)
+    assert np.array_equal(host(r.top_w).view(np.uint32), tw.view(np.uint32))
+    counts, offsets, tok_slot, pair_tok = oracle.moe_slots(te, E)
+    assert np.array_equal(host(r.counts), counts)
+    assert np.array_equal(host(r.offsets), offsets)
+    assert np.array_equal(host(r.tok_slot), tok_slot)
+    assert np.array_equal(host(r.pair_tok), pair_tok)
+    na = int(host(r.n_active)[0])
+    assert np.array_equal(host(r.active)[:na], np.nonzero(counts)[0])
+    if T > 64:
+        nt = int(host(r.n_tiles)[0])
+        want = [(e, m0) for e in range(E) for m0 in range(0, counts[e], 32)]
+        got = list(zip(host(r.tile_e)[:nt], host(r.tile_m0)[:nt]))
+        assert got == want
+
+
+def _unperm_h(h):
+    """library h order -> natural: element e of each 8-chunk sits at op_pos(e)."""
+    pos = np.array([(e >> 1) + 4 * (e & 1) for e in range(8)])
+    hh = h.reshape(h.shape[0], -1, 8)
+    return hh[:, :, pos].reshape(h.shape)
+
+
+@pytest.mark.parametrize("T", [1, 2, 4, 8, 16, 32])
+def test_experts_gemv_and_combine(gpu, oracle, T):
+    E, H, F, k = 64, 1024, 512, 8
+    print(f"moe gemv T={T}", flush=True)
+    ex = synth.experts(41, E, H, F)
+    xb, xf = synth.acts(41, f"x{T}", T, H)
+    l = synth.router_logits(41, f"l{T}", T, E)
+    out, h_ref, yp_ref = oracle.moe(xf, l, k, *ex, want_parts=True)
+    dex = _experts_dev(gpu, ex)
+    dx = to_dev(xb, gpu)
+    r = qwq4.moe_route(to_dev(l, gpu), k)
+    h, yp = qwq4.moe_experts_gemv(*dex, r, dx)
+    hh = _unperm_h(host(h).astype(np.float32))
+    assert rel_err(hh, h_ref) <= TOL
+    assert rel_err(host(yp), yp_ref) <= TOL
+    o32 = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
+    assert rel_err(o32, out) <= TOL
+    o16 = host(qwq4.moe_combine(yp, r, H, out_bf16=True))
+    assert bf16_err_ok(o16, out)
+
+
+def test_experts_full_config(gpu, oracle):
+    """256 experts, H=4096, F=1536, top-8, batch 8, symmetric and zero-point weights."""
+    E, H, F, k, T = 256, 4096, 1536, 8, 8
+    ex = synth.experts(42, E, H, F)
+    xb, xf = synth.acts(42, "x", T, H)
+    l = synth.router_logits(42, "l", T, E)
+    out = oracle.moe(xf, l, k, *ex)
+    dex = _experts_dev(gpu, ex)
+    r = qwq4.moe_route(to_dev(l, gpu), k)
+    h, yp = qwq4.moe_experts_gemv(*dex, r, to_dev(xb, gpu))
+    o = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
+    assert rel_err(o, out) <= TOL
+
+
+def test_combine_with_shared(gpu):
+    import torch
+    T, k, H = 3, 2, 64
+    yp = torch.arange(T * k * H, dtype=torch.float32, device=gpu).reshape(T * k, H) / 100
+    r = qwq4.Route(T, 8, k, gpu)
+    r.tok_slot.copy_(torch.tensor([[1, 0], [3, 2], [5, 4]], dtype=torch.int32))
+    r.top_w.copy_(torch.tensor([[0.25, 0.75], [0.5, 0.5], [1.0, 0.0]]))
+    shared = torch.ones((T, H), device=gpu)
+    o = host(qwq4.moe_combine(yp, r, H, shared=shared, out_bf16=False))
+    y = host(yp)
+    want = np.stack([1 + 0.25 * y[1] + 0.75 * y[0], 1 + 0.5 * y[3] + 0.5 * y[2], 1 + y[5] + 0 * y[4]])
+    assert np.allclose(o, want, rtol=1e-6)

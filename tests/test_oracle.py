@@ -1,0 +1,176 @@
+"""CPU oracle pinned against the reference's own code (golden vectors from
+oracle/_ref, see tests/golden/make_golden.py), independent library routines
+(numpy, torch) and closed forms."""
+import os
+
+import numpy as np
+import pytest
+
+from qwq4 import synth
+
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz"))
+
+
+# ---------------------------------------------------------------- numbers
+def test_f16_to_f32_matches_reference_on_every_pattern(oracle):
+    got = np.array([oracle.lib().o_f16_to_f32(int(v)) for v in GOLD["f16_all"]], np.float32)
+    assert np.array_equal(got.view(np.uint32), GOLD["f16_all_f32"].view(np.uint32))
+    # and numpy's own fp16 widening agrees wherever it is not NaN
+    npv = GOLD["f16_all"].view(np.float16).astype(np.float32)
+    ok = ~np.isnan(npv)
+    assert np.array_equal(npv[ok].view(np.uint32), got[ok].view(np.uint32))
+
+
+def test_f32_to_f16_matches_reference(oracle):
+    got = oracle.f32_to_f16(GOLD["f32_in"])
+    assert np.array_equal(got, GOLD["f32_to_f16"])
+    x = GOLD["f32_in"]
+    ok = ~np.isnan(x)
+    assert np.array_equal(x[ok].astype(np.float16).view(np.uint16), got[ok])
+
+
+def test_f32_to_bf16_is_round_to_nearest_even(oracle):
+    import torch
+    r = np.random.default_rng(5)
+    x = np.concatenate([r.normal(0, 1, 3000), r.normal(0, 1, 1000) * 1e30,
+                        [1 + 2**-8, 1 + 3 * 2**-8, -(1 + 2**-8), 0.0, -0.0, 3.3895314e38, np.inf]]).astype(np.float32)
+    got = oracle.f32_to_bf16(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    assert np.array_equal(synth.bf16_bits(x), want)
+    assert got[-7] == 0x3F80 and got[-6] == 0x3F82  # ties to even
+
+
+# ------------------------------------------------------------ q4 format
+def test_engine_order_matches_reference(oracle):
+    assert np.array_equal(oracle.pack_engine_order(GOLD["words_in"]), GOLD["words_eng"])
+    assert np.array_equal(oracle.unpack_engine_order(GOLD["words_eng"]), GOLD["words_in"])
+
+
+def test_quantizer_matches_reference(oracle):
+    words, scales = oracle.quantize_g128(GOLD["qsrc"])
+    assert np.array_equal(words, GOLD["q_words"])
+    assert np.array_equal(scales, GOLD["q_scales"])
+
+
+def test_unpack_against_byte_view(oracle):
+    W, _, _ = synth.q4_weights(1, "u", 24, 512)
+    got = oracle.q4_unpack(W, 24, 512)
+    b = W.view(np.uint8).reshape(24, 256)  # little-endian: byte j holds elements 2j (low) and 2j+1 (high)
+    want = np.stack([b & 0xF, b >> 4], axis=-1).reshape(24, 512)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("zeros", [False, True])
+def test_dequant_closed_form(oracle, zeros):
+    N, K = 16, 384
+    W, S, Z = synth.q4_weights(2, "d", N, K, zeros)
+    got = oracle.q4_dequant(W, S, Z, N, K)
+    q = oracle.q4_unpack(W, N, K).astype(np.int32)
+    z = synth.unpack_zeros(Z, K // 128).astype(np.int32) if zeros else np.full((N, K // 128), 8, np.int32)
+    s = S.view(np.float16).astype(np.float32)
+    want = ((q - np.repeat(z, 128, axis=1)).astype(np.float32) * np.repeat(s, 128, axis=1)).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_special_cases(oracle):
+    N, K = 8, 256
+    W, S, Z = synth.q4_weights(3, "s", N, K)
+    S[:, 0] = 0                                   # scale 0 -> exact zeros
+    q = oracle.q4_unpack(W, N, K)
+    z = np.zeros((N, 2), np.uint8)
+    z[:, 1] = q[:, 128]                           # zero equal to one element's nibble
+    Zp = synth.pack_zeros(z)
+    d = oracle.q4_dequant(W, S, Zp, N, K)
+    assert np.all(d[:, :128] == 0)
+    assert np.all(d[:, 128] == 0)
+
+
+def test_linear_vs_fp64_and_numpy(oracle):
+    N, K, T = 96, 1024, 3
+    W, S, Z = synth.q4_weights(4, "l", N, K)
+    _, x = synth.acts(4, "x", T, K)
+    y = oracle.q4_linear(W, S, Z, N, K, x)
+    y64 = oracle.q4_linear_f64(W, S, Z, N, K, x)
+    deq = oracle.q4_dequant(W, S, Z, N, K).astype(np.float64)
+    ref = x.astype(np.float64) @ deq.T
+    assert np.max(np.abs(y64 - ref)) <= 1e-9 * np.max(np.abs(ref))
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+def test_linear_exact_cases(oracle):
+    N, K = 32, 512
+    W, S, Z = synth.q4_weights(5, "e", N, K)
+    # one-hot x picks column k exactly: s * (q - z)
+    x = np.zeros((1, K), np.float32)
+    x[0, 300] = 1.0
+    y = oracle.q4_linear(W, S, Z, N, K, x)
+    deq = oracle.q4_dequant(W, S, Z, N, K)
+    assert np.array_equal(y[0], deq[:, 300])
+    # integer activations with unit scales: every partial sum is an exact integer
+    S1 = np.full_like(S, 0x3C00)  # fp16 1.0
+    xi = np.random.default_rng(0).integers(-8, 9, size=(2, K)).astype(np.float32)
+    yi = oracle.q4_linear(W, S1, Z, N, K, xi)
+    q = oracle.q4_unpack(W, N, K).astype(np.int64) - np.repeat(synth.unpack_zeros(Z, K // 128).astype(np.int64), 128, 1)
+    assert np.array_equal(yi.astype(np.int64), xi.astype(np.int64) @ q.T)
+    # zero activations
+    assert np.all(oracle.q4_linear(W, S, Z, N, K, np.zeros((1, K), np.float32)) == 0)
+
+
+# ------------------------------------------------------------- routing
+def test_route_order_and_weights(oracle):
+    T, E, k = 64, 256, 8
+    l = synth.router_logits(6, "r", T, E)
+    te, tw = oracle.route(l, k)
+    # exp is monotone: with no two selected probabilities equal, the order is
+    # the logits' order (ties to the lower index)
+    order = np.lexsort((np.arange(E)[None, :].repeat(T, 0), -l), axis=1)[:, :k]
+    assert np.array_equal(te, order)
+    p = np.exp((l - l.max(1, keepdims=True)).astype(np.float64))
+    sel = np.take_along_axis(p, te, 1)
+    assert np.allclose(tw, sel / sel.sum(1, keepdims=True), rtol=1e-6, atol=0)
+    assert np.allclose(tw.astype(np.float64).sum(1), 1.0, atol=1e-6)
+
+
+def test_route_ties_to_lower_index(oracle):
+    l = np.zeros((2, 16), np.float32)
+    l[0, [3, 7, 11]] = 2.0
+    te, tw = oracle.route(l, 4)
+    assert list(te[0]) == [3, 7, 11, 0]
+    assert list(te[1]) == [0, 1, 2, 3]
+    assert np.all(tw[1] == np.float32(0.25))
+
+
+def test_slots_invariants(oracle):
+    T, E, k = 40, 32, 4
+    te, _ = oracle.route(synth.router_logits(7, "s", T, E), k)
+    counts, offsets, tok_slot, pair_tok = oracle.moe_slots(te, E)
+    assert np.array_equal(counts, np.bincount(te.ravel(), minlength=E))
+    assert np.array_equal(offsets, np.concatenate([[0], np.cumsum(counts)]))
+    assert np.array_equal(np.sort(tok_slot.ravel()), np.arange(T * k))
+    for t in range(T):
+        for j in range(k):
+            s = tok_slot[t, j]
+            assert pair_tok[s] == t and offsets[te[t, j]] <= s < offsets[te[t, j] + 1]
+    for e in range(E):  # tokens ascending within an expert
+        seg = pair_tok[offsets[e]:offsets[e + 1]]
+        assert np.all(np.diff(seg) > 0)
+
+
+def test_moe_vs_dense_numpy(oracle):
+    T, E, H, F, k = 5, 8, 256, 256, 2
+    gate, up, down = synth.experts(8, E, H, F)
+    _, x = synth.acts(8, "x", T, H)
+    l = synth.router_logits(8, "l", T, E)
+    out = oracle.moe(x, l, k, gate, up, down)
+    te, tw = oracle.route(l, k)
+    deq = lambda w, n, kk: oracle.q4_dequant(w[0][e], w[1][e], w[2][e], n, kk).astype(np.float64)
+    ref = np.zeros((T, H))
+    for t in range(T):
+        for j in range(k):
+            e = te[t, j]
+            g = deq(gate, F, H) @ x[t]
+            u = deq(up, F, H) @ x[t]
+            h = g / (1 + np.exp(-g)) * u
+            ref[t] += tw[t, j] * (deq(down, H, F) @ h)
+    assert np.max(np.abs(out - ref)) <= 1e-5 * np.max(np.abs(ref))

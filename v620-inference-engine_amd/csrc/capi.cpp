@@ -1,0 +1,194 @@
+// C-ABI layer (include/qw/q4ops.h): argument checks, then one launch per
+// kernel on the caller's stream. Nothing here allocates or synchronises.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "q4_kernels.hpp"
+#include "qw/q4ops.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return QW_Q4_EINVAL;
+}
+
+int launched(const char *what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        g_err = std::string(what) + ": " + hipGetErrorString(e);
+        return QW_Q4_ELAUNCH;
+    }
+    g_err.clear();
+    return QW_Q4_OK;
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+hipStream_t st(void *s) { return static_cast<hipStream_t>(s); }
+
+#define REQUIRE(cond, ...)                             \
+    do {                                               \
+        if (!(cond)) return fail(__VA_ARGS__);         \
+    } while (0)
+
+int check_q4(const char *fn, const uint32_t *W, const uint16_t *S, int64_t N, int64_t K) {
+    REQUIRE(W && S, "%s: null weight or scale pointer", fn);
+    REQUIRE(N >= 1, "%s: N = %lld must be >= 1", fn, (long long)N);
+    REQUIRE(K >= 128 && K % 128 == 0, "%s: K = %lld must be a positive multiple of 128", fn, (long long)K);
+    REQUIRE(aligned(W, 16), "%s: W must be 16-byte aligned", fn);
+    REQUIRE(aligned(S, 2), "%s: S must be 2-byte aligned", fn);
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qw_q4_abi_version(void) { return 1; }
+
+const char *qw_q4_last_error(void) { return g_err.c_str(); }
+
+int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint32_t *Z, const uint16_t *x, int xs, void *y, int ys,
+               int y_bf16, int N, int K, int M, int accumulate, void *stream) {
+    if (int r = check_q4("qw_q4_gemv", W, S, N, K)) return r;
+    REQUIRE(x && y, "qw_q4_gemv: null x or y");
+    REQUIRE(M >= 1 && M <= 32, "qw_q4_gemv: M = %d outside 1..32", M);
+    REQUIRE(xs >= K && xs % 8 == 0 && aligned(x, 16), "qw_q4_gemv: x stride %d must be >= K, a multiple of 8, x 16-byte aligned", xs);
+    REQUIRE(ys >= N || M == 1, "qw_q4_gemv: y stride %d < N", ys);
+    REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_q4_gemv: y misaligned");
+    qwq4::GemvArgs a{W, S, Z, x, xs, y, ys, y_bf16 != 0, N, K, M, accumulate != 0};
+    qwq4::launch_gemv(a, st(stream));
+    return launched("qw_q4_gemv");
+}
+
+size_t qw_q4_gemm_workspace_size(int T, int K) {
+    if (T < 1 || K < 128) return 0;
+    return qwq4::gemm_workspace_bytes(T, K);
+}
+
+int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint32_t *Z, const uint16_t *X, int ldx, int T, void *Y,
+               int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream) {
+    if (int r = check_q4("qw_q4_gemm", W, S, N, K)) return r;
+    REQUIRE(X && Y, "qw_q4_gemm: null X or Y");
+    REQUIRE(T >= 1, "qw_q4_gemm: T = %d must be >= 1", T);
+    REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(X, 16), "qw_q4_gemm: ldx %d must be >= K, a multiple of 8, X 16-byte aligned", ldx);
+    REQUIRE(ldy >= N, "qw_q4_gemm: ldy %d < N", ldy);
+    REQUIRE(aligned(Y, y_bf16 ? 2 : 4), "qw_q4_gemm: Y misaligned");
+    const size_t need = qwq4::gemm_workspace_bytes(T, K);
+    REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256),
+            "qw_q4_gemm: workspace needs %zu bytes, 256-byte aligned (got %zu)", need, workspace_bytes);
+    qwq4::GemmArgs a{W, S, Z, X, ldx, T, Y, ldy, y_bf16 != 0, N, K, workspace};
+    qwq4::launch_gemm(a, st(stream));
+    return launched("qw_q4_gemm");
+}
+
+int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_t *top_e, float *top_w,
+                 int32_t *counts, int32_t *offsets, int32_t *tok_slot, int32_t *pair_tok, int32_t *active,
+                 int32_t *n_active, int32_t *tile_e, int32_t *tile_m0, int32_t *n_tiles, void *stream) {
+    REQUIRE(logits && top_e && top_w && counts && offsets && tok_slot && pair_tok && active && n_active,
+            "qw_moe_route: null pointer");
+    REQUIRE(T >= 1 && E >= 1 && E <= 1024, "qw_moe_route: T = %d, E = %d (need T >= 1, 1 <= E <= 1024)", T, E);
+    REQUIRE(topk >= 1 && topk <= E && topk <= 64, "qw_moe_route: topk = %d outside 1..min(E, 64)", topk);
+    REQUIRE(tile_m >= 0, "qw_moe_route: tile_m < 0");
+    REQUIRE(tile_m == 0 || (tile_e && tile_m0 && n_tiles), "qw_moe_route: tile_m > 0 needs the tile outputs");
+    REQUIRE(int64_t(T) * topk < (1 << 30), "qw_moe_route: too many pairs");
+    const size_t lds = qwq4::route_lds_bytes(T, E) + (T <= 64 ? 64 * 64 * 4 : 0);
+    REQUIRE(lds <= 160 * 1024, "qw_moe_route: T = %d, E = %d needs %zu bytes of LDS (> 160 KiB)", T, E, lds);
+    qwq4::RouteArgs a{logits, T, E, topk, tile_m, top_e, top_w, counts, offsets, tok_slot, pair_tok, active,
+                      n_active, tile_e, tile_m0, n_tiles};
+    qwq4::launch_route(a, st(stream));
+    return launched("qw_moe_route");
+}
+
+int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint32_t *gz, const uint32_t *uw,
+                        const uint16_t *us, const uint32_t *uz, const uint32_t *dw, const uint16_t *ds,
+                        const uint32_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
+                        const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int T, int topk,
+                        uint16_t *h, float *yp, void *stream) {
+    if (int r = check_q4("qw_moe_experts_gemv(gate)", gw, gs, int64_t(E) * F, H)) return r;
+    if (int r = check_q4("qw_moe_experts_gemv(up)", uw, us, int64_t(E) * F, H)) return r;
+    if (int r = check_q4("qw_moe_experts_gemv(down)", dw, ds, int64_t(E) * H, F)) return r;
+    REQUIRE(offsets && active && n_active && pair_tok && x && h && yp, "qw_moe_experts_gemv: null pointer");
+    REQUIRE(T >= 1 && T <= 32, "qw_moe_experts_gemv: T = %d outside 1..32", T);
+    REQUIRE(topk >= 1 && topk <= E, "qw_moe_experts_gemv: topk = %d outside 1..E", topk);
+    REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(yp, 4), "qw_moe_experts_gemv: x/h must be 16-byte aligned");
+    qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, offsets, active, n_active, pair_tok,
+                        x, T, topk, h, yp};
+    qwq4::launch_moe_gemv(a, st(stream));
+    return launched("qw_moe_experts_gemv");
+}
+
+size_t qw_moe_grouped_workspace_size(int T, int topk, int E, int H, int F) {
+    if (T < 1 || topk < 1 || E < 1) return 0;
+    return qwq4::moe_grouped_workspace_bytes(T, topk, E, H, F);
+}
+
+int qw_moe_grouped_tile_m(void) { return qwq4::moe_grouped_tile_m(); }
+
+int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint32_t *gz, const uint32_t *uw,
+                           const uint16_t *us, const uint32_t *uz, const uint32_t *dw, const uint16_t *ds,
+                           const uint32_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
+                           const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
+                           int T, int topk, uint16_t *h, float *yp, void *workspace, size_t workspace_bytes,
+                           void *stream) {
+    if (int r = check_q4("qw_moe_experts_grouped(gate)", gw, gs, int64_t(E) * F, H)) return r;
+    if (int r = check_q4("qw_moe_experts_grouped(up)", uw, us, int64_t(E) * F, H)) return r;
+    if (int r = check_q4("qw_moe_experts_grouped(down)", dw, ds, int64_t(E) * H, F)) return r;
+    REQUIRE(offsets && pair_tok && tile_e && tile_m0 && n_tiles && x && h && yp,
+            "qw_moe_experts_grouped: null pointer");
+    REQUIRE(T >= 1 && topk >= 1 && topk <= E, "qw_moe_experts_grouped: T = %d, topk = %d", T, topk);
+    REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(yp, 4), "qw_moe_experts_grouped: x/h must be 16-byte aligned");
+    const size_t need = qwq4::moe_grouped_workspace_bytes(T, topk, E, H, F);
+    REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
+            "qw_moe_experts_grouped: workspace needs %zu bytes, 256-byte aligned", need);
+    qwq4::MoeGroupedArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, offsets, pair_tok, tile_e, tile_m0, n_tiles,
+                           x, T, topk, h, yp, workspace};
+    qwq4::launch_moe_grouped(a, st(stream));
+    return launched("qw_moe_experts_grouped");
+}
+
+int qw_moe_combine(const float *yp, const int32_t *tok_slot, const float *tok_w, const float *shared, int T, int topk,
+                   int H, void *out, int out_bf16, void *stream) {
+    REQUIRE(yp && tok_slot && tok_w && out, "qw_moe_combine: null pointer");
+    REQUIRE(T >= 1 && topk >= 1 && H >= 4 && H % 4 == 0, "qw_moe_combine: T = %d, topk = %d, H = %d (need H %% 4 == 0)", T,
+            topk, H);
+    REQUIRE(aligned(yp, 16) && (!shared || aligned(shared, 16)) && aligned(out, out_bf16 ? 8 : 16),
+            "qw_moe_combine: misaligned yp/shared/out");
+    qwq4::launch_combine(yp, tok_slot, tok_w, shared, T, topk, H, out, out_bf16 != 0, st(stream));
+    return launched("qw_moe_combine");
+}
+
+int qw_q4_unpack(const uint32_t *W, int64_t N, int64_t K, uint8_t *out, void *stream) {
+    REQUIRE(W && out && N >= 1 && K >= 8 && K % 8 == 0, "qw_q4_unpack: bad arguments");
+    REQUIRE(aligned(out, 8), "qw_q4_unpack: out must be 8-byte aligned");
+    qwq4::launch_unpack(W, N, K, out, st(stream));
+    return launched("qw_q4_unpack");
+}
+
+int qw_q4_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, float *out,
+                  void *stream) {
+    if (int r = check_q4("qw_q4_dequant", W, S, N, K)) return r;
+    REQUIRE(out && aligned(out, 16), "qw_q4_dequant: out must be 16-byte aligned");
+    qwq4::launch_dequant(W, S, Z, N, K, out, st(stream));
+    return launched("qw_q4_dequant");
+}
+
+int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream) {
+    REQUIRE(in && out && n_words >= 1, "qw_q4_from_engine_order: bad arguments");
+    qwq4::launch_from_engine_order(in, out, n_words, st(stream));
+    return launched("qw_q4_from_engine_order");
+}
+
+}  // extern "C"

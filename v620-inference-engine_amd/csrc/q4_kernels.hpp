@@ -1,0 +1,98 @@
+// Internal launcher interface between the C-ABI layer (capi.cpp) and the HIP
+// kernels. Shapes are validated by the caller (capi.cpp) before any launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace qwq4 {
+
+struct GemvArgs {
+    const uint32_t *W;
+    const uint16_t *S;
+    const uint32_t *Z;
+    const uint16_t *x;
+    int xs;
+    void *y;
+    int ys, y_bf16, N, K, M, accumulate;
+};
+void launch_gemv(const GemvArgs &a, hipStream_t s);
+
+struct MoeGemvArgs {
+    const uint32_t *gw;
+    const uint16_t *gs;
+    const uint32_t *gz;
+    const uint32_t *uw;
+    const uint16_t *us;
+    const uint32_t *uz;
+    const uint32_t *dw;
+    const uint16_t *ds;
+    const uint32_t *dz;
+    int E, H, F;
+    const int32_t *offsets, *active, *n_active, *pair_tok;
+    const uint16_t *x;
+    int T, topk;
+    uint16_t *h;
+    float *yp;
+};
+void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s);
+
+struct MoeGroupedArgs {
+    const uint32_t *gw;
+    const uint16_t *gs;
+    const uint32_t *gz;
+    const uint32_t *uw;
+    const uint16_t *us;
+    const uint32_t *uz;
+    const uint32_t *dw;
+    const uint16_t *ds;
+    const uint32_t *dz;
+    int E, H, F;
+    const int32_t *offsets, *pair_tok, *tile_e, *tile_m0, *n_tiles;
+    const uint16_t *x;
+    int T, topk;
+    uint16_t *h;
+    float *yp;
+    void *ws;
+};
+// Tokens per tile the grouped kernels expect in the routing tile list.
+int moe_grouped_tile_m();
+size_t moe_grouped_workspace_bytes(int T, int topk, int E, int H, int F);
+void launch_moe_grouped(const MoeGroupedArgs &a, hipStream_t s);
+
+struct RouteArgs {
+    const float *logits;
+    int T, E, topk, tile_m;
+    int32_t *top_e;
+    float *top_w;
+    int32_t *counts, *offsets, *tok_slot, *pair_tok, *active, *n_active;
+    int32_t *tile_e, *tile_m0, *n_tiles;
+};
+// LDS bytes the slot pass needs for (T, E); the C-ABI rejects larger inputs.
+size_t route_lds_bytes(int T, int E);
+void launch_route(const RouteArgs &a, hipStream_t s);
+
+void launch_combine(const float *yp, const int32_t *tok_slot, const float *tok_w, const float *shared, int T, int topk,
+                    int H, void *out, int out_bf16, hipStream_t s);
+
+void launch_unpack(const uint32_t *W, int64_t N, int64_t K, uint8_t *out, hipStream_t s);
+void launch_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, float *out,
+                    hipStream_t s);
+void launch_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, hipStream_t s);
+
+struct GemmArgs {
+    const uint32_t *W;
+    const uint16_t *S;
+    const uint32_t *Z;
+    const uint16_t *X;
+    int ldx, T;
+    void *Y;
+    int ldy, y_bf16, N, K;
+    void *ws;  // workspace: operand-ordered X and -BIAS * group sums
+};
+size_t gemm_workspace_bytes(int T, int K);
+void launch_gemm(const GemmArgs &a, hipStream_t s);
+
+}  // namespace qwq4

@@ -1,0 +1,221 @@
+"""Python binding of libqwq4.so (include/qw/q4ops.h) over ctypes.
+
+Device memory and streams come from PyTorch; every call goes through the C ABI
+to the HIP kernels. There is no fallback: if the library is missing or a call
+fails, a RuntimeError is raised.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libqwq4.so")
+_lib = None
+
+# every symbol include/qw/q4ops.h declares (checked by the CPU tests)
+SYMBOLS = (
+    "qw_q4_abi_version", "qw_q4_last_error", "qw_q4_gemv", "qw_q4_gemm_workspace_size", "qw_q4_gemm",
+    "qw_moe_route", "qw_moe_experts_gemv", "qw_moe_experts_grouped", "qw_moe_grouped_workspace_size", "qw_moe_grouped_tile_m",
+    "qw_moe_combine", "qw_q4_unpack", "qw_q4_dequant", "qw_q4_from_engine_order",
+)
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+
+_SIGS = {
+    "qw_q4_abi_version": ([], _I),
+    "qw_q4_last_error": ([], ctypes.c_char_p),
+    "qw_q4_gemv": ([_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_q4_gemm_workspace_size": ([_I, _I], _SZ),
+    "qw_q4_gemm": ([_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _SZ, _P], _I),
+    "qw_moe_route": ([_P, _I, _I, _I, _I] + [_P] * 11 + [_P], _I),
+    "qw_moe_experts_gemv": ([_P] * 9 + [_I, _I, _I] + [_P] * 5 + [_I, _I, _P, _P, _P], _I),
+    "qw_moe_grouped_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
+    "qw_moe_experts_grouped": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _P, _P, _P, _SZ, _P], _I),
+    "qw_moe_grouped_tile_m": ([], _I),
+    "qw_moe_combine": ([_P, _P, _P, _P, _I, _I, _I, _P, _I, _P], _I),
+    "qw_q4_unpack": ([_P, _I64, _I64, _P, _P], _I),
+    "qw_q4_dequant": ([_P, _P, _P, _I64, _I64, _P, _P], _I),
+    "qw_q4_from_engine_order": ([_P, _P, _I64, _P], _I),
+}
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with v620-inference-engine_amd/build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGS.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _check(rc, fn):
+    if rc != 0:
+        raise RuntimeError(f"{fn} failed ({rc}): {lib().qw_q4_last_error().decode()}")
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("qwq4: all tensors must be on the GPU")
+
+
+# ---------------------------------------------------------------- operators
+def gemv(W, S, Z, x, N, K, M=None, y=None, y_bf16=False, accumulate=False, xs=None, ys=None):
+    """y[m][n] (+)= sum_k deq(W)[n][k] x[m][k]. x: bf16-bits int16/uint16 or bfloat16 tensor."""
+    import torch
+    M = M if M is not None else x.shape[0]
+    xs = xs if xs is not None else x.stride(0) if x.dim() == 2 else K
+    if y is None:
+        y = torch.zeros((M, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=x.device)
+    ys = ys if ys is not None else (y.stride(0) if y.dim() == 2 else N)
+    _dev(W, S, Z, x, y)
+    rc = lib().qw_q4_gemv(_ptr(W), _ptr(S), _ptr(Z), _ptr(x), xs, _ptr(y), ys, int(y_bf16), N, K, M,
+                          int(accumulate), _stream())
+    _check(rc, "qw_q4_gemv")
+    return y
+
+
+def gemm_workspace_size(T, K):
+    return lib().qw_q4_gemm_workspace_size(T, K)
+
+
+def gemm(W, S, Z, X, N, K, Y=None, y_bf16=False, workspace=None):
+    import torch
+    T = X.shape[0]
+    if Y is None:
+        Y = torch.empty((T, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=X.device)
+    if workspace is None:
+        workspace = torch.empty(gemm_workspace_size(T, K), dtype=torch.uint8, device=X.device)
+    _dev(W, S, Z, X, Y, workspace)
+    rc = lib().qw_q4_gemm(_ptr(W), _ptr(S), _ptr(Z), _ptr(X), X.stride(0), T, _ptr(Y), Y.stride(0), int(y_bf16), N, K,
+                          _ptr(workspace), workspace.numel(), _stream())
+    _check(rc, "qw_q4_gemm")
+    return Y
+
+
+class Route:
+    """Device outputs of qw_moe_route."""
+
+    def __init__(self, T, E, topk, device, tile_m=0):
+        import torch
+        i32 = dict(dtype=torch.int32, device=device)
+        self.T, self.E, self.topk, self.tile_m = T, E, topk, tile_m
+        self.top_e = torch.empty((T, topk), **i32)
+        self.top_w = torch.empty((T, topk), dtype=torch.float32, device=device)
+        self.counts = torch.empty(E, **i32)
+        self.offsets = torch.empty(E + 1, **i32)
+        self.tok_slot = torch.empty((T, topk), **i32)
+        self.pair_tok = torch.empty(T * topk, **i32)
+        self.active = torch.empty(E, **i32)
+        self.n_active = torch.empty(1, **i32)
+        nt = (T * topk) // tile_m + E if tile_m else 0
+        self.tile_e = torch.empty(max(nt, 1), **i32) if tile_m else None
+        self.tile_m0 = torch.empty(max(nt, 1), **i32) if tile_m else None
+        self.n_tiles = torch.empty(1, **i32) if tile_m else None
+
+
+def moe_route(logits, topk, tile_m=0, out=None):
+    T, E = logits.shape
+    r = out if out is not None else Route(T, E, topk, logits.device, tile_m)
+    _dev(logits)
+    rc = lib().qw_moe_route(_ptr(logits), T, E, topk, tile_m, _ptr(r.top_e), _ptr(r.top_w), _ptr(r.counts),
+                            _ptr(r.offsets), _ptr(r.tok_slot), _ptr(r.pair_tok), _ptr(r.active), _ptr(r.n_active),
+                            _ptr(r.tile_e), _ptr(r.tile_m0), _ptr(r.n_tiles), _stream())
+    _check(rc, "qw_moe_route")
+    return r
+
+
+def moe_experts_gemv(gate, up, down, route, x, h=None, yp=None):
+    """gate/up/down: (W, S, Z) device tensors; returns (h fp16-bits, yp fp32)."""
+    import torch
+    E, F = gate[0].shape[0], gate[0].shape[1]
+    H = x.shape[1]
+    T, topk = route.T, route.topk
+    if h is None:
+        h = torch.empty((T * topk, F), dtype=torch.float16, device=x.device)
+    if yp is None:
+        yp = torch.empty((T * topk, H), dtype=torch.float32, device=x.device)
+    _dev(x, h, yp, *gate, *up, *down)
+    rc = lib().qw_moe_experts_gemv(*[_ptr(t) for t in (*gate, *up, *down)], E, H, F, _ptr(route.offsets),
+                                   _ptr(route.active), _ptr(route.n_active), _ptr(route.pair_tok), _ptr(x), T, topk,
+                                   _ptr(h), _ptr(yp), _stream())
+    _check(rc, "qw_moe_experts_gemv")
+    return h, yp
+
+
+def moe_grouped_tile_m():
+    return lib().qw_moe_grouped_tile_m()
+
+
+def moe_grouped_workspace_size(T, topk, E, H, F):
+    return lib().qw_moe_grouped_workspace_size(T, topk, E, H, F)
+
+
+def moe_experts_grouped(gate, up, down, route, x, h=None, yp=None, workspace=None):
+    import torch
+    E, F = gate[0].shape[0], gate[0].shape[1]
+    T, H = x.shape
+    topk = route.topk
+    if h is None:
+        h = torch.empty((T * topk, F), dtype=torch.float16, device=x.device)
+    if yp is None:
+        yp = torch.empty((T * topk, H), dtype=torch.float32, device=x.device)
+    if workspace is None:
+        workspace = torch.empty(max(moe_grouped_workspace_size(T, topk, E, H, F), 1), dtype=torch.uint8,
+                                device=x.device)
+    _dev(x, h, yp, workspace, *gate, *up, *down)
+    rc = lib().qw_moe_experts_grouped(*[_ptr(t) for t in (*gate, *up, *down)], E, H, F, _ptr(route.offsets),
+                                      _ptr(route.pair_tok), _ptr(route.tile_e), _ptr(route.tile_m0),
+                                      _ptr(route.n_tiles), _ptr(x), T, topk, _ptr(h), _ptr(yp), _ptr(workspace),
+                                      workspace.numel(), _stream())
+    _check(rc, "qw_moe_experts_grouped")
+    return h, yp
+
+
+def moe_combine(yp, route, H, shared=None, out=None, out_bf16=True):
+    import torch
+    T, topk = route.T, route.topk
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=yp.device)
+    _dev(yp, shared, out)
+    rc = lib().qw_moe_combine(_ptr(yp), _ptr(route.tok_slot), _ptr(route.top_w), _ptr(shared), T, topk, H, _ptr(out),
+                              int(out_bf16), _stream())
+    _check(rc, "qw_moe_combine")
+    return out
+
+
+def unpack(W, N, K):
+    import torch
+    out = torch.empty((N, K), dtype=torch.uint8, device=W.device)
+    _check(lib().qw_q4_unpack(_ptr(W), N, K, _ptr(out), _stream()), "qw_q4_unpack")
+    return out
+
+
+def dequant(W, S, Z, N, K):
+    import torch
+    out = torch.empty((N, K), dtype=torch.float32, device=W.device)
+    _check(lib().qw_q4_dequant(_ptr(W), _ptr(S), _ptr(Z), N, K, _ptr(out), _stream()), "qw_q4_dequant")
+    return out
+
+
+def from_engine_order(words):
+    import torch
+    out = torch.empty_like(words)
+    _check(lib().qw_q4_from_engine_order(_ptr(words), _ptr(out), words.numel(), _stream()), "qw_q4_from_engine_order")
+    return out
