@@ -39,20 +39,41 @@ def q4_bytes(N, K):
 
 
 def gen_q4(torch, dev, N, K, zeros=True, lead=(), seed=0):
+    """Seeded q4 weights generated in checkpoint order on the GPU, then tiled
+    (qw_q4_tile) into the device format the kernels read; lead = (E,) stacks
+    experts as one [E*N][K] matrix."""
+    import qwq4
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     G = K // 128
-    W = torch.randint(-2**31, 2**31 - 1, lead + (N, K // 8), generator=g, device=dev, dtype=torch.int32)
-    S = (torch.randn(lead + (N, G), generator=g, device=dev) * 0.02).abs().to(torch.float16)
-    Z = torch.randint(-2**31, 2**31 - 1, lead + (N, (G + 7) // 8), generator=g, device=dev,
+    R = N * (lead[0] if lead else 1)
+    W = torch.randint(-2**31, 2**31 - 1, (R, K // 8), generator=g, device=dev, dtype=torch.int32)
+    S = (torch.randn((R, G), generator=g, device=dev) * 0.02).abs().to(torch.float16)
+    Z = torch.randint(-2**31, 2**31 - 1, (R, (G + 7) // 8), generator=g, device=dev,
                       dtype=torch.int32) if zeros else None
-    return W, S, Z
+    t = qwq4.tile(W, S, Z, R, K)
+    del W, S, Z
+    return t
 
 
 def gen_x(torch, dev, M, K, seed=1):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     return torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+
+
+def graphed(torch, fn):
+    """Capture fn's launches into a HIP graph (the way the reference engine
+    replays its decode step, src/engine/decode.hip:166-181); returns replay."""
+    fn()  # warm: first-call set-up (kernel attributes) stays out of the graph
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            fn()
+    torch.cuda.synchronize()
+    return g.replay
 
 
 class Timer:
@@ -87,11 +108,13 @@ def bench_gemv(torch, qwq4, dev, steps, warmup):
         x = gen_x(torch, dev, M, FFN_DOWN_K, seed=M)
         y = torch.empty((M, VOCAB), dtype=torch.bfloat16, device=dev)
 
-        def step():
+        def launches():
             for (wq, wd) in layers:
                 qwq4.gemv(*wq, x, QKV, H, M, y=y, y_bf16=True, xs=x.stride(0), ys=y.stride(0))
                 qwq4.gemv(*wd, x, H, FFN_DOWN_K, M, y=y, y_bf16=True, xs=x.stride(0), ys=y.stride(0))
             qwq4.gemv(*head, x, VOCAB, H, M, y=y, y_bf16=True, xs=x.stride(0), ys=y.stride(0))
+
+        step = graphed(torch, launches)
 
         for _ in range(warmup):
             step()
@@ -134,10 +157,12 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
         yp = torch.empty((B * k, H), dtype=torch.float32, device=dev)
         o = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
 
-        def step():
+        def launches():
             qwq4.moe_route(logits, k, out=r)
-            qwq4.moe_experts_gemv(gate, up, down, r, x, h=h, yp=yp)
+            qwq4.moe_experts_gemv(gate, up, down, r, x, E, F, h=h, yp=yp)
             qwq4.moe_combine(yp, r, H, out=o)
+
+        step = graphed(torch, launches)
 
         for _ in range(warmup):
             step()
@@ -197,7 +222,7 @@ def bench_moe_prefill(torch, qwq4, dev, steps, warmup):
 
     def step():
         qwq4.moe_route(logits, k, tile_m=tm, out=r)
-        qwq4.moe_experts_grouped(gate, up, down, r, x, h=h, yp=yp, workspace=ws)
+        qwq4.moe_experts_grouped(gate, up, down, r, x, E, F, h=h, yp=yp, workspace=ws)
         qwq4.moe_combine(yp, r, H, out=o)
 
     for _ in range(warmup):
@@ -272,7 +297,7 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "q4 weights, bf16 x, fp32 acc",
         "data": "synthetic (seeded): uniform nibbles, |N(0,0.02)| fp16 scales, uniform 4-bit zeros, N(0,1) bf16 x",
         "config": {"workload": f"decode dense q4 GEMV, {L_LAYERS} layers x (4096->12288, 6144->4096) + LM head "
-                               f"4096->151936, batch 1/2/4/6/8, bf16 out",
+                               f"4096->151936, batch 1/2/4/6/8, bf16 out, one HIP graph per step",
                    "batches": list(BATCHES)},
     }
     if "gemv" in res:

@@ -28,15 +28,23 @@
  *   - Calls on different streams are independent; the library holds no state
  *     beyond the per-thread error string.
  *
- * q4 weight format (the compressed-tensors checkpoint order, docs/MODEL.md:34-37)
- *   W  uint32 [N][K/8]          element 8c+i of row n in bits 4i..4i+3 of word c
- *   S  fp16   [N][K/128]        scale per 128-element group along K
- *   Z  uint32 [N][ceil(G/8)]    4-bit zero of group g in bits 4(g%8) of word
- *                               g/8 (G = K/128); NULL = zero 8 for every group,
- *                               the reference's symmetric format
- *   weight = (q - z) * s, exactly, in fp32.
- *   K must be a multiple of 128. Activations are bf16 (uint16 bit patterns);
- *   accumulation is fp32.
+ * q4 weight formats
+ *   Checkpoint order (compressed-tensors, docs/MODEL.md:34-37), the input of
+ *   qw_q4_tile and the format of the bit-exact surface (unpack, dequant):
+ *     W  uint32 [N][K/8]        element 8c+i of row n in bits 4i..4i+3 of word c
+ *     S  fp16   [N][K/128]      scale per 128-element group along K
+ *     Z  uint32 [N][ceil(G/8)]  4-bit zero of group g in bits 4(g%8) of word g/8
+ *                               (G = K/128); NULL = zero 8 for every group, the
+ *                               reference's symmetric format
+ *   Tiled device order (what the matmul entry points read; written once at
+ *   load time by qw_q4_tile, the way the reference repacks at load time with
+ *   pack_int4_words, src/engine/weight_convert.cpp:61-71):
+ *     Wt uint32, N*K/8 words     16-row x 128-column tiles, 1 KB each, in the
+ *                               order one wave64 reads them (see q4_common.cuh)
+ *     St fp16, Zt u16            scales and zeros regrouped per 16-row tile
+ *   Sizes: qw_q4_tiled_size. weight = (q - z) * s, exactly, in fp32.
+ *   K must be a multiple of 128 and N (rows) of 16. Activations are bf16
+ *   (uint16 bit patterns); accumulation is fp32.
  */
 #ifndef QW_Q4OPS_H
 #define QW_Q4OPS_H
@@ -58,21 +66,31 @@ int qw_q4_abi_version(void);
 /* Message for the last error returned on this thread ("" if none). */
 const char *qw_q4_last_error(void);
 
-/* Decode GEMV (replaces gpu::gemv_rows, src/kernels/gemv.hpp:13-14):
+/* Load-time repack to the tiled device format (role of pack_int4_words,
+ * src/engine/weight_convert.cpp:61-71), its inverse, and the buffer sizes.
+ * Z may be NULL (then Zt is not written / not read). */
+void qw_q4_tiled_size(int64_t N, int64_t K, size_t *wt_bytes, size_t *st_bytes, size_t *zt_bytes);
+int qw_q4_tile(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, uint32_t *Wt,
+               uint16_t *St, uint16_t *Zt, void *stream);
+int qw_q4_untile(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt, int64_t N, int64_t K, uint32_t *W,
+                 uint16_t *S, uint32_t *Z, void *stream);
+
+/* Decode GEMV (replaces gpu::gemv_rows, src/kernels/gemv.hpp:13-14), tiled
+ * weights (Wt, St, Zt or NULL):
  *   y[m*ys + n] (+)= sum_k W[n][k] * x[m*xs + k],   m < M, n < N
  * x bf16 rows of stride xs (elements, a multiple of 8, x 16-byte aligned);
  * y fp32 (y_bf16 = 0) or bf16 (y_bf16 = 1, round to nearest even) rows of
  * stride ys; accumulate != 0 adds to y. 1 <= M <= 32. */
-int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint32_t *Z, const uint16_t *x, int xs, void *y, int ys,
+int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *x, int xs, void *y, int ys,
                int y_bf16, int N, int K, int M, int accumulate, void *stream);
 
-/* Prefill GEMM (replaces gpu::gemm, src/kernels/gemm.hpp:14-15, with q4
- * weights): Y[t][n] = sum_k X[t][k] * W[n][k], t < T. X bf16 rows of stride
+/* Prefill GEMM (replaces gpu::gemm, src/kernels/gemm.hpp:14-15, with tiled
+ * q4 weights): Y[t][n] = sum_k X[t][k] * W[n][k], t < T. X bf16 rows of stride
  * ldx; Y fp32 or bf16 rows of stride ldy. `workspace` (device memory of at
  * least qw_q4_gemm_workspace_size(T, K) bytes, 256-byte aligned) is scratch
  * for the activation pre-pass; it holds nothing between calls. */
 size_t qw_q4_gemm_workspace_size(int T, int K);
-int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint32_t *Z, const uint16_t *X, int ldx, int T, void *Y,
+int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *X, int ldx, int T, void *Y,
                int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Routing of T tokens over E experts (replaces gpu::moe_route_B for decode
@@ -97,14 +115,13 @@ int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_
  * moe.hpp:35-37). For every slot p of expert e (from qw_moe_route):
  *   h[p]  = silu(G_e x[pair_tok[p]]) * (U_e x[pair_tok[p]])     fp16 [T*k][F]
  *   yp[p] = D_e h[p]                                            fp32 [T*k][H]
- * gate/up: [E][F][H/8] words, [E][F][H/128] scales, [E][F][ceil(H/1024)] zeros;
- * down: [E][H][F/8], [E][H][F/128], [E][H][ceil(F/1024)]. x bf16 [T][H].
- * h is scratch in this library's own element order (each 8-element chunk
- * permuted); yp is in natural order. 1 <= T <= 32. Each expert's weights are
- * read once per call however many of the batch's tokens chose it. */
-int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint32_t *gz, const uint32_t *uw,
-                        const uint16_t *us, const uint32_t *uz, const uint32_t *dw, const uint16_t *ds,
-                        const uint32_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
+ * Weights are tiled (qw_q4_tile) over the stacked experts: gate and up as one
+ * [E*F][H] matrix each, down as [E*H][F]; zeros may be NULL. x bf16 [T][H].
+ * F and H multiples of 128. 1 <= T <= 32. Each expert's weights are read
+ * once per call however many of the batch's tokens chose it. */
+int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                        const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                        const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
                         const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int T, int topk,
                         uint16_t *h, float *yp, void *stream);
 
@@ -115,9 +132,9 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint32_t *
  * qw_moe_grouped_workspace_size(...) bytes (may be 0), 256-byte aligned. */
 int qw_moe_grouped_tile_m(void);
 size_t qw_moe_grouped_workspace_size(int T, int topk, int E, int H, int F);
-int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint32_t *gz, const uint32_t *uw,
-                           const uint16_t *us, const uint32_t *uz, const uint32_t *dw, const uint16_t *ds,
-                           const uint32_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
+int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                           const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                           const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
                            const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
                            int T, int topk, uint16_t *h, float *yp, void *workspace, size_t workspace_bytes,
                            void *stream);

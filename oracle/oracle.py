@@ -44,6 +44,7 @@ def lib():
         L.o_quantize_g128.argtypes = [_u16p, _i64, _u32p, _u16p]
         L.o_route.argtypes = [_f32p, _int, _int, _int, _i32p, _f32p]
         L.o_moe_slots.argtypes = [_i32p, _int, _int, _int, _i32p, _i32p, _i32p, _i32p]
+        L.o_q4_tile.argtypes = [_u32p, _u16p, _vp, _i64, _i64, _u32p, _u16p, _vp]
         L.o_moe.argtypes = [_f32p, _int, _int, _int, _int, _int, _f32p] + [_u32p, _u16p, _vp] * 3 + [_f32p, _vp, _vp, _int]
         for n in ("o_bf16_to_f32", "o_f16_to_f32"):
             getattr(L, n).argtypes = [ctypes.c_uint16]
@@ -193,3 +194,16 @@ def moe(x, logits, topk, gate, up, down, threads=None, want_parts=False):
     if want_parts:
         return out, h, yp
     return out
+
+
+def q4_tile(W, S, Z, N, K):
+    """Checkpoint-order q4 -> the kernels' tiled format (Wt, St, Zt or None)."""
+    G = K // 128
+    GC = (G + 3) // 4
+    Wt = np.empty(N * K // 8, np.uint32)
+    St = np.empty(N // 16 * GC * 64, np.uint16)
+    Zt = np.empty(N // 16 * GC * 16, np.uint16) if Z is not None else None
+    W, S = _c(W, np.uint32), _c(S, np.uint16)
+    Zc = None if Z is None else _c(Z, np.uint32)
+    lib().o_q4_tile(W, S, _zp(Zc), N, K, Wt, St, None if Zt is None else Zt.ctypes.data_as(ctypes.c_void_p))
+    return Wt, St, Zt

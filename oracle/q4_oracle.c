@@ -418,3 +418,49 @@ void o_moe(const float *x, int T, int H, int F, int E, int topk, const float *lo
     free(tok_slot);
     free(pair_tok);
 }
+
+/* ------------------------------------------------- device tiled format */
+
+/* The kernels' weight layout (this build's load-time repack, the role of
+ * pack_int4_words in src/engine/weight_convert.cpp:61-71):
+ *   Wt  uint4 [N/16][G][4][16]: entry (sub, g, q, n) = the 16 bytes of row
+ *       16*sub+n covering words g*16+4q .. g*16+4q+3, each word with its
+ *       nibbles reordered so that element j (j < 4) sits at bits 8j and
+ *       element j+4 at bits 8j+4;
+ *   St  fp16  [N/16][ceil(G/4)][16][4]: St[sub][gc][n][j] = S[16 sub+n][4 gc+j]
+ *       (0 past G);
+ *   Zt  u16   [N/16][ceil(G/4)][16]: nibble j = zero of group 4 gc+j (0 past G).
+ * N must be a multiple of 16. */
+static uint32_t shuffle_word(uint32_t w) {
+    uint32_t r = 0;
+    for (int j = 0; j < 4; ++j) {
+        r |= ((w >> (4 * j)) & 0xfu) << (8 * j);
+        r |= ((w >> (4 * (j + 4))) & 0xfu) << (8 * j + 4);
+    }
+    return r;
+}
+
+void o_q4_tile(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, uint32_t *Wt, uint16_t *St,
+               uint16_t *Zt) {
+    const int64_t G = K / QGROUP, GC = (G + 3) / 4, subs = N / 16;
+    for (int64_t sub = 0; sub < subs; ++sub)
+        for (int64_t g = 0; g < G; ++g)
+            for (int q = 0; q < 4; ++q)
+                for (int n = 0; n < 16; ++n)
+                    for (int j = 0; j < 4; ++j) {
+                        const int64_t row = sub * 16 + n;
+                        Wt[(((sub * G + g) * 4 + q) * 16 + n) * 4 + j] = shuffle_word(W[row * (K / 8) + g * 16 + q * 4 + j]);
+                    }
+    for (int64_t sub = 0; sub < subs; ++sub)
+        for (int64_t gc = 0; gc < GC; ++gc)
+            for (int n = 0; n < 16; ++n) {
+                const int64_t row = sub * 16 + n;
+                uint16_t zt = 0;
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t g = gc * 4 + j;
+                    St[((sub * GC + gc) * 16 + n) * 4 + j] = g < G ? S[row * G + g] : 0;
+                    if (g < G && Z) zt |= (uint16_t)(zero_of(Z, row, G, g) << (4 * j));
+                }
+                if (Zt) Zt[(sub * GC + gc) * 16 + n] = zt;
+            }
+}

@@ -38,6 +38,8 @@ def test_abi_version():
                            ctypes.c_void_p(256), 4096, 0, 4096, 4096, 33, 0, None),
     lambda L: L.qw_moe_route(ctypes.c_void_p(256), 4, 256, 0, 0, *([ctypes.c_void_p(256)] * 11), None),
     lambda L: L.qw_moe_combine(None, None, None, None, 1, 8, 4096, None, 1, None),
+    lambda L: L.qw_q4_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(256), 4096,
+                           ctypes.c_void_p(256), 4096, 0, 4008, 4096, 1, 0, None),  # N % 16
     lambda L: L.qw_q4_gemm(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(256), 4096, 4096,
                            ctypes.c_void_p(256), 4096, 1, 4096, 4096, None, 0, None),
 ])

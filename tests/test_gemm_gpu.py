@@ -14,7 +14,8 @@ def test_gemm_small_full_check(gpu, oracle, T, N, K):
     print(f"gemm T={T} N={N} K={K}", flush=True)
     W, S, Z = synth.q4_weights(51, f"g{N}x{K}", N, K)
     xb, xf = synth.acts(51, f"x{T}x{K}", T, K)
-    Y = host(qwq4.gemm(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), to_dev(xb, gpu), N, K))
+    dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
+    Y = host(qwq4.gemm(dW, dS, dZ, to_dev(xb, gpu), N, K))
     assert rel_err(Y, oracle.q4_linear(W, S, Z, N, K, xf)) <= TOL
 
 
@@ -24,7 +25,8 @@ def test_gemm_prefill_chunk_sampled(gpu, oracle, N, K):
     T = 4096
     W, S, Z = synth.q4_weights(52, f"p{N}x{K}", N, K)
     xb, xf = synth.acts(52, f"px{K}", T, K)
-    Y = host(qwq4.gemm(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), to_dev(xb, gpu), N, K, y_bf16=True))
+    dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
+    Y = host(qwq4.gemm(dW, dS, dZ, to_dev(xb, gpu), N, K, y_bf16=True))
     r = np.random.default_rng(0)
     toks = np.sort(r.choice(T, 48, replace=False))
     rows = np.sort(r.choice(N, 512, replace=False))
@@ -38,9 +40,10 @@ def test_grouped_matches_oracle_small(gpu, oracle):
     xb, xf = synth.acts(61, "x", T, H)
     l = synth.router_logits(61, "l", T, E, bias_sigma=0.5)
     out, h_ref, yp_ref = oracle.moe(xf, l, k, *ex, want_parts=True)
-    dex = [tuple(to_dev(a, gpu) for a in w) for w in ex]
+    from test_moe_gpu import _experts_dev
+    (dg, du, dd), E, F = _experts_dev(gpu, ex)
     r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=qwq4.moe_grouped_tile_m())
-    h, yp = qwq4.moe_experts_grouped(*dex, r, to_dev(xb, gpu))
+    h, yp = qwq4.moe_experts_grouped(dg, du, dd, r, to_dev(xb, gpu), E, F)
     assert rel_err(host(yp), yp_ref) <= TOL
     o = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
     assert rel_err(o, out) <= TOL

@@ -14,7 +14,8 @@ SHAPES = [(256, 512), (384, 128), (4096, 4096), (12288, 4096), (4096, 6144), (15
 def _setup(dev, N, K, M, zeros=True, seed=11):
     W, S, Z = synth.q4_weights(seed, f"w{N}x{K}", N, K, zeros)
     xb, xf = synth.acts(seed, f"x{M}x{K}", M, K)
-    return (W, S, Z, xb, xf), (to_dev(W, dev), to_dev(S, dev), to_dev(Z, dev), to_dev(xb, dev))
+    dW, dS, dZ = qwq4.tile(to_dev(W, dev), to_dev(S, dev), to_dev(Z, dev), N, K)
+    return (W, S, Z, xb, xf), (dW, dS, dZ, to_dev(xb, dev))
 
 
 @pytest.mark.parametrize("N,K", SHAPES)
@@ -27,11 +28,11 @@ def test_gemv_fp32(gpu, oracle, N, K, M):
     assert rel_err(y, r) <= TOL
 
 
-@pytest.mark.parametrize("M", [1, 8, 16, 17, 32])
-def test_gemv_symmetric_and_wide(gpu, oracle, M):
-    N, K = 1024, 2048
+@pytest.mark.parametrize("M,K", [(1, 2048), (8, 2048), (16, 2048), (17, 2048), (32, 2048), (32, 6144), (13, 640)])
+def test_gemv_symmetric_and_wide(gpu, oracle, M, K):
+    N = 1024
     (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M, zeros=False)
-    y = host(qwq4.gemv(dW, dS, None, dx, N, K, M))
+    y = host(qwq4.gemv(dW, dS, dZ, dx, N, K, M))
     r = oracle.q4_linear(W, S, None, N, K, xf)
     assert rel_err(y, r) <= TOL
 
@@ -65,7 +66,7 @@ def test_gemv_rows_independent_bit_exact(gpu):
 
 def test_gemv_strides_accumulate_and_guard(gpu, oracle):
     import torch
-    N, K, M = 1000, 1024, 3   # N not a multiple of 16
+    N, K, M = 1008, 1024, 3   # N not a multiple of 128
     (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M)
     xs = K + 64
     xpad = torch.zeros((M, xs), dtype=torch.int16, device=gpu)
@@ -84,7 +85,7 @@ def test_gemv_special_inputs(gpu, oracle):
     import torch
     N, K = 512, 1024
     W, S, Z = synth.q4_weights(12, "sp", N, K)
-    dW, dS, dZ = to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu)
+    dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
     x = np.zeros((2, K), np.float32)
     x[1, 777] = 1.0
     y = host(qwq4.gemv(dW, dS, dZ, to_dev(synth.bf16_bits(x), gpu), N, K, 2))

@@ -174,3 +174,26 @@ def test_moe_vs_dense_numpy(oracle):
             h = g / (1 + np.exp(-g)) * u
             ref[t] += tw[t, j] * (deq(down, H, F) @ h)
     assert np.max(np.abs(out - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("N,K,zeros", [(32, 384, True), (16, 640, False)])
+def test_tile_against_numpy_restatement(oracle, N, K, zeros):
+    """The tiled format from reshapes: tile (sub, g, q, n) = row 16 sub + n,
+    words 16 g + 4 q .. +4, nibbles of each word reordered (j, j+4) per byte."""
+    W, S, Z = synth.q4_weights(9, "t", N, K, zeros)
+    Wt, St, Zt = oracle.q4_tile(W, S, Z, N, K)
+    G = K // 128
+    q = oracle.q4_unpack(W, N, K).reshape(N, K // 8, 2, 4)       # [row][word][half][j]
+    byte = q[:, :, 0, :] | (q[:, :, 1, :] << 4)                     # byte j = e_j | e_{j+4} << 4
+    words = byte.astype(np.uint32) @ (np.uint32(1) << (8 * np.arange(4, dtype=np.uint32)))
+    want = words.reshape(N // 16, 16, G, 4, 4).transpose(0, 2, 3, 1, 4).reshape(-1)
+    assert np.array_equal(Wt, want.astype(np.uint32))
+    GC = (G + 3) // 4
+    Sp = np.zeros((N, GC * 4), np.uint16)
+    Sp[:, :G] = S
+    assert np.array_equal(St, Sp.reshape(N // 16, 16, GC, 4).transpose(0, 2, 1, 3).reshape(-1))
+    if zeros:
+        z = np.zeros((N, GC * 4), np.uint16)
+        z[:, :G] = synth.unpack_zeros(Z, G)
+        zt = (z.reshape(N, GC, 4) << (4 * np.arange(4, dtype=np.uint16))).sum(-1).astype(np.uint16)
+        assert np.array_equal(Zt, zt.reshape(N // 16, 16, GC).transpose(0, 2, 1).reshape(-1))

@@ -45,10 +45,19 @@ hipStream_t st(void *s) { return static_cast<hipStream_t>(s); }
 
 int check_q4(const char *fn, const uint32_t *W, const uint16_t *S, int64_t N, int64_t K) {
     REQUIRE(W && S, "%s: null weight or scale pointer", fn);
-    REQUIRE(N >= 1, "%s: N = %lld must be >= 1", fn, (long long)N);
+    REQUIRE(N >= 16 && N % 16 == 0, "%s: N = %lld must be a positive multiple of 16", fn, (long long)N);
     REQUIRE(K >= 128 && K % 128 == 0, "%s: K = %lld must be a positive multiple of 128", fn, (long long)K);
     REQUIRE(aligned(W, 16), "%s: W must be 16-byte aligned", fn);
-    REQUIRE(aligned(S, 2), "%s: S must be 2-byte aligned", fn);
+    REQUIRE(aligned(S, 8), "%s: S must be 8-byte aligned", fn);
+    return 0;
+}
+
+// checkpoint-order arguments of the format functions (N any, K % 8 or 128)
+int check_ckpt(const char *fn, const uint32_t *W, const uint16_t *S, int64_t N, int64_t K) {
+    REQUIRE(W && S, "%s: null weight or scale pointer", fn);
+    REQUIRE(N >= 1, "%s: N = %lld must be >= 1", fn, (long long)N);
+    REQUIRE(K >= 128 && K % 128 == 0, "%s: K = %lld must be a positive multiple of 128", fn, (long long)K);
+    REQUIRE(aligned(W, 16) && aligned(S, 2), "%s: W must be 16-byte aligned", fn);
     return 0;
 }
 
@@ -60,7 +69,7 @@ int qw_q4_abi_version(void) { return 1; }
 
 const char *qw_q4_last_error(void) { return g_err.c_str(); }
 
-int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint32_t *Z, const uint16_t *x, int xs, void *y, int ys,
+int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *x, int xs, void *y, int ys,
                int y_bf16, int N, int K, int M, int accumulate, void *stream) {
     if (int r = check_q4("qw_q4_gemv", W, S, N, K)) return r;
     REQUIRE(x && y, "qw_q4_gemv: null x or y");
@@ -78,7 +87,7 @@ size_t qw_q4_gemm_workspace_size(int T, int K) {
     return qwq4::gemm_workspace_bytes(T, K);
 }
 
-int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint32_t *Z, const uint16_t *X, int ldx, int T, void *Y,
+int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *X, int ldx, int T, void *Y,
                int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream) {
     if (int r = check_q4("qw_q4_gemm", W, S, N, K)) return r;
     REQUIRE(X && Y, "qw_q4_gemm: null X or Y");
@@ -112,9 +121,9 @@ int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_
     return launched("qw_moe_route");
 }
 
-int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint32_t *gz, const uint32_t *uw,
-                        const uint16_t *us, const uint32_t *uz, const uint32_t *dw, const uint16_t *ds,
-                        const uint32_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
+int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                        const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                        const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
                         const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int T, int topk,
                         uint16_t *h, float *yp, void *stream) {
     if (int r = check_q4("qw_moe_experts_gemv(gate)", gw, gs, int64_t(E) * F, H)) return r;
@@ -137,9 +146,9 @@ size_t qw_moe_grouped_workspace_size(int T, int topk, int E, int H, int F) {
 
 int qw_moe_grouped_tile_m(void) { return qwq4::moe_grouped_tile_m(); }
 
-int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint32_t *gz, const uint32_t *uw,
-                           const uint16_t *us, const uint32_t *uz, const uint32_t *dw, const uint16_t *ds,
-                           const uint32_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
+int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                           const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                           const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
                            const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
                            int T, int topk, uint16_t *h, float *yp, void *workspace, size_t workspace_bytes,
                            void *stream) {
@@ -170,6 +179,33 @@ int qw_moe_combine(const float *yp, const int32_t *tok_slot, const float *tok_w,
     return launched("qw_moe_combine");
 }
 
+void qw_q4_tiled_size(int64_t N, int64_t K, size_t *wt_bytes, size_t *st_bytes, size_t *zt_bytes) {
+    const int64_t G = K / 128, GC = (G + 3) / 4;
+    if (wt_bytes) *wt_bytes = size_t(N) * size_t(K) / 2;
+    if (st_bytes) *st_bytes = size_t(N / 16) * size_t(GC) * 64 * 2;
+    if (zt_bytes) *zt_bytes = size_t(N / 16) * size_t(GC) * 16 * 2;
+}
+
+int qw_q4_tile(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, uint32_t *Wt,
+               uint16_t *St, uint16_t *Zt, void *stream) {
+    if (int r = check_ckpt("qw_q4_tile", W, S, N, K)) return r;
+    REQUIRE(N % 16 == 0, "qw_q4_tile: N = %lld must be a multiple of 16", (long long)N);
+    REQUIRE(Wt && St && aligned(Wt, 16), "qw_q4_tile: null or misaligned output");
+    REQUIRE(!Z || Zt, "qw_q4_tile: zeros given without a Zt output");
+    qwq4::launch_tile(W, S, Z, N, K, Wt, St, Zt, st(stream));
+    return launched("qw_q4_tile");
+}
+
+int qw_q4_untile(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt, int64_t N, int64_t K, uint32_t *W,
+                 uint16_t *S, uint32_t *Z, void *stream) {
+    if (int r = check_ckpt("qw_q4_untile", W, S, N, K)) return r;
+    REQUIRE(N % 16 == 0, "qw_q4_untile: N = %lld must be a multiple of 16", (long long)N);
+    REQUIRE(Wt && St && aligned(Wt, 16), "qw_q4_untile: null or misaligned input");
+    REQUIRE(!Zt || Z, "qw_q4_untile: Zt given without a Z output");
+    qwq4::launch_untile(Wt, St, Zt, N, K, W, S, Z, st(stream));
+    return launched("qw_q4_untile");
+}
+
 int qw_q4_unpack(const uint32_t *W, int64_t N, int64_t K, uint8_t *out, void *stream) {
     REQUIRE(W && out && N >= 1 && K >= 8 && K % 8 == 0, "qw_q4_unpack: bad arguments");
     REQUIRE(aligned(out, 8), "qw_q4_unpack: out must be 8-byte aligned");
@@ -179,7 +215,7 @@ int qw_q4_unpack(const uint32_t *W, int64_t N, int64_t K, uint8_t *out, void *st
 
 int qw_q4_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, float *out,
                   void *stream) {
-    if (int r = check_q4("qw_q4_dequant", W, S, N, K)) return r;
+    if (int r = check_ckpt("qw_q4_dequant", W, S, N, K)) return r;
     REQUIRE(out && aligned(out, 16), "qw_q4_dequant: out must be 16-byte aligned");
     qwq4::launch_dequant(W, S, Z, N, K, out, st(stream));
     return launched("qw_q4_dequant");

@@ -1,29 +1,31 @@
 // Device helpers shared by the q4 kernels (CDNA4 / gfx950, wave64).
 //
-// Weight format (the checkpoint's compressed-tensors order, kept as is on the
-// device; docs/MODEL.md:34-37 of the reference):
-//   W  uint32 [N][K/8]        element 8c+i of row n at bits 4i of word c
-//   S  fp16   [N][K/128]      scale of each 128-element group along K
-//   Z  uint32 [N][ceil(G/8)]  4-bit zero of group g at bits 4(g%8) of word g/8,
-//                             or null for the reference's fixed zero of 8
-//   w = (q - z) * s.
+// Device weight format ("tiled"; written once at load time by qw_q4_tile
+// from the checkpoint's compressed-tensors order, the role the reference's
+// pack_int4_words plays, src/engine/weight_convert.cpp:61-71):
+//   Wt  uint4 [N/16][G][4][16]   entry (sub, g, q, n) holds the 16 bytes of
+//       row 16 sub + n that cover K elements g*128 + 32q .. +32, i.e. exactly
+//       what lane 16q + n of a wave feeds the 16x16x32 MFMA for group g. One
+//       wave-wide load is 1 KB of contiguous HBM. Inside each 32-bit word the
+//       nibbles are reordered: element j (j < 4) at bits 8j, element j + 4 at
+//       bits 8j + 4.
+//   St  fp16  [N/16][ceil(G/4)][16][4]   scales, the 4 groups of a chunk per row
+//   Zt  u16   [N/16][ceil(G/4)][16]      4-bit zeros, group 4gc + j at bits 4j
+//       (absent: the reference's fixed zero of 8)
+//   w = (q - z) * s;  G = K / 128.
 //
-// How a nibble reaches an MFMA operand exactly. For a 32-bit word holding
-// elements e0..e7 and a group zero z:
-//   lo = (w      & 0x0F0F0F0F) + (16 - z) * 0x01010101   bytes e0,e2,e4,e6
-//   hi = (w >> 4 & 0x0F0F0F0F) + (16 - z) * 0x01010101   bytes e1,e3,e5,e7
+// How a nibble reaches an MFMA operand exactly. For a (reordered) word w and
+// a group zero z:
+//   lo = (w      & 0x0F0F0F0F) + (16 - z) * 0x01010101   bytes e0 e1 e2 e3
+//   hi = (w >> 4 & 0x0F0F0F0F) + (16 - z) * 0x01010101   bytes e4 e5 e6 e7
 // Each byte is v = 16 + q - z in [1, 31] (no carry between bytes). One
-// v_perm_b32 against a constant then places a byte under a high byte of 0x43
-// (bf16) or 0x64 (fp16): 0x43vv is the bf16 number 128 + v and 0x64vv the
-// fp16 number 1024 + v, both exact. So the operand holds BIAS + (q - z) with
-// BIAS = 144 (bf16) or 1040 (fp16), and the MFMA accumulator is started at
-// -BIAS * sum(x) over the group (itself one MFMA against a splat of -BIAS),
-// leaving sum x * (q - z) with every product exact in fp32. The group scale
-// is applied once per group, in fp32, on the accumulator.
-//
-// The eight operand elements of one lane therefore come in the order
-// e0,e2,e4,e6,e1,e3,e5,e7 ("operand order"). Activations are permuted into the
-// same order (act_perm), or stored in it by the kernel that writes them.
+// v_perm_b32 against a constant places two bytes under a high byte of 0x43
+// (bf16) or 0x64 (fp16): 0x43vv is the bf16 number 128 + v and 0x64vv the fp16
+// number 1024 + v, both exact. The operand thus holds BIAS + (q - z) with
+// BIAS = 144 (bf16) or 1040 (fp16), elements in natural K order, and the MFMA
+// accumulator is started at -BIAS * sum(x) over the group, leaving
+// sum x * (q - z) with every product exact in fp32. The group scale is
+// applied once per group, in fp32, on the accumulator.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -76,32 +78,19 @@ __device__ __forceinline__ f32x16 mfma32(const uint4 &a, const uint4 &b, const f
 // (16 - z) in every byte.
 __device__ __forceinline__ uint32_t zero_bytes(uint32_t z) { return (16u - z) * 0x01010101u; }
 
-// One packed word (8 nibbles) -> 8 operand elements BIAS + (q - z), operand order.
+// One reordered word (8 nibbles) -> 8 operand elements BIAS + (q - z), K order.
 template <typename T>
 __device__ __forceinline__ uint4 unpack8(uint32_t w, uint32_t zb) {
     const uint32_t lo = (w & 0x0F0F0F0Fu) + zb;
     const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) + zb;
     uint4 r;
     // byte selectors: 0-3 pick from the second source (lo/hi), 4 picks a byte of T::HI
-    r.x = __builtin_amdgcn_perm(T::HI, lo, 0x04010400u);  // e0, e2
-    r.y = __builtin_amdgcn_perm(T::HI, lo, 0x04030402u);  // e4, e6
-    r.z = __builtin_amdgcn_perm(T::HI, hi, 0x04010400u);  // e1, e3
-    r.w = __builtin_amdgcn_perm(T::HI, hi, 0x04030402u);  // e5, e7
+    r.x = __builtin_amdgcn_perm(T::HI, lo, 0x04010400u);  // e0, e1
+    r.y = __builtin_amdgcn_perm(T::HI, lo, 0x04030402u);  // e2, e3
+    r.z = __builtin_amdgcn_perm(T::HI, hi, 0x04010400u);  // e4, e5
+    r.w = __builtin_amdgcn_perm(T::HI, hi, 0x04030402u);  // e6, e7
     return r;
 }
-
-// Eight activations in natural order (x0..x7 as four 16-bit pairs) -> operand order.
-__device__ __forceinline__ uint4 act_perm(const uint4 &v) {
-    uint4 r;
-    r.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);  // x0, x2
-    r.y = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);  // x4, x6
-    r.z = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);  // x1, x3
-    r.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);  // x5, x7
-    return r;
-}
-
-// Position of natural element e (0..7) inside an operand-ordered 8-chunk.
-__host__ __device__ constexpr int op_pos(int e) { return (e >> 1) + 4 * (e & 1); }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 
@@ -118,5 +107,25 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __builtin
 __device__ __forceinline__ int group_zero(const uint32_t *Z, int64_t row, int zw, int g) {
     return Z ? int((Z[row * zw + (g >> 3)] >> (4 * (g & 7))) & 0xfu) : 8;
 }
+
+// Tiled-format addressing of one 16-row subtile.
+struct Q4Tile {
+    const uint4 *w;     // Wt + sub * G * 64
+    const uint16_t *s;  // St + sub * GC * 64
+    const uint16_t *z;  // Zt + sub * GC * 16, or null
+    __device__ __forceinline__ Q4Tile(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt, int64_t sub, int G) {
+        const int GC = (G + 3) / 4;
+        w = reinterpret_cast<const uint4 *>(Wt) + sub * G * 64;
+        s = St + sub * GC * 64;
+        z = Zt ? Zt + sub * GC * 16 : nullptr;
+    }
+    // lane's 16 bytes of group g, its row's scale and zero
+    __device__ __forceinline__ uint4 word4(int g, int lane) const { return w[g * 64 + lane]; }
+    __device__ __forceinline__ uint16_t scale(int g, int n) const { return s[(g >> 2) * 64 + n * 4 + (g & 3)]; }
+    // the 16-bit zero word holding group g's zero (z must be non-null); the
+    // zero itself is zero_of(word, g)
+    __device__ __forceinline__ uint32_t zero_word(int g, int n) const { return z[(g >> 2) * 16 + n]; }
+    __device__ __forceinline__ static uint32_t zero_of(uint32_t word, int g) { return (word >> (4 * (g & 3))) & 0xfu; }
+};
 
 }  // namespace qwq4

@@ -9,10 +9,18 @@
 
 namespace qwq4 {
 
+// Grid size of a persistent kernel on the current device: CUs times the
+// resident blocks per CU for this kernel, block size and dynamic LDS. Sets the
+// kernel's dynamic-LDS limit when it exceeds the 64 KiB default. Cached.
+struct LaunchShape {
+    int max_blocks, cus;
+};
+LaunchShape persistent_shape(const void *kernel, int threads, size_t lds);
+
 struct GemvArgs {
     const uint32_t *W;
     const uint16_t *S;
-    const uint32_t *Z;
+    const uint16_t *Z;
     const uint16_t *x;
     int xs;
     void *y;
@@ -23,13 +31,13 @@ void launch_gemv(const GemvArgs &a, hipStream_t s);
 struct MoeGemvArgs {
     const uint32_t *gw;
     const uint16_t *gs;
-    const uint32_t *gz;
+    const uint16_t *gz;
     const uint32_t *uw;
     const uint16_t *us;
-    const uint32_t *uz;
+    const uint16_t *uz;
     const uint32_t *dw;
     const uint16_t *ds;
-    const uint32_t *dz;
+    const uint16_t *dz;
     int E, H, F;
     const int32_t *offsets, *active, *n_active, *pair_tok;
     const uint16_t *x;
@@ -42,13 +50,13 @@ void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s);
 struct MoeGroupedArgs {
     const uint32_t *gw;
     const uint16_t *gs;
-    const uint32_t *gz;
+    const uint16_t *gz;
     const uint32_t *uw;
     const uint16_t *us;
-    const uint32_t *uz;
+    const uint16_t *uz;
     const uint32_t *dw;
     const uint16_t *ds;
-    const uint32_t *dz;
+    const uint16_t *dz;
     int E, H, F;
     const int32_t *offsets, *pair_tok, *tile_e, *tile_m0, *n_tiles;
     const uint16_t *x;
@@ -77,6 +85,12 @@ void launch_route(const RouteArgs &a, hipStream_t s);
 void launch_combine(const float *yp, const int32_t *tok_slot, const float *tok_w, const float *shared, int T, int topk,
                     int H, void *out, int out_bf16, hipStream_t s);
 
+// checkpoint order <-> tiled device format (q4_common.cuh)
+void launch_tile(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, uint32_t *Wt,
+                 uint16_t *St, uint16_t *Zt, hipStream_t s);
+void launch_untile(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt, int64_t N, int64_t K, uint32_t *W,
+                   uint16_t *S, uint32_t *Z, hipStream_t s);
+bool gemv_fits(int M, int K);
 void launch_unpack(const uint32_t *W, int64_t N, int64_t K, uint8_t *out, hipStream_t s);
 void launch_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, float *out,
                     hipStream_t s);
@@ -85,7 +99,7 @@ void launch_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words
 struct GemmArgs {
     const uint32_t *W;
     const uint16_t *S;
-    const uint32_t *Z;
+    const uint16_t *Z;
     const uint16_t *X;
     int ldx, T;
     void *Y;

@@ -1,7 +1,11 @@
-// Format kernels: nibble unpack, exact dequantisation and conversion from the
+// Format kernels: the load-time repack into the tiled device format (and its
+// inverse), nibble unpack, exact dequantisation and conversion from the
 // reference engine's repacked word order. These are the bit-exact parity
 // surface of the q4 format (reference: src/ref/ref_model.cpp:108-114,
 // src/engine/weight_convert.cpp:61-71).
+#include <mutex>
+#include <vector>
+
 #include "q4_common.cuh"
 #include "q4_kernels.hpp"
 
@@ -59,7 +63,126 @@ __global__ void from_engine_kernel(const uint32_t *__restrict__ in, uint32_t *__
     out[i] = r;
 }
 
+LaunchShape persistent_shape(const void *kernel, int threads, size_t lds) {
+    struct Entry {
+        const void *k;
+        int dev, threads;
+        size_t lds;
+        LaunchShape shape;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(mu);
+    for (const Entry &e : cache)
+        if (e.k == kernel && e.dev == dev && e.threads == threads && e.lds == lds) return e.shape;
+    int cus = 0, per_cu = 0;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (lds > 64 * 1024) (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds);
+    if (cus < 1) cus = 1;
+    if (per_cu < 1) per_cu = 1;
+    const LaunchShape shape{cus * per_cu, cus};
+    cache.push_back({kernel, dev, threads, lds, shape});
+    return shape;
+}
+
+// element j (j < 4) of a checkpoint word -> bits 8j, element j + 4 -> bits 8j + 4
+__device__ __forceinline__ uint32_t shuffle_word(uint32_t w) {
+    const uint32_t lo = w & 0xFFFFu, hi = w >> 16;  // elements 0-3, 4-7
+    uint32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r |= (((lo >> (4 * j)) & 0xfu) | (((hi >> (4 * j)) & 0xfu) << 4)) << (8 * j);
+    return r;
+}
+
+__device__ __forceinline__ uint32_t unshuffle_word(uint32_t r) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        w |= ((r >> (8 * j)) & 0xfu) << (4 * j);
+        w |= ((r >> (8 * j + 4)) & 0xfu) << (4 * (j + 4));
+    }
+    return w;
+}
+
+// one thread per 16-byte tile entry (sub, g, q, n)
+__global__ void tile_w_kernel(const uint32_t *__restrict__ W, int64_t N, int64_t K, uint4 *__restrict__ Wt,
+                              int inverse, uint32_t *__restrict__ Wout, const uint4 *__restrict__ Win) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t G = K / QGROUP, total = N / 16 * G * 64;
+    if (i >= total) return;
+    const int n = int(i % 16), q = int(i / 16 % 4);
+    const int64_t g = i / 64 % G, sub = i / 64 / G;
+    const int64_t o = (sub * 16 + n) * (K / 8) + g * 16 + q * 4;
+    if (!inverse) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(W + o);
+        Wt[i] = make_uint4(shuffle_word(v.x), shuffle_word(v.y), shuffle_word(v.z), shuffle_word(v.w));
+    } else {
+        const uint4 v = Win[i];
+        *reinterpret_cast<uint4 *>(Wout + o) =
+            make_uint4(unshuffle_word(v.x), unshuffle_word(v.y), unshuffle_word(v.z), unshuffle_word(v.w));
+    }
+}
+
+// one thread per (sub, gc, n): 4 scales and the 4 zeros of a 4-group chunk
+__global__ void tile_sz_kernel(const uint16_t *__restrict__ S, const uint32_t *__restrict__ Z, int64_t N, int64_t K,
+                               uint16_t *__restrict__ St, uint16_t *__restrict__ Zt) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t G = K / QGROUP, GC = (G + 3) / 4;
+    if (i >= N / 16 * GC * 16) return;
+    const int n = int(i % 16);
+    const int64_t gc = i / 16 % GC, sub = i / 16 / GC, row = sub * 16 + n;
+    const int zw = int((G + 7) / 8);
+    uint32_t zt = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t g = gc * 4 + j;
+        St[i * 4 + j] = g < G ? S[row * G + g] : uint16_t(0);
+        if (Z && g < G) zt |= ((Z[row * zw + g / 8] >> (4 * (g % 8))) & 0xfu) << (4 * j);
+    }
+    if (Zt) Zt[i] = uint16_t(zt);
+}
+
+// inverse of tile_sz_kernel; Z words are rebuilt whole (one thread per row and word)
+__global__ void untile_sz_kernel(const uint16_t *__restrict__ St, const uint16_t *__restrict__ Zt, int64_t N,
+                                 int64_t K, uint16_t *__restrict__ S, uint32_t *__restrict__ Z) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t G = K / QGROUP, GC = (G + 3) / 4;
+    if (i >= N * G) return;
+    const int64_t row = i / G, g = i % G, sub = row / 16;
+    const int n = int(row % 16);
+    const int64_t t = (sub * GC + g / 4) * 16 + n;
+    S[i] = St[t * 4 + g % 4];
+    if (Z && g % 8 == 0) {
+        const int zw = int((G + 7) / 8);
+        uint32_t w = 0;
+        for (int j = 0; j < 8 && g + j < G; ++j) {
+            const int64_t gg = g + j;
+            const int64_t tt = (sub * GC + gg / 4) * 16 + n;
+            w |= ((uint32_t(Zt[tt]) >> (4 * (gg % 4))) & 0xfu) << (4 * j);
+        }
+        Z[row * zw + g / 8] = w;
+    }
+}
+
 static unsigned blocks(int64_t n, int b) { return unsigned((n + b - 1) / b); }
+
+void launch_tile(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, uint32_t *Wt,
+                 uint16_t *St, uint16_t *Zt, hipStream_t s) {
+    const int64_t G = K / QGROUP, GC = (G + 3) / 4;
+    const int64_t nw = N / 16 * G * 64, ns = N / 16 * GC * 16;
+    tile_w_kernel<<<blocks(nw, 256), 256, 0, s>>>(W, N, K, reinterpret_cast<uint4 *>(Wt), 0, nullptr, nullptr);
+    tile_sz_kernel<<<blocks(ns, 256), 256, 0, s>>>(S, Z, N, K, St, Z ? Zt : nullptr);
+}
+
+void launch_untile(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt, int64_t N, int64_t K, uint32_t *W,
+                   uint16_t *S, uint32_t *Z, hipStream_t s) {
+    const int64_t G = K / QGROUP, nw = N / 16 * G * 64;
+    tile_w_kernel<<<blocks(nw, 256), 256, 0, s>>>(nullptr, N, K, nullptr, 1, W, reinterpret_cast<const uint4 *>(Wt));
+    untile_sz_kernel<<<blocks(N * G, 256), 256, 0, s>>>(St, Zt, N, K, S, Zt ? Z : nullptr);
+}
 
 void launch_unpack(const uint32_t *W, int64_t N, int64_t K, uint8_t *out, hipStream_t s) {
     const int64_t n = N * (K / 8);

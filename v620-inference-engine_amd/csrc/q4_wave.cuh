@@ -1,68 +1,90 @@
-// The q4 MFMA wave core shared by the GEMV-shaped kernels: a wave owns a
-// 16-row weight subtile and a range of 128-wide K groups (see q4_gemv.hip).
+// The q4 MFMA wave core shared by the GEMV-shaped kernels (routed-expert
+// GEMVs, the grouped expert GEMM): a wave owns a 16-row weight subtile and a
+// range of 128-wide K groups.
+//
+// Lane l serves weight row n = l % 16 and K quarter q = l / 16 of every
+// group; the MFMA's other operand is the activations, lane l feeding token
+// row m = l % 16 (+16 per row block). Lanes whose token row is past M read a
+// valid row anyway: rows of the product do not mix, so those outputs are
+// simply not stored. Nothing on the load path is under a divergent branch.
 #pragma once
 
 #include "q4_common.cuh"
 
 namespace qwq4 {
 
-// Per-group contribution for NB weight subtiles that share their activations
-// (NB = 2 for the fused gate/up), over MB blocks of 16 token rows.
-//   wrow[nb]  lane's weight row (uint32 words), srow[nb] its scales, zrow[nb]
-//             its zero words (null: z = 8)
-//   arow[mb]  lane's activation row (16-bit elements), null if the lane's
-//             token row is beyond M
-//   OPORDER   activations already stored in operand order
-template <typename T, int MB, int NB, bool OPORDER>
-__device__ __forceinline__ void q4_groups(const uint32_t *const (&wrow)[NB], const uint16_t *const (&srow)[NB],
-                                          const uint32_t *const (&zrow)[NB], const uint16_t *const (&arow)[MB], int g0,
-                                          int g1, int q, f32x4 (&acc)[MB][NB]) {
+// Accumulates sum over groups [g0, g1) of s_g * (x . (q - z)) into acc for NB
+// weight subtiles sharing their activations (NB = 2: fused gate/up) and MB
+// blocks of 16 token rows.
+//   tile[nb]  the subtiles, arow[mb] the lane's activation row (T elements)
+// Groups are processed in chunks of CH; the weights of the next chunk are
+// requested before the current one is computed.
+template <typename T, int MB, int NB, bool HAS_Z, int CH>
+__device__ __forceinline__ void q4_groups(const Q4Tile (&tile)[NB], const uint16_t *const (&arow)[MB], int g0, int g1,
+                                          int lane, f32x4 (&acc)[MB][NB]) {
+    if (g0 >= g1) return;
+    const int q = lane / 16, n = lane % 16;
     const uint4 negb = make_uint4(T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS);
-
-    for (int g = g0; g < g1; ++g) {
-        uint4 wv[NB];
-        float s[NB];
-        uint32_t zb[NB];
+    uint4 wc[CH][NB];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            wv[nb] = *reinterpret_cast<const uint4 *>(wrow[nb] + g * 16 + q * 4);
-            s[nb] = f16_bits_to_f32(srow[nb][g]);
-            zb[nb] = zero_bytes(zrow[nb] ? (zrow[nb][g >> 3] >> (4 * (g & 7))) & 0xfu : 8u);
-        }
-        uint4 a[MB][4];
+    for (int c = 0; c < CH; ++c)
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            if (arow[mb]) {
-                const uint4 *src = reinterpret_cast<const uint4 *>(arow[mb] + g * QGROUP + q * 32);
+        for (int nb = 0; nb < NB; ++nb) wc[c][nb] = tile[nb].word4(min(g0 + c, g1 - 1), lane);
+    for (int gb = g0; gb < g1; gb += CH) {
+        uint4 wn[CH][NB];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) a[mb][t] = OPORDER ? src[t] : act_perm(src[t]);
-            } else {
+        for (int c = 0; c < CH; ++c)
 #pragma unroll
-                for (int t = 0; t < 4; ++t) a[mb][t] = make_uint4(0, 0, 0, 0);
+            for (int nb = 0; nb < NB; ++nb) wn[c][nb] = tile[nb].word4(min(gb + CH + c, g1 - 1), lane);
+        uint32_t sraw[CH][NB], zraw[CH][NB];
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int g = min(gb + c, g1 - 1);
+                sraw[c][nb] = tile[nb].scale(g, n);
+                if constexpr (HAS_Z) zraw[c][nb] = tile[nb].zero_word(g, n);
             }
-        }
-        f32x4 xsn[MB];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            xsn[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int t = 0; t < 4; ++t) xsn[mb] = mfma16<T>(a[mb][t], negb, xsn[mb]);
-        }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            uint4 b[4];
-            b[0] = unpack8<T>(wv[nb].x, zb[nb]);
-            b[1] = unpack8<T>(wv[nb].y, zb[nb]);
-            b[2] = unpack8<T>(wv[nb].z, zb[nb]);
-            b[3] = unpack8<T>(wv[nb].w, zb[nb]);
+        for (int c = 0; c < CH; ++c) {
+            const int g = gb + c;
+            if (g >= g1) break;
+            uint4 a[MB][4];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
-                f32x4 p = xsn[mb];
+                const uint4 *src = reinterpret_cast<const uint4 *>(arow[mb] + g * QGROUP + q * 32);
 #pragma unroll
-                for (int t = 0; t < 4; ++t) p = mfma16<T>(a[mb][t], b[t], p);
-                acc[mb][nb] += s[nb] * p;
+                for (int t = 0; t < 4; ++t) a[mb][t] = src[t];
+            }
+            f32x4 xsn[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                xsn[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xsn[mb] = mfma16<T>(a[mb][t], negb, xsn[mb]);
+            }
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(zraw[c][nb], g) : 8u);
+                const float s = f16_bits_to_f32(uint16_t(sraw[c][nb]));
+                uint4 b[4];
+                b[0] = unpack8<T>(wc[c][nb].x, zb);
+                b[1] = unpack8<T>(wc[c][nb].y, zb);
+                b[2] = unpack8<T>(wc[c][nb].z, zb);
+                b[3] = unpack8<T>(wc[c][nb].w, zb);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    f32x4 p = xsn[mb];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) p = mfma16<T>(a[mb][t], b[t], p);
+                    acc[mb][nb] += s * p;
+                }
             }
         }
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) wc[c][nb] = wn[c][nb];
     }
 }
 
@@ -88,6 +110,13 @@ __device__ __forceinline__ void ksplit_reduce(f32x4 (&acc)[MB][NB], int wave, in
                     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] += red[wave + j][mb * NB + nb][lane];
         }
     }
+}
+
+// silu(g) * u, saturated to the fp16 range, as fp16 bits.
+__device__ __forceinline__ uint16_t silu_mul_f16(float g, float u) {
+    float v = g / (1.f + __expf(-g)) * u;
+    v = fminf(fmaxf(v, -65504.f), 65504.f);
+    return __builtin_bit_cast(uint16_t, _Float16(v));
 }
 
 }  // namespace qwq4

@@ -16,6 +16,7 @@ SYMBOLS = (
     "qw_q4_abi_version", "qw_q4_last_error", "qw_q4_gemv", "qw_q4_gemm_workspace_size", "qw_q4_gemm",
     "qw_moe_route", "qw_moe_experts_gemv", "qw_moe_experts_grouped", "qw_moe_grouped_workspace_size", "qw_moe_grouped_tile_m",
     "qw_moe_combine", "qw_q4_unpack", "qw_q4_dequant", "qw_q4_from_engine_order",
+    "qw_q4_tiled_size", "qw_q4_tile", "qw_q4_untile",
 )
 
 _P = ctypes.c_void_p
@@ -35,6 +36,9 @@ _SIGS = {
     "qw_moe_experts_grouped": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _P, _P, _P, _SZ, _P], _I),
     "qw_moe_grouped_tile_m": ([], _I),
     "qw_moe_combine": ([_P, _P, _P, _P, _I, _I, _I, _P, _I, _P], _I),
+    "qw_q4_tiled_size": ([_I64, _I64, _P, _P, _P], None),
+    "qw_q4_tile": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P], _I),
+    "qw_q4_untile": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P], _I),
     "qw_q4_unpack": ([_P, _I64, _I64, _P, _P], _I),
     "qw_q4_dequant": ([_P, _P, _P, _I64, _I64, _P, _P], _I),
     "qw_q4_from_engine_order": ([_P, _P, _I64, _P], _I),
@@ -73,6 +77,43 @@ def _dev(*ts):
     for t in ts:
         if t is not None and not t.is_cuda:
             raise RuntimeError("qwq4: all tensors must be on the GPU")
+
+
+# ------------------------------------------------------------ weight format
+def tiled_size(N, K):
+    a, b, c = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+    lib().qw_q4_tiled_size(N, K, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+    return a.value, b.value, c.value
+
+
+def tile(W, S, Z, N, K):
+    """Checkpoint-order (W, S, Z) device tensors -> tiled (Wt, St, Zt or None)."""
+    import torch
+    wb, sb, zb = tiled_size(N, K)
+    Wt = torch.empty(wb // 4, dtype=torch.int32, device=W.device)
+    St = torch.empty(sb // 2, dtype=torch.int16, device=W.device)
+    Zt = torch.empty(zb // 2, dtype=torch.int16, device=W.device) if Z is not None else None
+    _dev(W, S, Z)
+    _check(lib().qw_q4_tile(_ptr(W), _ptr(S), _ptr(Z), N, K, _ptr(Wt), _ptr(St), _ptr(Zt), _stream()), "qw_q4_tile")
+    return Wt, St, Zt
+
+
+def untile(Wt, St, Zt, N, K):
+    import torch
+    G = K // 128
+    W = torch.empty((N, K // 8), dtype=torch.int32, device=Wt.device)
+    S = torch.empty((N, G), dtype=torch.int16, device=Wt.device)
+    Z = torch.empty((N, (G + 7) // 8), dtype=torch.int32, device=Wt.device) if Zt is not None else None
+    _check(lib().qw_q4_untile(_ptr(Wt), _ptr(St), _ptr(Zt), N, K, _ptr(W), _ptr(S), _ptr(Z), _stream()),
+           "qw_q4_untile")
+    return W, S, Z
+
+
+def tile_experts(W, S, Z, rows, K):
+    """[E][rows][...] checkpoint-order expert stacks -> one tiled [E*rows][K] matrix."""
+    E = W.shape[0]
+    return tile(W.reshape(E * rows, -1), S.reshape(E * rows, -1), None if Z is None else Z.reshape(E * rows, -1),
+                E * rows, K)
 
 
 # ---------------------------------------------------------------- operators
@@ -141,10 +182,9 @@ def moe_route(logits, topk, tile_m=0, out=None):
     return r
 
 
-def moe_experts_gemv(gate, up, down, route, x, h=None, yp=None):
-    """gate/up/down: (W, S, Z) device tensors; returns (h fp16-bits, yp fp32)."""
+def moe_experts_gemv(gate, up, down, route, x, E, F, h=None, yp=None):
+    """gate/up/down: tiled (Wt, St, Zt) of the stacked experts; returns (h fp16, yp fp32)."""
     import torch
-    E, F = gate[0].shape[0], gate[0].shape[1]
     H = x.shape[1]
     T, topk = route.T, route.topk
     if h is None:
@@ -167,9 +207,8 @@ def moe_grouped_workspace_size(T, topk, E, H, F):
     return lib().qw_moe_grouped_workspace_size(T, topk, E, H, F)
 
 
-def moe_experts_grouped(gate, up, down, route, x, h=None, yp=None, workspace=None):
+def moe_experts_grouped(gate, up, down, route, x, E, F, h=None, yp=None, workspace=None):
     import torch
-    E, F = gate[0].shape[0], gate[0].shape[1]
     T, H = x.shape
     topk = route.topk
     if h is None:
