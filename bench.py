@@ -187,8 +187,12 @@ def bench_gemm(torch, qwq4, dev, steps, warmup):
         ws = torch.empty(qwq4.gemm_workspace_size(T, K), dtype=torch.uint8, device=dev)
         Yh = torch.empty((T // 2, N), dtype=torch.bfloat16, device=dev)
         wsh = torch.empty(qwq4.gemm_workspace_size(T // 2, K), dtype=torch.uint8, device=dev)
-        for _ in range(warmup):
+        # warm up for >= 0.3 s so the timed region runs at steady clocks
+        t_end = time.perf_counter() + 0.3
+        while time.perf_counter() < t_end or warmup > 0:
             qwq4.gemm(*W, X, N, K, Y=Y, y_bf16=True, workspace=ws)
+            torch.cuda.synchronize()
+            warmup -= 1
         with Timer(torch) as t:
             for _ in range(steps):
                 qwq4.gemm(*W, X, N, K, Y=Y, y_bf16=True, workspace=ws)

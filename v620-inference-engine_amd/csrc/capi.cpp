@@ -94,7 +94,8 @@ int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
     REQUIRE(T >= 1, "qw_q4_gemm: T = %d must be >= 1", T);
     REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(X, 16), "qw_q4_gemm: ldx %d must be >= K, a multiple of 8, X 16-byte aligned", ldx);
     REQUIRE(ldy >= N, "qw_q4_gemm: ldy %d < N", ldy);
-    REQUIRE(aligned(Y, y_bf16 ? 2 : 4), "qw_q4_gemm: Y misaligned");
+    REQUIRE(aligned(Y, 16) && ldy % (y_bf16 ? 8 : 4) == 0,
+            "qw_q4_gemm: Y must be 16-byte aligned with rows of a multiple of 16 bytes (ldy %d)", ldy);
     const size_t need = qwq4::gemm_workspace_bytes(T, K);
     REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256),
             "qw_q4_gemm: workspace needs %zu bytes, 256-byte aligned (got %zu)", need, workspace_bytes);
