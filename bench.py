@@ -268,7 +268,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="all")
+    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, gemm, moe_prefill")
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -279,20 +279,22 @@ def main():
     import qwq4
     dev = torch.device("cuda:0")
     qwq4.lib()
-    wl = a.workload
+    wl = set(a.workload.split(","))
+    if "all" in wl:
+        wl = {"gemv", "moe", "gemm", "moe_prefill"}
     res = {}
-    if wl in ("all", "gemv"):
+    if "gemv" in wl:
         res["gemv"] = bench_gemv(torch, qwq4, dev, a.steps, a.warmup)
         print(f"# gemv {res['gemv']['GB_s']:.1f} GB/s", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
-    if wl in ("all", "moe"):
+    if "moe" in wl:
         res["moe_decode"] = bench_moe(torch, qwq4, dev, a.steps, a.warmup)
         print("# moe decode done", file=sys.stderr, flush=True)
-    if wl in ("all", "gemm"):
+    if "gemm" in wl:
         res["prefill_gemm"] = bench_gemm(torch, qwq4, dev, max(2, a.steps // 4), 1)
         print("# gemm done", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
-    if wl in ("all", "moe_prefill"):
+    if "moe_prefill" in wl:
         res["moe_prefill"] = bench_moe_prefill(torch, qwq4, dev, max(2, a.steps // 4), 1)
         print("# moe prefill done", file=sys.stderr, flush=True)
     line = {
@@ -313,7 +315,7 @@ def main():
                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                             "kernel": "q4_gemv_kernel", "avg_launch_us": round(g["avg_launch_us"], 3)}
     line["workloads"] = res
-    if not a.no_cpu and wl in ("all", "gemv"):
+    if not a.no_cpu and "gemv" in wl:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))
 

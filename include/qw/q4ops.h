@@ -129,7 +129,8 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
  * moe.hpp:29-32): the same outputs as qw_moe_experts_gemv for any T, over
  * the (expert, tile) list qw_moe_route writes when called with
  * tile_m = qw_moe_grouped_tile_m(). workspace: at least
- * qw_moe_grouped_workspace_size(...) bytes (may be 0), 256-byte aligned. */
+ * qw_moe_grouped_workspace_size(...) bytes (an fp16 copy of x),
+ * 256-byte aligned. */
 int qw_moe_grouped_tile_m(void);
 size_t qw_moe_grouped_workspace_size(int T, int topk, int E, int H, int F);
 int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,

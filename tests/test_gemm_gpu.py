@@ -34,16 +34,23 @@ def test_gemm_prefill_chunk_sampled(gpu, oracle, N, K):
     assert bf16_err_ok(Y[np.ix_(toks, rows)], ref)
 
 
-def test_grouped_matches_oracle_small(gpu, oracle):
-    E, H, F, k, T = 16, 512, 256, 4, 300
-    ex = synth.experts(61, E, H, F)
+# (E, H, F, k, T, zeros, bias): few tokens per expert (one partial tile each,
+# some experts empty); many per expert (several tiles, ragged last tile, F
+# not a multiple of 256); symmetric weights (no zero tensor).
+@pytest.mark.parametrize("E,H,F,k,T,zeros,bias", [(16, 512, 256, 4, 300, True, 0.5),
+                                                  (8, 256, 384, 2, 1100, True, 1.0),
+                                                  (64, 384, 128, 6, 40, False, 0.0)])
+def test_grouped_matches_oracle_small(gpu, oracle, E, H, F, k, T, zeros, bias):
+    print(f"grouped E={E} H={H} F={F} k={k} T={T} zeros={zeros}", flush=True)
+    ex = synth.experts(61, E, H, F, zeros=zeros)
     xb, xf = synth.acts(61, "x", T, H)
-    l = synth.router_logits(61, "l", T, E, bias_sigma=0.5)
+    l = synth.router_logits(61, "l", T, E, bias_sigma=bias)
     out, h_ref, yp_ref = oracle.moe(xf, l, k, *ex, want_parts=True)
     from test_moe_gpu import _experts_dev
     (dg, du, dd), E, F = _experts_dev(gpu, ex)
     r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=qwq4.moe_grouped_tile_m())
     h, yp = qwq4.moe_experts_grouped(dg, du, dd, r, to_dev(xb, gpu), E, F)
+    assert rel_err(host(h).astype(np.float32), h_ref) <= TOL
     assert rel_err(host(yp), yp_ref) <= TOL
     o = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
     assert rel_err(o, out) <= TOL

@@ -1,100 +1,153 @@
 // Grouped q4 expert GEMMs for prefill chunks (reference role:
-// gpu::moe_experts_T, src/kernels/moe_experts.hip:17-171).
+// gpu::moe_experts_T, src/kernels/moe_experts.hip:17-171, which dequantises
+// the expert's q4 weights into an fp16 LDS tile and multiplies gathered
+// token rows).
 //
-// Work is the (expert, 32-token tile) list written by the routing kernel
-// (qw_moe_route with tile_m = 32). This first version runs each tile through
-// the GEMV wave core: every wave owns 16 weight rows and the tile's 32 tokens.
+// Work is the (expert, tile of GROUPED_TILE_M slots) list written by the
+// routing kernel (qw_moe_route with tile_m = GROUPED_TILE_M); slots of one
+// expert are contiguous (offsets[e] ..), slot p carries token pair_tok[p].
+// Each block runs the shared q4 MFMA GEMM core (q4_gemm_core.cuh) on one
+// list entry and 256 weight rows:
+//   gate/up  A = the tile's gathered token rows of x (fp16 copy in the
+//            workspace), weight rows = 128 gate rows and the same 128 up rows,
+//            interleaved by 32 so each wave holds gate and up of the same
+//            columns; epilogue h = silu(g) * u in fp16 (saturated), the
+//            reference's fp16 intermediate.
+//   down     A = the tile's h rows (contiguous slots), 256 down rows, fp32 yp.
+// Blocks past the list's length (n_tiles, known only on the device) exit at
+// once; the grid is sized for the largest possible list.
+#include "q4_gemm_core.cuh"
 #include "q4_kernels.hpp"
-#include "q4_wave.cuh"
 
 namespace qwq4 {
 
-constexpr int GROUPED_TILE_M = 32;
-
-size_t moe_grouped_workspace_bytes(int, int, int, int, int) { return 0; }
-
-template <bool HAS_Z>
-__global__ __launch_bounds__(512) void moe_gate_up_tile_kernel(
-    const uint32_t *__restrict__ gw, const uint16_t *__restrict__ gs, const uint16_t *__restrict__ gz,
-    const uint32_t *__restrict__ uw, const uint16_t *__restrict__ us, const uint16_t *__restrict__ uz,
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ pair_tok, const int32_t *__restrict__ tile_e,
-    const int32_t *__restrict__ tile_m0, const int32_t *__restrict__ n_tiles, const uint16_t *__restrict__ x, int H,
-    int F, uint16_t *__restrict__ h) {
-    const int tile = blockIdx.y;
-    if (tile >= *n_tiles) return;
-    const int e = tile_e[tile], m0 = tile_m0[tile];
-    const int base = offsets[e] + m0, M = min(GROUPED_TILE_M, offsets[e + 1] - offsets[e] - m0);
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, q = lane / 16, n = lane % 16;
-    const int G = H / QGROUP, fsub = F / 16, lsub = blockIdx.x * 8 + wave;
-    const int64_t sub = int64_t(e) * fsub + min(lsub, fsub - 1);
-    const Q4Tile wt[2] = {Q4Tile(gw, gs, gz, sub, G), Q4Tile(uw, us, uz, sub, G)};
-    const uint16_t *arow[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) arow[mb] = x + int64_t(pair_tok[base + min(mb * 16 + n, M - 1)]) * H;
-    f32x4 acc[2][2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) acc[mb][0] = acc[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    q4_groups<BF16, 2, 2, HAS_Z, 2>(wt, arow, 0, G, lane, acc);
-    if (lsub >= fsub) return;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = mb * 16 + 4 * q + r;
-            if (m < M) h[int64_t(base + m) * F + lsub * 16 + n] = silu_mul_f16(acc[mb][0][r], acc[mb][1][r]);
-        }
-}
-
-template <bool HAS_Z>
-__global__ __launch_bounds__(512) void moe_down_tile_kernel(const uint32_t *__restrict__ dw,
-                                                            const uint16_t *__restrict__ ds,
-                                                            const uint16_t *__restrict__ dz,
-                                                            const int32_t *__restrict__ offsets,
-                                                            const int32_t *__restrict__ tile_e,
-                                                            const int32_t *__restrict__ tile_m0,
-                                                            const int32_t *__restrict__ n_tiles,
-                                                            const uint16_t *__restrict__ h, int H, int F,
-                                                            float *__restrict__ yp) {
-    const int tile = blockIdx.y;
-    if (tile >= *n_tiles) return;
-    const int e = tile_e[tile], m0 = tile_m0[tile];
-    const int base = offsets[e] + m0, M = min(GROUPED_TILE_M, offsets[e + 1] - offsets[e] - m0);
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, q = lane / 16, n = lane % 16;
-    const int G = F / QGROUP, hsub = H / 16, lsub = blockIdx.x * 8 + wave;
-    const int64_t sub = int64_t(e) * hsub + min(lsub, hsub - 1);
-    const Q4Tile wt[1] = {Q4Tile(dw, ds, dz, sub, G)};
-    const uint16_t *arow[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) arow[mb] = h + int64_t(base + min(mb * 16 + n, M - 1)) * F;
-    f32x4 acc[2][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}, {f32x4{0.f, 0.f, 0.f, 0.f}}};
-    q4_groups<F16, 2, 1, HAS_Z, 4>(wt, arow, 0, G, lane, acc);
-    if (lsub >= hsub) return;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = mb * 16 + 4 * q + r;
-            if (m < M) yp[int64_t(base + m) * H + lsub * 16 + n] = acc[mb][0][r];
-        }
-}
+constexpr int GROUPED_TILE_M = 128;
 
 int moe_grouped_tile_m() { return GROUPED_TILE_M; }
 
+size_t moe_grouped_workspace_bytes(int T, int, int, int H, int) { return gemm_workspace_bytes(T, H); }
+
+static __device__ __forceinline__ uint16_t f32_to_f16_sat(float v) {
+    v = fminf(fmaxf(v, -65504.f), 65504.f);
+    return __builtin_bit_cast(uint16_t, _Float16(v));
+}
+
+template <bool HAS_Z>
+__global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(
+    const uint32_t *__restrict__ gw, const uint16_t *__restrict__ gs, const uint16_t *__restrict__ gz,
+    const uint32_t *__restrict__ uw, const uint16_t *__restrict__ us, const uint16_t *__restrict__ uz,
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ pair_tok, const int32_t *__restrict__ tile_e,
+    const int32_t *__restrict__ tile_m0, const int32_t *__restrict__ n_tiles, const uint16_t *__restrict__ xh, int H,
+    int F, uint16_t *__restrict__ h) {
+    constexpr int BM = GROUPED_TILE_M;
+    using Sh = GemmShape<BM>;
+    static_assert(Sh::NJ == 2, "gate/up pairing assumes two 32-row MFMA tiles per wave");
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tile = blockIdx.y;
+    if (tile >= *n_tiles) return;
+    const int e = tile_e[tile], m0 = tile_m0[tile];
+    const int base = offsets[e] + m0, M = min(BM, offsets[e + 1] - offsets[e] - m0);
+    const int tid = threadIdx.x, wave = tid / WAVE;
+    const int j0 = blockIdx.x * 128;
+    // tile row r = tid / 2: 64-row band r / 64 covers columns j0 + 32 (r / 64)
+    // .. + 32; inside it rows 0-31 are gate, 32-63 up (wave-uniform choice)
+    const int r = tid / 2, col = (r / 64) * 32 + r % 32;
+    const bool up = (r % 64) >= 32;
+    const int64_t wrow = int64_t(e) * F + min(j0 + col, F - 1);
+    const BRow b = up ? BRow(uw, us, uz, wrow, H / QGROUP) : BRow(gw, gs, gz, wrow, H / QGROUP);
+    const uint16_t *ap[BM / 64];
+#pragma unroll
+    for (int j = 0; j < BM / 64; ++j) ap[j] = xh + int64_t(pair_tok[base + min(a_load_row(j), M - 1)]) * H;
+    f32x16 acc[2][Sh::NJ];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
+    gemm_tile<BM, HAS_Z>(smem, ap, b, H, acc);
+
+    // acc[i][0] (gate) and acc[i][1] (up) hold the same 32 columns
+    f32x16 hv[2][1];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const float g = acc[i][0][q], u = acc[i][1][q];
+            hv[i][0][q] = g / (1.f + __expf(-g)) * u;
+        }
+    const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
+    emit_tile<1, 2>(
+        smem + wave * 64 * 32 * 2, hv, [](float v, int, int) { return f32_to_f16_sat(v); },
+        [&](int tr, int c, uint4 v) {
+            const int m = wm * 64 + tr, j = j0 + wn2 * 32 + c;
+            if (m < M && j < F) *reinterpret_cast<uint4 *>(h + int64_t(base + m) * F + j) = v;
+        });
+}
+
+template <bool HAS_Z>
+__global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
+    const uint32_t *__restrict__ dw, const uint16_t *__restrict__ ds, const uint16_t *__restrict__ dz,
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ tile_e, const int32_t *__restrict__ tile_m0,
+    const int32_t *__restrict__ n_tiles, const uint16_t *__restrict__ h, int H, int F, float *__restrict__ yp) {
+    constexpr int BM = GROUPED_TILE_M;
+    using Sh = GemmShape<BM>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tile = blockIdx.y;
+    if (tile >= *n_tiles) return;
+    const int e = tile_e[tile], m0 = tile_m0[tile];
+    const int base = offsets[e] + m0, M = min(BM, offsets[e + 1] - offsets[e] - m0);
+    const int tid = threadIdx.x, wave = tid / WAVE;
+    const int n0 = blockIdx.x * GB_N;
+    const BRow b(dw, ds, dz, int64_t(e) * H + min(n0 + tid / 2, H - 1), F / QGROUP);
+    const uint16_t *ap[BM / 64];
+#pragma unroll
+    for (int j = 0; j < BM / 64; ++j) ap[j] = h + int64_t(base + min(a_load_row(j), M - 1)) * F;
+    f32x16 acc[2][Sh::NJ];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
+    gemm_tile<BM, HAS_Z>(smem, ap, b, F, acc);
+
+    const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
+    emit_tile<Sh::NJ, 4>(
+        smem + wave * 64 * 32 * 4, acc, [](float, int, int) { return uint16_t(0); },
+        [&](int tr, int c, uint4 v) {
+            const int m = wm * 64 + tr, n = n0 + wn2 * Sh::WNR + c;
+            if (m < M && n < H) *reinterpret_cast<uint4 *>(yp + int64_t(base + m) * H + n) = v;
+        });
+}
+
+template <class K>
+static void set_lds(K kern) {
+    (void)persistent_shape(reinterpret_cast<const void *>(kern), G_THREADS, GEMM_LDS);  // sets the LDS limit
+}
+
 void launch_moe_grouped(const MoeGroupedArgs &a, hipStream_t s) {
+    uint16_t *xh = static_cast<uint16_t *>(a.ws);
+    launch_x_to_f16(a.x, a.H, a.T, a.H, xh, s);
     const int max_tiles = a.T * a.topk / GROUPED_TILE_M + a.E;
-    const dim3 g1(unsigned((a.F + 127) / 128), unsigned(max_tiles)), g2(unsigned((a.H + 127) / 128), unsigned(max_tiles));
-    if (a.gz)
-        moe_gate_up_tile_kernel<true><<<g1, 512, 0, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets, a.pair_tok,
-                                                         a.tile_e, a.tile_m0, a.n_tiles, a.x, a.H, a.F, a.h);
-    else
-        moe_gate_up_tile_kernel<false><<<g1, 512, 0, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets, a.pair_tok,
-                                                          a.tile_e, a.tile_m0, a.n_tiles, a.x, a.H, a.F, a.h);
-    if (a.dz)
-        moe_down_tile_kernel<true><<<g2, 512, 0, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0, a.n_tiles,
-                                                      a.h, a.H, a.F, a.yp);
-    else
-        moe_down_tile_kernel<false><<<g2, 512, 0, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0, a.n_tiles,
-                                                       a.h, a.H, a.F, a.yp);
+    const dim3 g1(unsigned((a.F + 127) / 128), unsigned(max_tiles)),
+        g2(unsigned((a.H + GB_N - 1) / GB_N), unsigned(max_tiles));
+    if (a.gz) {
+        set_lds(moe_gate_up_gemm_kernel<true>);
+        moe_gate_up_gemm_kernel<true><<<g1, G_THREADS, GEMM_LDS, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets,
+                                                                      a.pair_tok, a.tile_e, a.tile_m0, a.n_tiles, xh,
+                                                                      a.H, a.F, a.h);
+    } else {
+        set_lds(moe_gate_up_gemm_kernel<false>);
+        moe_gate_up_gemm_kernel<false><<<g1, G_THREADS, GEMM_LDS, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets,
+                                                                       a.pair_tok, a.tile_e, a.tile_m0, a.n_tiles, xh,
+                                                                       a.H, a.F, a.h);
+    }
+    if (a.dz) {
+        set_lds(moe_down_gemm_kernel<true>);
+        moe_down_gemm_kernel<true><<<g2, G_THREADS, GEMM_LDS, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0,
+                                                                   a.n_tiles, a.h, a.H, a.F, a.yp);
+    } else {
+        set_lds(moe_down_gemm_kernel<false>);
+        moe_down_gemm_kernel<false><<<g2, G_THREADS, GEMM_LDS, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0,
+                                                                    a.n_tiles, a.h, a.H, a.F, a.yp);
+    }
 }
 
 }  // namespace qwq4

@@ -104,9 +104,11 @@ struct GemmArgs {
     int ldx, T;
     void *Y;
     int ldy, y_bf16, N, K;
-    void *ws;  // workspace: operand-ordered X and -BIAS * group sums
+    void *ws;  // workspace: fp16 copy of X
 };
 size_t gemm_workspace_bytes(int T, int K);
+// bf16 [T][ldx] -> fp16 [T][K] (saturating), the GEMMs' A operand.
+void launch_x_to_f16(const uint16_t *X, int ldx, int T, int K, uint16_t *Xh, hipStream_t s);
 void launch_gemm(const GemmArgs &a, hipStream_t s);
 
 }  // namespace qwq4
