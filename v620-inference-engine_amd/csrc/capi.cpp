@@ -114,7 +114,7 @@ int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_
     REQUIRE(tile_m >= 0, "qw_moe_route: tile_m < 0");
     REQUIRE(tile_m == 0 || (tile_e && tile_m0 && n_tiles), "qw_moe_route: tile_m > 0 needs the tile outputs");
     REQUIRE(int64_t(T) * topk < (1 << 30), "qw_moe_route: too many pairs");
-    const size_t lds = qwq4::route_lds_bytes(T, E) + (T <= 64 ? 64 * 64 * 4 : 0);
+    const size_t lds = T <= 64 ? 0 : qwq4::route_lds_bytes(T, E);
     REQUIRE(lds <= 160 * 1024, "qw_moe_route: T = %d, E = %d needs %zu bytes of LDS (> 160 KiB)", T, E, lds);
     qwq4::RouteArgs a{logits, T, E, topk, tile_m, top_e, top_w, counts, offsets, tok_slot, pair_tok, active,
                       n_active, tile_e, tile_m0, n_tiles};
@@ -132,6 +132,7 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
     if (int r = check_q4("qw_moe_experts_gemv(down)", dw, ds, int64_t(E) * H, F)) return r;
     REQUIRE(offsets && active && n_active && pair_tok && x && h && yp, "qw_moe_experts_gemv: null pointer");
     REQUIRE(T >= 1 && T <= 32, "qw_moe_experts_gemv: T = %d outside 1..32", T);
+    REQUIRE(qwq4::moe_gemv_supported(H, F), "qw_moe_experts_gemv: H = %d, F = %d too large", H, F);
     REQUIRE(topk >= 1 && topk <= E, "qw_moe_experts_gemv: topk = %d outside 1..E", topk);
     REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(yp, 4), "qw_moe_experts_gemv: x/h must be 16-byte aligned");
     qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, offsets, active, n_active, pair_tok,

@@ -1,0 +1,257 @@
+// Gathered per-expert q4 GEMVs for routed decode tokens (reference role:
+// gpu::moe_experts_P, src/kernels/moe_experts.hip:177-245; arithmetic of
+// ref::Model::moe, src/ref/ref_model.cpp:434-463).
+//
+// grid (row blocks of one expert, max active experts). Block y serves the
+// y-th expert with tokens (active[] ascending); its M tokens are the slots
+// offsets[e] .. offsets[e+1]-1, slot p carrying token pair_tok[p]. Expert e's
+// weights are rows e*F .. of the stacked [E*F][H] gate and up matrices and
+// rows e*H .. of the [E*H][F] down matrix (tiled format).
+//
+// The block runs over the expert's tokens in chunks of R rows (as many as fit
+// the LDS budget; with decode batches nearly every expert has one chunk, so
+// its weights come from HBM once per call however many tokens chose it). Per
+// chunk each wave requests its whole K range of one subtile up front, the
+// chunk's rows (x gathered through pair_tok, or h) go to LDS by direct loads,
+// every wave multiplies, and the KS partial sums of each subtile are reduced
+// through LDS in a fixed order.
+//   gate/up  waves = subtiles x {gate, up} x KS; the reducing wave also
+//            forms h = silu(g) * u (fp16, saturated, the reference's fp16
+//            intermediate) from the two sums it holds.
+//   down     waves = subtiles x KS; yp fp32.
+#include "q4_gemv_core.cuh"
+#include "q4_kernels.hpp"
+
+namespace qwq4 {
+
+__host__ __device__ inline size_t moe_lds_bytes(int R, int K) {
+    return size_t(x_pieces(R, K)) * 16 + size_t(8) * WAVE * 16;
+}
+
+__device__ __forceinline__ uint16_t silu_mul_f16(float g, float u) {
+    float v = g / (1.f + __expf(-g)) * u;
+    v = fminf(fmaxf(v, -65504.f), 65504.f);
+    return __builtin_bit_cast(uint16_t, _Float16(v));
+}
+
+// Reads the block's expert: n_active and active[y] are requested together
+// (one latency), and the weight loads need only e.
+__device__ __forceinline__ int block_expert(const int32_t *n_active, const int32_t *active, int E) {
+    const int na = *n_active, e = active[blockIdx.y];
+    return int(blockIdx.y) < na ? min(max(e, 0), E - 1) : -1;
+}
+
+// Rows 0..M-1 of K 16-bit elements (row m at row(m), a wave-uniform address)
+// -> LDS [M][K], as stage_rows_issue, but row by row so that the row address
+// is a scalar: the gathered token index comes by a scalar load, which does
+// not wait behind the weight loads in flight. K / 8 must be a multiple of 64.
+template <class RowFn>
+__device__ __forceinline__ void stage_rows_uniform(RowFn row, int M, int K, uint4 *xl) {
+    const int kc = K / 8, wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nw = blockDim.x / WAVE;
+    for (int m = 0; m < M; ++m) {
+        const uint16_t *r = row(m);
+        for (int c = wave * WAVE; c < kc; c += nw * WAVE)
+            __builtin_amdgcn_global_load_lds(r + (c + lane) * 8, xl + m * kc + c, 16, 0, 0);
+    }
+}
+
+// The lane index, as a value the compiler cannot see through: the per-lane
+// weight addresses derived from it are recomputed in every chunk instead of
+// being hoisted out of the chunk loop and held (2 registers each) across it.
+__device__ __forceinline__ int opaque_lane() {
+    int l = int(threadIdx.x) % WAVE;
+    asm volatile("" : "+v"(l));
+    return l;
+}
+
+template <int KS, int GW, bool HAS_Z>
+__global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
+    const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
+    const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
+    const int32_t *__restrict__ n_active, const int32_t *__restrict__ pair_tok, const uint16_t *__restrict__ x, int E,
+    int H, int F, int R, uint16_t *__restrict__ h) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int e = block_expert(n_active, active, E);
+    if (e < 0) return;
+    constexpr int SUB = 8 / (2 * KS);
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
+              n = lane % 16;
+    const int sl = wave / (2 * KS), mat = (wave / KS) % 2, kp = wave % KS;
+    const int G = H / QGROUP, gpk = G / KS, fsub = F / 16, kc = H / 8;
+    const int lsub = blockIdx.x * SUB + sl;
+    const int64_t sub = int64_t(e) * fsub + min(lsub, fsub - 1);
+    const Q4Tile t = mat ? Q4Tile(uw, us, uz, sub, G) : Q4Tile(gw, gs, gz, sub, G);
+    // the first chunk's weights go out before the slot range is known (an
+    // active expert has at least one token)
+    WaveRange<GW, HAS_Z> wr;
+    wr.fetch(t, kp * gpk, gpk, opaque_lane());
+    const int base = offsets[e], M = offsets[e + 1] - base;
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(R, H));
+    int m0 = 0;
+    do {  // M >= 1: the first chunk always runs (its weights are already requested)
+        const int mc = min(R, M - m0);
+        if (m0 > 0) {
+            // later chunks refetch (from L2): nothing stays live across chunks
+            wr.fetch(t, kp * gpk, gpk, opaque_lane());
+            lds_barrier();  // the previous chunk's rows and partials are consumed
+        }  // the previous chunk's rows and partials are consumed
+        if (kc % WAVE == 0)
+            stage_rows_uniform([&](int m) { return x + int64_t(pair_tok[base + m0 + m]) * H; }, mc, H, xl);
+        else
+            stage_rows_issue([&](int m) { return x + int64_t(pair_tok[base + m0 + m]) * H; }, mc, H, xl);
+        __syncthreads();
+        const uint4 *xr[1] = {xl + min(n, mc - 1) * kc + q * 4};
+        f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+        wr.template compute<BF16, 1>(xr, acc);
+        red[wave * WAVE + lane] = acc[0];
+        lds_barrier();
+        if (mat == 0 && kp == 0 && lsub < fsub) {
+            f32x4 g = red[wave * WAVE + lane], u = red[(wave + KS) * WAVE + lane];
+#pragma unroll
+            for (int j = 1; j < KS; ++j) {
+                g += red[(wave + j) * WAVE + lane];
+                u += red[(wave + KS + j) * WAVE + lane];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 4 * q + r;
+                if (m < mc) h[int64_t(base + m0 + m) * F + lsub * 16 + n] = silu_mul_f16(g[r], u[r]);
+            }
+        }
+        m0 += R;
+    } while (m0 < M);
+}
+
+template <int KS, int GW, bool HAS_Z>
+__global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz,
+                                                            const int32_t *__restrict__ offsets,
+                                                            const int32_t *__restrict__ active,
+                                                            const int32_t *__restrict__ n_active,
+                                                            const uint16_t *__restrict__ h, int E, int H, int F, int R,
+                                                            float *__restrict__ yp) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int e = block_expert(n_active, active, E);
+    if (e < 0) return;
+    constexpr int SUB = 8 / KS;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
+              n = lane % 16;
+    const int sl = wave / KS, kp = wave % KS;
+    const int G = F / QGROUP, gpk = G / KS, hsub = H / 16, kc = F / 8;
+    const int lsub = blockIdx.x * SUB + sl;
+    const Q4Tile t(dw, ds, dz, int64_t(e) * hsub + min(lsub, hsub - 1), G);
+    WaveRange<GW, HAS_Z> wr;
+    wr.fetch(t, kp * gpk, gpk, opaque_lane());
+    const int base = offsets[e], M = offsets[e + 1] - base;
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(R, F));
+    int m0 = 0;
+    do {  // M >= 1: the first chunk always runs (its weights are already requested)
+        const int mc = min(R, M - m0);
+        if (m0 > 0) {
+            wr.fetch(t, kp * gpk, gpk, opaque_lane());
+            lds_barrier();
+        }
+        if (kc % WAVE == 0)
+            stage_rows_uniform([&](int m) { return h + int64_t(base + m0 + m) * F; }, mc, F, xl);
+        else
+            stage_rows_issue([&](int m) { return h + int64_t(base + m0 + m) * F; }, mc, F, xl);
+        __syncthreads();
+        const uint4 *xr[1] = {xl + min(n, mc - 1) * kc + q * 4};
+        f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+        wr.template compute<F16, 1>(xr, acc);
+        if constexpr (KS > 1) {
+            red[wave * WAVE + lane] = acc[0];
+            lds_barrier();
+            if (kp == 0) {
+#pragma unroll
+                for (int j = 1; j < KS; ++j) acc[0] += red[(wave + j) * WAVE + lane];
+            }
+        }
+        if (kp == 0 && lsub < hsub) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 4 * q + r;
+                if (m < mc) yp[int64_t(base + m0 + m) * H + lsub * 16 + n] = acc[0][r];
+            }
+        }
+        m0 += R;
+    } while (m0 < M);
+}
+
+// K split: the largest power of two <= kmax dividing G with at most 16 groups
+// per wave; GW: the register budget for a wave's groups.
+static int pick_ks(int G, int kmax) {
+    int ks = 1;
+    while (ks < kmax && G % (ks * 2) == 0) ks *= 2;
+    return ks;
+}
+
+template <int KS, int GW, bool HAS_Z>
+static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
+    auto kern = moe_gate_up_gemv_kernel<KS, GW, HAS_Z>;
+    const size_t lds = moe_lds_bytes(R, a.H);
+    if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
+    constexpr int SUB = 8 / (2 * KS);
+    const dim3 grid(unsigned((a.F / 16 + SUB - 1) / SUB), unsigned(max_active));
+    kern<<<grid, 512, lds, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets, a.active, a.n_active, a.pair_tok, a.x,
+                                a.E, a.H, a.F, R, a.h);
+}
+
+template <int KS, int GW, bool HAS_Z>
+static void launch_down(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
+    auto kern = moe_down_gemv_kernel<KS, GW, HAS_Z>;
+    const size_t lds = moe_lds_bytes(R, a.F);
+    if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
+    constexpr int SUB = 8 / KS;
+    const dim3 grid(unsigned((a.H / 16 + SUB - 1) / SUB), unsigned(max_active));
+    kern<<<grid, 512, lds, s>>>(a.dw, a.ds, a.dz, a.offsets, a.active, a.n_active, a.h, a.E, a.H, a.F, R, a.yp);
+}
+
+template <bool DOWN, int KS, bool HAS_Z>
+static void launch_gw(const MoeGemvArgs &a, int max_active, int R, int gpk, hipStream_t s) {
+    if (gpk <= 4) {
+        if constexpr (DOWN) launch_down<KS, 4, HAS_Z>(a, max_active, R, s);
+        else launch_gate_up<KS, 4, HAS_Z>(a, max_active, R, s);
+    } else if (gpk <= 8) {
+        if constexpr (DOWN) launch_down<KS, 8, HAS_Z>(a, max_active, R, s);
+        else launch_gate_up<KS, 8, HAS_Z>(a, max_active, R, s);
+    } else {
+        if constexpr (DOWN) launch_down<KS, 16, HAS_Z>(a, max_active, R, s);
+        else launch_gate_up<KS, 16, HAS_Z>(a, max_active, R, s);
+    }
+}
+
+template <bool DOWN, bool HAS_Z>
+static void launch_one(const MoeGemvArgs &a, int max_active, hipStream_t s) {
+    const int K = DOWN ? a.F : a.H, G = K / QGROUP;
+    const int ks = pick_ks(G, DOWN ? 8 : 4);
+    const int gpk = G / ks;
+    // rows per block: a decode batch's tokens of one expert, as many as keep
+    // the staged activations within 32 KB (two blocks per CU)
+    int R = a.T < 16 ? a.T : 16;
+    while (R > 1 && size_t(R) * K * 2 > 32 * 1024) --R;
+    switch (ks) {
+        case 1: launch_gw<DOWN, 1, HAS_Z>(a, max_active, R, gpk, s); break;
+        case 2: launch_gw<DOWN, 2, HAS_Z>(a, max_active, R, gpk, s); break;
+        case 4: launch_gw<DOWN, 4, HAS_Z>(a, max_active, R, gpk, s); break;
+        default:
+            if constexpr (DOWN) launch_gw<DOWN, 8, HAS_Z>(a, max_active, R, gpk, s);
+            break;
+    }
+}
+
+bool moe_gemv_supported(int H, int F) {
+    // each wave holds at most 16 groups of its K range
+    return H / QGROUP / pick_ks(H / QGROUP, 4) <= 16 && F / QGROUP / pick_ks(F / QGROUP, 8) <= 16;
+}
+
+void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s) {
+    const int max_active = a.T * a.topk < a.E ? a.T * a.topk : a.E;
+    if (a.gz) launch_one<false, true>(a, max_active, s);
+    else launch_one<false, false>(a, max_active, s);
+    if (a.dz) launch_one<true, true>(a, max_active, s);
+    else launch_one<true, false>(a, max_active, s);
+}
+
+}  // namespace qwq4

@@ -213,19 +213,70 @@ __device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
     }
 }
 
-// Decode batches (T <= 64): selections and slots in one launch.
-__global__ __launch_bounds__(1024) void route_fused_kernel(RouteArgs a) {
-    extern __shared__ unsigned char smem[];
+// Decode batches (T <= 64): selections and slots in one launch. A token
+// picks an expert at most once, so the tokens of expert e are the set bits of
+// one 64-bit mask; a pair's rank among them is a popcount below its bit.
+__global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
     __shared__ int32_t s_te[64 * 64];
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    for (int t = wave; t < a.T; t += 16) {
-        topk_wave(a.logits + int64_t(t) * a.E, a.E, a.topk, lane, s_te + t * a.topk, a.top_w + int64_t(t) * a.topk);
+    __shared__ unsigned long long s_mask[1024];
+    __shared__ int32_t s_off[1024];
+    __shared__ int32_t s_sum[16][3];
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int T = a.T, E = a.E, k = a.topk, P = T * k;
+    if (tid < E) s_mask[tid] = 0ull;
+    for (int t = wave; t < T; t += 16)
+        topk_wave(a.logits + int64_t(t) * E, E, k, lane, s_te + t * k, a.top_w + int64_t(t) * k);
+    __syncthreads();
+    for (int i = tid; i < P; i += blockDim.x) {
+        a.top_e[i] = s_te[i];
+        atomicOr(&s_mask[s_te[i]], 1ull << (i / k));
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < a.T * a.topk; i += blockDim.x) a.top_e[i] = s_te[i];
-    SlotLds L;
-    slot_lds_layout(a.T, a.E, &L, smem);
-    route_slots(s_te, a, L);
+    // exclusive scans over the experts (one per thread): pairs, non-empty
+    // experts, tiles
+    const int c = tid < E ? __popcll(s_mask[tid]) : 0;
+    const int v[3] = {c, c > 0, a.tile_m > 0 ? (c + a.tile_m - 1) / a.tile_m : 0};
+    int inc[3] = {v[0], v[1], v[2]};
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int u = __shfl_up(inc[j], o, WAVE);
+            if (lane >= o) inc[j] += u;
+        }
+    }
+    if (lane == WAVE - 1) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) s_sum[wave][j] = inc[j];
+    }
+    __syncthreads();
+    int ex[3] = {inc[0] - v[0], inc[1] - v[1], inc[2] - v[2]};
+    for (int w = 0; w < wave; ++w) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) ex[j] += s_sum[w][j];
+    }
+    if (tid < E) {
+        s_off[tid] = ex[0];
+        a.offsets[tid] = ex[0];
+        a.counts[tid] = c;
+        if (c > 0) a.active[ex[1]] = tid;
+        for (int j = 0; j < v[2]; ++j) {
+            a.tile_e[ex[2] + j] = tid;
+            a.tile_m0[ex[2] + j] = j * a.tile_m;
+        }
+        if (tid == E - 1) {
+            a.offsets[E] = ex[0] + c;
+            *a.n_active = ex[1] + v[1];
+            if (a.tile_m > 0) *a.n_tiles = ex[2] + v[2];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < P; i += blockDim.x) {
+        const int e = s_te[i], t = i / k;
+        const int slot = s_off[e] + __popcll(s_mask[e] & ((1ull << t) - 1ull));
+        a.tok_slot[i] = slot;
+        a.pair_tok[slot] = t;
+    }
 }
 
 __global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a) {
@@ -237,11 +288,8 @@ __global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a) {
 
 void launch_route(const RouteArgs &a, hipStream_t s) {
     const size_t lds = route_lds_bytes(a.T, a.E);
-    if (a.T <= 64 && a.topk <= 64) {
-        if (lds > 48 * 1024)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(route_fused_kernel),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-        route_fused_kernel<<<1, 1024, lds, s>>>(a);
+    if (a.T <= 64) {
+        route_small_kernel<<<1, 1024, 0, s>>>(a);
     } else {
         if (lds > 48 * 1024)
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(route_slots_kernel),

@@ -1,23 +1,12 @@
-// q4 GEMV for decode rows (M <= 32) and the gathered per-expert GEMV of routed
-// MoE tokens, on the gfx950 16x16x32 MFMA.
+// Dense q4 GEMV for decode rows (M <= 32 per launch), on the gfx950
+// 16x16x32 MFMA.
 //
-// Reference roles: gpu::gemv_rows (src/kernels/gemv.hip:7-42, decode
-// projections and LM head, fp16 weights there) and gpu::moe_experts_P
-// (src/kernels/moe_experts.hip:189-245). The arithmetic is
+// Reference role: gpu::gemv_rows (src/kernels/gemv.hip:7-42, decode
+// projections and LM head, fp16 weights there). The arithmetic is
 // ref::Model::expert_linear (src/ref/ref_model.cpp:100-119) with a per-group
-// zero point.
-//
-// Work split. A wave owns a 16-row subtile of the tiled weights and a
-// contiguous range of the 128-wide K groups; KS waves of a 512-thread block
-// share one subtile (a K split, reduced through LDS in a fixed order), so
-// small N still fills the chip. Lane l serves weight row n = l % 16 and
-// K-quarter q = l / 16 of every group: one 16-byte load per lane per group,
-// 1 KB of contiguous HBM per wave-instruction, the nibbles unpacked in
-// registers (q4_common.cuh). The MFMA's other operand is the activations:
-// lane l feeds token row m = l % 16, so the 16x16 result holds every
-// (token, row) pair; each lane ends with one weight row n and four token rows
-// 4(l/16) + r, so the group scale and zero are one value per lane.
-#include "q4_wave.cuh"
+// zero point. The wave-level work (one 16-row subtile x a K range, lane map)
+// is in q4_gemv_core.cuh.
+#include "q4_gemv_core.cuh"
 #include "q4_kernels.hpp"
 
 namespace qwq4 {
@@ -33,72 +22,15 @@ namespace qwq4 {
 //           runs on across subtiles.
 // Both stage the M activation rows (bf16) in LDS once per block. The MFMA
 // accumulator starts at -144 * sum(x) of the group (an MFMA against a splat
-// of -144), see q4_common.cuh.
+// of -144), see q4_common.cuh. KS waves of a block sharing a subtile reduce
+// their partial sums through LDS in a fixed order (deterministic).
 
-__host__ __device__ inline int x_pieces(int M, int K);
 __host__ __device__ inline size_t dense_lds_bytes(int M, int K, int MB) {
     return size_t(x_pieces(M, K)) * 16 + size_t(8) * MB * WAVE * 16;
 }
 
-// LDS-only barrier: orders this block's LDS traffic without draining the
-// global-memory loads in flight.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// x rows 0..M-1 of K bf16 -> LDS with direct global->LDS loads (no
-// registers; 1 KB per wave instruction). They are issued before the weight
-// loads, and the barrier that follows those waits for both, so activations
-// (L2) and weights (HBM) are all requested before anything waits.
-__host__ __device__ inline int x_pieces(int M, int K) {  // 16-byte pieces, rounded to whole waves
-    return (M * (K / 8) + WAVE - 1) / WAVE * WAVE;
-}
-
 __device__ __forceinline__ void stage_x_issue(const uint16_t *__restrict__ x, int xs, int M, int K, uint4 *xl) {
-    const int kc = K / 8, total = M * kc, wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int nw = blockDim.x / WAVE;
-    for (int base = wave * WAVE; base < total; base += nw * WAVE) {
-        const int i = min(base + lane, total - 1), m = i / kc, c = i - m * kc;
-        __builtin_amdgcn_global_load_lds(x + int64_t(m) * xs + c * 8, xl + base, 16, 0, 0);
-    }
-}
-
-__device__ __forceinline__ void store_y(void *y, int64_t o, float v, int y_bf16, int accumulate) {
-    if (y_bf16) {
-        uint16_t *yb = static_cast<uint16_t *>(y);
-        if (accumulate) v += bf16_bits_to_f32(yb[o]);
-        yb[o] = f32_to_bf16_rne(v);
-    } else {
-        float *yf = static_cast<float *>(y);
-        if (accumulate) v += yf[o];
-        yf[o] = v;
-    }
-}
-
-// One group of one subtile: acc[mb] += s * (x . (q - z)) for the lane's rows.
-template <int MB>
-__device__ __forceinline__ void dense_group(const uint4 &w, uint32_t zb, float s, const uint4 *const (&xr)[MB], int g,
-                                            f32x4 (&acc)[MB]) {
-    const uint4 negb = make_uint4(BF16::NEG_BIAS, BF16::NEG_BIAS, BF16::NEG_BIAS, BF16::NEG_BIAS);
-    uint4 b[4];
-    b[0] = unpack8<BF16>(w.x, zb);
-    b[1] = unpack8<BF16>(w.y, zb);
-    b[2] = unpack8<BF16>(w.z, zb);
-    b[3] = unpack8<BF16>(w.w, zb);
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-        uint4 a[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) a[t] = xr[mb][g * 16 + t];
-        f32x4 p = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) p = mfma16<BF16>(a[t], negb, p);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) p = mfma16<BF16>(a[t], b[t], p);
-        acc[mb] += s * p;
-    }
+    stage_rows_issue([&](int m) { return x + int64_t(m) * xs; }, M, K, xl);
 }
 
 template <int MB>
@@ -134,15 +66,8 @@ __global__ __launch_bounds__(512) void q4_gemv_block_kernel(const uint32_t *Wt,
     f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(M, K));
     stage_x_issue(x, xs, M, K, xl);
     const Q4Tile t(Wt, St, Zt, min(sub, nsub - 1), G);
-    uint4 w[GW];
-    uint32_t sv[GW], zv[GW];
-#pragma unroll
-    for (int c = 0; c < GW; ++c) {
-        const int g = g0 + min(c, gpk - 1);
-        w[c] = t.word4(g, lane);
-        sv[c] = t.scale(g, n);
-        if constexpr (HAS_Z) zv[c] = t.zero_word(g, n);
-    }
+    WaveRange<GW, HAS_Z> wr;
+    wr.fetch(t, g0, gpk, lane);
     __syncthreads();
     const uint4 *xr[MB];
 #pragma unroll
@@ -150,13 +75,7 @@ __global__ __launch_bounds__(512) void q4_gemv_block_kernel(const uint32_t *Wt,
     f32x4 acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < GW; ++c) {
-        if (c >= gpk) break;
-        const int g = g0 + c;
-        const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(zv[c], g) : 8u);
-        dense_group<MB>(w[c], zb, f16_bits_to_f32(uint16_t(sv[c])), xr, g, acc);
-    }
+    wr.template compute<BF16, MB>(xr, acc);
     if constexpr (KS > 1) {
         if (kp != 0) {
 #pragma unroll
@@ -354,133 +273,6 @@ void launch_gemv(const GemvArgs &a, hipStream_t s) {
         b.y = static_cast<char *>(a.y) + int64_t(m0) * a.ys * ysz;
         launch_gemv_fit(b, s);
     }
-}
-
-// ------------------------------------------------ routed-expert GEMVs
-// grid (row blocks of one expert, max active experts). Block y serves the
-// y-th expert with tokens (active[] ascending); its M tokens are the slots
-// offsets[e] .. offsets[e+1]-1. Expert e's weights are rows e*F .. of the
-// stacked [E*F][H] (gate, up) and [E*H][F] (down) tiled matrices.
-
-// gate/up fused with SiLU * up: h[slot][F] (fp16).
-template <int KS, int MB, bool HAS_Z>
-__global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
-    const uint32_t *__restrict__ gw, const uint16_t *__restrict__ gs, const uint16_t *__restrict__ gz,
-    const uint32_t *__restrict__ uw, const uint16_t *__restrict__ us, const uint16_t *__restrict__ uz,
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ active, const int32_t *__restrict__ n_active,
-    const int32_t *__restrict__ pair_tok, const uint16_t *__restrict__ x, int H, int F, uint16_t *__restrict__ h) {
-    if (int(blockIdx.y) >= *n_active) return;
-    constexpr int SUB = 8 / KS;
-    const int e = active[blockIdx.y];
-    const int base = offsets[e], M = offsets[e + 1] - base;
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, q = lane / 16, n = lane % 16;
-    const int lsub = blockIdx.x * SUB + wave / KS, kp = wave % KS;
-    const int G = H / QGROUP, gpk = G / KS, fsub = F / 16;
-    const int64_t sub = int64_t(e) * fsub + min(lsub, fsub - 1);
-    const Q4Tile tile[2] = {Q4Tile(gw, gs, gz, sub, G), Q4Tile(uw, us, uz, sub, G)};
-    const uint16_t *arow[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) arow[mb] = x + int64_t(pair_tok[base + min(mb * 16 + n, M - 1)]) * H;
-    f32x4 acc[MB][2];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb][0] = acc[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    q4_groups<BF16, MB, 2, HAS_Z, MB == 1 ? 4 : 2>(tile, arow, kp * gpk, kp * gpk + gpk, lane, acc);
-    ksplit_reduce<MB, 2, KS>(acc, wave, kp, lane);
-    if (kp != 0 || lsub >= fsub) return;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = mb * 16 + 4 * q + r;
-            if (m < M) h[int64_t(base + m) * F + lsub * 16 + n] = silu_mul_f16(acc[mb][0][r], acc[mb][1][r]);
-        }
-}
-
-// down: yp[slot][H] (fp32) = D_e h[slot].
-template <int KS, int MB, bool HAS_Z>
-__global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *__restrict__ dw,
-                                                            const uint16_t *__restrict__ ds,
-                                                            const uint16_t *__restrict__ dz,
-                                                            const int32_t *__restrict__ offsets,
-                                                            const int32_t *__restrict__ active,
-                                                            const int32_t *__restrict__ n_active,
-                                                            const uint16_t *__restrict__ h, int H, int F,
-                                                            float *__restrict__ yp) {
-    if (int(blockIdx.y) >= *n_active) return;
-    constexpr int SUB = 8 / KS;
-    const int e = active[blockIdx.y];
-    const int base = offsets[e], M = offsets[e + 1] - base;
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, q = lane / 16, n = lane % 16;
-    const int lsub = blockIdx.x * SUB + wave / KS, kp = wave % KS;
-    const int G = F / QGROUP, gpk = G / KS, hsub = H / 16;
-    const int64_t sub = int64_t(e) * hsub + min(lsub, hsub - 1);
-    const Q4Tile tile[1] = {Q4Tile(dw, ds, dz, sub, G)};
-    const uint16_t *arow[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) arow[mb] = h + int64_t(base + min(mb * 16 + n, M - 1)) * F;
-    f32x4 acc[MB][1];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    q4_groups<F16, MB, 1, HAS_Z, 4>(tile, arow, kp * gpk, kp * gpk + gpk, lane, acc);
-    ksplit_reduce<MB, 1, KS>(acc, wave, kp, lane);
-    if (kp != 0 || lsub >= hsub) return;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = mb * 16 + 4 * q + r;
-            if (m < M) yp[int64_t(base + m) * H + lsub * 16 + n] = acc[mb][0][r];
-        }
-}
-
-template <int KS, int MB, bool HAS_Z>
-static void launch_moe_gemv_t(const MoeGemvArgs &a, int max_active, bool down, hipStream_t s) {
-    const int rows = down ? a.H : a.F;
-    const int subtiles = rows / 16;
-    const dim3 grid(unsigned((subtiles + (8 / KS) - 1) / (8 / KS)), unsigned(max_active)), block(512);
-    if (!down)
-        moe_gate_up_gemv_kernel<KS, MB, HAS_Z><<<grid, block, 0, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets,
-                                                                      a.active, a.n_active, a.pair_tok, a.x, a.H, a.F,
-                                                                      a.h);
-    else
-        moe_down_gemv_kernel<KS, MB, HAS_Z><<<grid, block, 0, s>>>(a.dw, a.ds, a.dz, a.offsets, a.active, a.n_active,
-                                                                   a.h, a.H, a.F, a.yp);
-}
-
-template <int KS>
-static void launch_moe_gemv_ks(const MoeGemvArgs &a, int max_active, bool down, hipStream_t s) {
-    const bool z = down ? a.dz != nullptr : a.gz != nullptr;
-    if (a.T > 16) {
-        if (z) launch_moe_gemv_t<KS, 2, true>(a, max_active, down, s);
-        else launch_moe_gemv_t<KS, 2, false>(a, max_active, down, s);
-    } else {
-        if (z) launch_moe_gemv_t<KS, 1, true>(a, max_active, down, s);
-        else launch_moe_gemv_t<KS, 1, false>(a, max_active, down, s);
-    }
-}
-
-static void launch_moe_one(const MoeGemvArgs &a, bool down, hipStream_t s) {
-    const int max_active = a.T * a.topk < a.E ? a.T * a.topk : a.E;
-    const int rows = down ? a.H : a.F, G = (down ? a.F : a.H) / QGROUP;
-    // the K split is sized for the expected number of distinct experts
-    // E (1 - (1 - k/E)^T) of T tokens routed uniformly
-    double miss = 1.0;
-    for (int t = 0; t < a.T; ++t) miss *= 1.0 - double(a.topk) / a.E;
-    int64_t expect = int64_t(a.E * (1.0 - miss));
-    if (expect < a.topk) expect = a.topk;
-    int ks = 1;
-    while (ks < 8 && int64_t(rows / 16) * expect * ks < 2048 && G % (ks * 2) == 0) ks *= 2;
-    switch (ks) {
-        case 1: launch_moe_gemv_ks<1>(a, max_active, down, s); break;
-        case 2: launch_moe_gemv_ks<2>(a, max_active, down, s); break;
-        case 4: launch_moe_gemv_ks<4>(a, max_active, down, s); break;
-        default: launch_moe_gemv_ks<8>(a, max_active, down, s); break;
-    }
-}
-
-void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s) {
-    launch_moe_one(a, false, s);
-    launch_moe_one(a, true, s);
 }
 
 }  // namespace qwq4

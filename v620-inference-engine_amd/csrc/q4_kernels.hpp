@@ -46,6 +46,8 @@ struct MoeGemvArgs {
     float *yp;
 };
 void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s);
+// Whether the expert GEMVs take these sizes (a wave holds <= 16 groups of its K range).
+bool moe_gemv_supported(int H, int F);
 
 struct MoeGroupedArgs {
     const uint32_t *gw;
