@@ -55,16 +55,7 @@ __device__ __forceinline__ void stage_rows_uniform(RowFn row, int M, int K, uint
     }
 }
 
-// The lane index, as a value the compiler cannot see through: the per-lane
-// weight addresses derived from it are recomputed in every chunk instead of
-// being hoisted out of the chunk loop and held (2 registers each) across it.
-__device__ __forceinline__ int opaque_lane() {
-    int l = int(threadIdx.x) % WAVE;
-    asm volatile("" : "+v"(l));
-    return l;
-}
-
-template <int KS, int GW, bool HAS_Z>
+template <int KS, int GW, bool HAS_Z, bool CH4>
 __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
     const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
@@ -83,7 +74,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     const Q4Tile t = mat ? Q4Tile(uw, us, uz, sub, G) : Q4Tile(gw, gs, gz, sub, G);
     // the first chunk's weights go out before the slot range is known (an
     // active expert has at least one token)
-    WaveRange<GW, HAS_Z> wr;
+    WaveRange<GW, HAS_Z, CH4> wr;
     wr.fetch(t, kp * gpk, gpk, opaque_lane());
     const int base = offsets[e], M = offsets[e + 1] - base;
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
@@ -123,7 +114,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     } while (m0 < M);
 }
 
-template <int KS, int GW, bool HAS_Z>
+template <int KS, int GW, bool HAS_Z, bool CH4>
 __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz,
                                                             const int32_t *__restrict__ offsets,
                                                             const int32_t *__restrict__ active,
@@ -140,7 +131,7 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
     const int G = F / QGROUP, gpk = G / KS, hsub = H / 16, kc = F / 8;
     const int lsub = blockIdx.x * SUB + sl;
     const Q4Tile t(dw, ds, dz, int64_t(e) * hsub + min(lsub, hsub - 1), G);
-    WaveRange<GW, HAS_Z> wr;
+    WaveRange<GW, HAS_Z, CH4> wr;
     wr.fetch(t, kp * gpk, gpk, opaque_lane());
     const int base = offsets[e], M = offsets[e + 1] - base;
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
@@ -187,9 +178,9 @@ static int pick_ks(int G, int kmax) {
     return ks;
 }
 
-template <int KS, int GW, bool HAS_Z>
+template <int KS, int GW, bool HAS_Z, bool CH4>
 static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
-    auto kern = moe_gate_up_gemv_kernel<KS, GW, HAS_Z>;
+    auto kern = moe_gate_up_gemv_kernel<KS, GW, HAS_Z, CH4>;
     const size_t lds = moe_lds_bytes(R, a.H);
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
     constexpr int SUB = 8 / (2 * KS);
@@ -198,9 +189,9 @@ static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStrea
                                 a.E, a.H, a.F, R, a.h);
 }
 
-template <int KS, int GW, bool HAS_Z>
+template <int KS, int GW, bool HAS_Z, bool CH4>
 static void launch_down(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
-    auto kern = moe_down_gemv_kernel<KS, GW, HAS_Z>;
+    auto kern = moe_down_gemv_kernel<KS, GW, HAS_Z, CH4>;
     const size_t lds = moe_lds_bytes(R, a.F);
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
     constexpr int SUB = 8 / KS;
@@ -208,18 +199,20 @@ static void launch_down(const MoeGemvArgs &a, int max_active, int R, hipStream_t
     kern<<<grid, 512, lds, s>>>(a.dw, a.ds, a.dz, a.offsets, a.active, a.n_active, a.h, a.E, a.H, a.F, R, a.yp);
 }
 
+template <bool DOWN, int KS, int GW, bool HAS_Z, bool CH4>
+static void launch_kind(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
+    if constexpr (DOWN) launch_down<KS, GW, HAS_Z, CH4>(a, max_active, R, s);
+    else launch_gate_up<KS, GW, HAS_Z, CH4>(a, max_active, R, s);
+}
+
 template <bool DOWN, int KS, bool HAS_Z>
 static void launch_gw(const MoeGemvArgs &a, int max_active, int R, int gpk, hipStream_t s) {
-    if (gpk <= 4) {
-        if constexpr (DOWN) launch_down<KS, 4, HAS_Z>(a, max_active, R, s);
-        else launch_gate_up<KS, 4, HAS_Z>(a, max_active, R, s);
-    } else if (gpk <= 8) {
-        if constexpr (DOWN) launch_down<KS, 8, HAS_Z>(a, max_active, R, s);
-        else launch_gate_up<KS, 8, HAS_Z>(a, max_active, R, s);
-    } else {
-        if constexpr (DOWN) launch_down<KS, 16, HAS_Z>(a, max_active, R, s);
-        else launch_gate_up<KS, 16, HAS_Z>(a, max_active, R, s);
-    }
+    if (gpk == 4) launch_kind<DOWN, KS, 4, HAS_Z, true>(a, max_active, R, s);
+    else if (gpk < 4) launch_kind<DOWN, KS, 4, HAS_Z, false>(a, max_active, R, s);
+    else if (gpk == 8) launch_kind<DOWN, KS, 8, HAS_Z, true>(a, max_active, R, s);
+    else if (gpk < 8) launch_kind<DOWN, KS, 8, HAS_Z, false>(a, max_active, R, s);
+    else if (gpk % 4 == 0) launch_kind<DOWN, KS, 16, HAS_Z, true>(a, max_active, R, s);
+    else launch_kind<DOWN, KS, 16, HAS_Z, false>(a, max_active, R, s);
 }
 
 template <bool DOWN, bool HAS_Z>

@@ -12,21 +12,26 @@
 namespace qwq4 {
 
 // ------------------------------------------------------------ dense GEMV
-// Two schedules over the same wave work (one 16-row subtile x a K range):
-//   block   small and medium N: KS waves share a subtile (K split), each
-//           block is one item of 8/KS subtiles, and every wave requests its
-//           whole K range (<= 16 groups, <= 16 KB) before anything else;
-//   stream  large N (LM head): persistent waves, one subtile at a time over
-//           all of K in chunks of 8 groups, the next chunk (weights, scales,
-//           zeros) in flight while the current one is computed; the stream
-//           runs on across subtiles.
-// Both stage the M activation rows (bf16) in LDS once per block. The MFMA
-// accumulator starts at -144 * sum(x) of the group (an MFMA against a splat
-// of -144), see q4_common.cuh. KS waves of a block sharing a subtile reduce
-// their partial sums through LDS in a fixed order (deterministic).
+// Work item = SUB consecutive 16-row subtiles; each subtile's K groups are
+// split over KS waves (a block has KS * SUB <= 16 waves), a wave's range being
+// gpk = G / KS groups, ideally 4 (one 4-group chunk: its scales are one 8-byte
+// load, its zeros one 16-bit word). Every wave requests its whole range of
+// weights (after the block's activation rows, bf16, staged in LDS by direct
+// loads) before anything waits. The MFMA accumulator starts at -144 * sum(x)
+// of the group (an MFMA against a splat of -144), see q4_common.cuh. The KS
+// partial sums of a subtile are reduced through LDS in a fixed order
+// (deterministic).
+//
+// Blocks are as many as stay resident in one round: block b takes items b,
+// b + gridDim.x, ... with the activations staged once. With more than one
+// item per block (PF) the next item's weights are requested before the
+// current one is computed. A wave range of more than GW groups runs in
+// passes of GW.
 
-__host__ __device__ inline size_t dense_lds_bytes(int M, int K, int MB) {
-    return size_t(x_pieces(M, K)) * 16 + size_t(8) * MB * WAVE * 16;
+constexpr int DENSE_GW = 4;
+
+__host__ __device__ inline size_t dense_lds_bytes(int M, int K, int MB, int waves) {
+    return size_t(x_pieces(M, K)) * 16 + size_t(2) * waves * MB * WAVE * 16;
 }
 
 __device__ __forceinline__ void stage_x_issue(const uint16_t *__restrict__ x, int xs, int M, int K, uint4 *xl) {
@@ -46,205 +51,160 @@ __device__ __forceinline__ void store_rows(const f32x4 (&acc)[MB], void *y, int 
         }
 }
 
-// ---- block schedule
-template <int KS, int MB, bool HAS_Z, int GW>
-__global__ __launch_bounds__(512) void q4_gemv_block_kernel(const uint32_t *Wt,
-                                                            const uint16_t *St,
-                                                            const uint16_t *Zt,
-                                                            const uint16_t *__restrict__ x, int xs,
-                                                            void *__restrict__ y, int ys, int y_bf16, int N, int K,
-                                                            int M, int accumulate) {
+// Sums the KS partials of each subtile (buffer rb, [waves][MB][64] f32x4)
+// into the k-part 0 wave's acc, in k-part order.
+template <int MB>
+__device__ __forceinline__ void ksplit_sum(f32x4 (&acc)[MB], f32x4 *rb, int KS, int wave, int kp, int lane) {
+    if (KS == 1) return;
+    if (kp != 0) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) rb[(wave * MB + mb) * WAVE + lane] = acc[mb];
+    }
+    lds_barrier();
+    if (kp == 0) {
+        // four partials in flight per step (KS is a runtime value), added in
+        // k-part order
+        const int last = wave + KS - 1;
+        for (int i0 = 1; i0 < KS; i0 += 4) {
+            f32x4 part[4][MB];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) part[j][mb] = rb[(min(wave + i0 + j, last) * MB + mb) * WAVE + lane];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (i0 + j < KS) {
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) acc[mb] += part[j][mb];
+                }
+        }
+    }
+}
+
+template <int NW, int MB, bool HAS_Z, bool CH4, bool PF, bool KSNW>
+__global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt,
+                                                             const uint16_t *__restrict__ x, int xs,
+                                                             void *__restrict__ y, int ys, int y_bf16, int N, int K,
+                                                             int M, int accumulate, int KS_, int SUB_) {
+    // KSNW: one subtile per item, split over all NW waves (compile-time)
+    const int KS = KSNW ? NW : KS_, SUB = KSNW ? 1 : SUB_;
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int SUB = 8 / KS;
-    const int G = K / QGROUP, kc = K / 8, nsub = N / 16, gpk = G / KS;
-    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, q = lane / 16, n = lane % 16;
+    constexpr int GW = DENSE_GW;
+    const int G = K / QGROUP, kc = K / 8, nsub = N / 16, gpk = G / KS, items = (nsub + SUB - 1) / SUB;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE,
+              q = lane / 16, n = lane % 16, waves = KSNW ? NW : int(blockDim.x) / WAVE;
     const int sl = wave / KS, kp = wave % KS, g0 = kp * gpk;
-    const int sub = blockIdx.x * SUB + sl;
-    // activations (L2) and then the wave's whole K range of weights (HBM) are
-    // requested before anything waits
+    auto tile_of = [&](int item) { return Q4Tile(Wt, St, Zt, min(item * SUB + sl, nsub - 1), G); };
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
     f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(M, K));
     stage_x_issue(x, xs, M, K, xl);
-    const Q4Tile t(Wt, St, Zt, min(sub, nsub - 1), G);
-    WaveRange<GW, HAS_Z> wr;
-    wr.fetch(t, g0, gpk, lane);
+    WaveRange<GW, HAS_Z, CH4> wr[1];
+    wr[0].fetch(tile_of(blockIdx.x), g0, min(gpk, GW), lane);
     __syncthreads();
     const uint4 *xr[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) xr[mb] = xl + min(mb * 16 + n, M - 1) * kc + q * 4;
-    f32x4 acc[MB];
+    if constexpr (!PF) {
+        f32x4 acc[1][MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    wr.template compute<BF16, MB>(xr, acc);
-    if constexpr (KS > 1) {
-        if (kp != 0) {
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) red[(wave * MB + mb) * WAVE + lane] = acc[mb];
+        for (int mb = 0; mb < MB; ++mb) acc[0][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        compute_shared_x<BF16, MB, 1>(wr, xr, acc);
+        // longer ranges: further passes of GW groups
+        for (int p = GW; p < gpk; p += GW) {
+            wr[0].fetch(tile_of(blockIdx.x), g0 + p, min(gpk - p, GW), opaque_lane());
+            compute_shared_x<BF16, MB, 1>(wr, xr, acc);
         }
-        lds_barrier();
-        if (kp == 0) {
+        ksplit_sum<MB>(acc[0], red, KS, wave, kp, lane);
+        const int sub = blockIdx.x * SUB + sl;
+        if (kp == 0 && sub < nsub) store_rows<MB>(acc[0], y, ys, y_bf16, accumulate, M, sub, lane);
+    } else {
+        // gpk <= GW here
+        WaveRange<GW, HAS_Z, CH4> wn[1];
+        int par = 0;
+        for (int item = blockIdx.x; item < items; item += gridDim.x) {
+            wn[0].fetch(tile_of(min(item + int(gridDim.x), items - 1)), g0, gpk, opaque_lane());
+            f32x4 acc[1][MB];
 #pragma unroll
-            for (int j = 1; j < KS; ++j)
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) acc[mb] += red[((wave + j) * MB + mb) * WAVE + lane];
+            for (int mb = 0; mb < MB; ++mb) acc[0][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            compute_shared_x<BF16, MB, 1>(wr, xr, acc);
+            // partials double-buffered by item parity: the barrier of item
+            // i + 1 orders item i's reads before item i + 2's writes
+            ksplit_sum<MB>(acc[0], red + par * (waves * MB * WAVE), KS, wave, kp, lane);
+            par ^= 1;
+            const int sub = item * SUB + sl;
+            if (kp == 0 && sub < nsub) store_rows<MB>(acc[0], y, ys, y_bf16, accumulate, M, sub, lane);
+            wr[0] = wn[0];
         }
     }
-    if (kp == 0 && sub < nsub) store_rows<MB>(acc, y, ys, y_bf16, accumulate, M, sub, lane);
 }
 
-// ---- stream schedule
-constexpr int STREAM_CH = 4;
-
-__host__ __device__ inline size_t stream_lds_bytes(int M, int K, int MB) {
-    return size_t(x_pieces(M, K)) * 16 + size_t(K / QGROUP) * 16 * MB * 4;
-}
-
-template <int MB, bool HAS_Z>
-__global__ __launch_bounds__(512) void q4_gemv_stream_kernel(const uint32_t *Wt, const uint16_t *St,
-                                                             const uint16_t *Zt, const uint16_t *__restrict__ x,
-                                                             int xs, void *__restrict__ y, int ys, int y_bf16, int N,
-                                                             int K, int M, int accumulate) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int CH = STREAM_CH, MR = 16 * MB;
-    const int G = K / QGROUP, kc = K / 8, nsub = N / 16, nch = (G + CH - 1) / CH;
-    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, q = lane / 16, n = lane % 16;
-    const int stride = gridDim.x * 8;
-    int sub = blockIdx.x * 8 + wave, ch = 0;
-    // one chunk: 4 groups of weights, their 4 scales (one 8-byte load) and zero word
-    uint4 wc[CH], wn[CH];
-    uint2 sc, sn;
-    uint32_t zc = 0, zn = 0;
-    auto fetch = [&](int sb, int chk, uint4 (&w)[CH], uint2 &sv, uint32_t &zv) {
-        const Q4Tile t(Wt, St, Zt, min(sb, nsub - 1), G);
-#pragma unroll
-        for (int c = 0; c < CH; ++c) w[c] = t.word4(min(chk * CH + c, G - 1), lane);
-        sv = *reinterpret_cast<const uint2 *>(t.s + chk * 64 + n * 4);
-        if constexpr (HAS_Z) zv = t.z[chk * 16 + n];
-    };
-    uint4 *xl = reinterpret_cast<uint4 *>(smem);
-    float *corr = reinterpret_cast<float *>(xl + x_pieces(M, K));
-    stage_x_issue(x, xs, M, K, xl);
-    fetch(sub, ch, wc, sc, zc);
-    __syncthreads();
-    // corr[g][m] = -144 * sum of group g of row min(m, M-1)
-    for (int i = tid; i < G * MR; i += blockDim.x) {
-        const int g = i / MR, m = min(i - g * MR, M - 1);
-        const uint4 *src = xl + m * kc + g * 16;
-        float sum = 0.f;
-        for (int c = 0; c < 16; ++c) {
-            const uint4 v = src[c];
-            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                sum += bf16_bits_to_f32(uint16_t(w4[j])) + bf16_bits_to_f32(uint16_t(w4[j] >> 16));
-        }
-        corr[i] = -144.f * sum;
-    }
-    lds_barrier();
-    const uint4 *xr[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) xr[mb] = xl + min(mb * 16 + n, M - 1) * kc + q * 4;
-    f32x4 acc[MB];
-    while (sub < nsub) {
-        int nsb = sub, nchk = ch + 1;
-        if (nchk == nch) {
-            nchk = 0;
-            nsb += stride;
-        }
-        fetch(nsb, nchk, wn, sn, zn);
-        if (ch == 0) {
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int g = ch * CH + c;
-            if (g >= G) break;
-            const uint32_t zb = zero_bytes(HAS_Z ? (zc >> (4 * c)) & 0xfu : 8u);
-            const uint32_t s2 = c < 2 ? sc.x : sc.y;
-            const float s = f16_bits_to_f32(uint16_t(c % 2 ? s2 >> 16 : s2));
-            uint4 b[4];
-            b[0] = unpack8<BF16>(wc[c].x, zb);
-            b[1] = unpack8<BF16>(wc[c].y, zb);
-            b[2] = unpack8<BF16>(wc[c].z, zb);
-            b[3] = unpack8<BF16>(wc[c].w, zb);
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) {
-                f32x4 p = *reinterpret_cast<const f32x4 *>(corr + g * MR + mb * 16 + 4 * q);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) p = mfma16<BF16>(xr[mb][g * 16 + t], b[t], p);
-                acc[mb] += s * p;
+// K split: gpk = 4 where G allows (KS = G / 4 <= 16), else the largest
+// divisor of G up to 16 (fewest groups per wave). SUB: subtiles per item,
+// filling blocks of 8, 12 or 16 waves (the kernel's launch bound NW).
+static void dense_split(int G, int &KS, int &SUB, int &NW) {
+    KS = 1;
+    if (G % 4 == 0 && G / 4 <= 16) KS = G / 4;
+    else
+        for (int k = 16; k >= 1; --k)
+            if (G % k == 0) {
+                KS = k;
+                break;
             }
+    NW = 16;
+    for (int nw : {8, 12, 16})
+        if (nw % KS == 0) {
+            NW = nw;
+            break;
         }
-        if (ch == nch - 1) store_rows<MB>(acc, y, ys, y_bf16, accumulate, M, sub, lane);
-#pragma unroll
-        for (int c = 0; c < CH; ++c) wc[c] = wn[c];
-        sc = sn;
-        zc = zn;
-        sub = nsb;
-        ch = nchk;
+    SUB = NW / KS;
+}
+
+template <int NW, int MB, bool HAS_Z, bool CH4, bool KSNW>
+static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
+    const int waves = KS * SUB, threads = waves * WAVE, gpk = a.K / QGROUP / KS;
+    const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves);
+    const int nsub = a.N / 16, items = (nsub + SUB - 1) / SUB;
+    auto one = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, false, KSNW>;
+    const LaunchShape ls = persistent_shape(reinterpret_cast<const void *>(one), threads, lds);
+    if (items <= ls.max_blocks || gpk > DENSE_GW) {
+        one<<<items, threads, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.y, a.ys, a.y_bf16, a.N, a.K, a.M, a.accumulate,
+                                        KS, SUB);
+        return;
     }
+    auto pf = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, true, KSNW>;
+    const LaunchShape lp = persistent_shape(reinterpret_cast<const void *>(pf), threads, lds);
+    const int per = (items + lp.max_blocks - 1) / lp.max_blocks, blocks = (items + per - 1) / per;
+    pf<<<blocks, threads, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.y, a.ys, a.y_bf16, a.N, a.K, a.M, a.accumulate, KS,
+                                    SUB);
 }
 
-template <int MB, bool HAS_Z>
-static void launch_stream(const GemvArgs &a, size_t, hipStream_t s) {
-    auto kern = q4_gemv_stream_kernel<MB, HAS_Z>;
-    const size_t lds = stream_lds_bytes(a.M, a.K, MB);
-    const int nsub = a.N / 16;
-    const LaunchShape ls = persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
-    const int want = (nsub + 7) / 8;
-    const int blocks = want < ls.max_blocks ? want : ls.max_blocks;
-    kern<<<blocks, 512, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.y, a.ys, a.y_bf16, a.N, a.K, a.M, a.accumulate);
-}
-
-template <int KS, int MB, bool HAS_Z, int GW>
-static void launch_block(const GemvArgs &a, size_t lds, hipStream_t s) {
-    auto kern = q4_gemv_block_kernel<KS, MB, HAS_Z, GW>;
-    const int nsub = a.N / 16, blocks = (nsub + (8 / KS) - 1) / (8 / KS);
-    if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
-    kern<<<blocks, 512, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.y, a.ys, a.y_bf16, a.N, a.K, a.M, a.accumulate);
-}
-
-template <int KS, int MB, bool HAS_Z>
-static void launch_block_gw(const GemvArgs &a, size_t lds, hipStream_t s) {
-    const int gpk = a.K / QGROUP / KS;
-    if (gpk <= 4) launch_block<KS, MB, HAS_Z, 4>(a, lds, s);
-    else if (gpk <= 8) launch_block<KS, MB, HAS_Z, 8>(a, lds, s);
-    else launch_block<KS, MB, HAS_Z, 16>(a, lds, s);
+template <int MB, bool HAS_Z, bool CH4>
+static void launch_dense_nw(const GemvArgs &a, int KS, int SUB, int NW, hipStream_t s) {
+    if (NW == 8) {
+        if (KS == 8) launch_dense_t<8, MB, HAS_Z, CH4, true>(a, KS, SUB, s);
+        else launch_dense_t<8, MB, HAS_Z, CH4, false>(a, KS, SUB, s);
+    } else if (NW == 12) {
+        if (KS == 12) launch_dense_t<12, MB, HAS_Z, CH4, true>(a, KS, SUB, s);
+        else launch_dense_t<12, MB, HAS_Z, CH4, false>(a, KS, SUB, s);
+    } else {
+        if (KS == 16) launch_dense_t<16, MB, HAS_Z, CH4, true>(a, KS, SUB, s);
+        else launch_dense_t<16, MB, HAS_Z, CH4, false>(a, KS, SUB, s);
+    }
 }
 
 template <int MB, bool HAS_Z>
 static void launch_dense(const GemvArgs &a, hipStream_t s) {
-    const int G = a.K / QGROUP, nsub = a.N / 16;
-    const size_t lds = dense_lds_bytes(a.M, a.K, MB);
-    int cus = 0, dev = 0;
-    (void)hipGetDevice(&dev);
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    const int64_t want = int64_t(12) * (cus > 0 ? cus : 256);  // waves: 12 per CU
-    if (nsub >= want) {
-        launch_stream<MB, HAS_Z>(a, lds, s);
-        return;
-    }
-    // K split: the largest power of two <= 8 dividing G (measured: more,
-    // shorter waves finish sooner than fewer, longer ones)
-    int ks = 1;
-    while (ks < 8 && G % (ks * 2) == 0) ks *= 2;
-    if (G / ks > 16) {
-        launch_stream<MB, HAS_Z>(a, lds, s);
-        return;
-    }
-    switch (ks) {
-        case 1: launch_block_gw<1, MB, HAS_Z>(a, lds, s); break;
-        case 2: launch_block_gw<2, MB, HAS_Z>(a, lds, s); break;
-        case 4: launch_block_gw<4, MB, HAS_Z>(a, lds, s); break;
-        default: launch_block_gw<8, MB, HAS_Z>(a, lds, s); break;
-    }
+    int KS, SUB, NW;
+    dense_split(a.K / QGROUP, KS, SUB, NW);
+    if ((a.K / QGROUP / KS) % 4 == 0) launch_dense_nw<MB, HAS_Z, true>(a, KS, SUB, NW, s);
+    else launch_dense_nw<MB, HAS_Z, false>(a, KS, SUB, NW, s);
 }
 
 bool gemv_fits(int M, int K) {
     const int MB = M <= 16 ? 1 : 2;
-    const size_t l1 = dense_lds_bytes(M, K, MB), l2 = stream_lds_bytes(M, K, MB);
-    return (l1 > l2 ? l1 : l2) <= 160 * 1024;
+    int KS, SUB, NW;
+    dense_split(K / QGROUP, KS, SUB, NW);
+    return dense_lds_bytes(M, K, MB, KS * SUB) <= 160 * 1024;
 }
 
 static void launch_gemv_fit(const GemvArgs &a, hipStream_t s) {

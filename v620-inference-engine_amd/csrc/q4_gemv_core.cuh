@@ -40,6 +40,15 @@ __device__ __forceinline__ void stage_rows_issue(RowFn row, int M, int K, uint4 
     }
 }
 
+// The lane index, as a value the compiler cannot see through: per-lane
+// addresses derived from it inside a loop are recomputed per iteration
+// instead of being hoisted out and held (2 registers each) across it.
+__device__ __forceinline__ int opaque_lane() {
+    int l = int(threadIdx.x) % WAVE;
+    asm volatile("" : "+v"(l));
+    return l;
+}
+
 // One group of one subtile: acc[mb] += s * (x . (q - z)) for the lane's rows.
 // xr[mb] points at the lane's activation row (LDS) at K quarter q.
 template <typename T, int MB>
@@ -66,8 +75,12 @@ __device__ __forceinline__ void dense_group(const uint4 &w, uint32_t zb, float s
 }
 
 // A wave's whole K range of one subtile (groups g0 .. g0 + n - 1, n <= GW),
-// requested up front into registers.
-template <int GW, bool HAS_Z>
+// requested up front into registers. CH4: the range is whole 4-group chunks
+// (g0 and n multiples of 4), so each chunk's scales are one 8-byte load and
+// its zeros one 16-bit word; otherwise one scale and one zero load per group.
+// (A compile-time choice: a runtime branch between the two puts waits between
+// the loads.)
+template <int GW, bool HAS_Z, bool CH4 = false>
 struct WaveRange {
     uint4 w[GW];
     uint32_t sv[GW], zv[GW];
@@ -77,11 +90,30 @@ struct WaveRange {
         n = n_;
         const int r = lane % 16;
 #pragma unroll
-        for (int c = 0; c < GW; ++c) {
-            const int g = g0 + min(c, n - 1);
-            w[c] = t.word4(g, lane);
-            sv[c] = t.scale(g, r);
-            if constexpr (HAS_Z) zv[c] = t.zero_word(g, r);
+        for (int c = 0; c < GW; ++c) w[c] = t.word4(g0 + min(c, n - 1), lane);
+        if constexpr (CH4) {
+            static_assert(GW % 4 == 0, "whole chunks");
+#pragma unroll
+            for (int j = 0; j < GW / 4; ++j) {
+                const int gc = (g0 >> 2) + min(j, n / 4 - 1);
+                const uint2 s4 = *reinterpret_cast<const uint2 *>(t.s + gc * 64 + r * 4);
+                sv[4 * j] = s4.x;
+                sv[4 * j + 1] = s4.x >> 16;
+                sv[4 * j + 2] = s4.y;
+                sv[4 * j + 3] = s4.y >> 16;
+                if constexpr (HAS_Z) {
+                    const uint32_t z4 = t.z[gc * 16 + r];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) zv[4 * j + i] = z4;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < GW; ++c) {
+                const int g = g0 + min(c, n - 1);
+                sv[c] = t.scale(g, r);
+                if constexpr (HAS_Z) zv[c] = t.zero_word(g, r);
+            }
         }
     }
     template <typename T, int MB>
@@ -96,6 +128,49 @@ struct WaveRange {
         }
     }
 };
+
+// NS subtiles over the same groups (wr[j] fetched with equal g0 and n): the
+// activation fragments and the -BIAS * sum(x) correction of each group are
+// read and formed once for all of them.
+template <typename T, int MB, int NS, int GW, bool HAS_Z, bool CH4>
+__device__ __forceinline__ void compute_shared_x(const WaveRange<GW, HAS_Z, CH4> (&wr)[NS], const uint4 *const (&xr)[MB],
+                                                 f32x4 (&acc)[NS][MB]) {
+    const uint4 negb = make_uint4(T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS);
+    const int g0 = wr[0].g0, n = wr[0].n;
+#pragma unroll
+    for (int c = 0; c < GW; ++c) {
+        if (c < n) {
+            const int g = g0 + c;
+            uint4 a[MB][4];
+            f32x4 pc[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) a[mb][t] = xr[mb][g * 16 + t];
+                pc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) pc[mb] = mfma16<T>(a[mb][t], negb, pc[mb]);
+            }
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(wr[j].zv[c], g) : 8u);
+                const float sc = f16_bits_to_f32(uint16_t(wr[j].sv[c]));
+                uint4 b[4];
+                b[0] = unpack8<T>(wr[j].w[c].x, zb);
+                b[1] = unpack8<T>(wr[j].w[c].y, zb);
+                b[2] = unpack8<T>(wr[j].w[c].z, zb);
+                b[3] = unpack8<T>(wr[j].w[c].w, zb);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    f32x4 p = pc[mb];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) p = mfma16<T>(a[mb][t], b[t], p);
+                    acc[j][mb] += sc * p;
+                }
+            }
+        }
+    }
+}
 
 __device__ __forceinline__ void store_y(void *y, int64_t o, float v, int y_bf16, int accumulate) {
     if (y_bf16) {
