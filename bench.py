@@ -31,6 +31,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
 L_LAYERS = 24
 BATCHES = (1, 2, 4, 6, 8)
+DOM_BATCHES = (1, 2, 4)
 H, QKV, FFN_DOWN_K, VOCAB = 4096, 12288, 6144, 151936
 
 
@@ -104,6 +105,7 @@ def bench_gemv(torch, qwq4, dev, steps, warmup):
     step_bytes_w = L_LAYERS * (q4_bytes(QKV, H) + q4_bytes(H, FFN_DOWN_K)) + q4_bytes(VOCAB, H)
     per_m = {}
     tot_bytes = tot_ms = 0.0
+    dom_us, dom_bytes = [], []
     for M in BATCHES:
         x = gen_x(torch, dev, M, FFN_DOWN_K, seed=M)
         y = torch.empty((M, VOCAB), dtype=torch.bfloat16, device=dev)
@@ -127,15 +129,34 @@ def bench_gemv(torch, qwq4, dev, steps, warmup):
                     "tokens_s": M * steps / (t.ms * 1e-3)}
         tot_bytes += b
         tot_ms += t.ms
-    launches = 2 * L_LAYERS + 1
+
+        # the dominant kernel alone: the 4096->12288 projection, launched back
+        # to back over the 24 layers' weights (a 627 MB pool, beyond the
+        # Infinity Cache) in one graph; average launch duration from events
+        def dom():
+            for (wq, _) in layers:
+                qwq4.gemv(*wq, x, QKV, H, M, y=y, y_bf16=True, xs=x.stride(0), ys=y.stride(0))
+
+        dstep = graphed(torch, dom)
+        for _ in range(warmup):
+            dstep()
+        with Timer(torch) as td:
+            for _ in range(steps):
+                dstep()
+        dom_us.append(td.ms * 1e3 / (steps * L_LAYERS))
+        dom_bytes.append(q4_bytes(QKV, H) + M * H * 2 + M * QKV * 2)
     return {
         "GB_s": tot_bytes / (tot_ms * 1e-3) / 1e9,
         "ms_per_step": tot_ms / (steps * len(BATCHES)),
         "per_batch": per_m,
         "bytes_per_step_weights": step_bytes_w,
-        "launches_per_step": launches,
-        "avg_launch_us": tot_ms * 1e3 / (steps * len(BATCHES) * launches),
-        "avg_bytes_per_launch": tot_bytes / (steps * len(BATCHES) * launches),
+        "launches_per_step": 2 * L_LAYERS + 1,
+        # roofline subset: batches 1, 2, 4, which run one kernel instantiation
+        # (single item per block); 6 and 8 run the prefetching one
+        "dominant": {"shape": f"{H}->{QKV}", "batches": list(DOM_BATCHES),
+                     "avg_launch_us": sum(dom_us[BATCHES.index(m)] for m in DOM_BATCHES) / len(DOM_BATCHES),
+                     "avg_bytes_per_launch": sum(dom_bytes[BATCHES.index(m)] for m in DOM_BATCHES) / len(DOM_BATCHES),
+                     "per_batch_us": dict(zip(BATCHES, dom_us))},
     }
 
 
@@ -239,6 +260,18 @@ def bench_moe_prefill(torch, qwq4, dev, steps, warmup):
             "tokens_s": T * steps / (t.ms * 1e-3)}
 
 
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    PMC summary (FETCH_SIZE and WRITE_SIZE, each scaled by the copy-kernel
+    calibration recorded there); None when absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_4096x12288_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["traffic_bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 # ------------------------------------------------------------ CPU baseline
 def cpu_baseline(budget_s=12.0):
     """The C oracle (oracle/q4_oracle.c, the reference's expert_linear scheme) on
@@ -263,14 +296,77 @@ def cpu_baseline(budget_s=12.0):
                       f"{runs} passes in {dt:.1f} s"}
 
 
+# ------------------------------------------------ HBM traffic (rocprofv3 PMC)
+COPY_BYTES = 512 << 20
+
+
+def traffic_probe(torch, qwq4, dev):
+    """Launches for the PMC runs: the dominant kernel (4096->12288 over the
+    24-layer weight pool, each batch of DOM_BATCHES once per layer) and a plain
+    copy of COPY_BYTES, whose counter readings calibrate the byte counters."""
+    layers = [gen_q4(torch, dev, QKV, H, seed=2 * l) for l in range(L_LAYERS)]
+    for M in DOM_BATCHES:
+        x = gen_x(torch, dev, M, H, seed=M)
+        y = torch.empty((M, QKV), dtype=torch.bfloat16, device=dev)
+        for wq in layers:
+            qwq4.gemv(*wq, x, QKV, H, M, y=y, y_bf16=True)
+    torch.cuda.synchronize()
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def parse_pmc(fetch_dir, write_dir, out_path):
+    """Reduces two rocprofv3 --pmc runs of `--workload traffic` (FETCH_SIZE,
+    then WRITE_SIZE; KiB per dispatch) to HBM bytes per launch of the dominant
+    kernel, each counter scaled by copy bytes / its reading for the copy."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        gemv, copies = [], []
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r.get("Counter_Name") != counter:
+                    continue
+                v = float(r["Counter_Value"]) * 1024.0
+                if "q4_gemv_block_kernel<8, 1, true, true, false, true>" in r["Kernel_Name"]:
+                    gemv.append(v)
+                elif "copy" in r["Kernel_Name"].lower():
+                    copies.append((int(r["Grid_Size"]), v))
+        big = max(g for g, _ in copies)  # the COPY_BYTES copies, not torch's small casts
+        cv = [v for g, v in copies if g == big]
+        return {"gemv": sum(gemv) / len(gemv), "copy": sum(cv) / len(cv)}
+
+    fe, wr = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    kf, kw = COPY_BYTES / fe["copy"], COPY_BYTES / wr["copy"]
+    res = {"kernel": "q4_gemv_block_kernel (4096->12288), batches " + ",".join(map(str, DOM_BATCHES)),
+           "fetch_raw_bytes": fe["gemv"], "write_raw_bytes": wr["gemv"],
+           "copy_fetch_raw_bytes": fe["copy"], "copy_write_raw_bytes": wr["copy"],
+           "fetch_scale": kf, "write_scale": kw,
+           "traffic_bytes_per_launch": int(fe["gemv"] * kf + wr["gemv"] * kw),
+           "algorithmic_bytes_per_launch": int(q4_bytes(QKV, H) + sum(M * (H + QKV) * 2 for M in DOM_BATCHES) /
+                                               len(DOM_BATCHES))}
+    with open(out_path, "w") as f:
+        json.dump(res, f, indent=1)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, gemm, moe_prefill")
+    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, gemm, moe_prefill; or traffic (launches for PMC runs)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--parse-pmc", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT_JSON"),
+                    help="reduce two rocprofv3 --pmc runs of --workload traffic to bytes per launch")
     a = ap.parse_args()
+    if a.parse_pmc:
+        print(json.dumps(parse_pmc(*a.parse_pmc)))
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: --gpus must be 1 (no collectives, "
                                    "no multi-GPU path)"}))
@@ -279,6 +375,9 @@ def main():
     import qwq4
     dev = torch.device("cuda:0")
     qwq4.lib()
+    if a.workload == "traffic":
+        traffic_probe(torch, qwq4, dev)
+        return
     wl = set(a.workload.split(","))
     if "all" in wl:
         wl = {"gemv", "moe", "gemm", "moe_prefill"}
@@ -310,10 +409,13 @@ def main():
         g = res["gemv"]
         line["value"] = round(g["GB_s"], 1)
         line["ms_per_step"] = round(g["ms_per_step"], 4)
-        ach = g["avg_bytes_per_launch"] / (g["avg_launch_us"] * 1e-6) / 1e9
+        d = g["dominant"]
+        ach = d["avg_bytes_per_launch"] / (d["avg_launch_us"] * 1e-6) / 1e9
         line["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                            "kernel": "q4_gemv_kernel", "avg_launch_us": round(g["avg_launch_us"], 3)}
+                            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                            "kernel": "q4_gemv_block_kernel<8, 1, true, true, false, true> (4096->12288, batch 1/2/4)",
+                            "avg_launch_us": round(d["avg_launch_us"], 3),
+                            "algorithmic_bytes_per_launch": int(d["avg_bytes_per_launch"])}
     line["workloads"] = res
     if not a.no_cpu and "gemv" in wl:
         line["cpu_baseline"] = cpu_baseline()
