@@ -41,20 +41,6 @@ __device__ __forceinline__ int block_expert(const int32_t *n_active, const int32
     return int(blockIdx.y) < na ? min(max(e, 0), E - 1) : -1;
 }
 
-// Rows 0..M-1 of K 16-bit elements (row m at row(m), a wave-uniform address)
-// -> LDS [M][K], as stage_rows_issue, but row by row so that the row address
-// is a scalar: the gathered token index comes by a scalar load, which does
-// not wait behind the weight loads in flight. K / 8 must be a multiple of 64.
-template <class RowFn>
-__device__ __forceinline__ void stage_rows_uniform(RowFn row, int M, int K, uint4 *xl) {
-    const int kc = K / 8, wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nw = blockDim.x / WAVE;
-    for (int m = 0; m < M; ++m) {
-        const uint16_t *r = row(m);
-        for (int c = wave * WAVE; c < kc; c += nw * WAVE)
-            __builtin_amdgcn_global_load_lds(r + (c + lane) * 8, xl + m * kc + c, 16, 0, 0);
-    }
-}
-
 template <int KS, int GW, bool HAS_Z, bool CH4>
 __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
@@ -68,7 +54,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
               n = lane % 16;
     const int sl = wave / (2 * KS), mat = (wave / KS) % 2, kp = wave % KS;
-    const int G = H / QGROUP, gpk = G / KS, fsub = F / 16, kc = H / 8;
+    const int G = H / QGROUP, gpk = G / KS, fsub = F / 16, kc = x_row_stride(H);
     const int lsub = blockIdx.x * SUB + sl;
     const int64_t sub = int64_t(e) * fsub + min(lsub, fsub - 1);
     const Q4Tile t = mat ? Q4Tile(uw, us, uz, sub, G) : Q4Tile(gw, gs, gz, sub, G);
@@ -87,10 +73,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
             wr.fetch(t, kp * gpk, gpk, opaque_lane());
             lds_barrier();  // the previous chunk's rows and partials are consumed
         }  // the previous chunk's rows and partials are consumed
-        if (kc % WAVE == 0)
-            stage_rows_uniform([&](int m) { return x + int64_t(pair_tok[base + m0 + m]) * H; }, mc, H, xl);
-        else
-            stage_rows_issue([&](int m) { return x + int64_t(pair_tok[base + m0 + m]) * H; }, mc, H, xl);
+        stage_rows_issue([&](int m) { return x + int64_t(pair_tok[base + m0 + m]) * H; }, mc, H, xl);
         __syncthreads();
         const uint4 *xr[1] = {xl + min(n, mc - 1) * kc + q * 4};
         f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -128,7 +111,7 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
               n = lane % 16;
     const int sl = wave / KS, kp = wave % KS;
-    const int G = F / QGROUP, gpk = G / KS, hsub = H / 16, kc = F / 8;
+    const int G = F / QGROUP, gpk = G / KS, hsub = H / 16, kc = x_row_stride(F);
     const int lsub = blockIdx.x * SUB + sl;
     const Q4Tile t(dw, ds, dz, int64_t(e) * hsub + min(lsub, hsub - 1), G);
     WaveRange<GW, HAS_Z, CH4> wr;
@@ -143,10 +126,7 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
             wr.fetch(t, kp * gpk, gpk, opaque_lane());
             lds_barrier();
         }
-        if (kc % WAVE == 0)
-            stage_rows_uniform([&](int m) { return h + int64_t(base + m0 + m) * F; }, mc, F, xl);
-        else
-            stage_rows_issue([&](int m) { return h + int64_t(base + m0 + m) * F; }, mc, F, xl);
+        stage_rows_issue([&](int m) { return h + int64_t(base + m0 + m) * F; }, mc, F, xl);
         __syncthreads();
         const uint4 *xr[1] = {xl + min(n, mc - 1) * kc + q * 4};
         f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};

@@ -30,8 +30,11 @@ namespace qwq4 {
 
 constexpr int DENSE_GW = 4;
 
-__host__ __device__ inline size_t dense_lds_bytes(int M, int K, int MB, int waves) {
-    return size_t(x_pieces(M, K)) * 16 + size_t(2) * waves * MB * WAVE * 16;
+// partial sums: one slot per wave that is not a k-part 0, double-buffered
+__host__ __device__ inline int red_slots(int waves, int KS) { return waves - waves / KS; }
+
+__host__ __device__ inline size_t dense_lds_bytes(int M, int K, int MB, int waves, int KS) {
+    return size_t(x_pieces(M, K)) * 16 + size_t(2) * red_slots(waves, KS) * MB * WAVE * 16;
 }
 
 __device__ __forceinline__ void stage_x_issue(const uint16_t *__restrict__ x, int xs, int M, int K, uint4 *xl) {
@@ -51,26 +54,28 @@ __device__ __forceinline__ void store_rows(const f32x4 (&acc)[MB], void *y, int 
         }
 }
 
-// Sums the KS partials of each subtile (buffer rb, [waves][MB][64] f32x4)
+// Sums the KS partials of each subtile (buffer rb: one [MB][64] f32x4 slot
+// per wave with k-part != 0, red_slots of them)
 // into the k-part 0 wave's acc, in k-part order.
 template <int MB>
 __device__ __forceinline__ void ksplit_sum(f32x4 (&acc)[MB], f32x4 *rb, int KS, int wave, int kp, int lane) {
     if (KS == 1) return;
+    const int slot0 = (wave / KS) * (KS - 1);  // the subtile's first partial slot
     if (kp != 0) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) rb[(wave * MB + mb) * WAVE + lane] = acc[mb];
+        for (int mb = 0; mb < MB; ++mb) rb[(slot0 + kp - 1) * MB * WAVE + mb * WAVE + lane] = acc[mb];
     }
     lds_barrier();
     if (kp == 0) {
         // four partials in flight per step (KS is a runtime value), added in
         // k-part order
-        const int last = wave + KS - 1;
         for (int i0 = 1; i0 < KS; i0 += 4) {
             f32x4 part[4][MB];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb) part[j][mb] = rb[(min(wave + i0 + j, last) * MB + mb) * WAVE + lane];
+                for (int mb = 0; mb < MB; ++mb)
+                    part[j][mb] = rb[(slot0 + min(i0 + j, KS - 1) - 1) * MB * WAVE + mb * WAVE + lane];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 if (i0 + j < KS) {
@@ -90,7 +95,7 @@ __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t
     const int KS = KSNW ? NW : KS_, SUB = KSNW ? 1 : SUB_;
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int GW = DENSE_GW;
-    const int G = K / QGROUP, kc = K / 8, nsub = N / 16, gpk = G / KS, items = (nsub + SUB - 1) / SUB;
+    const int G = K / QGROUP, kc = x_row_stride(K), nsub = N / 16, gpk = G / KS, items = (nsub + SUB - 1) / SUB;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE,
               q = lane / 16, n = lane % 16, waves = KSNW ? NW : int(blockDim.x) / WAVE;
     const int sl = wave / KS, kp = wave % KS, g0 = kp * gpk;
@@ -129,7 +134,7 @@ __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t
             compute_shared_x<BF16, MB, 1>(wr, xr, acc);
             // partials double-buffered by item parity: the barrier of item
             // i + 1 orders item i's reads before item i + 2's writes
-            ksplit_sum<MB>(acc[0], red + par * (waves * MB * WAVE), KS, wave, kp, lane);
+            ksplit_sum<MB>(acc[0], red + par * (red_slots(waves, KS) * MB * WAVE), KS, wave, kp, lane);
             par ^= 1;
             const int sub = item * SUB + sl;
             if (kp == 0 && sub < nsub) store_rows<MB>(acc[0], y, ys, y_bf16, accumulate, M, sub, lane);
@@ -162,7 +167,7 @@ static void dense_split(int G, int &KS, int &SUB, int &NW) {
 template <int NW, int MB, bool HAS_Z, bool CH4, bool KSNW>
 static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
     const int waves = KS * SUB, threads = waves * WAVE, gpk = a.K / QGROUP / KS;
-    const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves);
+    const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
     const int nsub = a.N / 16, items = (nsub + SUB - 1) / SUB;
     auto one = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, false, KSNW>;
     const LaunchShape ls = persistent_shape(reinterpret_cast<const void *>(one), threads, lds);
@@ -173,7 +178,16 @@ static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
     }
     auto pf = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, true, KSNW>;
     const LaunchShape lp = persistent_shape(reinterpret_cast<const void *>(pf), threads, lds);
-    const int per = (items + lp.max_blocks - 1) / lp.max_blocks, blocks = (items + per - 1) / per;
+    // every CU gets the same number of items: blocks per CU = the largest
+    // divisor of the per-CU item count that stays resident
+    const int ipc = (items + lp.cus - 1) / lp.cus, bmax = lp.max_blocks / lp.cus > 0 ? lp.max_blocks / lp.cus : 1;
+    int bpc = 1;
+    for (int d = bmax; d >= 1; --d)
+        if (ipc % d == 0) {
+            bpc = d;
+            break;
+        }
+    const int per = (items + lp.cus * bpc - 1) / (lp.cus * bpc), blocks = (items + per - 1) / per;
     pf<<<blocks, threads, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.y, a.ys, a.y_bf16, a.N, a.K, a.M, a.accumulate, KS,
                                     SUB);
 }
@@ -204,7 +218,7 @@ bool gemv_fits(int M, int K) {
     const int MB = M <= 16 ? 1 : 2;
     int KS, SUB, NW;
     dense_split(K / QGROUP, KS, SUB, NW);
-    return dense_lds_bytes(M, K, MB, KS * SUB) <= 160 * 1024;
+    return dense_lds_bytes(M, K, MB, KS * SUB, KS) <= 160 * 1024;
 }
 
 static void launch_gemv_fit(const GemvArgs &a, hipStream_t s) {

@@ -22,21 +22,44 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// 16-byte pieces of M activation rows of K elements, rounded to whole waves.
-__host__ __device__ inline int x_pieces(int M, int K) { return (M * (K / 8) + WAVE - 1) / WAVE * WAVE; }
+// LDS row stride, in 16-byte pieces, of staged activation rows of K
+// elements: K / 8, plus one piece when K / 8 is a multiple of 64. A b128 read
+// pass serves 16 lanes that read 16 different rows at the same column; with a
+// row stride that is a multiple of 256 bytes they would all hit the same
+// banks (a 16-way conflict at 16 rows), the extra piece spreads them over 16
+// bank groups. Padded rows are staged row by row (each wave instruction's
+// 64 pieces stay inside one row).
+__host__ __device__ inline int x_row_stride(int K) {
+    const int kc = K / 8;
+    return kc % 64 == 0 ? kc + 1 : kc;
+}
 
-// Rows 0..M-1 (row m starts at row(m)) of K 16-bit elements -> LDS [M][K]
-// with direct global->LDS loads (no registers; 1 KB per wave instruction).
-// Issued before the weight loads; the barrier that follows those waits for
-// both, so activations (L2) and weights (HBM) are requested before anything
-// waits.
+// 16-byte pieces of M staged rows, rounded to whole waves.
+__host__ __device__ inline int x_pieces(int M, int K) { return (M * x_row_stride(K) + WAVE - 1) / WAVE * WAVE; }
+
+// Rows 0..M-1 (row m starts at row(m)) of K 16-bit elements -> LDS, row m at
+// xl + m * x_row_stride(K), by direct global->LDS loads (no registers; 1 KB
+// per wave instruction). Issued before the weight loads; the barrier that
+// follows those waits for both, so activations (L2) and weights (HBM) are
+// requested before anything waits. With padded rows the row address is
+// wave-uniform (row(m) may then come from a scalar load, which does not wait
+// behind vector loads in flight).
 template <class RowFn>
 __device__ __forceinline__ void stage_rows_issue(RowFn row, int M, int K, uint4 *xl) {
-    const int kc = K / 8, total = M * kc, wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int nw = blockDim.x / WAVE;
-    for (int base = wave * WAVE; base < total; base += nw * WAVE) {
-        const int i = min(base + lane, total - 1), m = i / kc, c = i - m * kc;
-        __builtin_amdgcn_global_load_lds(row(m) + c * 8, xl + base, 16, 0, 0);
+    const int kc = K / 8, wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nw = blockDim.x / WAVE;
+    if (kc % WAVE == 0) {
+        const int st = kc + 1;
+        for (int m = 0; m < M; ++m) {
+            const uint16_t *r = row(m);
+            for (int c = wave * WAVE; c < kc; c += nw * WAVE)
+                __builtin_amdgcn_global_load_lds(r + (c + lane) * 8, xl + m * st + c, 16, 0, 0);
+        }
+    } else {
+        const int total = M * kc;
+        for (int base = wave * WAVE; base < total; base += nw * WAVE) {
+            const int i = min(base + lane, total - 1), m = i / kc, c = i - m * kc;
+            __builtin_amdgcn_global_load_lds(row(m) + c * 8, xl + base, 16, 0, 0);
+        }
     }
 }
 
