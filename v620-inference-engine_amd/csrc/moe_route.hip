@@ -15,62 +15,113 @@
 // exp is evaluated in double and rounded once to float, i.e. the correctly
 // rounded expf the CPU path uses, so selection and weights match it bit for
 // bit.
-#include <climits>
 
 #include "q4_common.cuh"
 #include "q4_kernels.hpp"
 
 namespace qwq4 {
 
-constexpr int MAX_PER = 16;  // logits per lane: E <= 1024
 
-// One wave routes one token. Lane j < k ends with the j-th selection.
+// ---- wave-wide reductions and scans on DPP (row-local lane permutes, no
+// LDS traffic) plus readlane across the four 16-lane rows
+#define QW_DPP(v, ctrl, rm, bm, bc) \
+    uint32_t(__builtin_amdgcn_update_dpp(0, int(v), ctrl, rm, bm, bc))
+
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <-> 7 - i within 8
+constexpr int DPP_MIRROR = 0x140;       // lane i <-> 15 - i within 16
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane(int(uint32_t(v)), l);
+    const uint32_t hi = __builtin_amdgcn_readlane(int(uint32_t(v >> 32)), l);
+    return (uint64_t(hi) << 32) | lo;
+}
+
+// Maximum of a 64-bit key over the wave (every lane gets it).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#define QW_MAX_STEP(ctrl)                                                              \
+    {                                                                                  \
+        const uint64_t o = (uint64_t(QW_DPP(uint32_t(v >> 32), ctrl, 0xf, 0xf, false)) << 32) | \
+                           QW_DPP(uint32_t(v), ctrl, 0xf, 0xf, false);                 \
+        v = o > v ? o : v;                                                             \
+    }
+    QW_MAX_STEP(DPP_XOR1)
+    QW_MAX_STEP(DPP_XOR2)
+    QW_MAX_STEP(DPP_HALF_MIRROR)
+    QW_MAX_STEP(DPP_MIRROR)
+#undef QW_MAX_STEP
+    const uint64_t r0 = readlane64(v, 0), r1 = readlane64(v, 16), r2 = readlane64(v, 32), r3 = readlane64(v, 48);
+    const uint64_t a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
+    return a > b ? a : b;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#define QW_FMAX_STEP(ctrl) v = fmaxf(v, __builtin_bit_cast(float, QW_DPP(__builtin_bit_cast(uint32_t, v), ctrl, 0xf, 0xf, false)));
+    QW_FMAX_STEP(DPP_XOR1)
+    QW_FMAX_STEP(DPP_XOR2)
+    QW_FMAX_STEP(DPP_HALF_MIRROR)
+    QW_FMAX_STEP(DPP_MIRROR)
+#undef QW_FMAX_STEP
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Inclusive prefix sum over the wave's 64 lanes (the GCN row_shr /
+// row_bcast sequence).
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t x) {
+    uint32_t s = x + QW_DPP(x, 0x111, 0xf, 0xf, true);   // row_shr:1
+    s += QW_DPP(x, 0x112, 0xf, 0xf, true);               // row_shr:2
+    s += QW_DPP(x, 0x113, 0xf, 0xf, true);               // row_shr:3
+    s += QW_DPP(s, 0x114, 0xf, 0xe, true);               // row_shr:4, banks 1-3
+    s += QW_DPP(s, 0x118, 0xf, 0xc, true);               // row_shr:8, banks 2-3
+    s += QW_DPP(s, 0x142, 0xa, 0xf, false);              // row_bcast:15 into rows 1, 3
+    s += QW_DPP(s, 0x143, 0xc, 0xf, false);              // row_bcast:31 into rows 2, 3
+    return s;
+}
+
+// One wave routes one token; the wave's lanes hold PER logits each (expert
+// lane + 64 i). A selection key packs the probability's bits (p >= 0, so
+// they order like p) over the complement of the expert index, so one 64-bit
+// maximum picks the largest p and, among equal p, the lowest index. Lane
+// j < k ends with the j-th selection.
+template <int PER>
 __device__ __forceinline__ void topk_wave(const float *l, int E, int k, int lane, int32_t *te, float *tw) {
-    float p[MAX_PER];
+    float v[PER];
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < MAX_PER; ++i) {
+    for (int i = 0; i < PER; ++i) {
         const int idx = lane + WAVE * i;
-        p[i] = idx < E ? l[idx] : -INFINITY;
-        mx = fmaxf(mx, p[i]);
+        v[i] = idx < E ? l[idx] : -INFINITY;
+        mx = fmaxf(mx, v[i]);
     }
+    mx = wave_max_f32(mx);
+    uint64_t key[PER];
 #pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, WAVE));
-#pragma unroll
-    for (int i = 0; i < MAX_PER; ++i) {
+    for (int i = 0; i < PER; ++i) {
         const int idx = lane + WAVE * i;
-        p[i] = idx < E ? float(exp(double(p[i] - mx))) : -2.f;
+        const float p = float(exp(double(v[i] - mx)));
+        key[i] = idx < E ? (uint64_t(__builtin_bit_cast(uint32_t, p)) << 32) | uint32_t(~uint32_t(idx)) : 0ull;
     }
     double top = 0.0;
     int my_e = 0;
     float my_p = 0.f;
     for (int j = 0; j < k; ++j) {
-        float bv = -3.f;
-        int bi = INT_MAX;
+        uint64_t best = key[0];
 #pragma unroll
-        for (int i = 0; i < MAX_PER; ++i)
-            if (p[i] > bv) {  // ascending index within the lane: the first maximum wins
-                bv = p[i];
-                bi = lane + WAVE * i;
-            }
+        for (int i = 1; i < PER; ++i) best = key[i] > best ? key[i] : best;
+        const uint64_t w = wave_max_u64(best);
 #pragma unroll
-        for (int o = WAVE / 2; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, WAVE);
-            const int oi = __shfl_xor(bi, o, WAVE);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if ((bi % WAVE) == lane) {
-#pragma unroll
-            for (int i = 0; i < MAX_PER; ++i)
-                if (i == bi / WAVE) p[i] = -1.f;
-        }
-        top += double(bv);
+        for (int i = 0; i < PER; ++i)
+            if (key[i] == w) key[i] = 0ull;  // taken
+        const float p = __builtin_bit_cast(float, uint32_t(w >> 32));
+        top += double(p);
         if (lane == j) {
-            my_e = bi;
-            my_p = bv;
+            my_e = int(~uint32_t(w));
+            my_p = p;
         }
     }
     if (lane < k) {
@@ -79,11 +130,12 @@ __device__ __forceinline__ void topk_wave(const float *l, int E, int k, int lane
     }
 }
 
+template <int PER>
 __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict__ logits, int T, int E, int k,
                                                          int32_t *__restrict__ top_e, float *__restrict__ top_w) {
     const int t = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     if (t >= T) return;
-    topk_wave(logits + int64_t(t) * E, E, k, lane, top_e + int64_t(t) * k, top_w + int64_t(t) * k);
+    topk_wave<PER>(logits + int64_t(t) * E, E, k, lane, top_e + int64_t(t) * k, top_w + int64_t(t) * k);
 }
 
 struct SlotLds {
@@ -216,58 +268,53 @@ __device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
 // Decode batches (T <= 64): selections and slots in one launch. A token
 // picks an expert at most once, so the tokens of expert e are the set bits of
 // one 64-bit mask; a pair's rank among them is a popcount below its bit.
+template <int PER>
 __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
     __shared__ int32_t s_te[64 * 64];
     __shared__ unsigned long long s_mask[1024];
     __shared__ int32_t s_off[1024];
-    __shared__ int32_t s_sum[16][3];
+    __shared__ uint32_t s_sum[16][2];
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int T = a.T, E = a.E, k = a.topk, P = T * k;
     if (tid < E) s_mask[tid] = 0ull;
     for (int t = wave; t < T; t += 16)
-        topk_wave(a.logits + int64_t(t) * E, E, k, lane, s_te + t * k, a.top_w + int64_t(t) * k);
+        topk_wave<PER>(a.logits + int64_t(t) * E, E, k, lane, s_te + t * k, a.top_w + int64_t(t) * k);
     __syncthreads();
     for (int i = tid; i < P; i += blockDim.x) {
         a.top_e[i] = s_te[i];
         atomicOr(&s_mask[s_te[i]], 1ull << (i / k));
     }
     __syncthreads();
-    // exclusive scans over the experts (one per thread): pairs, non-empty
-    // experts, tiles
+    // exclusive scans over the experts (one per thread): pairs and non-empty
+    // experts packed in one word (both < 2^16), tiles in another
     const int c = tid < E ? __popcll(s_mask[tid]) : 0;
-    const int v[3] = {c, c > 0, a.tile_m > 0 ? (c + a.tile_m - 1) / a.tile_m : 0};
-    int inc[3] = {v[0], v[1], v[2]};
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int u = __shfl_up(inc[j], o, WAVE);
-            if (lane >= o) inc[j] += u;
-        }
-    }
+    const int nt = a.tile_m > 0 ? (c + a.tile_m - 1) / a.tile_m : 0;
+    const uint32_t v0 = uint32_t(c) | (uint32_t(c > 0) << 16), v1 = uint32_t(nt);
+    const uint32_t i0 = wave_scan_incl(v0), i1 = a.tile_m > 0 ? wave_scan_incl(v1) : 0u;
     if (lane == WAVE - 1) {
-#pragma unroll
-        for (int j = 0; j < 3; ++j) s_sum[wave][j] = inc[j];
+        s_sum[wave][0] = i0;
+        s_sum[wave][1] = i1;
     }
     __syncthreads();
-    int ex[3] = {inc[0] - v[0], inc[1] - v[1], inc[2] - v[2]};
+    uint32_t e0 = i0 - v0, e1 = i1 - v1;
     for (int w = 0; w < wave; ++w) {
-#pragma unroll
-        for (int j = 0; j < 3; ++j) ex[j] += s_sum[w][j];
+        e0 += s_sum[w][0];
+        e1 += s_sum[w][1];
     }
+    const int off = int(e0 & 0xffffu), act = int(e0 >> 16), tile0 = int(e1);
     if (tid < E) {
-        s_off[tid] = ex[0];
-        a.offsets[tid] = ex[0];
+        s_off[tid] = off;
+        a.offsets[tid] = off;
         a.counts[tid] = c;
-        if (c > 0) a.active[ex[1]] = tid;
-        for (int j = 0; j < v[2]; ++j) {
-            a.tile_e[ex[2] + j] = tid;
-            a.tile_m0[ex[2] + j] = j * a.tile_m;
+        if (c > 0) a.active[act] = tid;
+        for (int j = 0; j < nt; ++j) {
+            a.tile_e[tile0 + j] = tid;
+            a.tile_m0[tile0 + j] = j * a.tile_m;
         }
         if (tid == E - 1) {
-            a.offsets[E] = ex[0] + c;
-            *a.n_active = ex[1] + v[1];
-            if (a.tile_m > 0) *a.n_tiles = ex[2] + v[2];
+            a.offsets[E] = off + c;
+            *a.n_active = act + (c > 0);
+            if (a.tile_m > 0) *a.n_tiles = tile0 + nt;
         }
     }
     __syncthreads();
@@ -289,12 +336,21 @@ __global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a) {
 void launch_route(const RouteArgs &a, hipStream_t s) {
     const size_t lds = route_lds_bytes(a.T, a.E);
     if (a.T <= 64) {
-        route_small_kernel<<<1, 1024, 0, s>>>(a);
+        const int per = (a.E + WAVE - 1) / WAVE;
+        if (per <= 1) route_small_kernel<1><<<1, 1024, 0, s>>>(a);
+        else if (per <= 2) route_small_kernel<2><<<1, 1024, 0, s>>>(a);
+        else if (per <= 4) route_small_kernel<4><<<1, 1024, 0, s>>>(a);
+        else if (per <= 8) route_small_kernel<8><<<1, 1024, 0, s>>>(a);
+        else route_small_kernel<16><<<1, 1024, 0, s>>>(a);
     } else {
         if (lds > 48 * 1024)
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(route_slots_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-        route_topk_kernel<<<(a.T + 3) / 4, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
+        const int per = (a.E + WAVE - 1) / WAVE;
+        const unsigned g = unsigned((a.T + 3) / 4);
+        if (per <= 4) route_topk_kernel<4><<<g, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
+        else if (per <= 8) route_topk_kernel<8><<<g, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
+        else route_topk_kernel<16><<<g, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
         route_slots_kernel<<<1, 1024, lds, s>>>(a);
     }
 }

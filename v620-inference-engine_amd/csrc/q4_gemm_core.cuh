@@ -8,8 +8,9 @@
 // LDS (2 x (32 + 32) KB). For the next stage, the A tile goes global -> LDS
 // by direct loads (1 KB = 8 rows per wave instruction, any row addresses)
 // and the weight tile (8 KB of q4; two threads per weight row) into
-// registers, dequantised and written to LDS in two halves interleaved with
-// the current stage's MFMAs; fragment reads run one 16-K step ahead.
+// registers two stages ahead, dequantised and written to LDS in two halves
+// interleaved with the MFMAs of the stage before its own; fragment reads run
+// one 16-K step ahead.
 //
 // Numerics: each weight becomes fp16((q - z) * s) (exact subtraction, one
 // rounding); products and sums run on the fp16 MFMA with fp32 accumulation.
@@ -93,21 +94,26 @@ __device__ __forceinline__ void gemm_tile(unsigned char *smem, const uint16_t *c
         }
     };
     const int brow = tid / 2, bq = tid % 2;
-    uint4 wr;
-    uint32_t sr = 0, zr = 0;
-    auto issue_b = [&](int ks) {  // quarter 2(ks%2) + bq of group ks/2
+    // raw weights of one stage: this thread's quarter 2(ks%2) + bq of group
+    // ks/2, its scale and zero word
+    struct BRaw {
+        uint4 w;
+        uint32_t s, z;
+    };
+    auto issue_b = [&](int ks, BRaw &r) {
+        ks = min(ks, nk - 1);  // past the end: a valid (unused) load keeps the code branch-free
         const int g = ks / 2;
-        wr = b.w[g * 64 + ((ks % 2) * 2 + bq) * 16];
-        sr = b.s[(g >> 2) * 64 + (g & 3)];
-        if constexpr (HAS_Z) zr = b.z[(g >> 2) * 16];
+        r.w = b.w[g * 64 + ((ks % 2) * 2 + bq) * 16];
+        r.s = b.s[(g >> 2) * 64 + (g & 3)];
+        if constexpr (HAS_Z) r.z = b.z[(g >> 2) * 16];
     };
     // half h of the dequant (2 of the 4 words), written swizzled
-    auto commit_b = [&](int ks, unsigned char *dst, int h) {
+    auto commit_b = [&](int ks, const BRaw &r, unsigned char *dst, int h) {
         const int g = ks / 2;
-        const uint32_t zb = zero_bytes(HAS_Z ? (zr >> (4 * (g & 3))) & 0xfu : 8u);
-        const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(sr));
+        const uint32_t zb = zero_bytes(HAS_Z ? (r.z >> (4 * (g & 3))) & 0xfu : 8u);
+        const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(r.s));
         const h2 s2 = {sc, sc};
-        const uint32_t words[4] = {wr.x, wr.y, wr.z, wr.w};
+        const uint32_t words[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
 #pragma unroll
         for (int c = 2 * h; c < 2 * h + 2; ++c)
             *reinterpret_cast<uint4 *>(dst + swz(brow, bq * 4 + c)) = dequant8(words[c], zb, s2);
@@ -123,8 +129,9 @@ __device__ __forceinline__ void gemm_tile(unsigned char *smem, const uint16_t *c
             bf[j] = *reinterpret_cast<const uint4 *>(bb + swz(wn2 * S::WNR + j * 32 + l32, c));
     };
     // MFMAs of one stage; fragments of step kk+1 are read during step kk, and
-    // the next stage's weights are dequantised in two halves between them
-    auto compute = [&](const unsigned char *a, const unsigned char *bb, int ksn, unsigned char *dstb) {
+    // the next stage's weights (raw, loaded a stage earlier) are dequantised
+    // in two halves between them
+    auto compute = [&](const unsigned char *a, const unsigned char *bb, int ksn, const BRaw &rn, unsigned char *dstb) {
         uint4 af[2], bf[NJ], an[2], bn[NJ];
         read_frags(a, bb, 0, af, bf);
 #pragma unroll
@@ -134,7 +141,7 @@ __device__ __forceinline__ void gemm_tile(unsigned char *smem, const uint16_t *c
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32<F16>(af[i], bf[j], acc[i][j]);
-            if (ksn >= 0 && (kk == 1 || kk == 3)) commit_b(ksn, dstb, kk / 2);
+            if (ksn >= 0 && (kk == 1 || kk == 3)) commit_b(ksn, rn, dstb, kk / 2);
             // interleave: one MFMA, then up to four VALU instructions
 #pragma unroll
             for (int q = 0; q < 2 * NJ; ++q) {
@@ -148,20 +155,28 @@ __device__ __forceinline__ void gemm_tile(unsigned char *smem, const uint16_t *c
         }
     };
 
+    // Stage ks (parity p): the A tile of ks + 1 goes to LDS by direct loads
+    // and the raw weights of ks + 2 into register set p, both requested
+    // before the stage's MFMAs (the barrier that ends the stage waits for
+    // them); the weights of ks + 1 (set 1 - p, loaded during the previous
+    // stage) are dequantised into LDS between the MFMAs.
+    BRaw rs[2];
     issue_a(0, bufA(0));
-    issue_b(0);
-    commit_b(0, bufB(0), 0);
-    commit_b(0, bufB(0), 1);
+    issue_b(0, rs[0]);
+    commit_b(0, rs[0], bufB(0), 0);
+    commit_b(0, rs[0], bufB(0), 1);
+    issue_b(1, rs[1]);
     __syncthreads();
-    for (int ks = 0; ks < nk; ++ks) {
-        const int cur = ks & 1, nxt = cur ^ 1;
+    auto stage = [&](int ks, BRaw &mine, const BRaw &next, int p) {
         const bool more = ks + 1 < nk;
-        if (more) {
-            issue_a(ks + 1, bufA(nxt));
-            issue_b(ks + 1);
-        }
-        compute(bufA(cur), bufB(cur), more ? ks + 1 : -1, bufB(nxt));
+        if (more) issue_a(ks + 1, bufA(p ^ 1));
+        issue_b(ks + 2, mine);
+        compute(bufA(p), bufB(p), more ? ks + 1 : -1, next, bufB(p ^ 1));
         __syncthreads();
+    };
+    for (int ks = 0; ks < nk; ks += 2) {  // nk is even (K is a multiple of 128)
+        stage(ks, rs[0], rs[1], 0);
+        stage(ks + 1, rs[1], rs[0], 1);
     }
 }
 
