@@ -1,0 +1,82 @@
+"""HIP-graph capture of a decode layer's q4 calls (the reference records its
+whole decode step into a graph, src/engine/decode.hip:166-181).
+
+One decode layer: QKV projection, routing, gathered experts, combine and the
+down projection, plus a prefill GEMM, captured once and replayed several
+times with the program's own eager work and synchronisations in between.
+Every replay must reproduce the eager results bit for bit (all kernels are
+deterministic), and the eager results must match the oracle.
+"""
+import numpy as np
+import pytest
+
+import qwq4
+from qwq4 import synth
+from _gpu_util import TOL, bf16_err_ok, host, rel_err, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def test_decode_layer_graph_replays(gpu, oracle):
+    import torch
+    M, H, QKV, E, F, k = 4, 1024, 1536, 32, 256, 4
+    print(f"graph decode layer M={M} H={H} E={E} F={F} k={k}", flush=True)
+    Wq = synth.q4_weights(71, "gq", QKV, H)
+    Wd = synth.q4_weights(71, "gd", H, F * 2)
+    ex = synth.experts(71, E, H, F)
+    xb, xf = synth.acts(71, "gx", M, H)
+    hb, hf = synth.acts(71, "gh", M, F * 2)
+    l = synth.router_logits(71, "gl", M, E)
+    T = 256
+    Xb, Xf = synth.acts(71, "gX", T, H)
+
+    dq = qwq4.tile(*(to_dev(a, gpu) for a in Wq), QKV, H)
+    dd = qwq4.tile(*(to_dev(a, gpu) for a in Wd), H, F * 2)
+    from test_moe_gpu import _experts_dev
+    (eg, eu, ed), _, _ = _experts_dev(gpu, ex)
+    x, h2, logits, X = to_dev(xb, gpu), to_dev(hb, gpu), to_dev(l, gpu), to_dev(Xb, gpu)
+
+    # preallocated outputs: nothing is allocated inside the capture
+    yq = torch.empty((M, QKV), dtype=torch.bfloat16, device=gpu)
+    yd = torch.empty((M, H), dtype=torch.float32, device=gpu)
+    r = qwq4.Route(M, E, k, gpu)
+    h = torch.empty((M * k, F), dtype=torch.float16, device=gpu)
+    yp = torch.empty((M * k, H), dtype=torch.float32, device=gpu)
+    out = torch.empty((M, H), dtype=torch.float32, device=gpu)
+    Y = torch.empty((T, QKV), dtype=torch.float32, device=gpu)
+    ws = torch.empty(qwq4.gemm_workspace_size(T, H), dtype=torch.uint8, device=gpu)
+
+    def layer():
+        qwq4.gemv(*dq, x, QKV, H, M, y=yq, y_bf16=True)
+        qwq4.moe_route(logits, k, out=r)
+        qwq4.moe_experts_gemv(eg, eu, ed, r, x, E, F, h=h, yp=yp)
+        qwq4.moe_combine(yp, r, H, out=out, out_bf16=False)
+        qwq4.gemv(*dd, h2, H, F * 2, M, y=yd)
+        qwq4.gemm(*dq, X, QKV, H, Y=Y, workspace=ws)
+
+    outs = (yq, yd, out, Y, r.top_e, r.pair_tok, h)
+    layer()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+
+    # eager results against the oracle
+    assert bf16_err_ok(host(yq), oracle.q4_linear(*Wq, QKV, H, xf))
+    assert rel_err(host(yd), oracle.q4_linear(*Wd, H, F * 2, hf)) <= TOL
+    assert rel_err(host(out), oracle.moe(xf, l, k, *ex)) <= TOL
+    assert rel_err(host(Y), oracle.q4_linear(*Wq, QKV, H, Xf)) <= TOL
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            layer()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for o in outs:
+            o.zero_()        # eager work between replays, on torch's stream
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o.view(torch.uint8), e.view(torch.uint8)), f"replay {rep}"
