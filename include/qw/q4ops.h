@@ -153,6 +153,38 @@ int qw_q4_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64
                   void *stream);
 int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream);
 
+/* Scale conversion as the reference does it at load (weight_convert.cpp:19-26):
+ * bf16 -> fp16 bits, magnitudes above 65504 saturated, round to nearest even. */
+int qw_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, void *stream);
+
+/* ---- Checkpoint loading (role of the reference's loader, src/core/safetensors.cpp
+ * and src/engine/weights.hip:352-402).
+ * A safetensors file, mapped read-only and indexed by tensor name. */
+typedef struct qw_st_file qw_st_file;
+int qw_st_open(const char *path, qw_st_file **out);
+void qw_st_close(qw_st_file *f);
+/* Number of tensors and the i-th name (sorted), for listing. */
+int qw_st_count(const qw_st_file *f);
+const char *qw_st_name(const qw_st_file *f, int i);
+/* One tensor's header entry: dtype ("I32", "BF16", ...; dtype holds >= 16
+ * bytes), shape (up to 8 dims), and its bytes in the mapping (host memory). */
+int qw_st_tensor(const qw_st_file *f, const char *name, char *dtype, int64_t *shape, int *ndim, const void **data,
+                 size_t *nbytes);
+
+/* One compressed-tensors q4 projection, "<prefix>.weight_packed" (I32
+ * [N][K/8], checkpoint order) and "<prefix>.weight_scale" (BF16 or F16
+ * [N][K/128]), straight into the tiled device format (symmetric: zero 8, Zt
+ * not written). Wt/St may point inside a larger tiled matrix (stacked
+ * experts): see qw_q4_tiled_offset. `staging` is device memory of at least
+ * qw_q4_load_staging_size(N, K) bytes, 256-byte aligned, in use until the
+ * stream's work is done. The copy from the mapping is synchronous. */
+size_t qw_q4_load_staging_size(int64_t N, int64_t K);
+int qw_q4_load(const qw_st_file *f, const char *prefix, int64_t N, int64_t K, uint32_t *Wt, uint16_t *St, void *staging,
+               size_t staging_bytes, void *stream);
+/* Byte offsets of row row0 (a multiple of 16) inside tiled Wt, St, Zt of K
+ * columns: expert e of a stacked [E*F][K] matrix starts at row e*F. */
+void qw_q4_tiled_offset(int64_t row0, int64_t K, size_t *wt_off, size_t *st_off, size_t *zt_off);
+
 #ifdef __cplusplus
 }
 #endif

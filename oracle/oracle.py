@@ -49,6 +49,8 @@ def lib():
         for n in ("o_bf16_to_f32", "o_f16_to_f32"):
             getattr(L, n).argtypes = [ctypes.c_uint16]
             getattr(L, n).restype = ctypes.c_float
+        L.o_bf16_to_f16.argtypes = [ctypes.c_uint16]
+        L.o_bf16_to_f16.restype = ctypes.c_uint16
         for n in ("o_f32_to_f16", "o_f32_to_bf16"):
             getattr(L, n).argtypes = [ctypes.c_float]
             getattr(L, n).restype = ctypes.c_uint16
@@ -83,6 +85,12 @@ def f32_to_f16(x):
 def f32_to_bf16(x):
     x = np.asarray(x, np.float32)
     return np.array([lib().o_f32_to_bf16(float(v)) for v in x.ravel()], np.uint16).reshape(x.shape)
+
+
+def bf16_to_f16(b):
+    """weight_convert.cpp:19-26: saturating bf16 -> fp16 bits."""
+    b = np.asarray(b, np.uint16)
+    return np.array([lib().o_bf16_to_f16(int(v)) for v in b.ravel()], np.uint16).reshape(b.shape)
 
 
 def bf16_to_f32(b):

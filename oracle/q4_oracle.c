@@ -93,6 +93,14 @@ uint16_t o_f32_to_f16(float f) {
     return (uint16_t)half;
 }
 
+/* src/engine/weight_convert.cpp:19-26: bf16 -> fp16 at load, magnitudes above
+ * the fp16 maximum saturated to +-65504 (infinities too; NaN stays NaN). */
+uint16_t o_bf16_to_f16(uint16_t b) {
+    float f = o_bf16_to_f32(b);
+    if (fabsf(f) > 65504.f) f = f > 0 ? 65504.f : -65504.f;
+    return o_f32_to_f16(f);
+}
+
 /* Round-to-nearest-even fp32 -> bf16 (NaN kept quiet). The reference has no
  * bf16 writer (gfx1030 has no bf16); this is the IEEE rule the outputs use. */
 uint16_t o_f32_to_bf16(float f) {

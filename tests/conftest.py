@@ -29,3 +29,10 @@ def gpu():
     import qwq4
     qwq4.lib()
     return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def lib():
+    """The C-ABI library, loaded on the host (no GPU call)."""
+    import qwq4
+    return qwq4.lib()

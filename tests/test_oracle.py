@@ -29,6 +29,16 @@ def test_f32_to_f16_matches_reference(oracle):
     assert np.array_equal(x[ok].astype(np.float16).view(np.uint16), got[ok])
 
 
+def test_bf16_to_f16_matches_reference(oracle):
+    got = oracle.bf16_to_f16(GOLD["bf16_in"])
+    assert np.array_equal(got, GOLD["bf16_to_f16"])
+    # independent: numpy's fp16 cast of the clipped value (NaN aside)
+    f = oracle.bf16_to_f32(GOLD["bf16_in"])
+    ok = ~np.isnan(f)
+    ref = np.clip(f[ok], -65504, 65504).astype(np.float16).view(np.uint16)
+    assert np.array_equal(got[ok], ref)
+
+
 def test_f32_to_bf16_is_round_to_nearest_even(oracle):
     import torch
     r = np.random.default_rng(5)

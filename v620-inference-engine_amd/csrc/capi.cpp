@@ -5,9 +5,16 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "q4_kernels.hpp"
 #include "qw/q4ops.h"
+#include "st_loader.hpp"
+
+struct qw_st_file {
+    qwq4::StFile f;
+    std::vector<const qwq4::StTensor *> order;
+};
 
 namespace {
 
@@ -227,6 +234,103 @@ int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, 
     REQUIRE(in && out && n_words >= 1, "qw_q4_from_engine_order: bad arguments");
     qwq4::launch_from_engine_order(in, out, n_words, st(stream));
     return launched("qw_q4_from_engine_order");
+}
+
+int qw_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, void *stream) {
+    REQUIRE(in && out && n >= 0, "qw_bf16_to_f16: bad arguments");
+    if (n == 0) return QW_Q4_OK;
+    qwq4::launch_bf16_to_f16(in, out, n, st(stream));
+    return launched("qw_bf16_to_f16");
+}
+
+int qw_st_open(const char *path, qw_st_file **out) {
+    REQUIRE(path && out, "qw_st_open: null argument");
+    *out = nullptr;
+    auto *f = new qw_st_file;
+    std::string err;
+    if (!f->f.open(path, err)) {
+        delete f;
+        return fail("qw_st_open: %s", err.c_str());
+    }
+    for (auto &kv : f->f.tensors()) f->order.push_back(&kv.second);
+    *out = f;
+    g_err.clear();
+    return QW_Q4_OK;
+}
+
+void qw_st_close(qw_st_file *f) { delete f; }
+
+int qw_st_count(const qw_st_file *f) { return f ? int(f->order.size()) : 0; }
+
+const char *qw_st_name(const qw_st_file *f, int i) {
+    return f && i >= 0 && i < int(f->order.size()) ? f->order[i]->name.c_str() : nullptr;
+}
+
+int qw_st_tensor(const qw_st_file *f, const char *name, char *dtype, int64_t *shape, int *ndim, const void **data,
+                 size_t *nbytes) {
+    REQUIRE(f && name, "qw_st_tensor: null argument");
+    const qwq4::StTensor *t = f->f.find(name);
+    REQUIRE(t, "qw_st_tensor: no tensor named %s", name);
+    REQUIRE(t->shape.size() <= 8, "qw_st_tensor: %s has more than 8 dimensions", name);
+    if (dtype) std::snprintf(dtype, 16, "%s", t->dtype.c_str());
+    if (shape)
+        for (size_t i = 0; i < t->shape.size(); ++i) shape[i] = t->shape[i];
+    if (ndim) *ndim = int(t->shape.size());
+    if (data) *data = t->data;
+    if (nbytes) *nbytes = t->nbytes;
+    g_err.clear();
+    return QW_Q4_OK;
+}
+
+static size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
+
+size_t qw_q4_load_staging_size(int64_t N, int64_t K) {
+    if (N < 1 || K < 128) return 0;
+    const size_t G = size_t(K / 128);
+    return round256(size_t(N) * size_t(K) / 2) + 2 * round256(size_t(N) * G * 2);
+}
+
+void qw_q4_tiled_offset(int64_t row0, int64_t K, size_t *wt_off, size_t *st_off, size_t *zt_off) {
+    const int64_t G = K / 128, GC = (G + 3) / 4, sub = row0 / 16;
+    if (wt_off) *wt_off = size_t(sub) * size_t(G) * 64 * 16;
+    if (st_off) *st_off = size_t(sub) * size_t(GC) * 64 * 2;
+    if (zt_off) *zt_off = size_t(sub) * size_t(GC) * 16 * 2;
+}
+
+int qw_q4_load(const qw_st_file *f, const char *prefix, int64_t N, int64_t K, uint32_t *Wt, uint16_t *St, void *staging,
+               size_t staging_bytes, void *stream) {
+    REQUIRE(f && prefix && Wt && St && staging, "qw_q4_load: null argument");
+    REQUIRE(N >= 16 && N % 16 == 0 && K >= 128 && K % 128 == 0, "qw_q4_load: N = %lld, K = %lld (need multiples of 16, 128)",
+            (long long)N, (long long)K);
+    REQUIRE(aligned(Wt, 16) && aligned(St, 8) && aligned(staging, 256), "qw_q4_load: misaligned Wt, St or staging");
+    const size_t need = qw_q4_load_staging_size(N, K);
+    REQUIRE(staging_bytes >= need, "qw_q4_load: staging needs %zu bytes", need);
+    const std::string pw = std::string(prefix) + ".weight_packed", ps = std::string(prefix) + ".weight_scale";
+    const qwq4::StTensor *tw = f->f.find(pw), *ts = f->f.find(ps);
+    REQUIRE(tw && ts, "qw_q4_load: %s or %s missing", pw.c_str(), ps.c_str());
+    const int64_t G = K / 128;
+    REQUIRE(tw->dtype == "I32" && tw->shape.size() == 2 && tw->shape[0] == N && tw->shape[1] == K / 8,
+            "qw_q4_load: %s must be I32 [%lld][%lld]", pw.c_str(), (long long)N, (long long)(K / 8));
+    REQUIRE((ts->dtype == "BF16" || ts->dtype == "F16") && ts->shape.size() == 2 && ts->shape[0] == N &&
+                ts->shape[1] == G,
+            "qw_q4_load: %s must be BF16 or F16 [%lld][%lld]", ps.c_str(), (long long)N, (long long)G);
+    unsigned char *stg = static_cast<unsigned char *>(staging);
+    uint32_t *W = reinterpret_cast<uint32_t *>(stg);
+    uint16_t *Ssrc = reinterpret_cast<uint16_t *>(stg + round256(tw->nbytes));
+    uint16_t *S16 = reinterpret_cast<uint16_t *>(stg + round256(tw->nbytes) + round256(ts->nbytes));
+    hipError_t e = hipMemcpyAsync(W, tw->data, tw->nbytes, hipMemcpyHostToDevice, st(stream));
+    if (e == hipSuccess) e = hipMemcpyAsync(Ssrc, ts->data, ts->nbytes, hipMemcpyHostToDevice, st(stream));
+    if (e != hipSuccess) {
+        g_err = std::string("qw_q4_load: copy: ") + hipGetErrorString(e);
+        return QW_Q4_ELAUNCH;
+    }
+    const uint16_t *S = Ssrc;
+    if (ts->dtype == "BF16") {
+        qwq4::launch_bf16_to_f16(Ssrc, S16, N * G, st(stream));
+        S = S16;
+    }
+    qwq4::launch_tile(W, S, nullptr, N, K, Wt, St, nullptr, st(stream));
+    return launched("qw_q4_load");
 }
 
 }  // extern "C"

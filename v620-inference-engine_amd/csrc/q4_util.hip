@@ -167,7 +167,44 @@ __global__ void untile_sz_kernel(const uint16_t *__restrict__ St, const uint16_t
     }
 }
 
+// bf16 -> fp16 bits as the reference converts checkpoint scales at load
+// (src/engine/weight_convert.cpp:19-26): magnitudes above 65504 saturate
+// (infinities too), NaN stays NaN (quiet, 0x7e00 | sign), round to nearest
+// even, fp16 subnormals kept. Integer arithmetic, so every pattern matches the
+// host conversion (src/core/common.hpp:76-97).
+__device__ __forceinline__ uint16_t bf16_to_f16_sat(uint16_t b) {
+    uint32_t u = uint32_t(b) << 16;
+    const uint32_t sign = (u >> 16) & 0x8000u, ex8 = (u >> 23) & 0xffu;
+    if (ex8 == 0xffu && (u & 0x7fffffu)) return uint16_t(sign | 0x7e00u);
+    if (__builtin_bit_cast(float, u & 0x7fffffffu) > 65504.f) return uint16_t(sign | 0x7bffu);
+    const int32_t ex = int32_t(ex8) - 127 + 15;
+    uint32_t man = u & 0x7fffffu;
+    if (ex <= 0) {
+        if (ex < -10) return uint16_t(sign);
+        man |= 0x800000u;
+        const uint32_t shift = uint32_t(14 - ex);
+        uint32_t half = man >> shift;
+        const uint32_t rem = man & ((1u << shift) - 1u), mid = 1u << (shift - 1);
+        if (rem > mid || (rem == mid && (half & 1u))) ++half;
+        return uint16_t(sign | half);
+    }
+    uint32_t half = sign | (uint32_t(ex) << 10) | (man >> 13);
+    const uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) ++half;
+    return uint16_t(half);
+}
+
+__global__ __launch_bounds__(256) void bf16_to_f16_kernel(const uint16_t *__restrict__ in, int64_t n,
+                                                         uint16_t *__restrict__ out) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = bf16_to_f16_sat(in[i]);
+}
+
 static unsigned blocks(int64_t n, int b) { return unsigned((n + b - 1) / b); }
+
+void launch_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, hipStream_t s) {
+    bf16_to_f16_kernel<<<blocks(n, 256), 256, 0, s>>>(in, n, out);
+}
 
 void launch_tile(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, uint32_t *Wt,
                  uint16_t *St, uint16_t *Zt, hipStream_t s) {

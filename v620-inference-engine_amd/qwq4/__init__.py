@@ -16,7 +16,9 @@ SYMBOLS = (
     "qw_q4_abi_version", "qw_q4_last_error", "qw_q4_gemv", "qw_q4_gemm_workspace_size", "qw_q4_gemm",
     "qw_moe_route", "qw_moe_experts_gemv", "qw_moe_experts_grouped", "qw_moe_grouped_workspace_size", "qw_moe_grouped_tile_m",
     "qw_moe_combine", "qw_q4_unpack", "qw_q4_dequant", "qw_q4_from_engine_order",
-    "qw_q4_tiled_size", "qw_q4_tile", "qw_q4_untile",
+    "qw_q4_tiled_size", "qw_q4_tile", "qw_q4_untile", "qw_bf16_to_f16",
+    "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
+    "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
 )
 
 _P = ctypes.c_void_p
@@ -42,6 +44,15 @@ _SIGS = {
     "qw_q4_unpack": ([_P, _I64, _I64, _P, _P], _I),
     "qw_q4_dequant": ([_P, _P, _P, _I64, _I64, _P, _P], _I),
     "qw_q4_from_engine_order": ([_P, _P, _I64, _P], _I),
+    "qw_bf16_to_f16": ([_P, _P, _I64, _P], _I),
+    "qw_st_open": ([ctypes.c_char_p, _P], _I),
+    "qw_st_close": ([_P], None),
+    "qw_st_count": ([_P], _I),
+    "qw_st_name": ([_P, _I], ctypes.c_char_p),
+    "qw_st_tensor": ([_P, ctypes.c_char_p, _P, _P, _P, _P, _P], _I),
+    "qw_q4_load_staging_size": ([_I64, _I64], _SZ),
+    "qw_q4_load": ([_P, ctypes.c_char_p, _I64, _I64, _P, _P, _P, _SZ, _P], _I),
+    "qw_q4_tiled_offset": ([_I64, _I64, _P, _P, _P], None),
 }
 
 
@@ -50,6 +61,10 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: build it with v620-inference-engine_amd/build.py")
+        # torch first: its HIP runtime (same soname as the one the library
+        # links) is then the only one in the process, so streams and device
+        # pointers from torch are the library's own
+        import torch  # noqa: F401
         L = ctypes.CDLL(LIB_PATH)
         for name, (args, res) in _SIGS.items():
             f = getattr(L, name)
@@ -257,4 +272,80 @@ def from_engine_order(words):
     import torch
     out = torch.empty_like(words)
     _check(lib().qw_q4_from_engine_order(_ptr(words), _ptr(out), words.numel(), _stream()), "qw_q4_from_engine_order")
+    return out
+
+
+# -------------------------------------------------------- checkpoint loading
+def bf16_to_f16(x, out=None):
+    """bf16 bits (int16/uint16 or bfloat16 tensor) -> fp16 bits, saturating as
+    the reference converts scales at load."""
+    import torch
+    out = out if out is not None else torch.empty(x.shape, dtype=torch.int16, device=x.device)
+    _dev(x, out)
+    _check(lib().qw_bf16_to_f16(_ptr(x), _ptr(out), x.numel(), _stream()), "qw_bf16_to_f16")
+    return out
+
+
+class StFile:
+    """A safetensors file mapped by the library (host side)."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        _check(lib().qw_st_open(os.fsencode(path), ctypes.byref(h)), "qw_st_open")
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().qw_st_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def names(self):
+        return [lib().qw_st_name(self._h, i).decode() for i in range(lib().qw_st_count(self._h))]
+
+    def info(self, name):
+        """(dtype, shape, nbytes) of one tensor."""
+        dt = ctypes.create_string_buffer(16)
+        shape = (ctypes.c_int64 * 8)()
+        nd, nb, data = ctypes.c_int(), ctypes.c_size_t(), ctypes.c_void_p()
+        _check(lib().qw_st_tensor(self._h, name.encode(), dt, shape, ctypes.byref(nd), ctypes.byref(data),
+                                  ctypes.byref(nb)), "qw_st_tensor")
+        return dt.value.decode(), tuple(shape[i] for i in range(nd.value)), nb.value
+
+
+def tiled_offset(row0, K):
+    a, b, c = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+    lib().qw_q4_tiled_offset(row0, K, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+    return a.value, b.value, c.value
+
+
+def load_q4(st, prefix, N, K, out=None, row0=0, device=None):
+    """Loads "<prefix>.weight_packed/.weight_scale" of an StFile into tiled
+    device tensors (Wt, St, None). With out=(Wt, St, Zt) of a larger tiled
+    matrix, writes rows row0 .. row0 + N - 1 of it (stacked experts)."""
+    import torch
+    device = device or torch.device("cuda", torch.cuda.current_device())
+    if out is None:
+        wb, sb, _ = tiled_size(N, K)
+        out = (torch.empty(wb // 4, dtype=torch.int32, device=device),
+               torch.empty(sb // 2, dtype=torch.int16, device=device), None)
+    Wt, St_ = out[0], out[1]
+    ow, os_, _ = tiled_offset(row0, K)
+    staging = torch.empty(lib().qw_q4_load_staging_size(N, K), dtype=torch.uint8, device=Wt.device)
+    _dev(Wt, St_, staging)
+    rc = lib().qw_q4_load(st._h, prefix.encode(), N, K, ctypes.c_void_p(Wt.data_ptr() + ow),
+                          ctypes.c_void_p(St_.data_ptr() + os_), _ptr(staging), staging.numel(), _stream())
+    _check(rc, "qw_q4_load")
+    torch.cuda.current_stream().synchronize()  # staging is freed on return
     return out
