@@ -167,6 +167,9 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
     up = gen_q4(torch, dev, F, H, lead=(E,), seed=11)
     down = gen_q4(torch, dev, H, F, lead=(E,), seed=12)
     per_expert = q4_bytes(F, H) * 2 + q4_bytes(H, F)
+    gr = torch.Generator(device=dev)
+    gr.manual_seed(13)
+    router_w = torch.randn((E, H), generator=gr, device=dev) * 0.02
     out = {}
     for B in batches:
         x = gen_x(torch, dev, B, H, seed=100 + B)
@@ -194,6 +197,23 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
         b = U * per_expert
         out[B] = {"distinct_experts": U, "GB_s": b * steps / (t.ms * 1e-3) / 1e9, "us_per_step": t.ms * 1e3 / steps,
                   "tokens_s": B * steps / (t.ms * 1e-3)}
+
+        # the fused block (qw_moe_decode): fp32 router GEMV + routing, experts,
+        # combine inside the down projection; bytes add the router weights
+        buf = qwq4.MoeDecode(B, E, k, H, F, dev)
+        ob = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
+
+        def fused():
+            qwq4.moe_decode(router_w, x, k, gate, up, down, E, F, buf=buf, out=ob)
+
+        fstep = graphed(torch, fused)
+        for _ in range(warmup):
+            fstep()
+        with Timer(torch) as tf:
+            for _ in range(steps):
+                fstep()
+        bf = b + E * H * 4
+        out[B]["block"] = {"GB_s": bf * steps / (tf.ms * 1e-3) / 1e9, "us_per_step": tf.ms * 1e3 / steps}
     return out
 
 

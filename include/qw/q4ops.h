@@ -153,6 +153,26 @@ int qw_q4_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64
                   void *stream);
 int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream);
 
+/* A routed-MoE decode block in three launches (the engine's decode step calls
+ * router GEMV -> route -> experts -> combine back to back, src/engine/decode.hip:99-111;
+ * math of ref::Model::moe, src/ref/ref_model.cpp:406-463):
+ *   logits = x . router_w^T (fp32 weights [E][H], the reference's fp32 router);
+ *   routing as qw_moe_route; experts as qw_moe_experts_gemv;
+ *   out[t] = shared[t] + sum_i top_w[t][i] * yp[tok_slot[t][i]]   (fp32 or bf16)
+ * The router GEMV and routing share a launch, and the combine runs inside the
+ * down projection. Outputs: out, logits [T][E], top_e, top_w, tok_slot [T][k],
+ * h, yp (as qw_moe_experts_gemv). shared fp32 [T][H] or NULL (e.g. the shared
+ * expert's output). 1 <= T <= 32.
+ * workspace: qw_moe_decode_workspace_size(...) bytes, 256-byte aligned, filled
+ * with zeros once before its first use (it holds completion counters that
+ * every call leaves at zero); calls that share a workspace must not overlap. */
+size_t qw_moe_decode_workspace_size(int T, int E, int topk, int H, int F);
+int qw_moe_decode(const float *router_w, const uint16_t *x, int T, int E, int topk, const uint32_t *gw,
+                  const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
+                  const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
+                  void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
+                  uint16_t *h, float *yp, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Scale conversion as the reference does it at load (weight_convert.cpp:19-26):
  * bf16 -> fp16 bits, magnitudes above 65504 saturated, round to nearest even. */
 int qw_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, void *stream);

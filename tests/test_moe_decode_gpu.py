@@ -1,0 +1,67 @@
+"""Fused MoE decode block (qw_moe_decode): fp32 router GEMV, routing, gathered
+experts and the combine folded into the down projection, against the oracle.
+
+Routing is checked on the block's own logits (the oracle routes the same
+fp32 values, so the selection must match bit for bit); the logits themselves
+against an fp64 product; the output against the oracle's MoE on those logits.
+"""
+import numpy as np
+import pytest
+
+import qwq4
+from qwq4 import synth
+from _gpu_util import TOL, bf16_err_ok, host, rel_err, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(gpu, seed, T, E, H, F, k, with_shared):
+    ex = synth.experts(seed, E, H, F)
+    xb, xf = synth.acts(seed, "dx", T, H)
+    r = np.random.default_rng(seed)
+    Wr = (r.standard_normal((E, H)) * 0.05).astype(np.float32)
+    shared = r.standard_normal((T, H)).astype(np.float32) if with_shared else None
+    from test_moe_gpu import _experts_dev
+    (g, u, d), _, _ = _experts_dev(gpu, ex)
+    return ex, xb, xf, Wr, shared, (g, u, d)
+
+
+@pytest.mark.parametrize("T,E,H,F,k,shared,bf16", [(1, 64, 1024, 256, 4, False, False), (5, 64, 1024, 256, 4, True, False),
+                                                   (32, 32, 512, 384, 6, True, True), (8, 256, 4096, 1536, 8, True, True)])
+def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
+    print(f"moe_decode T={T} E={E} H={H} F={F} k={k}", flush=True)
+    ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 40 + T, T, E, H, F, k, shared)
+    buf = qwq4.MoeDecode(T, E, k, H, F, gpu)
+    outs = []
+    for _ in range(3):   # repeated calls: counters left at zero, identical results
+        out, _ = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, buf=buf,
+                                 shared=to_dev(sh, gpu), out_bf16=bf16)
+        outs.append(host(out))
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    logits = host(buf.logits)
+    ref_l = xf.astype(np.float64) @ Wr.astype(np.float64).T
+    assert rel_err(logits, ref_l) <= 1e-5
+    te, tw = oracle.route(logits, k)
+    assert np.array_equal(host(buf.top_e), te)
+    assert np.all(np.abs(host(buf.top_w) - tw) <= 4 * 2.0**-24 * np.abs(tw))
+    ref = oracle.moe(xf, logits, k, *ex)
+    if sh is not None:
+        ref = ref + sh
+    if bf16:
+        assert bf16_err_ok(outs[0], ref)
+    else:
+        assert rel_err(outs[0], ref) <= TOL
+
+
+def test_moe_decode_matches_unfused_path(gpu):
+    T, E, H, F, k = 6, 64, 1024, 256, 4
+    ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 77, T, E, H, F, k, True)
+    out, buf = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
+                               out_bf16=False)
+    r = qwq4.moe_route(buf.logits, k)
+    h, yp = qwq4.moe_experts_gemv(g, u, d, r, to_dev(xb, gpu), E, F)
+    o2 = qwq4.moe_combine(yp, r, H, shared=to_dev(sh, gpu), out_bf16=False)
+    assert np.array_equal(host(r.top_e), host(buf.top_e))
+    assert np.array_equal(host(yp), host(buf.yp))
+    assert rel_err(host(out), host(o2)) <= 1e-6

@@ -333,4 +333,75 @@ int qw_q4_load(const qw_st_file *f, const char *prefix, int64_t N, int64_t K, ui
     return launched("qw_q4_load");
 }
 
+// ---- fused MoE decode block
+namespace {
+struct DecodeLayout {
+    int kl, ksplit, rows;
+    size_t part, counts, offsets, pair_tok, active, n_active, rcounter, dcounters, total;
+};
+DecodeLayout decode_layout(int T, int E, int topk, int H, int F) {
+    DecodeLayout L{};
+    // router K slices of 512 (128 when H is not a multiple of 512): many
+    // blocks stream the fp32 router weights, each stages T x kl activations
+    L.kl = H % 512 == 0 ? 512 : 128;
+    L.ksplit = H / L.kl;
+    L.rows = qwq4::moe_down_row_blocks(H, F);
+    auto r = [](size_t b) { return (b + 255) & ~size_t(255); };
+    size_t o = 0;
+    L.part = o;
+    o += r(size_t(L.ksplit) * T * E * 4);
+    L.counts = o;
+    o += r(size_t(E) * 4);
+    L.offsets = o;
+    o += r(size_t(E + 1) * 4);
+    L.pair_tok = o;
+    o += r(size_t(T) * topk * 4);
+    L.active = o;
+    o += r(size_t(E) * 4);
+    L.n_active = o;
+    o += 256;
+    L.rcounter = o;
+    o += r(size_t(1 + (E + 15) / 16) * 4);
+    L.dcounters = o;
+    o += r(size_t(L.rows) * 4);
+    L.total = o;
+    return L;
+}
+}  // namespace
+
+size_t qw_moe_decode_workspace_size(int T, int E, int topk, int H, int F) {
+    if (T < 1 || E < 1 || topk < 1 || H < 128 || F < 128) return 0;
+    return decode_layout(T, E, topk, H, F).total;
+}
+
+int qw_moe_decode(const float *router_w, const uint16_t *x, int T, int E, int topk, const uint32_t *gw,
+                  const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
+                  const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
+                  void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
+                  uint16_t *h, float *yp, void *workspace, size_t workspace_bytes, void *stream) {
+    if (int r = check_q4("qw_moe_decode(gate)", gw, gs, int64_t(E) * F, H)) return r;
+    if (int r = check_q4("qw_moe_decode(up)", uw, us, int64_t(E) * F, H)) return r;
+    if (int r = check_q4("qw_moe_decode(down)", dw, ds, int64_t(E) * H, F)) return r;
+    REQUIRE(router_w && x && out && logits && top_e && top_w && tok_slot && h && yp && workspace,
+            "qw_moe_decode: null pointer");
+    REQUIRE(T >= 1 && T <= 32, "qw_moe_decode: T = %d outside 1..32", T);
+    REQUIRE(E >= 1 && E <= 1024 && topk >= 1 && topk <= E && topk <= 64, "qw_moe_decode: E = %d, topk = %d", E, topk);
+    REQUIRE(qwq4::moe_gemv_supported(H, F), "qw_moe_decode: H = %d, F = %d too large", H, F);
+    REQUIRE(aligned(router_w, 16) && aligned(x, 16) && aligned(h, 16) && aligned(workspace, 256),
+            "qw_moe_decode: router_w, x, h must be 16-byte and workspace 256-byte aligned");
+    const DecodeLayout L = decode_layout(T, E, topk, H, F);
+    REQUIRE(workspace_bytes >= L.total, "qw_moe_decode: workspace needs %zu bytes", L.total);
+    unsigned char *w = static_cast<unsigned char *>(workspace);
+    auto at = [&](size_t off) { return reinterpret_cast<int32_t *>(w + off); };
+    qwq4::RouteArgs ra{logits, T, E, topk, 0, top_e, top_w, at(L.counts), at(L.offsets), tok_slot, at(L.pair_tok),
+                       at(L.active), at(L.n_active), nullptr, nullptr, nullptr};
+    qwq4::RouterArgs rr{router_w, x, H, L.kl, reinterpret_cast<float *>(w + L.part), logits, at(L.rcounter)};
+    qwq4::launch_router_route(ra, rr, st(stream));
+    const qwq4::CombineArgs cmb{at(L.dcounters), tok_slot, top_w, shared, out, out_bf16};
+    qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, at(L.offsets), at(L.active), at(L.n_active),
+                        at(L.pair_tok), x, T, topk, h, yp, &cmb};
+    qwq4::launch_moe_gemv(a, st(stream));
+    return launched("qw_moe_decode");
+}
+
 }  // extern "C"

@@ -97,13 +97,16 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     } while (m0 < M);
 }
 
-template <int KS, int GW, bool HAS_Z, bool CH4>
+// CMB: the last block of each row block (over the active experts, counted
+// on a device-scope counter) also forms the combined output of those rows
+// for every token, in the fixed selection order, then clears the counter.
+template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB>
 __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz,
                                                             const int32_t *__restrict__ offsets,
                                                             const int32_t *__restrict__ active,
                                                             const int32_t *__restrict__ n_active,
                                                             const uint16_t *__restrict__ h, int E, int H, int F, int R,
-                                                            float *__restrict__ yp) {
+                                                            float *__restrict__ yp, CombineArgs c, int T, int topk) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int e = block_expert(n_active, active, E);
     if (e < 0) return;
@@ -143,11 +146,27 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = 4 * q + r;
-                if (m < mc) yp[int64_t(base + m0 + m) * H + lsub * 16 + n] = acc[0][r];
+                if (m < mc) {
+                    float *dst = yp + int64_t(base + m0 + m) * H + lsub * 16 + n;
+                    if constexpr (CMB) st_agent(dst, acc[0][r]);
+                    else *dst = acc[0][r];
+                }
             }
         }
         m0 += R;
     } while (m0 < M);
+    if constexpr (CMB) {
+        if (!count_last_block(&c.counters[blockIdx.x], *n_active)) return;
+        const int r0 = blockIdx.x * SUB * 16, nr = min(SUB * 16, H - r0);
+        for (int i = tid; i < T * nr; i += blockDim.x) {
+            const int tk = i / nr, j = r0 + (i - tk * nr);
+            float v = c.shared ? c.shared[int64_t(tk) * H + j] : 0.f;
+            for (int q2 = 0; q2 < topk; ++q2)
+                v += c.tok_w[tk * topk + q2] * ld_agent(yp + int64_t(c.tok_slot[tk * topk + q2]) * H + j);
+            if (c.out_bf16) static_cast<uint16_t *>(c.out)[int64_t(tk) * H + j] = f32_to_bf16_rne(v);
+            else static_cast<float *>(c.out)[int64_t(tk) * H + j] = v;
+        }
+    }
 }
 
 // K split: the largest power of two <= kmax dividing G with at most 16 groups
@@ -169,14 +188,22 @@ static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStrea
                                 a.E, a.H, a.F, R, a.h);
 }
 
-template <int KS, int GW, bool HAS_Z, bool CH4>
-static void launch_down(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
-    auto kern = moe_down_gemv_kernel<KS, GW, HAS_Z, CH4>;
+template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB>
+static void launch_down_c(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
+    auto kern = moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB>;
     const size_t lds = moe_lds_bytes(R, a.F);
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
     constexpr int SUB = 8 / KS;
     const dim3 grid(unsigned((a.H / 16 + SUB - 1) / SUB), unsigned(max_active));
-    kern<<<grid, 512, lds, s>>>(a.dw, a.ds, a.dz, a.offsets, a.active, a.n_active, a.h, a.E, a.H, a.F, R, a.yp);
+    const CombineArgs c = a.cmb ? *a.cmb : CombineArgs{};
+    kern<<<grid, 512, lds, s>>>(a.dw, a.ds, a.dz, a.offsets, a.active, a.n_active, a.h, a.E, a.H, a.F, R, a.yp, c,
+                                a.T, a.topk);
+}
+
+template <int KS, int GW, bool HAS_Z, bool CH4>
+static void launch_down(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
+    if (a.cmb) launch_down_c<KS, GW, HAS_Z, CH4, true>(a, max_active, R, s);
+    else launch_down_c<KS, GW, HAS_Z, CH4, false>(a, max_active, R, s);
 }
 
 template <bool DOWN, int KS, int GW, bool HAS_Z, bool CH4>
@@ -212,6 +239,11 @@ static void launch_one(const MoeGemvArgs &a, int max_active, hipStream_t s) {
             if constexpr (DOWN) launch_gw<DOWN, 8, HAS_Z>(a, max_active, R, gpk, s);
             break;
     }
+}
+
+int moe_down_row_blocks(int H, int F) {
+    const int sub = 8 / pick_ks(F / QGROUP, 8);
+    return (H / 16 + sub - 1) / sub;
 }
 
 bool moe_gemv_supported(int H, int F) {

@@ -88,14 +88,14 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t x) {
 // they order like p) over the complement of the expert index, so one 64-bit
 // maximum picks the largest p and, among equal p, the lowest index. Lane
 // j < k ends with the j-th selection.
-template <int PER>
-__device__ __forceinline__ void topk_wave(const float *l, int E, int k, int lane, int32_t *te, float *tw) {
+template <int PER, class LogitFn>
+__device__ __forceinline__ void topk_wave(LogitFn logit, int E, int k, int lane, int32_t *te, float *tw) {
     float v[PER];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int idx = lane + WAVE * i;
-        v[i] = idx < E ? l[idx] : -INFINITY;
+        v[i] = idx < E ? logit(idx) : -INFINITY;
         mx = fmaxf(mx, v[i]);
     }
     mx = wave_max_f32(mx);
@@ -135,7 +135,8 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict
                                                          int32_t *__restrict__ top_e, float *__restrict__ top_w) {
     const int t = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     if (t >= T) return;
-    topk_wave<PER>(logits + int64_t(t) * E, E, k, lane, top_e + int64_t(t) * k, top_w + int64_t(t) * k);
+    const float *l = logits + int64_t(t) * E;
+    topk_wave<PER>([&](int i) { return l[i]; }, E, k, lane, top_e + int64_t(t) * k, top_w + int64_t(t) * k);
 }
 
 struct SlotLds {
@@ -268,8 +269,10 @@ __device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
 // Decode batches (T <= 64): selections and slots in one launch. A token
 // picks an expert at most once, so the tokens of expert e are the set bits of
 // one 64-bit mask; a pair's rank among them is a popcount below its bit.
-template <int PER>
-__global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
+// The whole routing of a decode batch by one block of 1024 threads; logit(t)
+// gives token t's row loader (expert index -> logit).
+template <int PER, class RowFn>
+__device__ __forceinline__ void route_small_body(const RouteArgs &a, RowFn logit_row) {
     __shared__ int32_t s_te[64 * 64];
     __shared__ unsigned long long s_mask[1024];
     __shared__ int32_t s_off[1024];
@@ -278,7 +281,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
     const int T = a.T, E = a.E, k = a.topk, P = T * k;
     if (tid < E) s_mask[tid] = 0ull;
     for (int t = wave; t < T; t += 16)
-        topk_wave<PER>(a.logits + int64_t(t) * E, E, k, lane, s_te + t * k, a.top_w + int64_t(t) * k);
+        topk_wave<PER>(logit_row(t), E, k, lane, s_te + t * k, a.top_w + int64_t(t) * k);
     __syncthreads();
     for (int i = tid; i < P; i += blockDim.x) {
         a.top_e[i] = s_te[i];
@@ -324,6 +327,120 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
         a.tok_slot[i] = slot;
         a.pair_tok[slot] = t;
     }
+}
+
+template <int PER>
+__global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
+    route_small_body<PER>(a, [&](int t) {
+        const float *l = a.logits + int64_t(t) * a.E;
+        return [l](int i) { return l[i]; };
+    });
+}
+
+// ---- router GEMV and routing of a decode batch in one launch
+// Block (g, ks) computes the fp32 logits of experts 16g .. 16g + 15 (one per
+// wave) over K slice ks for every token and writes them as partial sums. The
+// last block of group g to finish adds its slices into the logits; the last
+// group to finish routes. Counters (device scope) are cleared for the next
+// call by the blocks that count last.
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#define QW_FSUM_STEP(ctrl) v += __builtin_bit_cast(float, QW_DPP(__builtin_bit_cast(uint32_t, v), ctrl, 0xf, 0xf, false));
+    QW_FSUM_STEP(DPP_XOR1)
+    QW_FSUM_STEP(DPP_XOR2)
+    QW_FSUM_STEP(DPP_HALF_MIRROR)
+    QW_FSUM_STEP(DPP_MIRROR)
+#undef QW_FSUM_STEP
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+template <int PER>
+__global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterArgs r) {
+    extern __shared__ __align__(16) unsigned char smem[];  // x slice, [T][kl] bf16
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int T = a.T, E = a.E, H = r.H, kc = r.kl / 8, k0 = blockIdx.y * r.kl;
+    const int e = blockIdx.x * 16 + wave;
+    // kl <= 512: each lane owns at most one run of 8 weights of its expert's
+    // slice; they are requested before the activations are staged
+    const bool mine = e < E && lane < kc;
+    float4 w0 = {0.f, 0.f, 0.f, 0.f}, w1 = w0;
+    if (mine) {
+        const float *w = r.w + int64_t(e) * H + k0 + lane * 8;
+        w0 = *reinterpret_cast<const float4 *>(w);
+        w1 = *reinterpret_cast<const float4 *>(w + 4);
+    }
+    uint4 *xs = reinterpret_cast<uint4 *>(smem);
+    for (int i = tid; i < T * kc; i += blockDim.x) {
+        const int t = i / kc, c = i - t * kc;
+        xs[i] = *reinterpret_cast<const uint4 *>(r.x + int64_t(t) * H + k0 + c * 8);
+    }
+    __syncthreads();
+    if (e < E) {
+#pragma unroll
+        for (int t = 0; t < 64; ++t) {
+            if (t < T) {
+                float s = 0.f;
+                if (mine) {
+                    const uint4 v = xs[t * kc + lane];
+                    s = fmaf(w0.x, bf16_bits_to_f32(uint16_t(v.x)), s);
+                    s = fmaf(w0.y, bf16_bits_to_f32(uint16_t(v.x >> 16)), s);
+                    s = fmaf(w0.z, bf16_bits_to_f32(uint16_t(v.y)), s);
+                    s = fmaf(w0.w, bf16_bits_to_f32(uint16_t(v.y >> 16)), s);
+                    s = fmaf(w1.x, bf16_bits_to_f32(uint16_t(v.z)), s);
+                    s = fmaf(w1.y, bf16_bits_to_f32(uint16_t(v.z >> 16)), s);
+                    s = fmaf(w1.z, bf16_bits_to_f32(uint16_t(v.w)), s);
+                    s = fmaf(w1.w, bf16_bits_to_f32(uint16_t(v.w >> 16)), s);
+                }
+                const float v = wave_sum_f32(s);
+                if (lane == 0) st_agent(r.part + (int64_t(blockIdx.y) * T + t) * E + e, v);
+            }
+        }
+    }
+    // the last slice block of each group of 16 experts adds the group's
+    // slices in slice order (up to 8 loads in flight per logit)
+    if (!count_last_block(r.counter + 1 + blockIdx.x, int(gridDim.y))) return;
+    const int e0 = blockIdx.x * 16, ng = min(16, E - e0), ksplit = gridDim.y, TE = T * E;
+    for (int i = tid; i < T * ng; i += blockDim.x) {
+        const int t = i / ng, o = t * E + e0 + (i - t * ng);
+        float v = 0.f;
+        for (int j0 = 0; j0 < ksplit; j0 += 8) {
+            float pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pv[j] = j0 + j < ksplit ? ld_agent(r.part + int64_t(j0 + j) * TE + o) : 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v += pv[j];
+        }
+        st_agent(r.logits + o, v);
+    }
+    // and the last group to finish routes
+    if (!count_last_block(r.counter, int(gridDim.x))) return;
+    route_small_body<PER>(a, [&](int t) {
+        const float *l = r.logits + int64_t(t) * E;
+        return [l](int i) { return ld_agent(l + i); };
+    });
+}
+
+size_t router_lds_bytes(int T, int kl) { return size_t(T) * kl * 2; }
+
+void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s) {
+    // callers guarantee kl in {128, 512}, H % kl == 0 and T <= 64
+    const int per = (a.E + WAVE - 1) / WAVE;
+    const dim3 grid(unsigned((a.E + 15) / 16), unsigned(r.H / r.kl));
+    const size_t lds = router_lds_bytes(a.T, r.kl);
+    auto go = [&](auto kern) {
+        if (lds > 48 * 1024)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      int(lds));
+        kern<<<grid, 1024, lds, s>>>(a, r);
+    };
+    if (per <= 1) go(router_route_kernel<1>);
+    else if (per <= 2) go(router_route_kernel<2>);
+    else if (per <= 4) go(router_route_kernel<4>);
+    else if (per <= 8) go(router_route_kernel<8>);
+    else go(router_route_kernel<16>);
 }
 
 __global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a) {

@@ -128,4 +128,34 @@ struct Q4Tile {
     __device__ __forceinline__ static uint32_t zero_of(uint32_t word, int g) { return (word >> (4 * (g & 3))) & 0xfu; }
 };
 
+// Hand-off between the blocks of one launch ("the last block to finish a
+// range also reduces it"). Each XCD has its own L2, so an agent-scope fence
+// writes back or invalidates the whole L2 of the executing XCD; done by
+// thousands of producer blocks that costs more than the kernel itself.
+// Instead only the handed-off values are coherent at agent scope: producers
+// store them as agent-scope atomics (written through the XCD's L2), wait for
+// those stores to complete, and then count the block on an agent-scope atomic
+// counter; the block that counts last reads the values with agent-scope
+// atomic loads (served past its L2).
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Counts the calling block on *counter; true in every thread of the block
+// that counted total-th. Every thread's earlier st_agent stores are complete
+// before the count. The last block resets the counter to zero.
+__device__ __forceinline__ bool count_last_block(int *counter, int total) {
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores acknowledged
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+        if (s_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return s_last;
+}
+
 }  // namespace qwq4

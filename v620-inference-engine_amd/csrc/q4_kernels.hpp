@@ -28,6 +28,19 @@ struct GemvArgs {
 };
 void launch_gemv(const GemvArgs &a, hipStream_t s);
 
+// Weighted combine folded into the down projection (see launch_moe_gemv):
+// out[t][j] = shared[t][j] + sum_i tok_w[t][i] * yp[tok_slot[t][i]][j].
+struct CombineArgs {
+    int32_t *counters;  // one per down row block, zero between calls
+    const int32_t *tok_slot;
+    const float *tok_w;
+    const float *shared;  // fp32 [T][H] or null
+    void *out;
+    int out_bf16;
+};
+// Down row blocks of the decode experts for H (the counters combine needs).
+int moe_down_row_blocks(int H, int F);
+
 struct MoeGemvArgs {
     const uint32_t *gw;
     const uint16_t *gs;
@@ -44,6 +57,7 @@ struct MoeGemvArgs {
     int T, topk;
     uint16_t *h;
     float *yp;
+    const CombineArgs *cmb;  // null: yp only
 };
 void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s);
 // Whether the expert GEMVs take these sizes (a wave holds <= 16 groups of its K range).
@@ -80,6 +94,17 @@ struct RouteArgs {
     int32_t *counts, *offsets, *tok_slot, *pair_tok, *active, *n_active;
     int32_t *tile_e, *tile_m0, *n_tiles;
 };
+// fp32 router GEMV fused with the decode routing (T <= 64).
+struct RouterArgs {
+    const float *w;     // [E][H]
+    const uint16_t *x;  // bf16 [T][H]
+    int H, kl;          // K slice per block (a multiple of 8 dividing H)
+    float *part;        // [H / kl][T][E] partial logits
+    float *logits;      // [T][E]
+    int32_t *counter;   // [1 + ceil(E / 16)], zero between calls
+};
+size_t router_lds_bytes(int T, int kl);
+void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
 // LDS bytes the slot pass needs for (T, E); the C-ABI rejects larger inputs.
 size_t route_lds_bytes(int T, int E);
 void launch_route(const RouteArgs &a, hipStream_t s);

@@ -19,6 +19,7 @@ SYMBOLS = (
     "qw_q4_tiled_size", "qw_q4_tile", "qw_q4_untile", "qw_bf16_to_f16",
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
+    "qw_moe_decode_workspace_size", "qw_moe_decode",
 )
 
 _P = ctypes.c_void_p
@@ -45,6 +46,8 @@ _SIGS = {
     "qw_q4_dequant": ([_P, _P, _P, _I64, _I64, _P, _P], _I),
     "qw_q4_from_engine_order": ([_P, _P, _I64, _P], _I),
     "qw_bf16_to_f16": ([_P, _P, _I64, _P], _I),
+    "qw_moe_decode_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
+    "qw_moe_decode": ([_P, _P, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
     "qw_st_close": ([_P], None),
     "qw_st_count": ([_P], _I),
@@ -273,6 +276,39 @@ def from_engine_order(words):
     out = torch.empty_like(words)
     _check(lib().qw_q4_from_engine_order(_ptr(words), _ptr(out), words.numel(), _stream()), "qw_q4_from_engine_order")
     return out
+
+
+class MoeDecode:
+    """Buffers of the fused decode block (qw_moe_decode) for T tokens."""
+
+    def __init__(self, T, E, topk, H, F, device):
+        import torch
+        i32 = dict(dtype=torch.int32, device=device)
+        self.T, self.E, self.topk, self.H, self.F = T, E, topk, H, F
+        self.logits = torch.empty((T, E), dtype=torch.float32, device=device)
+        self.top_e = torch.empty((T, topk), **i32)
+        self.top_w = torch.empty((T, topk), dtype=torch.float32, device=device)
+        self.tok_slot = torch.empty((T, topk), **i32)
+        self.h = torch.empty((T * topk, F), dtype=torch.float16, device=device)
+        self.yp = torch.empty((T * topk, H), dtype=torch.float32, device=device)
+        # zero once: holds completion counters every call leaves at zero
+        self.ws = torch.zeros(lib().qw_moe_decode_workspace_size(T, E, topk, H, F), dtype=torch.uint8, device=device)
+
+
+def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, out=None, out_bf16=True):
+    """Router GEMV + routing + experts + combine for a decode batch (3 launches)."""
+    import torch
+    T, H = x.shape
+    buf = buf if buf is not None else MoeDecode(T, E, topk, H, F, x.device)
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=x.device)
+    _dev(router_w, x, shared, out, *gate, *up, *down)
+    rc = lib().qw_moe_decode(_ptr(router_w), _ptr(x), T, E, topk, *map(_ptr, gate), *map(_ptr, up), *map(_ptr, down),
+                             H, F, _ptr(shared), _ptr(out), int(out_bf16), _ptr(buf.logits), _ptr(buf.top_e),
+                             _ptr(buf.top_w), _ptr(buf.tok_slot), _ptr(buf.h), _ptr(buf.yp), _ptr(buf.ws),
+                             buf.ws.numel(), _stream())
+    _check(rc, "qw_moe_decode")
+    return out, buf
 
 
 # -------------------------------------------------------- checkpoint loading
