@@ -205,6 +205,27 @@ int qw_q4_load(const qw_st_file *f, const char *prefix, int64_t N, int64_t K, ui
  * columns: expert e of a stacked [E*F][K] matrix starts at row e*F. */
 void qw_q4_tiled_offset(int64_t row0, int64_t K, size_t *wt_off, size_t *st_off, size_t *zt_off);
 
+/* ---- Converted-weights cache (role of the reference's WeightCache,
+ * src/engine/weights.hip:26-164): the buffers a load fills, in order, kept in
+ * one file; the next load with the same key uploads them instead of reading
+ * and converting the checkpoint. `key` identifies the checkpoint (the caller
+ * hashes its files, sizes and conversion options); the library adds its own
+ * tiled-layout version. qw_wcache_open never fails on a missing, stale or
+ * damaged file: *mode = 2 (replaying) when `path` is a complete cache with this
+ * key, else 1 (recording into "<path>.tmp", renamed by qw_wcache_finish), or
+ * 0 (off; qw_q4_last_error says why). put/get copy synchronously on `stream`
+ * (load time only, not capture-safe); src/dst are device memory when
+ * on_device, else host memory. put is a no-op unless recording; get fails
+ * (EINVAL) unless replaying a piece of exactly `bytes` bytes. */
+typedef struct qw_wcache qw_wcache;
+int qw_wcache_open(const char *path, uint64_t key, qw_wcache **out, int *mode);
+int qw_wcache_put(qw_wcache *c, const void *src, size_t bytes, int on_device, void *stream);
+int qw_wcache_get(qw_wcache *c, void *dst, size_t bytes, int on_device, void *stream);
+/* Recording: completes and renames the file. Replaying: fails unless every
+ * piece was read. */
+int qw_wcache_finish(qw_wcache *c);
+void qw_wcache_close(qw_wcache *c);
+
 #ifdef __cplusplus
 }
 #endif

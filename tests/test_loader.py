@@ -111,3 +111,113 @@ def test_bf16_to_f16_device_matches_reference(gpu, oracle):
                     (np.arange(65536, dtype=np.uint32).astype(np.uint16), None)):
         got = host(qwq4.bf16_to_f16(to_dev(b, gpu))).view(np.uint16)
         assert np.array_equal(got, oracle.bf16_to_f16(b) if want is None else want)
+
+
+def _pieces():
+    import torch
+    g = torch.Generator().manual_seed(7)
+    return [torch.randint(0, 256, (n,), dtype=torch.uint8, generator=g) for n in (100, 64, 0, 4097)]
+
+
+def test_weight_cache_record_then_replay(tmp_path, lib):
+    import torch
+    p = str(tmp_path / "w.qwc")
+    ps = _pieces()
+    with qwq4.WCache(p, 1234) as c:
+        assert c.mode == "record"
+        for t in ps:
+            c.put(t)
+        assert not os.path.exists(p)       # only the .tmp until finished
+        c.finish()
+    assert os.path.exists(p) and not os.path.exists(p + ".tmp")
+    with qwq4.WCache(p, 1234) as c:
+        assert c.mode == "replay"
+        for t in ps:
+            got = torch.empty_like(t)
+            c.get(got)
+            assert torch.equal(got, t)
+        c.finish()
+
+
+def test_weight_cache_rejects_stale_and_damaged_files(tmp_path, lib):
+    import torch
+    p = str(tmp_path / "w.qwc")
+    ps = _pieces()
+    with qwq4.WCache(p, 5) as c:
+        for t in ps:
+            c.put(t)
+        c.finish()
+    good = open(p, "rb").read()
+    # another key records afresh (and leaves the old file until finished)
+    with qwq4.WCache(p, 6) as c:
+        assert c.mode == "record"
+    assert open(p, "rb").read() == good    # not finished: nothing replaced
+    # truncated, or a count that does not match: recorded afresh
+    for bad in (good[:-8], good[:-1], good[:200], good[:-8] + (99).to_bytes(8, "little")):
+        open(p, "wb").write(bad)
+        with qwq4.WCache(p, 5) as c:
+            assert c.mode == "record"
+    # replaying: a piece of another size, too many pieces, pieces left over
+    open(p, "wb").write(good)
+    with qwq4.WCache(p, 5) as c:
+        with pytest.raises(RuntimeError, match="expected"):
+            c.get(torch.empty(101, dtype=torch.uint8))
+    with qwq4.WCache(p, 5) as c:
+        c.get(torch.empty(100, dtype=torch.uint8))
+        with pytest.raises(RuntimeError, match="left unused"):
+            c.finish()
+    with qwq4.WCache(p, 5) as c:
+        for t in ps:
+            c.get(torch.empty_like(t))
+        with pytest.raises(RuntimeError, match="more pieces"):
+            c.get(torch.empty(1, dtype=torch.uint8))
+
+
+def test_weight_cache_off_when_unwritable(tmp_path, lib):
+    import torch
+    c = qwq4.WCache(str(tmp_path / "absent_dir" / "w.qwc"), 1)
+    assert c.mode == "off" and "cannot write" in c.why
+    c.put(torch.zeros(3, dtype=torch.uint8))   # a no-op
+    with pytest.raises(RuntimeError, match="not replaying"):
+        c.get(torch.zeros(3, dtype=torch.uint8))
+    c.finish()
+    c.close()
+
+
+def test_checkpoint_key_tracks_files(tmp_path):
+    a = tmp_path / "a.safetensors"
+    a.write_bytes(b"x" * 10)
+    k1 = qwq4.checkpoint_key([a])
+    assert k1 == qwq4.checkpoint_key([a]) and k1 != qwq4.checkpoint_key([a], "opt")
+    a.write_bytes(b"x" * 11)
+    assert qwq4.checkpoint_key([a]) != k1
+
+
+@pytest.mark.gpu
+def test_load_through_weight_cache(tmp_path, gpu):
+    import torch
+    E, N, K = 2, 32, 256
+    p = str(tmp_path / "experts.safetensors")
+    t = {}
+    for e in range(E):
+        t.update(_q4_tensors(20 + e, f"e.{e}.up_proj", N, K))
+    _write(p, t)
+    wb, sb, _ = qwq4.tiled_size(E * N, K)
+
+    def load(cache, st):
+        Wt = torch.zeros(wb // 4, dtype=torch.int32, device=gpu)
+        St = torch.zeros(sb // 2, dtype=torch.int16, device=gpu)
+        for e in range(E):
+            qwq4.load_q4(st, f"e.{e}.up_proj", N, K, out=(Wt, St, None), row0=e * N, cache=cache)
+        cache.finish()
+        return Wt, St
+
+    cp = str(tmp_path / "c.qwc")
+    key = qwq4.checkpoint_key([p])
+    with qwq4.StFile(p) as f, qwq4.WCache(cp, key) as c:
+        assert c.mode == "record"
+        W1, S1 = load(c, f)
+    with qwq4.WCache(cp, key) as c:
+        assert c.mode == "replay"
+        W2, S2 = load(c, None)     # no checkpoint read at all
+    assert torch.equal(W1, W2) and torch.equal(S1, S2)

@@ -4,12 +4,19 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 #include <string>
 #include <vector>
 
 #include "q4_kernels.hpp"
 #include "qw/q4ops.h"
 #include "st_loader.hpp"
+#include "wcache.hpp"
+
+struct qw_wcache {
+    qwq4::WCache c;
+    std::vector<unsigned char> host;  // staging of device pieces being recorded
+};
 
 struct qw_st_file {
     qwq4::StFile f;
@@ -405,3 +412,65 @@ int qw_moe_decode(const float *router_w, const uint16_t *x, int T, int E, int to
 }
 
 }  // extern "C"
+
+// ---- converted-weights cache
+int qw_wcache_open(const char *path, uint64_t key, qw_wcache **out, int *mode) {
+    REQUIRE(path && out, "qw_wcache_open: null argument");
+    *out = nullptr;
+    auto *c = new qw_wcache;
+    std::string err;
+    c->c.open(path, key, err);
+    *out = c;
+    if (mode) *mode = int(c->c.mode());
+    g_err = err;  // why the cache is off, when it is
+    return QW_Q4_OK;
+}
+
+void qw_wcache_close(qw_wcache *c) { delete c; }
+
+int qw_wcache_put(qw_wcache *c, const void *src, size_t bytes, int on_device, void *stream) {
+    REQUIRE(c && (src || bytes == 0), "qw_wcache_put: null argument");
+    if (c->c.mode() != qwq4::WCache::RECORD) return QW_Q4_OK;
+    const void *h = src;
+    if (on_device && bytes) {
+        c->host.resize(bytes);
+        hipError_t e = hipMemcpyAsync(c->host.data(), src, bytes, hipMemcpyDeviceToHost, st(stream));
+        if (e == hipSuccess) e = hipStreamSynchronize(st(stream));
+        if (e != hipSuccess) {
+            g_err = std::string("qw_wcache_put: ") + hipGetErrorString(e);
+            return QW_Q4_ELAUNCH;
+        }
+        h = c->host.data();
+    }
+    std::string err;
+    if (!c->c.put(h, bytes, err)) g_err = err;  // the recording is dropped; the load goes on
+    return QW_Q4_OK;
+}
+
+int qw_wcache_get(qw_wcache *c, void *dst, size_t bytes, int on_device, void *stream) {
+    REQUIRE(c && (dst || bytes == 0), "qw_wcache_get: null argument");
+    std::string err;
+    const void *src = c->c.next(bytes, err);
+    REQUIRE(src, "qw_wcache_get: %s", err.c_str());
+    if (!bytes) return QW_Q4_OK;
+    if (!on_device) {
+        std::memcpy(dst, src, bytes);
+        return QW_Q4_OK;
+    }
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(st(stream));
+    if (e != hipSuccess) {
+        g_err = std::string("qw_wcache_get: ") + hipGetErrorString(e);
+        return QW_Q4_ELAUNCH;
+    }
+    g_err.clear();
+    return QW_Q4_OK;
+}
+
+int qw_wcache_finish(qw_wcache *c) {
+    REQUIRE(c, "qw_wcache_finish: null argument");
+    std::string err;
+    REQUIRE(c->c.finish(err), "qw_wcache_finish: %s", err.c_str());
+    g_err.clear();
+    return QW_Q4_OK;
+}

@@ -20,6 +20,7 @@ SYMBOLS = (
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
     "qw_moe_decode_workspace_size", "qw_moe_decode",
+    "qw_wcache_open", "qw_wcache_put", "qw_wcache_get", "qw_wcache_finish", "qw_wcache_close",
 )
 
 _P = ctypes.c_void_p
@@ -50,6 +51,11 @@ _SIGS = {
     "qw_moe_decode": ([_P, _P, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
     "qw_st_close": ([_P], None),
+    "qw_wcache_open": ([ctypes.c_char_p, ctypes.c_uint64, _P, _P], _I),
+    "qw_wcache_put": ([_P, _P, ctypes.c_size_t, _I, _P], _I),
+    "qw_wcache_get": ([_P, _P, ctypes.c_size_t, _I, _P], _I),
+    "qw_wcache_finish": ([_P], _I),
+    "qw_wcache_close": ([_P], None),
     "qw_st_count": ([_P], _I),
     "qw_st_name": ([_P, _I], ctypes.c_char_p),
     "qw_st_tensor": ([_P, ctypes.c_char_p, _P, _P, _P, _P, _P], _I),
@@ -366,10 +372,12 @@ def tiled_offset(row0, K):
     return a.value, b.value, c.value
 
 
-def load_q4(st, prefix, N, K, out=None, row0=0, device=None):
+def load_q4(st, prefix, N, K, out=None, row0=0, device=None, cache=None):
     """Loads "<prefix>.weight_packed/.weight_scale" of an StFile into tiled
     device tensors (Wt, St, None). With out=(Wt, St, Zt) of a larger tiled
-    matrix, writes rows row0 .. row0 + N - 1 of it (stacked experts)."""
+    matrix, writes rows row0 .. row0 + N - 1 of it (stacked experts).
+    With a WCache: replaying, the rows come from the cache (st may be None);
+    recording, they are converted and appended to it."""
     import torch
     device = device or torch.device("cuda", torch.cuda.current_device())
     if out is None:
@@ -377,11 +385,91 @@ def load_q4(st, prefix, N, K, out=None, row0=0, device=None):
         out = (torch.empty(wb // 4, dtype=torch.int32, device=device),
                torch.empty(sb // 2, dtype=torch.int16, device=device), None)
     Wt, St_ = out[0], out[1]
+    _dev(Wt, St_)
     ow, os_, _ = tiled_offset(row0, K)
+    nw, ns, _ = tiled_size(N, K)
+    if ow + nw > Wt.numel() * Wt.element_size() or os_ + ns > St_.numel() * St_.element_size():
+        raise ValueError("load_q4: rows beyond the output tensors")
+    wp, sp = Wt.data_ptr() + ow, St_.data_ptr() + os_
+    if cache is not None and cache.mode == "replay":
+        cache.get_ptr(wp, nw)
+        cache.get_ptr(sp, ns)
+        return out
     staging = torch.empty(lib().qw_q4_load_staging_size(N, K), dtype=torch.uint8, device=Wt.device)
-    _dev(Wt, St_, staging)
-    rc = lib().qw_q4_load(st._h, prefix.encode(), N, K, ctypes.c_void_p(Wt.data_ptr() + ow),
-                          ctypes.c_void_p(St_.data_ptr() + os_), _ptr(staging), staging.numel(), _stream())
+    rc = lib().qw_q4_load(st._h, prefix.encode(), N, K, ctypes.c_void_p(wp), ctypes.c_void_p(sp), _ptr(staging),
+                          staging.numel(), _stream())
     _check(rc, "qw_q4_load")
     torch.cuda.current_stream().synchronize()  # staging is freed on return
+    if cache is not None:
+        cache.put_ptr(wp, nw)
+        cache.put_ptr(sp, ns)
     return out
+
+
+def checkpoint_key(paths, options=""):
+    """A 64-bit cache key for a checkpoint: names, sizes and modification
+    times of its files plus the caller's conversion options."""
+    import hashlib
+    h = hashlib.blake2b(digest_size=8)
+    for p in sorted(os.fspath(x) for x in paths):
+        st = os.stat(p)
+        h.update(f"{os.path.basename(p)}\0{st.st_size}\0{st.st_mtime_ns}\0".encode())
+    h.update(options.encode())
+    return int.from_bytes(h.digest(), "little")
+
+
+class WCache:
+    """Converted-weights cache file (qw_wcache_*). mode is "replay" when the
+    file is a complete cache for `key`, "record" while writing it (completed
+    by finish()), or "off" (reason in `why`)."""
+
+    _MODES = {0: "off", 1: "record", 2: "replay"}
+
+    def __init__(self, path, key):
+        h, m = ctypes.c_void_p(), ctypes.c_int()
+        _check(lib().qw_wcache_open(os.fsencode(path), ctypes.c_uint64(key), ctypes.byref(h), ctypes.byref(m)),
+               "qw_wcache_open")
+        self._h, self.mode = h, self._MODES[m.value]
+        self.why = lib().qw_q4_last_error().decode() if self.mode == "off" else ""
+
+    def put_ptr(self, ptr, nbytes, on_device=True):
+        _check(lib().qw_wcache_put(self._h, ctypes.c_void_p(ptr), nbytes, int(on_device),
+                                   _stream() if on_device else None), "qw_wcache_put")
+
+    def get_ptr(self, ptr, nbytes, on_device=True):
+        _check(lib().qw_wcache_get(self._h, ctypes.c_void_p(ptr), nbytes, int(on_device),
+                                   _stream() if on_device else None), "qw_wcache_get")
+
+    def put(self, t):
+        """Appends a contiguous tensor (device or host) while recording."""
+        if not t.is_contiguous():
+            raise ValueError("WCache.put: tensor must be contiguous")
+        self.put_ptr(t.data_ptr(), t.numel() * t.element_size(), t.is_cuda)
+
+    def get(self, t):
+        """Fills a contiguous tensor (device or host) with the next piece."""
+        if not t.is_contiguous():
+            raise ValueError("WCache.get: tensor must be contiguous")
+        self.get_ptr(t.data_ptr(), t.numel() * t.element_size(), t.is_cuda)
+
+    def finish(self):
+        _check(lib().qw_wcache_finish(self._h), "qw_wcache_finish")
+        if self.mode == "record":
+            self.mode = "off"
+
+    def close(self):
+        if self._h:
+            lib().qw_wcache_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
