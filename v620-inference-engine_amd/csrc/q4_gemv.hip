@@ -33,6 +33,7 @@ constexpr int DENSE_GW = 4;
 // partial sums: one slot per wave that is not a k-part 0, double-buffered
 __host__ __device__ inline int red_slots(int waves, int KS) { return waves - waves / KS; }
 
+// LDS: staged rows, then the partial-sum slots
 __host__ __device__ inline size_t dense_lds_bytes(int M, int K, int MB, int waves, int KS) {
     return size_t(x_pieces(M, K)) * 16 + size_t(2) * red_slots(waves, KS) * MB * WAVE * 16;
 }
@@ -86,38 +87,59 @@ __device__ __forceinline__ void ksplit_sum(f32x4 (&acc)[MB], f32x4 *rb, int KS, 
     }
 }
 
-template <int NW, int MB, bool HAS_Z, bool CH4, bool PF, bool KSNW>
+template <int NW, int MB, bool HAS_Z, bool CH4, bool PF, bool KSNW, int XPT, bool P4>
 __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt,
-                                                             const uint16_t *__restrict__ x, int xs,
+                                                             const uint16_t *x, int xs,
                                                              void *__restrict__ y, int ys, int y_bf16, int N, int K,
                                                              int M, int accumulate, int KS_, int SUB_) {
-    // KSNW: one subtile per item, split over all NW waves (compile-time)
+    // KSNW: one subtile per item, split over all NW waves, each wave exactly
+    // GW groups (all compile-time)
     const int KS = KSNW ? NW : KS_, SUB = KSNW ? 1 : SUB_;
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int GW = DENSE_GW;
-    const int G = K / QGROUP, kc = x_row_stride(K), nsub = N / 16, gpk = G / KS, items = (nsub + SUB - 1) / SUB;
+    const int G = KSNW ? NW * GW : K / QGROUP, kc = x_row_stride(K), nsub = N / 16, gpk = KSNW ? GW : G / KS,
+              items = (nsub + SUB - 1) / SUB;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE,
               q = lane / 16, n = lane % 16, waves = KSNW ? NW : int(blockDim.x) / WAVE;
     const int sl = wave / KS, kp = wave % KS, g0 = kp * gpk;
     auto tile_of = [&](int item) { return Q4Tile(Wt, St, Zt, min(item * SUB + sl, nsub - 1), G); };
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
     f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(M, K));
-    stage_x_issue(x, xs, M, K, xl);
+    // XPT > 0 (one piece per thread): activations through registers, so that
+    // each weight group is computed as it arrives; else direct into LDS
+    // (the compiler then drains every load in flight before the first LDS
+    // read)
+    uint4 xv[XPT > 0 ? XPT : 1];
+    if constexpr (XPT > 0) stage_regs_issue<XPT>(x, xs, M, K, xv);
+    else stage_x_issue(x, xs, M, K, xl);
+    asm volatile("" ::: "memory");  // every activation load goes out before the weight loads
     WaveRange<GW, HAS_Z, CH4> wr[1];
     wr[0].fetch(tile_of(blockIdx.x), g0, min(gpk, GW), lane);
-    __syncthreads();
+    if constexpr (XPT > 0) {
+        stage_regs_commit<XPT>(xv, M, K, xl);
+        lds_barrier();
+    } else {
+        __syncthreads();
+    }
     const uint4 *xr[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) xr[mb] = xl + min(mb * 16 + n, M - 1) * kc + q * 4;
+    // the lane's fragment of the packed correction tile (P4): token n % 4
+    // of group gb + n / 4
+    auto xp_of = [&](int gb) { return xl + min(n & 3, M - 1) * kc + min(gb + (n >> 2), G - 1) * 16 + q * 4; };
+    f32x4 pc[GW][MB];
+    group_bias<BF16, MB, GW, P4>(xr, xp_of(g0), g0, min(gpk, GW), pc);
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (!PF) {
         f32x4 acc[1][MB];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[0][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        compute_shared_x<BF16, MB, 1>(wr, xr, acc);
+        compute_pc<BF16, MB, 1>(wr, xr, pc, acc);
         // longer ranges: further passes of GW groups
         for (int p = GW; p < gpk; p += GW) {
             wr[0].fetch(tile_of(blockIdx.x), g0 + p, min(gpk - p, GW), opaque_lane());
-            compute_shared_x<BF16, MB, 1>(wr, xr, acc);
+            group_bias<BF16, MB, GW, P4>(xr, xp_of(g0 + p), g0 + p, min(gpk - p, GW), pc);
+            compute_pc<BF16, MB, 1>(wr, xr, pc, acc);
         }
         ksplit_sum<MB>(acc[0], red, KS, wave, kp, lane);
         const int sub = blockIdx.x * SUB + sl;
@@ -131,7 +153,7 @@ __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t
             f32x4 acc[1][MB];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) acc[0][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            compute_shared_x<BF16, MB, 1>(wr, xr, acc);
+            compute_pc<BF16, MB, 1>(wr, xr, pc, acc);  // the corrections of the block's groups serve every item
             // partials double-buffered by item parity: the barrier of item
             // i + 1 orders item i's reads before item i + 2's writes
             ksplit_sum<MB>(acc[0], red + par * (red_slots(waves, KS) * MB * WAVE), KS, wave, kp, lane);
@@ -164,19 +186,41 @@ static void dense_split(int G, int &KS, int &SUB, int &NW) {
     SUB = NW / KS;
 }
 
-template <int NW, int MB, bool HAS_Z, bool CH4, bool KSNW>
+// Blocks of one item each (items beyond the resident blocks run in further
+// rounds). XPT: pieces of activations per thread through registers, 0 for
+// direct loads into LDS.
+template <int NW, int MB, bool HAS_Z, bool CH4, bool KSNW, bool P4, int XPT>
+static void launch_dense_one(const GemvArgs &a, int KS, int SUB, int items, size_t lds, hipStream_t s) {
+    auto kern = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, false, KSNW, XPT, P4>;
+    const int threads = KS * SUB * WAVE;
+    if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), threads, lds);  // LDS limit
+    kern<<<items, threads, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.y, a.ys, a.y_bf16, a.N, a.K, a.M, a.accumulate, KS,
+                                     SUB);
+}
+
+// Small batches (at most one activation piece per thread) stage through
+// registers and run one item per block. Larger ones stage directly into LDS;
+// when their items exceed one round of resident blocks, the blocks stay
+// resident and prefetch their next item (PF). P4: batches of at most 4 rows
+// (packed group corrections).
+template <int NW, int MB, bool HAS_Z, bool CH4, bool KSNW, bool P4>
 static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
     const int waves = KS * SUB, threads = waves * WAVE, gpk = a.K / QGROUP / KS;
-    const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
     const int nsub = a.N / 16, items = (nsub + SUB - 1) / SUB;
-    auto one = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, false, KSNW>;
-    const LaunchShape ls = persistent_shape(reinterpret_cast<const void *>(one), threads, lds);
-    if (items <= ls.max_blocks || gpk > DENSE_GW) {
-        one<<<items, threads, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.y, a.ys, a.y_bf16, a.N, a.K, a.M, a.accumulate,
-                                        KS, SUB);
+    const int xpt = (a.M * (a.K / 8) + threads - 1) / threads;
+    if (MB == 1 && xpt <= 1) {
+        const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
+        launch_dense_one<NW, MB, HAS_Z, CH4, KSNW, P4, 1>(a, KS, SUB, items, lds, s);
         return;
     }
-    auto pf = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, true, KSNW>;
+    const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
+    auto one = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, false, KSNW, 0, P4>;
+    const LaunchShape ls = persistent_shape(reinterpret_cast<const void *>(one), threads, lds);
+    if (items <= ls.max_blocks || gpk > DENSE_GW) {
+        launch_dense_one<NW, MB, HAS_Z, CH4, KSNW, P4, 0>(a, KS, SUB, items, lds, s);
+        return;
+    }
+    auto pf = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, true, KSNW, 0, P4>;
     const LaunchShape lp = persistent_shape(reinterpret_cast<const void *>(pf), threads, lds);
     // every CU gets the same number of items: blocks per CU = the largest
     // divisor of the per-CU item count that stays resident
@@ -192,17 +236,18 @@ static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
                                     SUB);
 }
 
-template <int MB, bool HAS_Z, bool CH4>
+template <int MB, bool HAS_Z, bool CH4, bool P4>
 static void launch_dense_nw(const GemvArgs &a, int KS, int SUB, int NW, hipStream_t s) {
+    const bool fit = KS == NW && a.K / QGROUP == NW * DENSE_GW;
     if (NW == 8) {
-        if (KS == 8) launch_dense_t<8, MB, HAS_Z, CH4, true>(a, KS, SUB, s);
-        else launch_dense_t<8, MB, HAS_Z, CH4, false>(a, KS, SUB, s);
+        if (fit) launch_dense_t<8, MB, HAS_Z, CH4, true, P4>(a, KS, SUB, s);
+        else launch_dense_t<8, MB, HAS_Z, CH4, false, P4>(a, KS, SUB, s);
     } else if (NW == 12) {
-        if (KS == 12) launch_dense_t<12, MB, HAS_Z, CH4, true>(a, KS, SUB, s);
-        else launch_dense_t<12, MB, HAS_Z, CH4, false>(a, KS, SUB, s);
+        if (fit) launch_dense_t<12, MB, HAS_Z, CH4, true, P4>(a, KS, SUB, s);
+        else launch_dense_t<12, MB, HAS_Z, CH4, false, P4>(a, KS, SUB, s);
     } else {
-        if (KS == 16) launch_dense_t<16, MB, HAS_Z, CH4, true>(a, KS, SUB, s);
-        else launch_dense_t<16, MB, HAS_Z, CH4, false>(a, KS, SUB, s);
+        if (fit) launch_dense_t<16, MB, HAS_Z, CH4, true, P4>(a, KS, SUB, s);
+        else launch_dense_t<16, MB, HAS_Z, CH4, false, P4>(a, KS, SUB, s);
     }
 }
 
@@ -210,8 +255,14 @@ template <int MB, bool HAS_Z>
 static void launch_dense(const GemvArgs &a, hipStream_t s) {
     int KS, SUB, NW;
     dense_split(a.K / QGROUP, KS, SUB, NW);
-    if ((a.K / QGROUP / KS) % 4 == 0) launch_dense_nw<MB, HAS_Z, true>(a, KS, SUB, NW, s);
-    else launch_dense_nw<MB, HAS_Z, false>(a, KS, SUB, NW, s);
+    const bool ch4 = (a.K / QGROUP / KS) % 4 == 0, p4 = MB == 1 && a.M <= 4;
+    if (ch4) {
+        if (p4) launch_dense_nw<MB, HAS_Z, true, MB == 1>(a, KS, SUB, NW, s);
+        else launch_dense_nw<MB, HAS_Z, true, false>(a, KS, SUB, NW, s);
+    } else {
+        if (p4) launch_dense_nw<MB, HAS_Z, false, MB == 1>(a, KS, SUB, NW, s);
+        else launch_dense_nw<MB, HAS_Z, false, false>(a, KS, SUB, NW, s);
+    }
 }
 
 bool gemv_fits(int M, int K) {

@@ -112,8 +112,8 @@ struct WaveRange {
         g0 = g0_;
         n = n_;
         const int r = lane % 16;
-#pragma unroll
-        for (int c = 0; c < GW; ++c) w[c] = t.word4(g0 + min(c, n - 1), lane);
+        // scales and zeros first: group c's compute then waits only for the
+        // words up to c (loads complete in order), not for the whole range
         if constexpr (CH4) {
             static_assert(GW % 4 == 0, "whole chunks");
 #pragma unroll
@@ -138,6 +138,8 @@ struct WaveRange {
                 if constexpr (HAS_Z) zv[c] = t.zero_word(g, r);
             }
         }
+#pragma unroll
+        for (int c = 0; c < GW; ++c) w[c] = t.word4(g0 + min(c, n - 1), lane);
     }
     template <typename T, int MB>
     __device__ __forceinline__ void compute(const uint4 *const (&xr)[MB], f32x4 (&acc)[MB]) const {
@@ -152,28 +154,94 @@ struct WaveRange {
     }
 };
 
-// NS subtiles over the same groups (wr[j] fetched with equal g0 and n): the
-// activation fragments and the -BIAS * sum(x) correction of each group are
-// read and formed once for all of them.
-template <typename T, int MB, int NS, int GW, bool HAS_Z, bool CH4>
-__device__ __forceinline__ void compute_shared_x(const WaveRange<GW, HAS_Z, CH4> (&wr)[NS], const uint4 *const (&xr)[MB],
-                                                 f32x4 (&acc)[NS][MB]) {
+// Activation rows through registers: thread t takes pieces t, t + nt, ...
+// of the M x K/8 pieces (XPT >= M * K / 8 / blockDim.x). Issued before the
+// weight loads; unlike direct-to-LDS loads (after which the compiler drains
+// every load in flight before the first LDS read), the compiler then waits
+// for exactly these, so each weight group is computed as soon as it arrives.
+template <int XPT>
+__device__ __forceinline__ void stage_regs_issue(const uint16_t *x, int xs, int M, int K, uint4 (&xv)[XPT]) {
+    const int kn = K / 8, P = M * kn, nt = blockDim.x;
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+        const int i = min(int(threadIdx.x) + j * nt, P - 1), m = i / kn, c = i - m * kn;
+        xv[j] = *reinterpret_cast<const uint4 *>(x + int64_t(m) * xs + c * 8);
+    }
+}
+
+// ... then into LDS (row m at xl + m * x_row_stride(K)).
+template <int XPT>
+__device__ __forceinline__ void stage_regs_commit(const uint4 (&xv)[XPT], int M, int K, uint4 *xl) {
+    const int kn = K / 8, kc = x_row_stride(K), P = M * kn, nt = blockDim.x;
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+        // unconditional store (a thread past the end rewrites the last piece
+        // with the same value): a conditional one lets the compiler sink the
+        // load down to it, behind the weight loads and their wait
+        const int i = min(int(threadIdx.x) + j * nt, P - 1), m = i / kn, c = i - m * kn;
+        xl[m * kc + c] = xv[j];
+    }
+}
+
+// The -BIAS * sum(x) correction of each of a wave's groups g0 .. g0 + n - 1
+// (n <= GW) for its token rows: the starting accumulator of that group's
+// product (MFMAs on the staged activations only, so they run while the
+// weights are still in flight). Per group, an MFMA chain over its four
+// 32-element slices against a splat of -BIAS.
+// P4 (at most 4 token rows, MB == 1): the four groups share one chain. Row
+// 4c + m of that tile holds token m of group g0 + c (xp: the lane's
+// fragment of it), so each row goes through exactly the arithmetic it gets
+// in a tile of its own, and 4 MFMAs serve what would take 16; the results,
+// equal across a row's 16 columns, are read out per (group, token).
+template <typename T, int MB, int GW, bool P4>
+__device__ __forceinline__ void group_bias(const uint4 *const (&xr)[MB], const uint4 *xp, int g0, int n,
+                                           f32x4 (&pc)[GW][MB]) {
     const uint4 negb = make_uint4(T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS);
+    if constexpr (P4) {
+        static_assert(MB == 1 && GW == 4, "packed correction: one row block, four groups");
+        f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c = mfma16<T>(xp[t], negb, c);
+        // (each element copied out first: a bit cast of the subscript c[r]
+        // itself reads element 0)
+        const float cv[4] = {c[0], c[1], c[2], c[3]};
+#pragma unroll
+        for (int g = 0; g < GW; ++g)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                pc[g][0][r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv[r]), 16 * g));
+    } else {
+#pragma unroll
+        for (int c = 0; c < GW; ++c) {
+            if (c < n) {
+                const int g = g0 + c;
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    pc[c][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) pc[c][mb] = mfma16<T>(xr[mb][g * 16 + t], negb, pc[c][mb]);
+                }
+            }
+        }
+    }
+}
+
+// NS subtiles over the same groups (wr[j] fetched with equal g0 and n): per
+// group, as its weights arrive, the 4 MFMAs of the product onto the group's
+// correction pc; the activation fragments are read once for all NS.
+template <typename T, int MB, int NS, int GW, bool HAS_Z, bool CH4>
+__device__ __forceinline__ void compute_pc(const WaveRange<GW, HAS_Z, CH4> (&wr)[NS], const uint4 *const (&xr)[MB],
+                                           const f32x4 (&pc)[GW][MB], f32x4 (&acc)[NS][MB]) {
     const int g0 = wr[0].g0, n = wr[0].n;
 #pragma unroll
     for (int c = 0; c < GW; ++c) {
         if (c < n) {
             const int g = g0 + c;
             uint4 a[MB][4];
-            f32x4 pc[MB];
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) {
+            for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                 for (int t = 0; t < 4; ++t) a[mb][t] = xr[mb][g * 16 + t];
-                pc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int t = 0; t < 4; ++t) pc[mb] = mfma16<T>(a[mb][t], negb, pc[mb]);
-            }
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
                 const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(wr[j].zv[c], g) : 8u);
@@ -185,7 +253,7 @@ __device__ __forceinline__ void compute_shared_x(const WaveRange<GW, HAS_Z, CH4>
                 b[3] = unpack8<T>(wr[j].w[c].w, zb);
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) {
-                    f32x4 p = pc[mb];
+                    f32x4 p = pc[c][mb];
 #pragma unroll
                     for (int t = 0; t < 4; ++t) p = mfma16<T>(a[mb][t], b[t], p);
                     acc[j][mb] += sc * p;
