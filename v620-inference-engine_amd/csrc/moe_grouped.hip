@@ -42,7 +42,6 @@ __global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(
     constexpr int BM = GROUPED_TILE_M;
     using Sh = GemmShape<BM>;
     static_assert(Sh::NJ == 2, "gate/up pairing assumes two 32-row MFMA tiles per wave");
-    extern __shared__ __align__(16) unsigned char smem[];
     const int tile = blockIdx.y;
     if (tile >= *n_tiles) return;
     const int e = tile_e[tile], m0 = tile_m0[tile];
@@ -63,7 +62,7 @@ __global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
-    gemm_tile<BM, HAS_Z>(smem, ap, b, H, acc);
+    unsigned char *ep = gemm_tile<BM, HAS_Z>(ap, b, H, acc);
 
     // acc[i][0] (gate) and acc[i][1] (up) hold the same 32 columns
     f32x16 hv[2][1];
@@ -76,7 +75,7 @@ __global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(
         }
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
     emit_tile<1, 2>(
-        smem + wave * 64 * 32 * 2, hv, [](float v, int, int) { return f32_to_f16_sat(v); },
+        ep + wave * 64 * 32 * 2, hv, [](float v, int, int) { return f32_to_f16_sat(v); },
         [&](int tr, int c, uint4 v) {
             const int m = wm * 64 + tr, j = j0 + wn2 * 32 + c;
             if (m < M && j < F) *reinterpret_cast<uint4 *>(h + int64_t(base + m) * F + j) = v;
@@ -90,7 +89,6 @@ __global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
     const int32_t *__restrict__ n_tiles, const uint16_t *__restrict__ h, int H, int F, float *__restrict__ yp) {
     constexpr int BM = GROUPED_TILE_M;
     using Sh = GemmShape<BM>;
-    extern __shared__ __align__(16) unsigned char smem[];
     const int tile = blockIdx.y;
     if (tile >= *n_tiles) return;
     const int e = tile_e[tile], m0 = tile_m0[tile];
@@ -106,20 +104,15 @@ __global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
-    gemm_tile<BM, HAS_Z>(smem, ap, b, F, acc);
+    unsigned char *ep = gemm_tile<BM, HAS_Z>(ap, b, F, acc);
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
     emit_tile<Sh::NJ, 4>(
-        smem + wave * 64 * 32 * 4, acc, [](float, int, int) { return uint16_t(0); },
+        ep + wave * 64 * 32 * 4, acc, [](float, int, int) { return uint16_t(0); },
         [&](int tr, int c, uint4 v) {
             const int m = wm * 64 + tr, n = n0 + wn2 * Sh::WNR + c;
             if (m < M && n < H) *reinterpret_cast<uint4 *>(yp + int64_t(base + m) * H + n) = v;
         });
-}
-
-template <class K>
-static void set_lds(K kern) {
-    (void)persistent_shape(reinterpret_cast<const void *>(kern), G_THREADS, GEMM_LDS);  // sets the LDS limit
 }
 
 void launch_moe_grouped(const MoeGroupedArgs &a, hipStream_t s) {
@@ -129,23 +122,19 @@ void launch_moe_grouped(const MoeGroupedArgs &a, hipStream_t s) {
     const dim3 g1(unsigned((a.F + 127) / 128), unsigned(max_tiles)),
         g2(unsigned((a.H + GB_N - 1) / GB_N), unsigned(max_tiles));
     if (a.gz) {
-        set_lds(moe_gate_up_gemm_kernel<true>);
-        moe_gate_up_gemm_kernel<true><<<g1, G_THREADS, GEMM_LDS, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets,
+        moe_gate_up_gemm_kernel<true><<<g1, G_THREADS, 0, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets,
                                                                       a.pair_tok, a.tile_e, a.tile_m0, a.n_tiles, xh,
                                                                       a.H, a.F, a.h);
     } else {
-        set_lds(moe_gate_up_gemm_kernel<false>);
-        moe_gate_up_gemm_kernel<false><<<g1, G_THREADS, GEMM_LDS, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets,
+        moe_gate_up_gemm_kernel<false><<<g1, G_THREADS, 0, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets,
                                                                        a.pair_tok, a.tile_e, a.tile_m0, a.n_tiles, xh,
                                                                        a.H, a.F, a.h);
     }
     if (a.dz) {
-        set_lds(moe_down_gemm_kernel<true>);
-        moe_down_gemm_kernel<true><<<g2, G_THREADS, GEMM_LDS, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0,
+        moe_down_gemm_kernel<true><<<g2, G_THREADS, 0, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0,
                                                                    a.n_tiles, a.h, a.H, a.F, a.yp);
     } else {
-        set_lds(moe_down_gemm_kernel<false>);
-        moe_down_gemm_kernel<false><<<g2, G_THREADS, GEMM_LDS, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0,
+        moe_down_gemm_kernel<false><<<g2, G_THREADS, 0, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0,
                                                                     a.n_tiles, a.h, a.H, a.F, a.yp);
     }
 }

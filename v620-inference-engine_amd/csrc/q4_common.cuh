@@ -55,6 +55,14 @@ struct F16 {
     typedef f16x8 vec;
 };
 
+// LDS-only barrier: orders this block's LDS traffic without draining the
+// global-memory loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <typename T>
 __device__ __forceinline__ f32x4 mfma16(const uint4 &a, const uint4 &b, const f32x4 &c) {
     if constexpr (__is_same(T, BF16))

@@ -53,12 +53,11 @@ void launch_x_to_f16(const uint16_t *X, int ldx, int T, int K, uint16_t *Xh, hip
 }
 
 template <bool HAS_Z, bool Y_BF16, int GB_M>
-__global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *__restrict__ Wt,
-                                                            const uint16_t *__restrict__ St,
-                                                            const uint16_t *__restrict__ Zt,
+__global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
+                                                            const uint16_t *St,
+                                                            const uint16_t *Zt,
                                                             const uint16_t *__restrict__ Xh, int T, void *__restrict__ Y,
                                                             int ldy, int N, int K) {
-    extern __shared__ __align__(16) unsigned char smem[];
     using Sh = GemmShape<GB_M>;
     const int tid = threadIdx.x, wave = tid / WAVE;
     // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs;
@@ -83,12 +82,12 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *__re
     const uint16_t *ap[GB_M / 64];
 #pragma unroll
     for (int j = 0; j < GB_M / 64; ++j) ap[j] = Xh + int64_t(min(t0 + a_load_row(j), T - 1)) * K;
-    gemm_tile<GB_M, HAS_Z>(smem, ap, b, K, acc);
+    unsigned char *ep = gemm_tile<GB_M, HAS_Z>(ap, b, K, acc);
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
     constexpr int YB = Y_BF16 ? 2 : 4;
     emit_tile<Sh::NJ, YB>(
-        smem + wave * 64 * 32 * YB, acc, [](float v, int, int) { return f32_to_bf16_rne(v); },
+        ep + wave * 64 * 32 * YB, acc, [](float v, int, int) { return f32_to_bf16_rne(v); },
         [&](int tr, int col, uint4 v) {
             const int t = t0 + wm * 64 + tr, n = n0 + wn2 * Sh::WNR + col;
             if (t < T && n < N)
@@ -99,9 +98,8 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *__re
 template <bool HAS_Z, bool Y_BF16, int GB_M>
 static void launch_gemm_t(const GemmArgs &a, const uint16_t *Xh, hipStream_t s) {
     auto kern = q4_gemm_kernel<HAS_Z, Y_BF16, GB_M>;
-    (void)persistent_shape(reinterpret_cast<const void *>(kern), G_THREADS, GEMM_LDS);  // sets the LDS limit
     const dim3 grid(unsigned((a.N + GB_N - 1) / GB_N), unsigned((a.T + GB_M - 1) / GB_M));
-    kern<<<grid, G_THREADS, GEMM_LDS, s>>>(a.W, a.S, a.Z, Xh, a.T, a.Y, a.ldy, a.N, a.K);
+    kern<<<grid, G_THREADS, 0, s>>>(a.W, a.S, a.Z, Xh, a.T, a.Y, a.ldy, a.N, a.K);
 }
 
 // 256-token tiles when they fill whole rounds of the chip, else 128

@@ -22,7 +22,7 @@ namespace qwq4 {
 
 constexpr int GB_N = 256, GB_K = 64, G_THREADS = 512, G_WAVES = 8;
 constexpr int TILE_BYTES = 256 * GB_K * 2;     // 32 KB: one operand of one stage (<= 256 rows)
-constexpr size_t GEMM_LDS = 4 * size_t(TILE_BYTES);
+constexpr size_t GEMM_LDS = 4 * size_t(TILE_BYTES);  // the stage buffers (static LDS)
 
 // byte offset of 16-byte chunk c (0..7) of row r in a [rows][64 fp16] tile.
 // gfx950 LDS serves 256 B (64 banks) per cycle: the 16 rows one pass of a
@@ -56,13 +56,16 @@ struct GemmShape {
 // 16-byte entries, scales and zero words.
 struct BRow {
     const uint4 *w;
-    const uint16_t *s, *z;
+    const uint16_t *s;
+    const uint32_t *z;  // the 32-bit word holding this row's 16-bit zero word (zs: its shift)
+    int zs;
     __device__ __forceinline__ BRow(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt, int64_t row, int G) {
         const int64_t sub = row / 16;
         const int n = int(row % 16), GC = (G + 3) / 4;
         w = reinterpret_cast<const uint4 *>(Wt) + sub * G * 64 + n;
         s = St + sub * GC * 64 + n * 4;
-        z = Zt ? Zt + sub * GC * 16 + n : nullptr;
+        z = Zt ? reinterpret_cast<const uint32_t *>(Zt + sub * GC * 16 + (n & ~1)) : nullptr;
+        zs = (n & 1) * 16;
     }
 };
 
@@ -73,14 +76,21 @@ __device__ __forceinline__ int a_load_row(int j) { return (j * G_WAVES + int(thr
 // acc += A_tile (GB_M x K; ap[j] = start of row a_load_row(j)) * W_tile^T
 // (256 rows; this thread's row is b). Ends with a barrier; the LDS is free
 // afterwards.
+// The four stage buffers are distinct LDS objects: the compiler can then tell
+// the direct-to-LDS loads into one A buffer from the fragment reads of the
+// other, and does not drain every load in flight before those reads (with
+// one LDS array it must assume they may alias). Returns the first buffer,
+// free for the epilogue.
 template <int GB_M, bool HAS_Z, class Acc>
-__device__ __forceinline__ void gemm_tile(unsigned char *smem, const uint16_t *const *ap, const BRow &b, int K, Acc &acc) {
+__device__ __forceinline__ unsigned char *gemm_tile(const uint16_t *const *ap, const BRow &b, int K, Acc &acc) {
     using S = GemmShape<GB_M>;
     constexpr int NJ = S::NJ;
+    __shared__ __align__(16) unsigned char lds_a0[TILE_BYTES], lds_a1[TILE_BYTES], lds_b0[TILE_BYTES],
+        lds_b1[TILE_BYTES];
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int nk = K / GB_K;
-    auto bufA = [&](int i) { return smem + 2 * i * TILE_BYTES; };
-    auto bufB = [&](int i) { return smem + (2 * i + 1) * TILE_BYTES; };
+    auto bufA = [&](int i) { return i ? lds_a1 : lds_a0; };
+    auto bufB = [&](int i) { return i ? lds_b1 : lds_b0; };
 
     // A tile: lane i of an instruction -> row rb + i/8 (= a_load_row(j)), LDS
     // slot i%8 holding the chunk swz() places there
@@ -105,7 +115,7 @@ __device__ __forceinline__ void gemm_tile(unsigned char *smem, const uint16_t *c
         const int g = ks / 2;
         r.w = b.w[g * 64 + ((ks % 2) * 2 + bq) * 16];
         r.s = b.s[(g >> 2) * 64 + (g & 3)];
-        if constexpr (HAS_Z) r.z = b.z[(g >> 2) * 16];
+        if constexpr (HAS_Z) r.z = b.z[(g >> 2) * 8] >> b.zs;  // (a 32-bit load: see BRow)
     };
     // half h of the dequant (2 of the 4 words), written swizzled
     auto commit_b = [&](int ks, const BRaw &r, unsigned char *dst, int h) {
@@ -169,15 +179,19 @@ __device__ __forceinline__ void gemm_tile(unsigned char *smem, const uint16_t *c
     __syncthreads();
     auto stage = [&](int ks, BRaw &mine, const BRaw &next, int p) {
         const bool more = ks + 1 < nk;
-        if (more) issue_a(ks + 1, bufA(p ^ 1));
         issue_b(ks + 2, mine);
+        // unconditional (the last stage reloads its own K range into the
+        // idle buffer): with a branch around them the compiler could no
+        // longer count which loads are in flight and would drain them all
+        issue_a(min(ks + 1, nk - 1), bufA(p ^ 1));
         compute(bufA(p), bufB(p), more ? ks + 1 : -1, next, bufB(p ^ 1));
-        __syncthreads();
+        lds_barrier();  // (also waits for this wave's A loads of ks + 1)
     };
     for (int ks = 0; ks < nk; ks += 2) {  // nk is even (K is a multiple of 128)
         stage(ks, rs[0], rs[1], 0);
         stage(ks + 1, rs[1], rs[0], 1);
     }
+    return lds_a0;
 }
 
 // Wave-private LDS transpose for the epilogue: the wave's acc[i][j] (rows

@@ -14,14 +14,6 @@
 
 namespace qwq4 {
 
-// LDS-only barrier: orders this block's LDS traffic without draining the
-// global-memory loads in flight.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // LDS row stride, in 16-byte pieces, of staged activation rows of K
 // elements: K / 8, plus one piece when K / 8 is a multiple of 64. A b128 read
 // pass serves 16 lanes that read 16 different rows at the same column; with a
