@@ -32,6 +32,8 @@ BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
 L_LAYERS = 24
 BATCHES = (1, 2, 4, 6, 8)
 DOM_BATCHES = (1, 2, 4)
+# name prefix of the dominant launches' instantiations (batch 1 and batches 2/4)
+DOM_KERNEL = "q4_gemv_block_kernel<8, 1, true, true, false, true"
 H, QKV, FFN_DOWN_K, VOCAB = 4096, 12288, 6144, 151936
 
 
@@ -97,6 +99,36 @@ class Timer:
 
 
 # ---------------------------------------------------------------- config 2
+def time_dominant(torch, qwq4, wqs, x, y, M, steps, warmup):
+    """The dominant kernel alone: the 4096->12288 projection, launched back to
+    back over the 24 layers' weights (a 627 MB pool, beyond the Infinity
+    Cache) in one graph; average launch duration (us) from HIP events on the
+    launching stream."""
+    def dom():
+        for wq in wqs:
+            qwq4.gemv(*wq, x, QKV, H, M, y=y, y_bf16=True, xs=x.stride(0), ys=y.stride(0))
+
+    dstep = graphed(torch, dom)
+    for _ in range(warmup):
+        dstep()
+    with Timer(torch) as td:
+        for _ in range(steps):
+            dstep()
+    return td.ms * 1e3 / (steps * len(wqs))
+
+
+def bench_dominant(torch, qwq4, dev, steps, warmup):
+    """Only the dominant launches (the command whose kernel trace is compared
+    with the bench line's roofline figures)."""
+    wqs = [gen_q4(torch, dev, QKV, H, seed=2 * l) for l in range(L_LAYERS)]
+    us = {}
+    for M in DOM_BATCHES:
+        x = gen_x(torch, dev, M, H, seed=M)
+        y = torch.empty((M, QKV), dtype=torch.bfloat16, device=dev)
+        us[M] = time_dominant(torch, qwq4, wqs, x, y, M, steps, warmup)
+    return {"per_batch_us": us, "avg_launch_us": sum(us.values()) / len(us)}
+
+
 def bench_gemv(torch, qwq4, dev, steps, warmup):
     layers = []
     for l in range(L_LAYERS):
@@ -130,20 +162,7 @@ def bench_gemv(torch, qwq4, dev, steps, warmup):
         tot_bytes += b
         tot_ms += t.ms
 
-        # the dominant kernel alone: the 4096->12288 projection, launched back
-        # to back over the 24 layers' weights (a 627 MB pool, beyond the
-        # Infinity Cache) in one graph; average launch duration from events
-        def dom():
-            for (wq, _) in layers:
-                qwq4.gemv(*wq, x, QKV, H, M, y=y, y_bf16=True, xs=x.stride(0), ys=y.stride(0))
-
-        dstep = graphed(torch, dom)
-        for _ in range(warmup):
-            dstep()
-        with Timer(torch) as td:
-            for _ in range(steps):
-                dstep()
-        dom_us.append(td.ms * 1e3 / (steps * L_LAYERS))
+        dom_us.append(time_dominant(torch, qwq4, [wq for (wq, _) in layers], x, y, M, steps, warmup))
         dom_bytes.append(q4_bytes(QKV, H) + M * H * 2 + M * QKV * 2)
     return {
         "GB_s": tot_bytes / (tot_ms * 1e-3) / 1e9,
@@ -151,8 +170,9 @@ def bench_gemv(torch, qwq4, dev, steps, warmup):
         "per_batch": per_m,
         "bytes_per_step_weights": step_bytes_w,
         "launches_per_step": 2 * L_LAYERS + 1,
-        # roofline subset: batches 1, 2, 4, which run one kernel instantiation
-        # (single item per block); 6 and 8 run the prefetching one
+        # roofline subset: batches 1, 2, 4 (one item per block; activations
+        # through registers at batch 1, direct to LDS at 2 and 4); 6 and 8 run
+        # the prefetching instantiation
         "dominant": {"shape": f"{H}->{QKV}", "batches": list(DOM_BATCHES),
                      "avg_launch_us": sum(dom_us[BATCHES.index(m)] for m in DOM_BATCHES) / len(DOM_BATCHES),
                      "avg_bytes_per_launch": sum(dom_bytes[BATCHES.index(m)] for m in DOM_BATCHES) / len(DOM_BATCHES),
@@ -352,7 +372,7 @@ def parse_pmc(fetch_dir, write_dir, out_path):
                 if r.get("Counter_Name") != counter:
                     continue
                 v = float(r["Counter_Value"]) * 1024.0
-                if "q4_gemv_block_kernel<8, 1, true, true, false, true>" in r["Kernel_Name"]:
+                if DOM_KERNEL in r["Kernel_Name"]:
                     gemv.append(v)
                 elif "copy" in r["Kernel_Name"].lower():
                     copies.append((int(r["Grid_Size"]), v))
@@ -379,7 +399,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, gemm, moe_prefill; or traffic (launches for PMC runs)")
+    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, gemm, moe_prefill; or traffic (launches for PMC runs), or dominant (the roofline kernel's launches alone)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parse-pmc", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT_JSON"),
                     help="reduce two rocprofv3 --pmc runs of --workload traffic to bytes per launch")
@@ -397,6 +417,9 @@ def main():
     qwq4.lib()
     if a.workload == "traffic":
         traffic_probe(torch, qwq4, dev)
+        return
+    if a.workload == "dominant":
+        print(json.dumps(bench_dominant(torch, qwq4, dev, a.steps, a.warmup)))
         return
     wl = set(a.workload.split(","))
     if "all" in wl:
@@ -433,7 +456,7 @@ def main():
         ach = d["avg_bytes_per_launch"] / (d["avg_launch_us"] * 1e-6) / 1e9
         line["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                            "kernel": "q4_gemv_block_kernel<8, 1, true, true, false, true> (4096->12288, batch 1/2/4)",
+                            "kernel": DOM_KERNEL + ", 1|0, true> (4096->12288, batch 1/2/4)",
                             "avg_launch_us": round(d["avg_launch_us"], 3),
                             "algorithmic_bytes_per_launch": int(d["avg_bytes_per_launch"])}
     line["workloads"] = res
