@@ -105,17 +105,18 @@ __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t
     auto tile_of = [&](int item) { return Q4Tile(Wt, St, Zt, min(item * SUB + sl, nsub - 1), G); };
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
     f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(M, K));
-    // XPT > 0 (one piece per thread): activations through registers, so that
+    // XPT > 0 (at most 4 pieces per thread): activations through registers, so that
     // each weight group is computed as it arrives; else direct into LDS
     // (the compiler then drains every load in flight before the first LDS
     // read)
-    uint4 xv[XPT > 0 ? XPT : 1];
+    XRegs xv;
     if constexpr (XPT > 0) stage_regs_issue<XPT>(x, xs, M, K, xv);
     else stage_x_issue(x, xs, M, K, xl);
-    asm volatile("" ::: "memory");  // every activation load goes out before the weight loads
+    __builtin_amdgcn_sched_barrier(0);  // every activation load goes out before the weight loads
     WaveRange<GW, HAS_Z, CH4> wr[1];
     wr[0].fetch(tile_of(blockIdx.x), g0, min(gpk, GW), lane);
     if constexpr (XPT > 0) {
+        __builtin_amdgcn_sched_barrier(0);  // and the LDS writes of the activations (which wait for them) after both
         stage_regs_commit<XPT>(xv, M, K, xl);
         lds_barrier();
     } else {
@@ -198,7 +199,7 @@ static void launch_dense_one(const GemvArgs &a, int KS, int SUB, int items, size
                                      SUB);
 }
 
-// Small batches (at most one activation piece per thread) stage through
+// Small batches (at most 4 activation pieces per thread) stage through
 // registers and run one item per block. Larger ones stage directly into LDS;
 // when their items exceed one round of resident blocks, the blocks stay
 // resident and prefetch their next item (PF). P4: batches of at most 4 rows
@@ -208,10 +209,14 @@ static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
     const int waves = KS * SUB, threads = waves * WAVE, gpk = a.K / QGROUP / KS;
     const int nsub = a.N / 16, items = (nsub + SUB - 1) / SUB;
     const int xpt = (a.M * (a.K / 8) + threads - 1) / threads;
-    if (MB == 1 && xpt <= 1) {
-        const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
-        launch_dense_one<NW, MB, HAS_Z, CH4, KSNW, P4, 1>(a, KS, SUB, items, lds, s);
-        return;
+    if constexpr (MB == 1) {
+        if (xpt <= 4) {
+            const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
+            if (xpt <= 1) launch_dense_one<NW, MB, HAS_Z, CH4, KSNW, P4, 1>(a, KS, SUB, items, lds, s);
+            else if (xpt <= 2) launch_dense_one<NW, MB, HAS_Z, CH4, KSNW, P4, 2>(a, KS, SUB, items, lds, s);
+            else launch_dense_one<NW, MB, HAS_Z, CH4, KSNW, P4, 4>(a, KS, SUB, items, lds, s);
+            return;
+        }
     }
     const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
     auto one = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, false, KSNW, 0, P4>;

@@ -146,24 +146,40 @@ struct WaveRange {
     }
 };
 
+// Activation pieces held in registers (up to 4 per thread). Named members
+// rather than an array: an array that lives across the scheduling barriers
+// below is kept in scratch memory by the compiler.
+struct XRegs {
+    uint4 v0, v1, v2, v3;
+    __device__ __forceinline__ void set(int j, const uint4 &v) {
+        if (j == 0) v0 = v;
+        else if (j == 1) v1 = v;
+        else if (j == 2) v2 = v;
+        else v3 = v;
+    }
+    __device__ __forceinline__ uint4 get(int j) const { return j == 0 ? v0 : j == 1 ? v1 : j == 2 ? v2 : v3; }
+};
+
 // Activation rows through registers: thread t takes pieces t, t + nt, ...
-// of the M x K/8 pieces (XPT >= M * K / 8 / blockDim.x). Issued before the
-// weight loads; unlike direct-to-LDS loads (after which the compiler drains
-// every load in flight before the first LDS read), the compiler then waits
-// for exactly these, so each weight group is computed as soon as it arrives.
+// of the M x K/8 pieces (XPT >= M * K / 8 / blockDim.x, XPT <= 4). Issued
+// before the weight loads; unlike direct-to-LDS loads (after which the
+// compiler drains every load in flight before the first LDS read), the
+// compiler then waits for exactly these, so each weight group is computed as
+// soon as it arrives.
 template <int XPT>
-__device__ __forceinline__ void stage_regs_issue(const uint16_t *x, int xs, int M, int K, uint4 (&xv)[XPT]) {
+__device__ __forceinline__ void stage_regs_issue(const uint16_t *x, int xs, int M, int K, XRegs &xv) {
+    static_assert(XPT >= 1 && XPT <= 4, "up to 4 pieces per thread");
     const int kn = K / 8, P = M * kn, nt = blockDim.x;
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
         const int i = min(int(threadIdx.x) + j * nt, P - 1), m = i / kn, c = i - m * kn;
-        xv[j] = *reinterpret_cast<const uint4 *>(x + int64_t(m) * xs + c * 8);
+        xv.set(j, *reinterpret_cast<const uint4 *>(x + int64_t(m) * xs + c * 8));
     }
 }
 
 // ... then into LDS (row m at xl + m * x_row_stride(K)).
 template <int XPT>
-__device__ __forceinline__ void stage_regs_commit(const uint4 (&xv)[XPT], int M, int K, uint4 *xl) {
+__device__ __forceinline__ void stage_regs_commit(const XRegs &xv, int M, int K, uint4 *xl) {
     const int kn = K / 8, kc = x_row_stride(K), P = M * kn, nt = blockDim.x;
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
@@ -171,7 +187,7 @@ __device__ __forceinline__ void stage_regs_commit(const uint4 (&xv)[XPT], int M,
         // with the same value): a conditional one lets the compiler sink the
         // load down to it, behind the weight loads and their wait
         const int i = min(int(threadIdx.x) + j * nt, P - 1), m = i / kn, c = i - m * kn;
-        xl[m * kc + c] = xv[j];
+        xl[m * kc + c] = xv.get(j);
     }
 }
 
