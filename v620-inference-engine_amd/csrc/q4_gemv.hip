@@ -127,9 +127,9 @@ __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t
     for (int mb = 0; mb < MB; ++mb) xr[mb] = xl + min(mb * 16 + n, M - 1) * kc + q * 4;
     // the lane's fragment of the packed correction tile (P4): token n % 4
     // of group gb + n / 4
-    auto xp_of = [&](int gb) { return xl + min(n & 3, M - 1) * kc + min(gb + (n >> 2), G - 1) * 16 + q * 4; };
+    auto xp_of = [&](int gb) { return packed_fragment(xl, kc, M, G, gb, lane); };
     f32x4 pc[GW][MB];
-    group_bias<BF16, MB, GW, P4>(xr, xp_of(g0), g0, min(gpk, GW), pc);
+    group_bias<BF16, MB, GW, P4>(xr, xp_of, g0, min(gpk, GW), pc);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (!PF) {
         f32x4 acc[1][MB];
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t
         // longer ranges: further passes of GW groups
         for (int p = GW; p < gpk; p += GW) {
             wr[0].fetch(tile_of(blockIdx.x), g0 + p, min(gpk - p, GW), opaque_lane());
-            group_bias<BF16, MB, GW, P4>(xr, xp_of(g0 + p), g0 + p, min(gpk - p, GW), pc);
+            group_bias<BF16, MB, GW, P4>(xr, xp_of, g0 + p, min(gpk - p, GW), pc);
             compute_pc<BF16, MB, 1>(wr, xr, pc, acc);
         }
         ksplit_sum<MB>(acc[0], red, KS, wave, kp, lane);

@@ -196,28 +196,36 @@ __device__ __forceinline__ void stage_regs_commit(const XRegs &xv, int M, int K,
 // product (MFMAs on the staged activations only, so they run while the
 // weights are still in flight). Per group, an MFMA chain over its four
 // 32-element slices against a splat of -BIAS.
-// P4 (at most 4 token rows, MB == 1): the four groups share one chain. Row
-// 4c + m of that tile holds token m of group g0 + c (xp: the lane's
-// fragment of it), so each row goes through exactly the arithmetic it gets
-// in a tile of its own, and 4 MFMAs serve what would take 16; the results,
-// equal across a row's 16 columns, are read out per (group, token).
-template <typename T, int MB, int GW, bool P4>
-__device__ __forceinline__ void group_bias(const uint4 *const (&xr)[MB], const uint4 *xp, int g0, int n,
+// P4 (at most 4 token rows, MB == 1): four groups share one chain. Row
+// 4c + m of such a tile holds token m of group gb + c (xp_of(gb): the lane's
+// fragment of the tile starting at group gb), so each row goes through
+// exactly the arithmetic it gets in a tile of its own, and 4 MFMAs serve
+// what would take 16; the results, equal across a row's 16 columns, are
+// read out per (group, token).
+template <typename T, int MB, int GW, bool P4, class XpFn>
+__device__ __forceinline__ void group_bias(const uint4 *const (&xr)[MB], XpFn xp_of, int g0, int n,
                                            f32x4 (&pc)[GW][MB]) {
     const uint4 negb = make_uint4(T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS);
     if constexpr (P4) {
-        static_assert(MB == 1 && GW == 4, "packed correction: one row block, four groups");
-        f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+        static_assert(MB == 1 && GW % 4 == 0, "packed correction: one row block, whole tiles of four groups");
 #pragma unroll
-        for (int t = 0; t < 4; ++t) c = mfma16<T>(xp[t], negb, c);
-        // (each element copied out first: a bit cast of the subscript c[r]
-        // itself reads element 0)
-        const float cv[4] = {c[0], c[1], c[2], c[3]};
+        for (int tl = 0; tl < GW / 4; ++tl) {
+            if (4 * tl < n) {
+                const uint4 *xp = xp_of(g0 + 4 * tl);
+                f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int g = 0; g < GW; ++g)
+                for (int t = 0; t < 4; ++t) c = mfma16<T>(xp[t], negb, c);
+                // (each element copied out first: a bit cast of the subscript
+                // c[r] itself reads element 0)
+                const float cv[4] = {c[0], c[1], c[2], c[3]};
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                pc[g][0][r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv[r]), 16 * g));
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        pc[4 * tl + g][0][r] =
+                            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv[r]), 16 * g));
+            }
+        }
     } else {
 #pragma unroll
         for (int c = 0; c < GW; ++c) {
@@ -232,6 +240,14 @@ __device__ __forceinline__ void group_bias(const uint4 *const (&xr)[MB], const u
             }
         }
     }
+}
+
+// The lane's fragment of a packed correction tile (token n % 4 of group
+// gb + n / 4, groups past the last one clamped to it) in rows staged at xl
+// with row stride kc (pieces), M rows, G groups.
+__device__ __forceinline__ const uint4 *packed_fragment(const uint4 *xl, int kc, int M, int G, int gb, int lane) {
+    const int n = lane % 16, q = lane / 16;
+    return xl + min(n & 3, M - 1) * kc + min(gb + (n >> 2), G - 1) * 16 + q * 4;
 }
 
 // NS subtiles over the same groups (wr[j] fetched with equal g0 and n): per
