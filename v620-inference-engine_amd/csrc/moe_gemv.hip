@@ -157,14 +157,34 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
     } while (m0 < M);
     if constexpr (CMB) {
         if (!count_last_block(&c.counters[blockIdx.x], *n_active)) return;
-        const int r0 = blockIdx.x * SUB * 16, nr = min(SUB * 16, H - r0);
-        for (int i = tid; i < T * nr; i += blockDim.x) {
-            const int tk = i / nr, j = r0 + (i - tk * nr);
-            float v = c.shared ? c.shared[int64_t(tk) * H + j] : 0.f;
-            for (int q2 = 0; q2 < topk; ++q2)
-                v += c.tok_w[tk * topk + q2] * ld_agent(yp + int64_t(c.tok_slot[tk * topk + q2]) * H + j);
-            if (c.out_bf16) static_cast<uint16_t *>(c.out)[int64_t(tk) * H + j] = f32_to_bf16_rne(v);
-            else static_cast<float *>(c.out)[int64_t(tk) * H + j] = v;
+        // The combine of rows r0 .. r0 + nr - 1 for every token, in the
+        // order of the unfused combine (shared row, then the selections in
+        // order). Per pass over qc selections: every (token, selection,
+        // row) value of yp is requested at once (one latency) into LDS (the
+        // staging area, free now), then each output element adds its own in
+        // order.
+        const int r0 = blockIdx.x * SUB * 16, nr = min(SUB * 16, H - r0), nt = blockDim.x;
+        float *ybuf = reinterpret_cast<float *>(smem);
+        for (int e0 = 0; e0 < T * nr; e0 += nt) {
+            const int ne = min(nt, T * nr - e0), e = e0 + tid;
+            const int tk = e / nr, j = r0 + (e - tk * nr);
+            float v = 0.f;
+            if (tid < ne && c.shared) v = c.shared[int64_t(tk) * H + j];
+            for (int q0 = 0; q0 < topk; q0 += c.qc) {
+                const int qn = min(c.qc, topk - q0);
+                for (int p = tid; p < ne * qn; p += nt) {
+                    const int qq = p / ne, ee = e0 + (p - qq * ne), tk2 = ee / nr, j2 = r0 + (ee - tk2 * nr);
+                    ybuf[p] = ld_agent(yp + int64_t(c.tok_slot[tk2 * topk + q0 + qq]) * H + j2);
+                }
+                __syncthreads();
+                if (tid < ne)
+                    for (int qq = 0; qq < qn; ++qq) v += c.tok_w[tk * topk + q0 + qq] * ybuf[qq * ne + tid];
+                __syncthreads();
+            }
+            if (tid < ne) {
+                if (c.out_bf16) static_cast<uint16_t *>(c.out)[int64_t(tk) * H + j] = f32_to_bf16_rne(v);
+                else static_cast<float *>(c.out)[int64_t(tk) * H + j] = v;
+            }
         }
     }
 }
@@ -195,7 +215,10 @@ static void launch_down_c(const MoeGemvArgs &a, int max_active, int R, hipStream
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
     constexpr int SUB = 8 / KS;
     const dim3 grid(unsigned((a.H / 16 + SUB - 1) / SUB), unsigned(max_active));
-    const CombineArgs c = a.cmb ? *a.cmb : CombineArgs{};
+    CombineArgs c = a.cmb ? *a.cmb : CombineArgs{};
+    c.qc = int(lds / 4 / 512);  // yp values of up to 512 elements x qc selections fit the staging LDS
+    if (c.qc > a.topk) c.qc = a.topk;
+    if (c.qc < 1) c.qc = 1;
     kern<<<grid, 512, lds, s>>>(a.dw, a.ds, a.dz, a.offsets, a.active, a.n_active, a.h, a.E, a.H, a.F, R, a.yp, c,
                                 a.T, a.topk);
 }

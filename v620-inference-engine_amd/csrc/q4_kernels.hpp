@@ -37,6 +37,7 @@ struct CombineArgs {
     const float *shared;  // fp32 [T][H] or null
     void *out;
     int out_bf16;
+    int qc;  // selections staged per pass of the combine (set by the launcher)
 };
 // Down row blocks of the decode experts for H (the counters combine needs).
 int moe_down_row_blocks(int H, int F);
