@@ -248,19 +248,24 @@ def bench_gemm(torch, qwq4, dev, steps, warmup):
         ws = torch.empty(qwq4.gemm_workspace_size(T, K), dtype=torch.uint8, device=dev)
         Yh = torch.empty((T // 2, N), dtype=torch.bfloat16, device=dev)
         wsh = torch.empty(qwq4.gemm_workspace_size(T // 2, K), dtype=torch.uint8, device=dev)
-        # warm up for >= 0.3 s so the timed region runs at steady clocks
-        t_end = time.perf_counter() + 0.3
+        # one HIP graph per step (the activation conversion and the GEMM, as a
+        # prefill step would record them); warm up for >= 1 s so the timed
+        # region runs at steady clocks
+        full = graphed(torch, lambda: qwq4.gemm(*W, X, N, K, Y=Y, y_bf16=True, workspace=ws))
+        halves = graphed(torch, lambda: [qwq4.gemm(*W, X[half * (T // 2):(half + 1) * (T // 2)], N, K, Y=Yh,
+                                                   y_bf16=True, workspace=wsh) for half in range(2)])
+        t_end = time.perf_counter() + 1.0
         while time.perf_counter() < t_end or warmup > 0:
-            qwq4.gemm(*W, X, N, K, Y=Y, y_bf16=True, workspace=ws)
+            full()
+            halves()
             torch.cuda.synchronize()
             warmup -= 1
         with Timer(torch) as t:
             for _ in range(steps):
-                qwq4.gemm(*W, X, N, K, Y=Y, y_bf16=True, workspace=ws)
+                full()
         with Timer(torch) as t2:
             for _ in range(steps):
-                for half in range(2):
-                    qwq4.gemm(*W, X[half * (T // 2):(half + 1) * (T // 2)], N, K, Y=Yh, y_bf16=True, workspace=wsh)
+                halves()
         flops = 2.0 * T * N * K
         res[f"{K}x{N}"] = {"TFLOP_s": flops * steps / (t.ms * 1e-3) / 1e12, "us": t.ms * 1e3 / steps,
                            "TFLOP_s_2x2048": flops * steps / (t2.ms * 1e-3) / 1e12,
@@ -290,11 +295,15 @@ def bench_moe_prefill(torch, qwq4, dev, steps, warmup):
         qwq4.moe_experts_grouped(gate, up, down, r, x, E, F, h=h, yp=yp, workspace=ws)
         qwq4.moe_combine(yp, r, H, out=o)
 
-    for _ in range(warmup):
-        step()
+    gstep = graphed(torch, step)  # one HIP graph per step, warmed for >= 1 s (steady clocks)
+    t_end = time.perf_counter() + 1.0
+    while time.perf_counter() < t_end or warmup > 0:
+        gstep()
+        torch.cuda.synchronize()
+        warmup -= 1
     with Timer(torch) as t:
         for _ in range(steps):
-            step()
+            gstep()
     flops = 2.0 * (k * T) * (2 * F * H + H * F)
     return {"TFLOP_s": flops * steps / (t.ms * 1e-3) / 1e12, "us_per_step": t.ms * 1e3 / steps,
             "tokens_s": T * steps / (t.ms * 1e-3)}
@@ -433,11 +442,11 @@ def main():
         res["moe_decode"] = bench_moe(torch, qwq4, dev, a.steps, a.warmup)
         print("# moe decode done", file=sys.stderr, flush=True)
     if "gemm" in wl:
-        res["prefill_gemm"] = bench_gemm(torch, qwq4, dev, max(2, a.steps // 4), 1)
+        res["prefill_gemm"] = bench_gemm(torch, qwq4, dev, max(4, a.steps), 1)
         print("# gemm done", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
     if "moe_prefill" in wl:
-        res["moe_prefill"] = bench_moe_prefill(torch, qwq4, dev, max(2, a.steps // 4), 1)
+        res["moe_prefill"] = bench_moe_prefill(torch, qwq4, dev, max(4, a.steps // 2), 1)
         print("# moe prefill done", file=sys.stderr, flush=True)
     line = {
         "metric": "q4 GEMV HBM GB/s (% of peak) at batch 1-8; q4 prefill GEMM TFLOP/s (% MFMA)",

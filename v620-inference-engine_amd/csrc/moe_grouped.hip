@@ -48,15 +48,15 @@ __global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(
     const int base = offsets[e] + m0, M = min(BM, offsets[e + 1] - offsets[e] - m0);
     const int tid = threadIdx.x, wave = tid / WAVE;
     const int j0 = blockIdx.x * 128;
-    // tile row r = tid / 2: 64-row band r / 64 covers columns j0 + 32 (r / 64)
+    // tile row r = b_tile_row(): 64-row band r / 64 covers columns j0 + 32 (r / 64)
     // .. + 32; inside it rows 0-31 are gate, 32-63 up (wave-uniform choice)
-    const int r = tid / 2, col = (r / 64) * 32 + r % 32;
+    const int r = b_tile_row(), col = (r / 64) * 32 + r % 32;
     const bool up = (r % 64) >= 32;
     const int64_t wrow = int64_t(e) * F + min(j0 + col, F - 1);
     const BRow b = up ? BRow(uw, us, uz, wrow, H / QGROUP) : BRow(gw, gs, gz, wrow, H / QGROUP);
-    const uint16_t *ap[BM / 64];
+    const uint16_t *ap[BM / 32];
 #pragma unroll
-    for (int j = 0; j < BM / 64; ++j) ap[j] = xh + int64_t(pair_tok[base + min(a_load_row(j), M - 1)]) * H;
+    for (int j = 0; j < BM / 32; ++j) ap[j] = xh + int64_t(pair_tok[base + min(a_load_row(j), M - 1)]) * H;
     f32x16 acc[2][Sh::NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -95,10 +95,10 @@ __global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
     const int base = offsets[e] + m0, M = min(BM, offsets[e + 1] - offsets[e] - m0);
     const int tid = threadIdx.x, wave = tid / WAVE;
     const int n0 = blockIdx.x * GB_N;
-    const BRow b(dw, ds, dz, int64_t(e) * H + min(n0 + tid / 2, H - 1), F / QGROUP);
-    const uint16_t *ap[BM / 64];
+    const BRow b(dw, ds, dz, int64_t(e) * H + min(n0 + b_tile_row(), H - 1), F / QGROUP);
+    const uint16_t *ap[BM / 32];
 #pragma unroll
-    for (int j = 0; j < BM / 64; ++j) ap[j] = h + int64_t(base + min(a_load_row(j), M - 1)) * F;
+    for (int j = 0; j < BM / 32; ++j) ap[j] = h + int64_t(base + min(a_load_row(j), M - 1)) * F;
     f32x16 acc[2][Sh::NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)

@@ -73,15 +73,15 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
         }
     }
     const int t0 = by * GB_M, n0 = bx * GB_N;
-    const BRow b(Wt, St, Zt, min(n0 + tid / 2, N - 1), K / QGROUP);
+    const BRow b(Wt, St, Zt, min(n0 + b_tile_row(), N - 1), K / QGROUP);
     f32x16 acc[2][Sh::NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
-    const uint16_t *ap[GB_M / 64];
+    const uint16_t *ap[GB_M / 32];
 #pragma unroll
-    for (int j = 0; j < GB_M / 64; ++j) ap[j] = Xh + int64_t(min(t0 + a_load_row(j), T - 1)) * K;
+    for (int j = 0; j < GB_M / 32; ++j) ap[j] = Xh + int64_t(min(t0 + a_load_row(j), T - 1)) * K;
     unsigned char *ep = gemm_tile<GB_M, HAS_Z>(ap, b, K, acc);
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;

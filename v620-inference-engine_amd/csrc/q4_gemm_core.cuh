@@ -5,12 +5,16 @@
 // Schedule. 8 waves (two per SIMD); GB_M = 256: waves 4 (rows of A) x 2
 // (weight rows) of 64 x 128 each, GB_M = 128: 2 x 4 of 64 x 64; MFMA
 // v_mfma_f32_32x32x16_f16. K runs in stages of 64 through a double-buffered
-// LDS (2 x (32 + 32) KB). For the next stage, the A tile goes global -> LDS
-// by direct loads (1 KB = 8 rows per wave instruction, any row addresses)
-// and the weight tile (8 KB of q4; two threads per weight row) into
-// registers two stages ahead, dequantised and written to LDS in two halves
-// interleaved with the MFMAs of the stage before its own; fragment reads run
-// one 16-K step ahead.
+// LDS (2 x (32 + 32) KB). Besides its MFMAs each wave has one loading role:
+//   waves 0-3 (one per SIMD) move the next stage's A tile global -> LDS by
+//     direct loads (1 KB = 8 rows per wave instruction, any row addresses);
+//   waves 4-7 load the weight tile (8 KB of q4, one thread per weight row)
+//     into registers two stages ahead and dequantise it into LDS in two
+//     halves interleaved with the MFMAs of the stage before its own.
+// The roles run as separate code paths: a wave with direct-to-LDS loads in
+// flight waits for all of its loads at every barrier, so the weight loads
+// must not be issued by those waves or they would get one stage, not two.
+// Fragment reads run one 16-K step ahead.
 //
 // Numerics: each weight becomes fp16((q - z) * s) (exact subtraction, one
 // rounding); products and sums run on the fp16 MFMA with fp32 accumulation.
@@ -52,8 +56,8 @@ struct GemmShape {
     static constexpr int NJ = WNR / 32;                // 32-row MFMA tiles per wave
 };
 
-// The thread's weight row (thread pair 2r, 2r+1 owns tile row r): its tiled
-// 16-byte entries, scales and zero words.
+// The weight row a thread of waves 4-7 loads and dequantises: tile row
+// tid % 256 (b_tile_row()); its tiled 16-byte entries, scales and zero words.
 struct BRow {
     const uint4 *w;
     const uint16_t *s;
@@ -69,13 +73,20 @@ struct BRow {
     }
 };
 
-// The A-tile row whose 16-byte pieces this thread loads in part j of a stage
-// (j < GB_M / 64): the caller resolves it to a row pointer once per block.
-__device__ __forceinline__ int a_load_row(int j) { return (j * G_WAVES + int(threadIdx.x) / WAVE) * 8 + int(threadIdx.x) % WAVE / 8; }
+constexpr int G_ROLE = G_WAVES / 2;  // waves per loading role
+
+__device__ __forceinline__ int b_tile_row() { return int(threadIdx.x) % 256; }
+
+// The A-tile row whose 16-byte pieces a thread of waves 0-3 loads in part j
+// of a stage (j < GB_M / 32): the caller resolves it to a row pointer once
+// per block (for all threads; only waves 0-3 use them).
+__device__ __forceinline__ int a_load_row(int j) {
+    return (j * G_ROLE + int(threadIdx.x) / WAVE % G_ROLE) * 8 + int(threadIdx.x) % WAVE / 8;
+}
 
 // acc += A_tile (GB_M x K; ap[j] = start of row a_load_row(j)) * W_tile^T
-// (256 rows; this thread's row is b). Ends with a barrier; the LDS is free
-// afterwards.
+// (256 rows; a weight-loading thread's row is b). Ends with a barrier; the
+// LDS is free afterwards.
 // The four stage buffers are distinct LDS objects: the compiler can then tell
 // the direct-to-LDS loads into one A buffer from the fragment reads of the
 // other, and does not drain every load in flight before those reads (with
@@ -87,46 +98,54 @@ __device__ __forceinline__ unsigned char *gemm_tile(const uint16_t *const *ap, c
     constexpr int NJ = S::NJ;
     __shared__ __align__(16) unsigned char lds_a0[TILE_BYTES], lds_a1[TILE_BYTES], lds_b0[TILE_BYTES],
         lds_b1[TILE_BYTES];
-    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
     const int nk = K / GB_K;
     auto bufA = [&](int i) { return i ? lds_a1 : lds_a0; };
     auto bufB = [&](int i) { return i ? lds_b1 : lds_b0; };
 
-    // A tile: lane i of an instruction -> row rb + i/8 (= a_load_row(j)), LDS
-    // slot i%8 holding the chunk swz() places there
+    // A tile (waves 0-3): lane i of an instruction -> row rb + i/8 (=
+    // a_load_row(j)), LDS slot i%8 holding the chunk swz() places there
     auto issue_a = [&](int ks, unsigned char *dst) {
-        const int k0 = ks * GB_K;
+        const int k0 = ks * GB_K, wa = wave % G_ROLE;
 #pragma unroll
-        for (int j = 0; j < GB_M / 8 / G_WAVES; ++j) {
-            const int rb = (j * G_WAVES + wave) * 8;
+        for (int j = 0; j < GB_M / 8 / G_ROLE; ++j) {
+            const int rb = (j * G_ROLE + wa) * 8;
             const int r = rb + lane / 8, c = (lane % 8) ^ ((r >> 1) & 7);
             __builtin_amdgcn_global_load_lds(ap[j] + k0 + c * 8, dst + rb * 128, 16, 0, 0);
         }
     };
-    const int brow = tid / 2, bq = tid % 2;
-    // raw weights of one stage: this thread's quarter 2(ks%2) + bq of group
-    // ks/2, its scale and zero word
-    struct BRaw {
-        uint4 w;
-        uint32_t s, z;
+    const int brow = b_tile_row();
+    // raw weights of one stage (waves 4-7): quarters 2(ks%2), 2(ks%2)+1 of
+    // group ks/2 of this thread's row, its scale and zero word
+    struct BRaw {  // exactly as loaded: nothing is computed from them before their use
+        uint4 w0, w1;
+        uint16_t s;
+        uint32_t z;
     };
     auto issue_b = [&](int ks, BRaw &r) {
         ks = min(ks, nk - 1);  // past the end: a valid (unused) load keeps the code branch-free
         const int g = ks / 2;
-        r.w = b.w[g * 64 + ((ks % 2) * 2 + bq) * 16];
+        r.w0 = b.w[g * 64 + ((ks % 2) * 2) * 16];
+        r.w1 = b.w[g * 64 + ((ks % 2) * 2 + 1) * 16];
         r.s = b.s[(g >> 2) * 64 + (g & 3)];
-        if constexpr (HAS_Z) r.z = b.z[(g >> 2) * 8] >> b.zs;  // (a 32-bit load: see BRow)
+        if constexpr (HAS_Z) r.z = b.z[(g >> 2) * 8];  // the 32-bit word holding the row's zeros (see BRow)
     };
-    // half h of the dequant (2 of the 4 words), written swizzled
+    // half h of the dequant (one of the two 16-byte entries: 4 chunks),
+    // written swizzled
     auto commit_b = [&](int ks, const BRaw &r, unsigned char *dst, int h) {
         const int g = ks / 2;
-        const uint32_t zb = zero_bytes(HAS_Z ? (r.z >> (4 * (g & 3))) & 0xfu : 8u);
-        const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(r.s));
+        // the scale and zero word are taken here, not earlier: the compiler
+        // would otherwise work them out right after their loads (waiting
+        // for them a stage early, and with them for everything issued since)
+        uint32_t zw = HAS_Z ? r.z : 0u, sw = r.s;
+        asm volatile("" : "+v"(zw), "+v"(sw));
+        const uint32_t zb = zero_bytes(HAS_Z ? (zw >> (b.zs + 4 * (g & 3))) & 0xfu : 8u);
+        const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(sw));
         const h2 s2 = {sc, sc};
-        const uint32_t words[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
+        const uint4 w = h ? r.w1 : r.w0;
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int c = 2 * h; c < 2 * h + 2; ++c)
-            *reinterpret_cast<uint4 *>(dst + swz(brow, bq * 4 + c)) = dequant8(words[c], zb, s2);
+        for (int c = 0; c < 4; ++c) *reinterpret_cast<uint4 *>(dst + swz(brow, h * 4 + c)) = dequant8(words[c], zb, s2);
     };
 
     const int wm = wave / S::NWN, wn2 = wave % S::NWN, l32 = lane % 32, lh = lane / 32;
@@ -138,10 +157,9 @@ __device__ __forceinline__ unsigned char *gemm_tile(const uint16_t *const *ap, c
         for (int j = 0; j < NJ; ++j)
             bf[j] = *reinterpret_cast<const uint4 *>(bb + swz(wn2 * S::WNR + j * 32 + l32, c));
     };
-    // MFMAs of one stage; fragments of step kk+1 are read during step kk, and
-    // the next stage's weights (raw, loaded a stage earlier) are dequantised
-    // in two halves between them
-    auto compute = [&](const unsigned char *a, const unsigned char *bb, int ksn, const BRaw &rn, unsigned char *dstb) {
+    // MFMAs of one stage; fragments of step kk+1 are read during step kk;
+    // extra(kk) runs between the MFMAs of step kk (the weight dequant)
+    auto compute = [&](const unsigned char *a, const unsigned char *bb, auto extra) {
         uint4 af[2], bf[NJ], an[2], bn[NJ];
         read_frags(a, bb, 0, af, bf);
 #pragma unroll
@@ -151,7 +169,7 @@ __device__ __forceinline__ unsigned char *gemm_tile(const uint16_t *const *ap, c
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32<F16>(af[i], bf[j], acc[i][j]);
-            if (ksn >= 0 && (kk == 1 || kk == 3)) commit_b(ksn, rn, dstb, kk / 2);
+            extra(kk);
             // interleave: one MFMA, then up to four VALU instructions
 #pragma unroll
             for (int q = 0; q < 2 * NJ; ++q) {
@@ -165,31 +183,46 @@ __device__ __forceinline__ unsigned char *gemm_tile(const uint16_t *const *ap, c
         }
     };
 
-    // Stage ks (parity p): the A tile of ks + 1 goes to LDS by direct loads
-    // and the raw weights of ks + 2 into register set p, both requested
-    // before the stage's MFMAs (the barrier that ends the stage waits for
-    // them); the weights of ks + 1 (set 1 - p, loaded during the previous
-    // stage) are dequantised into LDS between the MFMAs.
-    BRaw rs[2];
-    issue_a(0, bufA(0));
-    issue_b(0, rs[0]);
-    commit_b(0, rs[0], bufB(0), 0);
-    commit_b(0, rs[0], bufB(0), 1);
-    issue_b(1, rs[1]);
-    __syncthreads();
-    auto stage = [&](int ks, BRaw &mine, const BRaw &next, int p) {
-        const bool more = ks + 1 < nk;
-        issue_b(ks + 2, mine);
-        // unconditional (the last stage reloads its own K range into the
-        // idle buffer): with a branch around them the compiler could no
-        // longer count which loads are in flight and would drain them all
-        issue_a(min(ks + 1, nk - 1), bufA(p ^ 1));
-        compute(bufA(p), bufB(p), more ? ks + 1 : -1, next, bufB(p ^ 1));
-        lds_barrier();  // (also waits for this wave's A loads of ks + 1)
-    };
-    for (int ks = 0; ks < nk; ks += 2) {  // nk is even (K is a multiple of 128)
-        stage(ks, rs[0], rs[1], 0);
-        stage(ks + 1, rs[1], rs[0], 1);
+    if (wave < G_ROLE) {
+        // A role. Stage ks (parity p): the A tile of ks + 1 goes to LDS
+        // before the stage's MFMAs; the stage-ending barrier waits for it.
+        issue_a(0, bufA(0));
+        __syncthreads();
+        auto stage = [&](int ks, int p) {
+            // unconditional (the last stage reloads its own K range into the
+            // idle buffer): with a branch around them the compiler could no
+            // longer count which loads are in flight and would drain them all
+            issue_a(min(ks + 1, nk - 1), bufA(p ^ 1));
+            compute(bufA(p), bufB(p), [](int) {});
+            lds_barrier();
+        };
+        for (int ks = 0; ks < nk; ks += 2) {  // nk is even (K is a multiple of 128)
+            stage(ks, 0);
+            stage(ks + 1, 1);
+        }
+    } else {
+        // Weight role. Stage ks (parity p): the raw weights of ks + 2 into
+        // register set p, those of ks + 1 (set 1 - p) dequantised into LDS
+        // between the MFMAs; no direct loads pending, so the barriers wait
+        // for LDS traffic only and the weight loads keep two stages.
+        BRaw rs[2];
+        issue_b(0, rs[0]);
+        commit_b(0, rs[0], bufB(0), 0);
+        commit_b(0, rs[0], bufB(0), 1);
+        issue_b(1, rs[1]);
+        __syncthreads();
+        auto stage = [&](int ks, BRaw &mine, const BRaw &next, int p) {
+            const bool more = ks + 1 < nk;
+            issue_b(ks + 2, mine);
+            compute(bufA(p), bufB(p), [&](int kk) {
+                if (more && (kk == 1 || kk == 3)) commit_b(ks + 1, next, bufB(p ^ 1), kk / 2);
+            });
+            lds_barrier();
+        };
+        for (int ks = 0; ks < nk; ks += 2) {
+            stage(ks, rs[0], rs[1], 0);
+            stage(ks + 1, rs[1], rs[0], 1);
+        }
     }
     return lds_a0;
 }
