@@ -94,3 +94,28 @@ def test_combine_with_shared(gpu):
     y = host(yp)
     want = np.stack([1 + 0.25 * y[1] + 0.75 * y[0], 1 + 0.5 * y[3] + 0.5 * y[2], 1 + y[5] + 0 * y[4]])
     assert np.allclose(o, want, rtol=1e-6)
+
+
+@pytest.mark.parametrize("T", [8, 32])
+def test_decode_and_prefill_experts_agree(gpu, oracle, T):
+    """The decode path (gathered GEMVs, bf16 operands) and the prefill path
+    (grouped GEMM on fp16-dequantised weights) on the same routing agree
+    within 1% of max|y| (the reference's P-vs-T check, test_moe.hip), each
+    within the 2e-3 bar of the oracle."""
+    E, H, F, k = 32, 1024, 384, 4
+    print(f"moe decode vs prefill T={T}", flush=True)
+    ex = synth.experts(43, E, H, F)
+    xb, xf = synth.acts(43, f"x{T}", T, H)
+    l = synth.router_logits(43, f"l{T}", T, E, bias_sigma=0.5)
+    out = oracle.moe(xf, l, k, *ex)
+    (dg, du, dd), E, F = _experts_dev(gpu, ex)
+    dx, dl = to_dev(xb, gpu), to_dev(l, gpu)
+    r1 = qwq4.moe_route(dl, k)
+    _, yp1 = qwq4.moe_experts_gemv(dg, du, dd, r1, dx, E, F)
+    o1 = host(qwq4.moe_combine(yp1, r1, H, out_bf16=False))
+    r2 = qwq4.moe_route(dl, k, tile_m=qwq4.moe_grouped_tile_m())
+    _, yp2 = qwq4.moe_experts_grouped(dg, du, dd, r2, dx, E, F)
+    o2 = host(qwq4.moe_combine(yp2, r2, H, out_bf16=False))
+    assert np.array_equal(host(r1.tok_slot), host(r2.tok_slot))
+    assert np.max(np.abs(o1 - o2)) <= 0.01 * np.max(np.abs(o1))
+    assert rel_err(o1, out) <= TOL and rel_err(o2, out) <= TOL
