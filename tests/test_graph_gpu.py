@@ -2,8 +2,9 @@
 whole decode step into a graph, src/engine/decode.hip:166-181).
 
 One decode layer: QKV projection, routing, gathered experts, combine and the
-down projection, plus a prefill GEMM, captured once and replayed several
-times with the program's own eager work and synchronisations in between.
+down projection, the fused MoE block (router GEMV, routing, experts and the
+combine, whose cross-block counters must be left at zero by every call), plus
+a prefill GEMM, captured once and replayed several times with the program's own eager work and synchronisations in between.
 Every replay must reproduce the eager results bit for bit (all kernels are
 deterministic), and the eager results must match the oracle.
 """
@@ -45,6 +46,10 @@ def test_decode_layer_graph_replays(gpu, oracle):
     out = torch.empty((M, H), dtype=torch.float32, device=gpu)
     Y = torch.empty((T, QKV), dtype=torch.float32, device=gpu)
     ws = torch.empty(qwq4.gemm_workspace_size(T, H), dtype=torch.uint8, device=gpu)
+    Wr = (np.random.default_rng(71).standard_normal((E, H)) * 0.05).astype(np.float32)
+    router_w = to_dev(Wr, gpu)
+    mdb = qwq4.MoeDecode(M, E, k, H, F, gpu)
+    mout = torch.empty((M, H), dtype=torch.bfloat16, device=gpu)
 
     def layer():
         qwq4.gemv(*dq, x, QKV, H, M, y=yq, y_bf16=True)
@@ -53,8 +58,9 @@ def test_decode_layer_graph_replays(gpu, oracle):
         qwq4.moe_combine(yp, r, H, out=out, out_bf16=False)
         qwq4.gemv(*dd, h2, H, F * 2, M, y=yd)
         qwq4.gemm(*dq, X, QKV, H, Y=Y, workspace=ws)
+        qwq4.moe_decode(router_w, x, k, eg, eu, ed, E, F, buf=mdb, out=mout)
 
-    outs = (yq, yd, out, Y, r.top_e, r.pair_tok, h)
+    outs = (yq, yd, out, Y, r.top_e, r.pair_tok, h, mout, mdb.logits, mdb.top_e)
     layer()
     torch.cuda.synchronize()
     eager = [o.clone() for o in outs]
@@ -64,6 +70,8 @@ def test_decode_layer_graph_replays(gpu, oracle):
     assert rel_err(host(yd), oracle.q4_linear(*Wd, H, F * 2, hf)) <= TOL
     assert rel_err(host(out), oracle.moe(xf, l, k, *ex)) <= TOL
     assert rel_err(host(Y), oracle.q4_linear(*Wq, QKV, H, Xf)) <= TOL
+    ml = host(mdb.logits)
+    assert bf16_err_ok(host(mout), oracle.moe(xf, ml, k, *ex))
 
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
