@@ -104,8 +104,12 @@ int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
  *   slot), active [E] (experts with pairs, ascending; first *n_active valid),
  *   n_active [1].
  * Slots are deterministic: experts ascending, tokens ascending within one.
- * tile_m > 0 also writes a tile list for qw_moe_experts_grouped:
- *   tile_e, tile_m0 [T*k/tile_m + E], n_tiles [1]  (tile_m 0: may be NULL).
+ * tile_m != 0 also writes a tile list (for qw_moe_experts_grouped): per
+ * expert ascending, tiles over its slots offsets[e] + m0 ..:
+ *   tile_e, tile_m0 [T*k/|tile_m| + E], n_tiles [1]  (tile_m 0: may be NULL).
+ *   tile_m > 0: tiles of tile_m slots. tile_m = -g (mixed): the tile starting
+ *   rem slots before the end of the expert's range has 4g slots when rem > 3g,
+ *   2g when rem > g, else g.
  * Limits: 1 <= k <= min(E, 64), E <= 1024, T <= 8192 for E <= 256 (LDS). */
 int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_t *top_e, float *top_w,
                  int32_t *counts, int32_t *offsets, int32_t *tok_slot, int32_t *pair_tok, int32_t *active,
@@ -128,7 +132,8 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
 /* Grouped per-expert GEMMs for prefill chunks (replaces gpu::moe_experts_T,
  * moe.hpp:29-32): the same outputs as qw_moe_experts_gemv for any T, over
  * the (expert, tile) list qw_moe_route writes when called with
- * tile_m = qw_moe_grouped_tile_m(). workspace: at least
+ * tile_m = qw_moe_grouped_tile_m() (mixed tiles, -64: 256, 128 and 64
+ * slots). workspace: at least
  * qw_moe_grouped_workspace_size(...) bytes (an fp16 copy of x),
  * 256-byte aligned. */
 int qw_moe_grouped_tile_m(void);

@@ -46,6 +46,35 @@ def test_route_bit_exact(gpu, oracle, T, E, k):
         assert got == want
 
 
+def _mixed_tiles(counts, g):
+    """(expert, m0) of a mixed tile list (tile_m = -g) over per-expert counts."""
+    out = []
+    for e, c in enumerate(counts):
+        m0 = 0
+        while m0 < c:
+            out.append((e, m0))
+            rem = c - m0
+            m0 += 4 * g if rem > 3 * g else 2 * g if rem > g else g
+    return out
+
+
+@pytest.mark.parametrize("T,E,k", [(300, 16, 4), (1100, 8, 2), (4096, 256, 8)])
+def test_route_mixed_tiles(gpu, T, E, k):
+    print(f"route mixed tiles T={T} E={E} k={k}", flush=True)
+    l = synth.router_logits(33, f"m{T}", T, E, bias_sigma=1.0)
+    g = -qwq4.moe_grouped_tile_m()
+    r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=-g)
+    counts = host(r.counts)
+    want = _mixed_tiles(counts, g)
+    nt = int(host(r.n_tiles)[0])
+    assert nt <= T * k // g + E
+    got = list(zip(host(r.tile_e)[:nt].tolist(), host(r.tile_m0)[:nt].tolist()))
+    assert got == want
+    # the heights cover every remainder class at these sizes
+    rems = {min(4 * g, int(counts[e]) - m0) for e, m0 in want}
+    assert any(x > 2 * g for x in rems) and any(g < x <= 2 * g for x in rems) and any(x <= g for x in rems)
+
+
 @pytest.mark.parametrize("T,zeros", [(1, True), (2, True), (4, False), (8, True), (16, True), (17, False),
                                      (32, True)])
 def test_experts_gemv_and_combine(gpu, oracle, T, zeros):

@@ -125,8 +125,8 @@ int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_
             "qw_moe_route: null pointer");
     REQUIRE(T >= 1 && E >= 1 && E <= 1024, "qw_moe_route: T = %d, E = %d (need T >= 1, 1 <= E <= 1024)", T, E);
     REQUIRE(topk >= 1 && topk <= E && topk <= 64, "qw_moe_route: topk = %d outside 1..min(E, 64)", topk);
-    REQUIRE(tile_m >= 0, "qw_moe_route: tile_m < 0");
-    REQUIRE(tile_m == 0 || (tile_e && tile_m0 && n_tiles), "qw_moe_route: tile_m > 0 needs the tile outputs");
+    REQUIRE(tile_m > -4096 && tile_m < 4096, "qw_moe_route: |tile_m| >= 4096");
+    REQUIRE(tile_m == 0 || (tile_e && tile_m0 && n_tiles), "qw_moe_route: tile_m != 0 needs the tile outputs");
     REQUIRE(int64_t(T) * topk < (1 << 30), "qw_moe_route: too many pairs");
     const size_t lds = T <= 64 ? 0 : qwq4::route_lds_bytes(T, E);
     REQUIRE(lds <= 160 * 1024, "qw_moe_route: T = %d, E = %d needs %zu bytes of LDS (> 160 KiB)", T, E, lds);

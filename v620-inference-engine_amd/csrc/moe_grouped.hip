@@ -3,16 +3,18 @@
 // the expert's q4 weights into an fp16 LDS tile and multiplies gathered
 // token rows).
 //
-// Work is the (expert, tile of GROUPED_TILE_M slots) list written by the
-// routing kernel (qw_moe_route with tile_m = GROUPED_TILE_M); slots of one
-// expert are contiguous (offsets[e] ..), slot p carries token pair_tok[p].
-// Each block runs the shared q4 MFMA GEMM core (q4_gemm_core.cuh) on one
-// list entry and 256 weight rows:
+// Work is the (expert, tile) list written by the routing kernel
+// (qw_moe_route with tile_m = GROUPED_TILE_M = -64: mixed tiles of 256, 128
+// and 64 slots); slots of one expert are contiguous (offsets[e] ..), slot p
+// carries token pair_tok[p]. A tile's height follows from its start and the
+// expert's slot count (tile_rows). Each block runs the shared q4 MFMA GEMM
+// core (q4_gemm_core.cuh) at that height on one list entry and 256 weight
+// rows:
 //   gate/up  A = the tile's gathered token rows of x (fp16 copy in the
 //            workspace), weight rows = 128 gate rows and the same 128 up rows,
-//            interleaved by 32 so each wave holds gate and up of the same
-//            columns; epilogue h = silu(g) * u in fp16 (saturated), the
-//            reference's fp16 intermediate.
+//            interleaved by 32 (32-row groups alternate gate, up); epilogue
+//            h = silu(g) * u in fp16 (saturated), the reference's fp16
+//            intermediate.
 //   down     A = the tile's h rows (contiguous slots), 256 down rows, fp32 yp.
 // Blocks past the list's length (n_tiles, known only on the device) exit at
 // once; the grid is sized for the largest possible list.
@@ -21,7 +23,7 @@
 
 namespace qwq4 {
 
-constexpr int GROUPED_TILE_M = 128;
+constexpr int GROUPED_TILE_M = -64;
 
 int moe_grouped_tile_m() { return GROUPED_TILE_M; }
 
@@ -32,67 +34,101 @@ static __device__ __forceinline__ uint16_t f32_to_f16_sat(float v) {
     return __builtin_bit_cast(uint16_t, _Float16(v));
 }
 
-template <bool HAS_Z>
-__global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(
-    const uint32_t *__restrict__ gw, const uint16_t *__restrict__ gs, const uint16_t *__restrict__ gz,
-    const uint32_t *__restrict__ uw, const uint16_t *__restrict__ us, const uint16_t *__restrict__ uz,
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ pair_tok, const int32_t *__restrict__ tile_e,
-    const int32_t *__restrict__ tile_m0, const int32_t *__restrict__ n_tiles, const uint16_t *__restrict__ xh, int H,
-    int F, uint16_t *__restrict__ h) {
-    constexpr int BM = GROUPED_TILE_M;
+static __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + __expf(-g)) * u; }
+
+struct GateUpTile {
+    const uint32_t *gw, *uw;
+    const uint16_t *gs, *gz, *us, *uz;
+    const int32_t *pair_tok;
+    const uint16_t *xh;
+    int H, F;
+    uint16_t *h;
+};
+
+// One gate/up tile of BM slot rows (M of them real) starting at slot base.
+template <int BM, bool HAS_Z>
+__device__ __forceinline__ void gate_up_tile(const GateUpTile &a, int e, int base, int M, int j0) {
     using Sh = GemmShape<BM>;
-    static_assert(Sh::NJ == 2, "gate/up pairing assumes two 32-row MFMA tiles per wave");
-    const int tile = blockIdx.y;
-    if (tile >= *n_tiles) return;
-    const int e = tile_e[tile], m0 = tile_m0[tile];
-    const int base = offsets[e] + m0, M = min(BM, offsets[e + 1] - offsets[e] - m0);
     const int tid = threadIdx.x, wave = tid / WAVE;
-    const int j0 = blockIdx.x * 128;
-    // tile row r = b_tile_row(): 64-row band r / 64 covers columns j0 + 32 (r / 64)
-    // .. + 32; inside it rows 0-31 are gate, 32-63 up (wave-uniform choice)
+    // weight tile row r = b_tile_row(): 32-row group r / 32 is gate when even,
+    // up when odd, for columns j0 + 32 (r / 64) + r % 32 (wave-uniform choice)
     const int r = b_tile_row(), col = (r / 64) * 32 + r % 32;
     const bool up = (r % 64) >= 32;
-    const int64_t wrow = int64_t(e) * F + min(j0 + col, F - 1);
-    const BRow b = up ? BRow(uw, us, uz, wrow, H / QGROUP) : BRow(gw, gs, gz, wrow, H / QGROUP);
+    const int64_t wrow = int64_t(e) * a.F + min(j0 + col, a.F - 1);
+    const BRow b = up ? BRow(a.uw, a.us, a.uz, wrow, a.H / QGROUP) : BRow(a.gw, a.gs, a.gz, wrow, a.H / QGROUP);
     const uint16_t *ap[BM / 32];
 #pragma unroll
-    for (int j = 0; j < BM / 32; ++j) ap[j] = xh + int64_t(pair_tok[base + min(a_load_row(j), M - 1)]) * H;
+    for (int j = 0; j < BM / 32; ++j) ap[j] = a.xh + int64_t(a.pair_tok[base + min(a_load_row(j), M - 1)]) * a.H;
     f32x16 acc[2][Sh::NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
-    unsigned char *ep = gemm_tile<BM, HAS_Z>(ap, b, H, acc);
+    gemm_tile<BM, HAS_Z>(ap, b, a.H, acc);
 
-    // acc[i][0] (gate) and acc[i][1] (up) hold the same 32 columns
-    f32x16 hv[2][1];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const float g = acc[i][0][q], u = acc[i][1][q];
-            hv[i][0][q] = g / (1.f + __expf(-g)) * u;
-        }
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
-    emit_tile<1, 2>(
-        ep + wave * 64 * 32 * 2, hv, [](float v, int, int) { return f32_to_f16_sat(v); },
-        [&](int tr, int c, uint4 v) {
-            const int m = wm * 64 + tr, j = j0 + wn2 * 32 + c;
-            if (m < M && j < F) *reinterpret_cast<uint4 *>(h + int64_t(base + m) * F + j) = v;
-        });
+    auto store = [&](int cbase) {
+        return [&, cbase](int tr, int c, uint4 v) {
+            const int m = wm * 64 + tr, j = j0 + cbase + c;
+            if (m < M && j < a.F) *reinterpret_cast<uint4 *>(a.h + int64_t(base + m) * a.F + j) = v;
+        };
+    };
+    auto cvt = [](float v, int, int) { return f32_to_f16_sat(v); };
+    if constexpr (Sh::NJ >= 2) {
+        // the wave's 32-row groups 2p (gate) and 2p + 1 (up) hold the same
+        // 32 columns, wn2 * WNR / 2 + 32 p ..
+        f32x16 hv[2][Sh::NJ / 2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int p = 0; p < Sh::NJ / 2; ++p)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) hv[i][p][q] = silu_mul(acc[i][2 * p][q], acc[i][2 * p + 1][q]);
+        emit_tile<Sh::NJ / 2, 2>(epi_slot(wave), hv, cvt, store(wn2 * (Sh::WNR / 2)));
+    } else {
+        // one 32-row group per wave: wave 2p holds gate, 2p + 1 up of columns
+        // 32 p ..; the up wave hands its accumulators over through LDS
+        // (lds_a1, free after gemm_tile; same lane layout in both waves)
+        float *xbuf = reinterpret_cast<float *>(lds_a1) + (wave / 2) * (2 * 16 * WAVE);
+        const int lane = tid % WAVE;
+        if (wave & 1) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) xbuf[(i * 16 + q) * WAVE + lane] = acc[i][0][q];
+        }
+        __syncthreads();
+        if (!(wave & 1)) {
+            f32x16 hv[2][1];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) hv[i][0][q] = silu_mul(acc[i][0][q], xbuf[(i * 16 + q) * WAVE + lane]);
+            emit_tile<1, 2>(epi_slot(wave), hv, cvt, store((wave / 2) * 32));
+        }
+    }
 }
 
 template <bool HAS_Z>
-__global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
-    const uint32_t *__restrict__ dw, const uint16_t *__restrict__ ds, const uint16_t *__restrict__ dz,
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ tile_e, const int32_t *__restrict__ tile_m0,
-    const int32_t *__restrict__ n_tiles, const uint16_t *__restrict__ h, int H, int F, float *__restrict__ yp) {
-    constexpr int BM = GROUPED_TILE_M;
-    using Sh = GemmShape<BM>;
+__global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(GateUpTile a, const int32_t *__restrict__ offsets,
+                                                                     const int32_t *__restrict__ tile_e,
+                                                                     const int32_t *__restrict__ tile_m0,
+                                                                     const int32_t *__restrict__ n_tiles) {
     const int tile = blockIdx.y;
     if (tile >= *n_tiles) return;
-    const int e = tile_e[tile], m0 = tile_m0[tile];
-    const int base = offsets[e] + m0, M = min(BM, offsets[e + 1] - offsets[e] - m0);
+    const int e = tile_e[tile], m0 = tile_m0[tile], rem = offsets[e + 1] - offsets[e] - m0;
+    const int base = offsets[e] + m0, rows = tile_rows(rem, GROUPED_TILE_M), M = min(rows, rem);
+    const int j0 = blockIdx.x * 128;
+    if (rows == 256) gate_up_tile<256, HAS_Z>(a, e, base, M, j0);
+    else if (rows == 128) gate_up_tile<128, HAS_Z>(a, e, base, M, j0);
+    else gate_up_tile<64, HAS_Z>(a, e, base, M, j0);
+}
+
+// One down tile of BM slot rows (M real) starting at slot base.
+template <int BM, bool HAS_Z>
+__device__ __forceinline__ void down_tile(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int e,
+                                          int base, int M, const uint16_t *h, int H, int F, float *yp) {
+    using Sh = GemmShape<BM>;
     const int tid = threadIdx.x, wave = tid / WAVE;
     const int n0 = blockIdx.x * GB_N;
     const BRow b(dw, ds, dz, int64_t(e) * H + min(n0 + b_tile_row(), H - 1), F / QGROUP);
@@ -104,32 +140,40 @@ __global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
-    unsigned char *ep = gemm_tile<BM, HAS_Z>(ap, b, F, acc);
+    gemm_tile<BM, HAS_Z>(ap, b, F, acc);
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
     emit_tile<Sh::NJ, 4>(
-        ep + wave * 64 * 32 * 4, acc, [](float, int, int) { return uint16_t(0); },
+        epi_slot(wave), acc, [](float, int, int) { return uint16_t(0); },
         [&](int tr, int c, uint4 v) {
             const int m = wm * 64 + tr, n = n0 + wn2 * Sh::WNR + c;
             if (m < M && n < H) *reinterpret_cast<uint4 *>(yp + int64_t(base + m) * H + n) = v;
         });
 }
 
+template <bool HAS_Z>
+__global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
+    const uint32_t *__restrict__ dw, const uint16_t *__restrict__ ds, const uint16_t *__restrict__ dz,
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ tile_e, const int32_t *__restrict__ tile_m0,
+    const int32_t *__restrict__ n_tiles, const uint16_t *__restrict__ h, int H, int F, float *__restrict__ yp) {
+    const int tile = blockIdx.y;
+    if (tile >= *n_tiles) return;
+    const int e = tile_e[tile], m0 = tile_m0[tile], rem = offsets[e + 1] - offsets[e] - m0;
+    const int base = offsets[e] + m0, rows = tile_rows(rem, GROUPED_TILE_M), M = min(rows, rem);
+    if (rows == 256) down_tile<256, HAS_Z>(dw, ds, dz, e, base, M, h, H, F, yp);
+    else if (rows == 128) down_tile<128, HAS_Z>(dw, ds, dz, e, base, M, h, H, F, yp);
+    else down_tile<64, HAS_Z>(dw, ds, dz, e, base, M, h, H, F, yp);
+}
+
 void launch_moe_grouped(const MoeGroupedArgs &a, hipStream_t s) {
     uint16_t *xh = static_cast<uint16_t *>(a.ws);
     launch_x_to_f16(a.x, a.H, a.T, a.H, xh, s);
-    const int max_tiles = a.T * a.topk / GROUPED_TILE_M + a.E;
+    const int max_tiles = a.T * a.topk / -GROUPED_TILE_M + a.E;
     const dim3 g1(unsigned((a.F + 127) / 128), unsigned(max_tiles)),
         g2(unsigned((a.H + GB_N - 1) / GB_N), unsigned(max_tiles));
-    if (a.gz) {
-        moe_gate_up_gemm_kernel<true><<<g1, G_THREADS, 0, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets,
-                                                                      a.pair_tok, a.tile_e, a.tile_m0, a.n_tiles, xh,
-                                                                      a.H, a.F, a.h);
-    } else {
-        moe_gate_up_gemm_kernel<false><<<g1, G_THREADS, 0, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets,
-                                                                       a.pair_tok, a.tile_e, a.tile_m0, a.n_tiles, xh,
-                                                                       a.H, a.F, a.h);
-    }
+    const GateUpTile gu{a.gw, a.uw, a.gs, a.gz, a.us, a.uz, a.pair_tok, xh, a.H, a.F, a.h};
+    if (a.gz) moe_gate_up_gemm_kernel<true><<<g1, G_THREADS, 0, s>>>(gu, a.offsets, a.tile_e, a.tile_m0, a.n_tiles);
+    else moe_gate_up_gemm_kernel<false><<<g1, G_THREADS, 0, s>>>(gu, a.offsets, a.tile_e, a.tile_m0, a.n_tiles);
     if (a.dz) {
         moe_down_gemm_kernel<true><<<g2, G_THREADS, 0, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0,
                                                                    a.n_tiles, a.h, a.H, a.F, a.yp);

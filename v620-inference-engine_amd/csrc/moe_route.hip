@@ -187,7 +187,7 @@ __device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
                 const int c = L.cnt[e];
                 c_pairs += c;
                 c_act += c > 0;
-                c_tiles += a.tile_m > 0 ? (c + a.tile_m - 1) / a.tile_m : 0;
+                c_tiles += a.tile_m != 0 ? tile_count(c, a.tile_m) : 0;
             }
         }
         int ip = c_pairs, ia = c_act, it = c_tiles;
@@ -209,8 +209,8 @@ __device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
             a.offsets[e] = rp;
             a.counts[e] = c;
             if (c > 0) a.active[ra++] = e;
-            if (a.tile_m > 0)
-                for (int m0 = 0; m0 < c; m0 += a.tile_m) {
+            if (a.tile_m != 0)
+                for (int m0 = 0; m0 < c; m0 += tile_rows(c - m0, a.tile_m)) {
                     a.tile_e[rt] = e;
                     a.tile_m0[rt] = m0;
                     ++rt;
@@ -221,7 +221,7 @@ __device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
             L.off[E] = rp;
             a.offsets[E] = rp;
             *a.n_active = ra;
-            if (a.tile_m > 0) *a.n_tiles = rt;
+            if (a.tile_m != 0) *a.n_tiles = rt;
         }
     }
     __syncthreads();
@@ -291,9 +291,9 @@ __device__ __forceinline__ void route_small_body(const RouteArgs &a, RowFn logit
     // exclusive scans over the experts (one per thread): pairs and non-empty
     // experts packed in one word (both < 2^16), tiles in another
     const int c = tid < E ? __popcll(s_mask[tid]) : 0;
-    const int nt = a.tile_m > 0 ? (c + a.tile_m - 1) / a.tile_m : 0;
+    const int nt = a.tile_m != 0 ? tile_count(c, a.tile_m) : 0;
     const uint32_t v0 = uint32_t(c) | (uint32_t(c > 0) << 16), v1 = uint32_t(nt);
-    const uint32_t i0 = wave_scan_incl(v0), i1 = a.tile_m > 0 ? wave_scan_incl(v1) : 0u;
+    const uint32_t i0 = wave_scan_incl(v0), i1 = a.tile_m != 0 ? wave_scan_incl(v1) : 0u;
     if (lane == WAVE - 1) {
         s_sum[wave][0] = i0;
         s_sum[wave][1] = i1;
@@ -310,14 +310,14 @@ __device__ __forceinline__ void route_small_body(const RouteArgs &a, RowFn logit
         a.offsets[tid] = off;
         a.counts[tid] = c;
         if (c > 0) a.active[act] = tid;
-        for (int j = 0; j < nt; ++j) {
+        for (int j = 0, m0 = 0; j < nt; ++j, m0 += tile_rows(c - m0, a.tile_m)) {
             a.tile_e[tile0 + j] = tid;
-            a.tile_m0[tile0 + j] = j * a.tile_m;
+            a.tile_m0[tile0 + j] = m0;
         }
         if (tid == E - 1) {
             a.offsets[E] = off + c;
             *a.n_active = act + (c > 0);
-            if (a.tile_m > 0) *a.n_tiles = tile0 + nt;
+            if (a.tile_m != 0) *a.n_tiles = tile0 + nt;
         }
     }
     __syncthreads();

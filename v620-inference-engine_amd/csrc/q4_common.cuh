@@ -166,4 +166,23 @@ __device__ __forceinline__ bool count_last_block(int *counter, int total) {
     return s_last;
 }
 
+// Tile lists over an expert's contiguous slots (routing with tile_m != 0).
+// tile_m > 0: tiles of tile_m rows. tile_m = -g: mixed tiles; the tile that
+// starts rem slots before the end of the expert's range has 4g rows when
+// rem > 3g, 2g when rem > g, else g (the choice of least time per expert for
+// grouped GEMM tiles whose time per row falls with their height).
+__device__ __forceinline__ int tile_rows(int rem, int tile_m) {
+    if (tile_m > 0) return tile_m;
+    const int g = -tile_m;
+    return rem > 3 * g ? 4 * g : rem > g ? 2 * g : g;
+}
+
+// Number of tiles over c slots.
+__device__ __forceinline__ int tile_count(int c, int tile_m) {
+    if (tile_m > 0) return (c + tile_m - 1) / tile_m;
+    int n = 0;
+    for (int m0 = 0; m0 < c; m0 += tile_rows(c - m0, tile_m)) ++n;
+    return n;
+}
+
 }  // namespace qwq4

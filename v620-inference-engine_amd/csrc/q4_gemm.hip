@@ -82,12 +82,12 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
     const uint16_t *ap[GB_M / 32];
 #pragma unroll
     for (int j = 0; j < GB_M / 32; ++j) ap[j] = Xh + int64_t(min(t0 + a_load_row(j), T - 1)) * K;
-    unsigned char *ep = gemm_tile<GB_M, HAS_Z>(ap, b, K, acc);
+    gemm_tile<GB_M, HAS_Z>(ap, b, K, acc);
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
     constexpr int YB = Y_BF16 ? 2 : 4;
     emit_tile<Sh::NJ, YB>(
-        ep + wave * 64 * 32 * YB, acc, [](float v, int, int) { return f32_to_bf16_rne(v); },
+        epi_slot(wave), acc, [](float v, int, int) { return f32_to_bf16_rne(v); },
         [&](int tr, int col, uint4 v) {
             const int t = t0 + wm * 64 + tr, n = n0 + wn2 * Sh::WNR + col;
             if (t < T && n < N)

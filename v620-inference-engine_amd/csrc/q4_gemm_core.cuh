@@ -75,6 +75,23 @@ struct BRow {
 
 constexpr int G_ROLE = G_WAVES / 2;  // waves per loading role
 
+// The four stage buffers (A and weights, two stages each), at file scope so
+// that every tile shape instantiated in one kernel shares them. Distinct
+// objects: the compiler can then tell the direct-to-LDS loads into one A
+// buffer from the fragment reads of the other, and does not drain every load
+// in flight before those reads (with one LDS array it must assume they may
+// alias).
+static __shared__ __align__(16) unsigned char lds_a0[TILE_BYTES], lds_a1[TILE_BYTES], lds_b0[TILE_BYTES],
+    lds_b1[TILE_BYTES];
+
+constexpr int EPI_BYTES = 64 * 32 * 4;  // one wave's epilogue slot: a 64 x 32 slice of fp32
+
+// The wave's epilogue slot once gemm_tile has returned: waves 0-3 in lds_a0,
+// 4-7 in lds_b0 (lds_a1 and lds_b1 stay free for the caller).
+__device__ __forceinline__ unsigned char *epi_slot(int wave) {
+    return (wave < 4 ? lds_a0 : lds_b0) + (wave % 4) * EPI_BYTES;
+}
+
 __device__ __forceinline__ int b_tile_row() { return int(threadIdx.x) % 256; }
 
 // The A-tile row whose 16-byte pieces a thread of waves 0-3 loads in part j
@@ -86,18 +103,11 @@ __device__ __forceinline__ int a_load_row(int j) {
 
 // acc += A_tile (GB_M x K; ap[j] = start of row a_load_row(j)) * W_tile^T
 // (256 rows; a weight-loading thread's row is b). Ends with a barrier; the
-// LDS is free afterwards.
-// The four stage buffers are distinct LDS objects: the compiler can then tell
-// the direct-to-LDS loads into one A buffer from the fragment reads of the
-// other, and does not drain every load in flight before those reads (with
-// one LDS array it must assume they may alias). Returns the first buffer,
-// free for the epilogue.
+// LDS is free afterwards (epilogues: epi_slot).
 template <int GB_M, bool HAS_Z, class Acc>
-__device__ __forceinline__ unsigned char *gemm_tile(const uint16_t *const *ap, const BRow &b, int K, Acc &acc) {
+__device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow &b, int K, Acc &acc) {
     using S = GemmShape<GB_M>;
     constexpr int NJ = S::NJ;
-    __shared__ __align__(16) unsigned char lds_a0[TILE_BYTES], lds_a1[TILE_BYTES], lds_b0[TILE_BYTES],
-        lds_b1[TILE_BYTES];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
     const int nk = K / GB_K;
     auto bufA = [&](int i) { return i ? lds_a1 : lds_a0; };
@@ -224,7 +234,6 @@ __device__ __forceinline__ unsigned char *gemm_tile(const uint16_t *const *ap, c
             stage(ks + 1, rs[1], rs[0], 1);
         }
     }
-    return lds_a0;
 }
 
 // Wave-private LDS transpose for the epilogue: the wave's acc[i][j] (rows

@@ -189,7 +189,7 @@ class Route:
         self.pair_tok = torch.empty(T * topk, **i32)
         self.active = torch.empty(E, **i32)
         self.n_active = torch.empty(1, **i32)
-        nt = (T * topk) // tile_m + E if tile_m else 0
+        nt = (T * topk) // abs(tile_m) + E if tile_m else 0
         self.tile_e = torch.empty(max(nt, 1), **i32) if tile_m else None
         self.tile_m0 = torch.empty(max(nt, 1), **i32) if tile_m else None
         self.n_tiles = torch.empty(1, **i32) if tile_m else None
