@@ -181,30 +181,44 @@ def bench_gemv(torch, qwq4, dev, steps, warmup):
 
 
 # ---------------------------------------------------------------- config 3
+MOE_LAYERS = 8  # routing sets per step: successive blocks read different experts, as in a model's layers
+
+
 def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
-    E, F, k = 256, 1536, 8
+    """Config 3: each step runs MOE_LAYERS MoE blocks over one 256-expert pool,
+    each with its own activations, router logits (router weights for the
+    fused block) and so its own experts; bytes are the distinct experts each
+    block reads. Between two reads of one expert the step streams the other
+    blocks' experts (>= 8 x 9.4 MB at batch 1, past the 256 MB Infinity
+    Cache), so the weights come from HBM."""
+    E, F, k, L = 256, 1536, 8, MOE_LAYERS
     gate = gen_q4(torch, dev, F, H, lead=(E,), seed=10)
     up = gen_q4(torch, dev, F, H, lead=(E,), seed=11)
     down = gen_q4(torch, dev, H, F, lead=(E,), seed=12)
     per_expert = q4_bytes(F, H) * 2 + q4_bytes(H, F)
     gr = torch.Generator(device=dev)
     gr.manual_seed(13)
-    router_w = torch.randn((E, H), generator=gr, device=dev) * 0.02
+    router_w = [torch.randn((E, H), generator=gr, device=dev) * 0.02 for _ in range(L)]
     out = {}
     for B in batches:
-        x = gen_x(torch, dev, B, H, seed=100 + B)
+        xs = [gen_x(torch, dev, B, H, seed=100 + 16 * B + l) for l in range(L)]
         g = torch.Generator(device=dev)
         g.manual_seed(200 + B)
-        logits = torch.randn((B, E), generator=g, device=dev)
+        logits = [torch.randn((B, E), generator=g, device=dev) for _ in range(L)]
         r = qwq4.Route(B, E, k, dev)
         h = torch.empty((B * k, F), dtype=torch.float16, device=dev)
         yp = torch.empty((B * k, H), dtype=torch.float32, device=dev)
         o = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
+        U = 0
+        for l in range(L):
+            qwq4.moe_route(logits[l], k, out=r)
+            U += int(r.n_active.item())
 
         def launches():
-            qwq4.moe_route(logits, k, out=r)
-            qwq4.moe_experts_gemv(gate, up, down, r, x, E, F, h=h, yp=yp)
-            qwq4.moe_combine(yp, r, H, out=o)
+            for l in range(L):
+                qwq4.moe_route(logits[l], k, out=r)
+                qwq4.moe_experts_gemv(gate, up, down, r, xs[l], E, F, h=h, yp=yp)
+                qwq4.moe_combine(yp, r, H, out=o)
 
         step = graphed(torch, launches)
 
@@ -213,18 +227,22 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
         with Timer(torch) as t:
             for _ in range(steps):
                 step()
-        U = int(r.n_active.item())
         b = U * per_expert
-        out[B] = {"distinct_experts": U, "GB_s": b * steps / (t.ms * 1e-3) / 1e9, "us_per_step": t.ms * 1e3 / steps,
-                  "tokens_s": B * steps / (t.ms * 1e-3)}
+        out[B] = {"distinct_experts": U / L, "GB_s": b * steps / (t.ms * 1e-3) / 1e9,
+                  "us_per_block": t.ms * 1e3 / (steps * L), "tokens_s": B * L * steps / (t.ms * 1e-3)}
 
         # the fused block (qw_moe_decode): fp32 router GEMV + routing, experts,
         # combine inside the down projection; bytes add the router weights
         buf = qwq4.MoeDecode(B, E, k, H, F, dev)
         ob = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
+        Uf = 0
+        for l in range(L):
+            qwq4.moe_decode(router_w[l], xs[l], k, gate, up, down, E, F, buf=buf, out=ob)
+            Uf += int(torch.unique(buf.top_e).numel())
 
         def fused():
-            qwq4.moe_decode(router_w, x, k, gate, up, down, E, F, buf=buf, out=ob)
+            for l in range(L):
+                qwq4.moe_decode(router_w[l], xs[l], k, gate, up, down, E, F, buf=buf, out=ob)
 
         fstep = graphed(torch, fused)
         for _ in range(warmup):
@@ -232,8 +250,9 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
         with Timer(torch) as tf:
             for _ in range(steps):
                 fstep()
-        bf = b + E * H * 4
-        out[B]["block"] = {"GB_s": bf * steps / (tf.ms * 1e-3) / 1e9, "us_per_step": tf.ms * 1e3 / steps}
+        bf = Uf * per_expert + L * E * H * 4
+        out[B]["block"] = {"distinct_experts": Uf / L, "GB_s": bf * steps / (tf.ms * 1e-3) / 1e9,
+                           "us_per_block": tf.ms * 1e3 / (steps * L)}
     return out
 
 

@@ -27,7 +27,9 @@ def _case(gpu, seed, T, E, H, F, k, with_shared):
 
 
 @pytest.mark.parametrize("T,E,H,F,k,shared,bf16", [(1, 64, 1024, 256, 4, False, False), (5, 64, 1024, 256, 4, True, False),
-                                                   (32, 32, 512, 384, 6, True, True), (8, 256, 4096, 1536, 8, True, True)])
+                                                   (32, 32, 512, 384, 6, True, True), (8, 256, 4096, 1536, 8, True, True),
+                                                   (3, 64, 1024, 512, 4, False, False),
+                                                   (16, 64, 2048, 1536, 6, True, True)])
 def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
     print(f"moe_decode T={T} E={E} H={H} F={F} k={k}", flush=True)
     ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 40 + T, T, E, H, F, k, shared)
@@ -54,8 +56,12 @@ def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
         assert rel_err(outs[0], ref) <= TOL
 
 
-def test_moe_decode_matches_unfused_path(gpu):
-    T, E, H, F, k = 6, 64, 1024, 256, 4
+@pytest.mark.parametrize("F", [256, 512])
+def test_moe_decode_matches_unfused_path(gpu, F):
+    """The block against routing + experts + combine as separate calls: yp
+    bit-identical."""
+    T, E, H, k = 6, 64, 1024, 4
+    print(f"moe_decode vs unfused F={F}", flush=True)
     ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 77, T, E, H, F, k, True)
     out, buf = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
                                out_bf16=False)
