@@ -227,16 +227,10 @@ static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
     }
     auto pf = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, true, KSNW, 0, P4>;
     const LaunchShape lp = persistent_shape(reinterpret_cast<const void *>(pf), threads, lds);
-    // every CU gets the same number of items: blocks per CU = the largest
-    // divisor of the per-CU item count that stays resident
-    const int ipc = (items + lp.cus - 1) / lp.cus, bmax = lp.max_blocks / lp.cus > 0 ? lp.max_blocks / lp.cus : 1;
-    int bpc = 1;
-    for (int d = bmax; d >= 1; --d)
-        if (ipc % d == 0) {
-            bpc = d;
-            break;
-        }
-    const int per = (items + lp.cus * bpc - 1) / (lp.cus * bpc), blocks = (items + per - 1) / per;
+    // every resident slot gets a block; blocks take items grid-stride, so a
+    // CU's blocks together hold an even share of the items and every slot
+    // keeps weight loads in flight
+    const int blocks = items < lp.max_blocks ? items : lp.max_blocks;
     pf<<<blocks, threads, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.y, a.ys, a.y_bf16, a.N, a.K, a.M, a.accumulate, KS,
                                     SUB);
 }
