@@ -197,6 +197,15 @@ static int pick_ks(int G, int kmax) {
     return ks;
 }
 
+// Down projection: a split of 2 where a wave's range stays within 16
+// groups (fewer, larger blocks: each has more weight bytes in flight for its
+// fixed costs), else up to 8.
+static int down_ks(int G) {
+    int ks = pick_ks(G, 2);
+    while (G / ks > 16 && ks < 8 && G % (ks * 2) == 0) ks *= 2;
+    return ks;
+}
+
 template <int KS, int GW, bool HAS_Z, bool CH4>
 static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
     auto kern = moe_gate_up_gemv_kernel<KS, GW, HAS_Z, CH4>;
@@ -248,7 +257,7 @@ static void launch_gw(const MoeGemvArgs &a, int max_active, int R, int gpk, hipS
 template <bool DOWN, bool HAS_Z>
 static void launch_one(const MoeGemvArgs &a, int max_active, hipStream_t s) {
     const int K = DOWN ? a.F : a.H, G = K / QGROUP;
-    const int ks = pick_ks(G, DOWN ? 8 : 4);
+    const int ks = DOWN ? down_ks(G) : pick_ks(G, 4);
     const int gpk = G / ks;
     // rows per block: a decode batch's tokens of one expert, as many as keep
     // the staged activations within 32 KB (two blocks per CU)
@@ -265,13 +274,13 @@ static void launch_one(const MoeGemvArgs &a, int max_active, hipStream_t s) {
 }
 
 int moe_down_row_blocks(int H, int F) {
-    const int sub = 8 / pick_ks(F / QGROUP, 8);
+    const int sub = 8 / down_ks(F / QGROUP);
     return (H / 16 + sub - 1) / sub;
 }
 
 bool moe_gemv_supported(int H, int F) {
     // each wave holds at most 16 groups of its K range
-    return H / QGROUP / pick_ks(H / QGROUP, 4) <= 16 && F / QGROUP / pick_ks(F / QGROUP, 8) <= 16;
+    return H / QGROUP / pick_ks(H / QGROUP, 4) <= 16 && F / QGROUP / down_ks(F / QGROUP) <= 16;
 }
 
 void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s) {
