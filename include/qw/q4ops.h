@@ -158,14 +158,14 @@ int qw_q4_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64
                   void *stream);
 int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream);
 
-/* A routed-MoE decode block in three launches (the engine's decode step calls
+/* A routed-MoE decode block in three or four launches (the engine's decode step calls
  * router GEMV -> route -> experts -> combine back to back, src/engine/decode.hip:99-111;
  * math of ref::Model::moe, src/ref/ref_model.cpp:406-463):
  *   logits = x . router_w^T (fp32 weights [E][H], the reference's fp32 router);
  *   routing as qw_moe_route; experts as qw_moe_experts_gemv;
  *   out[t] = shared[t] + sum_i top_w[t][i] * yp[tok_slot[t][i]]   (fp32 or bf16)
- * The router GEMV and routing share a launch, and the combine runs inside the
- * down projection. Outputs: out, logits [T][E], top_e, top_w, tok_slot [T][k],
+ * The router GEMV and routing share a launch; up to T = 4 the combine runs
+ * inside the down projection, above that in a launch of its own. Outputs: out, logits [T][E], top_e, top_w, tok_slot [T][k],
  * h, yp (as qw_moe_experts_gemv). shared fp32 [T][H] or NULL (e.g. the shared
  * expert's output). 1 <= T <= 32.
  * workspace: qw_moe_decode_workspace_size(...) bytes, 256-byte aligned, filled

@@ -404,10 +404,15 @@ int qw_moe_decode(const float *router_w, const uint16_t *x, int T, int E, int to
                        at(L.active), at(L.n_active), nullptr, nullptr, nullptr};
     qwq4::RouterArgs rr{router_w, x, H, L.kl, reinterpret_cast<float *>(w + L.part), logits, at(L.rcounter)};
     qwq4::launch_router_route(ra, rr, st(stream));
+    // up to 4 tokens the combine runs in the down projection's last blocks
+    // (one launch less); from there on its own launch is faster than the
+    // serial tail it adds to those blocks
+    const bool fold = T <= 4;
     const qwq4::CombineArgs cmb{at(L.dcounters), tok_slot, top_w, shared, out, out_bf16};
     qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, at(L.offsets), at(L.active), at(L.n_active),
-                        at(L.pair_tok), x, T, topk, h, yp, &cmb};
+                        at(L.pair_tok), x, T, topk, h, yp, fold ? &cmb : nullptr};
     qwq4::launch_moe_gemv(a, st(stream));
+    if (!fold) qwq4::launch_combine(yp, tok_slot, top_w, shared, T, topk, H, out, out_bf16, st(stream));
     return launched("qw_moe_decode");
 }
 

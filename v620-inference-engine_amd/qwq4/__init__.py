@@ -302,7 +302,7 @@ class MoeDecode:
 
 
 def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, out=None, out_bf16=True):
-    """Router GEMV + routing + experts + combine for a decode batch (3 launches)."""
+    """Router GEMV + routing + experts + combine for a decode batch (3 launches; 4 above 4 tokens)."""
     import torch
     T, H = x.shape
     buf = buf if buf is not None else MoeDecode(T, E, topk, H, F, x.device)
