@@ -31,6 +31,8 @@ constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
 constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <-> 7 - i within 8
 constexpr int DPP_MIRROR = 0x140;       // lane i <-> 15 - i within 16
+constexpr int DPP_BCAST15 = 0x142;      // lane 15 of each row into the next row
+constexpr int DPP_BCAST31 = 0x143;      // lane 31 into rows 2 and 3
 
 __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
     const uint32_t lo = __builtin_amdgcn_readlane(int(uint32_t(v)), l);
@@ -40,6 +42,12 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
 
 // Maximum of a 64-bit key over the wave (every lane gets it).
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#define QW_MAX_STEP_RM(ctrl, rm)                                                       \
+    {                                                                                  \
+        const uint64_t o = (uint64_t(QW_DPP(uint32_t(v >> 32), ctrl, rm, 0xf, false)) << 32) | \
+                           QW_DPP(uint32_t(v), ctrl, rm, 0xf, false);                  \
+        v = o > v ? o : v;                                                             \
+    }
 #define QW_MAX_STEP(ctrl)                                                              \
     {                                                                                  \
         const uint64_t o = (uint64_t(QW_DPP(uint32_t(v >> 32), ctrl, 0xf, 0xf, false)) << 32) | \
@@ -50,10 +58,14 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     QW_MAX_STEP(DPP_XOR2)
     QW_MAX_STEP(DPP_HALF_MIRROR)
     QW_MAX_STEP(DPP_MIRROR)
+    // rows combined by broadcasts: lane 15 of rows 0, 2 into rows 1, 3, then
+    // lane 31 into rows 2, 3; lane 63 ends with the wave's maximum (other
+    // lanes may hold partial values)
+    QW_MAX_STEP_RM(DPP_BCAST15, 0xa)
+    QW_MAX_STEP_RM(DPP_BCAST31, 0xc)
 #undef QW_MAX_STEP
-    const uint64_t r0 = readlane64(v, 0), r1 = readlane64(v, 16), r2 = readlane64(v, 32), r3 = readlane64(v, 48);
-    const uint64_t a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
-    return a > b ? a : b;
+#undef QW_MAX_STEP_RM
+    return readlane64(v, 63);
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
@@ -63,11 +75,14 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     QW_FMAX_STEP(DPP_HALF_MIRROR)
     QW_FMAX_STEP(DPP_MIRROR)
 #undef QW_FMAX_STEP
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+    // as in wave_max_u64 (masked-off lanes read 0 and may end wrong; only
+    // lane 63, in both masks, is read)
+#define QW_FMAX_STEP_RM(ctrl, rm) \
+    v = fmaxf(v, __builtin_bit_cast(float, QW_DPP(__builtin_bit_cast(uint32_t, v), ctrl, rm, 0xf, false)));
+    QW_FMAX_STEP_RM(DPP_BCAST15, 0xa)
+    QW_FMAX_STEP_RM(DPP_BCAST31, 0xc)
+#undef QW_FMAX_STEP_RM
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Inclusive prefix sum over the wave's 64 lanes (the GCN row_shr /
