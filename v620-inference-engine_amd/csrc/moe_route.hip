@@ -467,7 +467,10 @@ __global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a) {
 
 void launch_route(const RouteArgs &a, hipStream_t s) {
     const size_t lds = route_lds_bytes(a.T, a.E);
-    if (a.T <= 64) {
+    // one block while each of its 16 waves routes at most one token; beyond,
+    // top-k in parallel blocks and the slots in a second launch (32 tokens:
+    // 9.8 against 12.1 us)
+    if (a.T <= 16) {
         const int per = (a.E + WAVE - 1) / WAVE;
         if (per <= 1) route_small_kernel<1><<<1, 1024, 0, s>>>(a);
         else if (per <= 2) route_small_kernel<2><<<1, 1024, 0, s>>>(a);
