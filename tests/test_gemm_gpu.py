@@ -54,3 +54,29 @@ def test_grouped_matches_oracle_small(gpu, oracle, E, H, F, k, T, zeros, bias):
     assert rel_err(host(yp), yp_ref) <= TOL
     o = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
     assert rel_err(o, out) <= TOL
+
+
+def test_grouped_full_config_sampled(gpu, oracle):
+    """The MoE prefill configuration at full size: 4096 tokens, 256 experts
+    (H 4096, F 1536), top-8, router logits with a per-expert bias N(0, 0.5).
+    The whole chunk runs on the device (mixed 256/128/64-slot tiles); 32
+    sampled tokens, first and last among them, are checked against the oracle
+    (a token's output depends only on its own routing and activation row)."""
+    E, H, F, k, T = 256, 4096, 1536, 8, 4096
+    print("grouped full config T=4096", flush=True)
+    ex = synth.experts(42, E, H, F)
+    xb, xf = synth.acts(62, "x", T, H)
+    l = synth.router_logits(62, "l", T, E, bias_sigma=0.5)
+    from test_moe_gpu import _experts_dev
+    (dg, du, dd), E, F = _experts_dev(gpu, ex)
+    g = -qwq4.moe_grouped_tile_m()
+    r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=-g)
+    _, yp = qwq4.moe_experts_grouped(dg, du, dd, r, to_dev(xb, gpu), E, F)
+    o = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
+    counts = host(r.counts)
+    rems = [int(c) - m0 for c in counts for m0 in range(0, int(c), g)]
+    assert max(counts) > 4 * g and any(0 < x <= g for x in rems)  # tiles of every height occur
+    idx = np.random.default_rng(5).choice(T, 32, replace=False)
+    idx[:2] = [0, T - 1]
+    ref = oracle.moe(xf[idx], l[idx], k, *ex)
+    assert rel_err(o[idx], ref) <= TOL

@@ -28,6 +28,18 @@ def test_gemv_fp32(gpu, oracle, N, K, M):
     assert rel_err(y, r) <= TOL
 
 
+@pytest.mark.parametrize("N,K", [(12288, 4096), (4096, 6144)])
+@pytest.mark.parametrize("M", [3, 5, 7])
+def test_gemv_odd_batches(gpu, oracle, N, K, M):
+    """Batches between the benchmarked ones (packed corrections with clamped
+    rows, register or direct activation staging)."""
+    print(f"gemv odd N={N} K={K} M={M}", flush=True)
+    (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M, seed=13)
+    y = host(qwq4.gemv(dW, dS, dZ, dx, N, K, M))
+    r = oracle.q4_linear(W, S, Z, N, K, xf)
+    assert rel_err(y, r) <= TOL
+
+
 @pytest.mark.parametrize("M,K", [(1, 2048), (8, 2048), (16, 2048), (17, 2048), (32, 2048), (32, 6144), (13, 640)])
 def test_gemv_symmetric_and_wide(gpu, oracle, M, K):
     N = 1024
