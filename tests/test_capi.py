@@ -42,6 +42,16 @@ def test_abi_version():
                            ctypes.c_void_p(256), 4096, 0, 4008, 4096, 1, 0, None),  # N % 16
     lambda L: L.qw_q4_gemm(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(256), 4096, 4096,
                            ctypes.c_void_p(256), 4096, 1, 4096, 4096, None, 0, None),
+    lambda L: L.qw_q4_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(264), 4096,
+                           ctypes.c_void_p(256), 4096, 0, 4096, 4096, 1, 0, None),  # x not 16-byte aligned
+    lambda L: L.qw_moe_experts_gemv(*([ctypes.c_void_p(256)] * 9), 256, 4096, 1536, *([ctypes.c_void_p(256)] * 5),
+                                    33, 8, ctypes.c_void_p(256), ctypes.c_void_p(256), None),  # T > 32
+    lambda L: L.qw_moe_experts_grouped(*([ctypes.c_void_p(256)] * 9), 256, 4096, 1536,
+                                       *([ctypes.c_void_p(256)] * 6), 4096, 8, ctypes.c_void_p(256),
+                                       ctypes.c_void_p(256), ctypes.c_void_p(256), 0, None),  # workspace too small
+    lambda L: L.qw_moe_decode(ctypes.c_void_p(256), ctypes.c_void_p(256), 33, 256, 8,
+                              *([ctypes.c_void_p(256)] * 9), 4096, 1536, None, ctypes.c_void_p(256), 1,
+                              *([ctypes.c_void_p(256)] * 7), 1 << 30, None),  # T > 32
 ])
 def test_bad_arguments_are_rejected(call):
     L = qwq4.lib()
