@@ -484,7 +484,7 @@ def main():
         ach = d["avg_bytes_per_launch"] / (d["avg_launch_us"] * 1e-6) / 1e9
         line["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                            "kernel": DOM_KERNEL + ", 1|0, true> (4096->12288, batch 1/2/4)",
+                            "kernel": DOM_KERNEL + ", 1|2|4, true> (4096->12288, batch 1/2/4; the middle value is activation pieces per thread)",
                             "avg_launch_us": round(d["avg_launch_us"], 3),
                             "algorithmic_bytes_per_launch": int(d["avg_bytes_per_launch"])}
     line["workloads"] = res
