@@ -20,16 +20,19 @@ def test_gemm_small_full_check(gpu, oracle, T, N, K):
 
 
 @pytest.mark.parametrize("N,K", [(12288, 4096), (4096, 6144)])
-def test_gemm_prefill_chunk_sampled(gpu, oracle, N, K):
-    """4096-token chunk, bf16 out; checked on sampled tokens and rows (fp64 oracle)."""
-    T = 4096
+@pytest.mark.parametrize("T", [4096, 2048])
+def test_gemm_prefill_chunk_sampled(gpu, oracle, N, K, T):
+    """4096-token chunk (256 x 256 tiles) and a 2048-token micro-batch (256
+    tokens x 128 weight rows), bf16 out; checked on sampled tokens and rows
+    (fp64 oracle), first and last included."""
+    print(f"gemm sampled T={T} N={N} K={K}", flush=True)
     W, S, Z = synth.q4_weights(52, f"p{N}x{K}", N, K)
     xb, xf = synth.acts(52, f"px{K}", T, K)
     dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
     Y = host(qwq4.gemm(dW, dS, dZ, to_dev(xb, gpu), N, K, y_bf16=True))
     r = np.random.default_rng(0)
-    toks = np.sort(r.choice(T, 48, replace=False))
-    rows = np.sort(r.choice(N, 512, replace=False))
+    toks = np.sort(np.unique(np.r_[0, T - 1, r.choice(T, 48, replace=False)]))
+    rows = np.sort(np.unique(np.r_[0, N - 1, r.choice(N, 512, replace=False)]))
     ref = oracle.q4_linear(W[rows], S[rows], Z[rows], len(rows), K, xf[toks])
     assert bf16_err_ok(Y[np.ix_(toks, rows)], ref)
 

@@ -52,13 +52,13 @@ void launch_x_to_f16(const uint16_t *X, int ldx, int T, int K, uint16_t *Xh, hip
     x_to_f16_kernel<<<unsigned((n8 + 255) / 256), 256, 0, s>>>(X, ldx, T, K, Xh);
 }
 
-template <bool HAS_Z, bool Y_BF16, int GB_M>
+template <bool HAS_Z, bool Y_BF16, int GB_M, int BN = GB_N>
 __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
                                                             const uint16_t *St,
                                                             const uint16_t *Zt,
                                                             const uint16_t *__restrict__ Xh, int T, void *__restrict__ Y,
                                                             int ldy, int N, int K) {
-    using Sh = GemmShape<GB_M>;
+    using Sh = GemmShape<GB_M, BN>;
     const int tid = threadIdx.x, wave = tid / WAVE;
     // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs;
     // give each XCD a contiguous, token-major range of tiles so the blocks
@@ -72,8 +72,8 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
             bx = lin % gridDim.x;
         }
     }
-    const int t0 = by * GB_M, n0 = bx * GB_N;
-    const BRow b(Wt, St, Zt, min(n0 + b_tile_row(), N - 1), K / QGROUP);
+    const int t0 = by * GB_M, n0 = bx * BN;
+    const BRow b(Wt, St, Zt, min(n0 + b_tile_row<BN>(), N - 1), K / QGROUP);
     f32x16 acc[2][Sh::NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
     const uint16_t *ap[GB_M / 32];
 #pragma unroll
     for (int j = 0; j < GB_M / 32; ++j) ap[j] = Xh + int64_t(min(t0 + a_load_row(j), T - 1)) * K;
-    gemm_tile<GB_M, HAS_Z>(ap, b, K, acc);
+    gemm_tile<GB_M, HAS_Z, BN>(ap, b, K, acc);
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
     constexpr int YB = Y_BF16 ? 2 : 4;
@@ -95,24 +95,29 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
         });
 }
 
-template <bool HAS_Z, bool Y_BF16, int GB_M>
+template <bool HAS_Z, bool Y_BF16, int GB_M, int BN = GB_N>
 static void launch_gemm_t(const GemmArgs &a, const uint16_t *Xh, hipStream_t s) {
-    auto kern = q4_gemm_kernel<HAS_Z, Y_BF16, GB_M>;
-    const dim3 grid(unsigned((a.N + GB_N - 1) / GB_N), unsigned((a.T + GB_M - 1) / GB_M));
+    auto kern = q4_gemm_kernel<HAS_Z, Y_BF16, GB_M, BN>;
+    const dim3 grid(unsigned((a.N + BN - 1) / BN), unsigned((a.T + GB_M - 1) / GB_M));
     kern<<<grid, G_THREADS, 0, s>>>(a.W, a.S, a.Z, Xh, a.T, a.Y, a.ldy, a.N, a.K);
 }
 
-// 256-token tiles when they fill whole rounds of the chip, else 128
+// 256 x 256 tiles when they fill whole rounds of the chip (or many rounds);
+// else 256 tokens x 128 weight rows when those do (the same dequant work per
+// MFMA, e.g. 2048-token micro-batches); else 128 x 256.
 template <bool HAS_Z, bool Y_BF16>
 static void launch_gemm_m(const GemmArgs &a, const uint16_t *Xh, hipStream_t s) {
     int cus = 0, dev = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (cus < 1) cus = 256;
-    const int64_t nb = int64_t((a.N + GB_N - 1) / GB_N) * ((a.T + 255) / 256);
-    const double rounds = double(nb) / cus;
-    const bool big = rounds >= 4.0 || (rounds >= 1.0 && rounds - double(int64_t(rounds)) < 0.01);
-    if (big) launch_gemm_t<HAS_Z, Y_BF16, 256>(a, Xh, s);
+    auto whole = [&](int64_t nb) {
+        const double rounds = double(nb) / cus;
+        return rounds >= 4.0 || (rounds >= 1.0 && rounds - double(int64_t(rounds)) < 0.01);
+    };
+    const int64_t t256 = (a.T + 255) / 256;
+    if (whole(int64_t((a.N + 255) / 256) * t256)) launch_gemm_t<HAS_Z, Y_BF16, 256>(a, Xh, s);
+    else if (whole(int64_t((a.N + 127) / 128) * t256)) launch_gemm_t<HAS_Z, Y_BF16, 256, 128>(a, Xh, s);
     else launch_gemm_t<HAS_Z, Y_BF16, 128>(a, Xh, s);
 }
 

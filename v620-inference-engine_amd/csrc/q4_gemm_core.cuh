@@ -49,15 +49,18 @@ __device__ __forceinline__ uint4 dequant8(uint32_t w, uint32_t zb, h2 s2) {
     return r;
 }
 
-template <int GB_M>
+// GB_M rows of A by BN weight rows (BN = 256, or 128 where a 256 x 256
+// grid would leave a partial round)
+template <int GB_M, int BN = GB_N>
 struct GemmShape {
     static constexpr int NWN = G_WAVES / (GB_M / 64);  // waves along the weight rows
-    static constexpr int WNR = GB_N / NWN;             // weight rows per wave
+    static constexpr int WNR = BN / NWN;               // weight rows per wave
     static constexpr int NJ = WNR / 32;                // 32-row MFMA tiles per wave
 };
 
 // The weight row a thread of waves 4-7 loads and dequantises: tile row
-// tid % 256 (b_tile_row()); its tiled 16-byte entries, scales and zero words.
+// tid % BN (b_tile_row<BN>()); its tiled 16-byte entries, scales and zero
+// words. With BN = 128 two threads share a row, one per 32-K half of a stage.
 struct BRow {
     const uint4 *w;
     const uint16_t *s;
@@ -92,7 +95,8 @@ __device__ __forceinline__ unsigned char *epi_slot(int wave) {
     return (wave < 4 ? lds_a0 : lds_b0) + (wave % 4) * EPI_BYTES;
 }
 
-__device__ __forceinline__ int b_tile_row() { return int(threadIdx.x) % 256; }
+template <int BN = GB_N>
+__device__ __forceinline__ int b_tile_row() { return int(threadIdx.x) % BN; }
 
 // The A-tile row whose 16-byte pieces a thread of waves 0-3 loads in part j
 // of a stage (j < GB_M / 32): the caller resolves it to a row pointer once
@@ -102,11 +106,13 @@ __device__ __forceinline__ int a_load_row(int j) {
 }
 
 // acc += A_tile (GB_M x K; ap[j] = start of row a_load_row(j)) * W_tile^T
-// (256 rows; a weight-loading thread's row is b). Ends with a barrier; the
+// (BN rows; a weight-loading thread's row is b). Ends with a barrier; the
 // LDS is free afterwards (epilogues: epi_slot).
-template <int GB_M, bool HAS_Z, class Acc>
+template <int GB_M, bool HAS_Z, int BN = GB_N, class Acc>
 __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow &b, int K, Acc &acc) {
-    using S = GemmShape<GB_M>;
+    using S = GemmShape<GB_M, BN>;
+    static_assert(BN == 256 || BN == 128, "weight tile of 256 or 128 rows");
+    constexpr int NH = BN == 256 ? 2 : 1;  // 16-byte weight entries (32 K) per thread and stage
     constexpr int NJ = S::NJ;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
     const int nk = K / GB_K;
@@ -124,25 +130,31 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
             __builtin_amdgcn_global_load_lds(ap[j] + k0 + c * 8, dst + rb * 128, 16, 0, 0);
         }
     };
-    const int brow = b_tile_row();
+    const int brow = b_tile_row<BN>(), bh = BN == 256 ? 0 : (tid % 256) / 128;  // bh: this thread's half (BN 128)
     // raw weights of one stage (waves 4-7): quarters 2(ks%2), 2(ks%2)+1 of
-    // group ks/2 of this thread's row, its scale and zero word
+    // group ks/2 of this thread's row (BN 128: quarter 2(ks%2) + bh only),
+    // its scale and zero word
     struct BRaw {  // exactly as loaded: nothing is computed from them before their use
-        uint4 w0, w1;
+        uint4 w0, w1;  // (w1 unused with BN 128)
         uint16_t s;
         uint32_t z;
     };
     auto issue_b = [&](int ks, BRaw &r) {
         ks = min(ks, nk - 1);  // past the end: a valid (unused) load keeps the code branch-free
         const int g = ks / 2;
-        r.w0 = b.w[g * 64 + ((ks % 2) * 2) * 16];
-        r.w1 = b.w[g * 64 + ((ks % 2) * 2 + 1) * 16];
+        if constexpr (NH == 2) {
+            r.w0 = b.w[g * 64 + ((ks % 2) * 2) * 16];
+            r.w1 = b.w[g * 64 + ((ks % 2) * 2 + 1) * 16];
+        } else {
+            r.w0 = b.w[g * 64 + ((ks % 2) * 2 + bh) * 16];
+        }
         r.s = b.s[(g >> 2) * 64 + (g & 3)];
         if constexpr (HAS_Z) r.z = b.z[(g >> 2) * 8];  // the 32-bit word holding the row's zeros (see BRow)
     };
     // half h of the dequant (one of the two 16-byte entries: 4 chunks),
-    // written swizzled
+    // written swizzled (BN 128: the thread's own half bh)
     auto commit_b = [&](int ks, const BRaw &r, unsigned char *dst, int h) {
+        if constexpr (NH == 1) h = bh;
         const int g = ks / 2;
         // the scale and zero word are taken here, not earlier: the compiler
         // would otherwise work them out right after their loads (waiting
@@ -152,7 +164,7 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
         const uint32_t zb = zero_bytes(HAS_Z ? (zw >> (b.zs + 4 * (g & 3))) & 0xfu : 8u);
         const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(sw));
         const h2 s2 = {sc, sc};
-        const uint4 w = h ? r.w1 : r.w0;
+        const uint4 w = (NH == 1 || !h) ? r.w0 : r.w1;
         const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) *reinterpret_cast<uint4 *>(dst + swz(brow, h * 4 + c)) = dequant8(words[c], zb, s2);
@@ -218,14 +230,14 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
         BRaw rs[2];
         issue_b(0, rs[0]);
         commit_b(0, rs[0], bufB(0), 0);
-        commit_b(0, rs[0], bufB(0), 1);
+        if constexpr (NH == 2) commit_b(0, rs[0], bufB(0), 1);
         issue_b(1, rs[1]);
         __syncthreads();
         auto stage = [&](int ks, BRaw &mine, const BRaw &next, int p) {
             const bool more = ks + 1 < nk;
             issue_b(ks + 2, mine);
             compute(bufA(p), bufB(p), [&](int kk) {
-                if (more && (kk == 1 || kk == 3)) commit_b(ks + 1, next, bufB(p ^ 1), kk / 2);
+                if (more && (kk == 1 || (NH == 2 && kk == 3))) commit_b(ks + 1, next, bufB(p ^ 1), kk / 2);
             });
             lds_barrier();
         };
