@@ -248,6 +248,7 @@ template <bool DOWN, int KS, bool HAS_Z>
 static void launch_gw(const MoeGemvArgs &a, int max_active, int R, int gpk, hipStream_t s) {
     if (gpk == 4) launch_kind<DOWN, KS, 4, HAS_Z, true>(a, max_active, R, s);
     else if (gpk < 4) launch_kind<DOWN, KS, 4, HAS_Z, false>(a, max_active, R, s);
+    else if (gpk == 6) launch_kind<DOWN, KS, 6, HAS_Z, false>(a, max_active, R, s);  // down at F = 1536
     else if (gpk == 8) launch_kind<DOWN, KS, 8, HAS_Z, true>(a, max_active, R, s);
     else if (gpk < 8) launch_kind<DOWN, KS, 8, HAS_Z, false>(a, max_active, R, s);
     else if (gpk % 4 == 0) launch_kind<DOWN, KS, 16, HAS_Z, true>(a, max_active, R, s);
