@@ -158,9 +158,12 @@ struct SlotLds {
     int32_t *cnt, *off;
     unsigned long long *mask;  // [16 waves][E]
     uint16_t *cc;              // [chunks][E]
+    uint16_t *te;              // [T][k] copy of the selections, or null (see slot_lds_bytes)
 };
 
-__host__ __device__ inline size_t slot_lds_layout(int T, int E, SlotLds *p, unsigned char *base) {
+// P16: also a 16-bit copy of the T x k selections (the chunk passes then read
+// LDS instead of strided global words).
+__host__ __device__ inline size_t slot_lds_layout(int T, int E, SlotLds *p, unsigned char *base, int P16 = 0) {
     const size_t n_chunks = size_t(T + WAVE - 1) / WAVE;
     size_t o = 0;
     const size_t cnt = o;
@@ -172,16 +175,28 @@ __host__ __device__ inline size_t slot_lds_layout(int T, int E, SlotLds *p, unsi
     o += size_t(16) * E * 8;
     const size_t cc = o;
     o += n_chunks * E * 2;
+    o = (o + 15) & ~size_t(15);
+    const size_t te = o;
+    o += size_t(P16) * 2;
     if (p) {
         p->cnt = reinterpret_cast<int32_t *>(base + cnt);
         p->off = reinterpret_cast<int32_t *>(base + off);
         p->mask = reinterpret_cast<unsigned long long *>(base + mask);
         p->cc = reinterpret_cast<uint16_t *>(base + cc);
+        p->te = P16 ? reinterpret_cast<uint16_t *>(base + te) : nullptr;
     }
     return o;
 }
 
 size_t route_lds_bytes(int T, int E) { return slot_lds_layout(T, E, nullptr, nullptr); }
+
+// The slots launch's LDS and whether it holds the selection copy (when that
+// fits the 160 KB of a CU and E fits 16 bits).
+static size_t slot_lds_bytes(int T, int E, int k, int &P16) {
+    P16 = E <= 65535 ? T * k : 0;
+    if (P16 && slot_lds_layout(T, E, nullptr, nullptr, P16) > 160 * 1024) P16 = 0;
+    return slot_lds_layout(T, E, nullptr, nullptr, P16);
+}
 
 // counts, offsets, active list, tile list and slots from the selections te
 // (LDS or global). Whole block (1024 threads) participates.
@@ -191,8 +206,13 @@ __device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
     for (int e = tid; e < E; e += blockDim.x) L.cnt[e] = 0;
     for (int i = tid; i < 16 * E; i += blockDim.x) L.mask[i] = 0ull;
     __syncthreads();
-    for (int i = tid; i < P; i += blockDim.x) atomicAdd(&L.cnt[te[i]], 1);
+    for (int i = tid; i < P; i += blockDim.x) {
+        const int e = te[i];
+        if (L.te) L.te[i] = uint16_t(e);
+        atomicAdd(&L.cnt[e], 1);
+    }
     __syncthreads();
+    auto sel = [&](int i) { return L.te ? int(L.te[i]) : te[i]; };
     if (wave == 0) {  // three exclusive scans over the experts: pairs, non-empty experts, tiles
         const int per = (E + WAVE - 1) / WAVE, e0 = lane * per;
         int c_pairs = 0, c_act = 0, c_tiles = 0;
@@ -248,7 +268,7 @@ __device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
         for (int r = 0; r < rounds; ++r) {
             const int c = r * 16 + wave, t = c * WAVE + lane;
             if (c < n_chunks && t < T)
-                for (int j = 0; j < k; ++j) atomicOr(&M[te[t * k + j]], 1ull << lane);
+                for (int j = 0; j < k; ++j) atomicOr(&M[sel(t * k + j)], 1ull << lane);
             __syncthreads();
             if (c < n_chunks) {
                 if (pass == 0) {
@@ -256,7 +276,7 @@ __device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
                 } else if (t < T) {
                     const unsigned long long below = (1ull << lane) - 1ull;
                     for (int j = 0; j < k; ++j) {
-                        const int e = te[t * k + j];
+                        const int e = sel(t * k + j);
                         const int slot = L.off[e] + L.cc[size_t(c) * E + e] + __popcll(M[e] & below);
                         a.tok_slot[t * k + j] = slot;
                         a.pair_tok[slot] = t;
@@ -458,15 +478,16 @@ void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s)
     else go(router_route_kernel<16>);
 }
 
-__global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a) {
+__global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a, int P16) {
     extern __shared__ unsigned char smem[];
     SlotLds L;
-    slot_lds_layout(a.T, a.E, &L, smem);
+    slot_lds_layout(a.T, a.E, &L, smem, P16);
     route_slots(a.top_e, a, L);
 }
 
 void launch_route(const RouteArgs &a, hipStream_t s) {
-    const size_t lds = route_lds_bytes(a.T, a.E);
+    int P16 = 0;
+    const size_t lds = slot_lds_bytes(a.T, a.E, a.topk, P16);
     // one block while each of its 16 waves routes at most one token; beyond,
     // top-k in parallel blocks and the slots in a second launch (32 tokens:
     // 9.8 against 12.1 us)
@@ -486,7 +507,7 @@ void launch_route(const RouteArgs &a, hipStream_t s) {
         if (per <= 4) route_topk_kernel<4><<<g, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
         else if (per <= 8) route_topk_kernel<8><<<g, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
         else route_topk_kernel<16><<<g, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
-        route_slots_kernel<<<1, 1024, lds, s>>>(a);
+        route_slots_kernel<<<1, 1024, lds, s>>>(a, P16);
     }
 }
 
