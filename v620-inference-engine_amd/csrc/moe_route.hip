@@ -519,14 +519,26 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     const int t = blockIdx.x, j = (blockIdx.y * 256 + threadIdx.x) * 4;
     if (j >= H) return;
     float4 acc = shared ? *reinterpret_cast<const float4 *>(shared + int64_t(t) * H + j) : make_float4(0, 0, 0, 0);
-    for (int i = 0; i < k; ++i) {
-        const int slot = tok_slot[t * k + i];
-        const float w = tok_w[t * k + i];
-        const float4 v = *reinterpret_cast<const float4 *>(yp + int64_t(slot) * H + j);
-        acc.x += w * v.x;
-        acc.y += w * v.y;
-        acc.z += w * v.z;
-        acc.w += w * v.w;
+    // up to 8 selections' rows requested together, then added in selection
+    // order (the same sums as one at a time)
+    for (int i0 = 0; i0 < k; i0 += 8) {
+        float4 v[8];
+        float w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = min(i0 + u, k - 1);
+            w[u] = tok_w[t * k + i];
+            v[u] = *reinterpret_cast<const float4 *>(yp + int64_t(tok_slot[t * k + i]) * H + j);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (i0 + u < k) {
+                acc.x += w[u] * v[u].x;
+                acc.y += w[u] * v[u].y;
+                acc.z += w[u] * v[u].z;
+                acc.w += w[u] * v[u].w;
+            }
+        }
     }
     if (out_bf16) {
         uint16_t *o = static_cast<uint16_t *>(out) + int64_t(t) * H + j;
