@@ -210,7 +210,18 @@ static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
     const int nsub = a.N / 16, items = (nsub + SUB - 1) / SUB;
     const int xpt = (a.M * (a.K / 8) + threads - 1) / threads;
     if constexpr (MB == 1) {
-        if (xpt <= 4) {
+        // batches of 4 rows over more items than one round of resident
+        // blocks (the LM head) run faster as the persistent prefetching blocks
+        // below (151936 rows at batch 4: 60 against 65 us; at batches 1-3
+        // the register path stays ahead: 51 against 58 at batch 1, 57.5
+        // against 59 at batch 3)
+        bool regs = xpt <= 4;
+        if (regs && a.M >= 4 && gpk <= DENSE_GW) {
+            auto pf = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, true, KSNW, 0, P4>;
+            const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
+            regs = items <= persistent_shape(reinterpret_cast<const void *>(pf), threads, lds).max_blocks;
+        }
+        if (regs) {
             const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
             if (xpt <= 1) launch_dense_one<NW, MB, HAS_Z, CH4, KSNW, P4, 1>(a, KS, SUB, items, lds, s);
             else if (xpt <= 2) launch_dense_one<NW, MB, HAS_Z, CH4, KSNW, P4, 2>(a, KS, SUB, items, lds, s);
