@@ -37,6 +37,23 @@ def test_gemm_prefill_chunk_sampled(gpu, oracle, N, K, T):
     assert bf16_err_ok(Y[np.ix_(toks, rows)], ref)
 
 
+def test_gemm_microbatch_fp32_out(gpu, oracle):
+    """2048-token micro-batch (256 tokens x 128 weight rows per block) with
+    fp32 output, symmetric weights; sampled tokens and rows, first and last
+    included."""
+    N, K, T = 12288, 4096, 2048
+    print("gemm micro-batch fp32 out", flush=True)
+    W, S, _ = synth.q4_weights(53, f"m{N}x{K}", N, K, zeros=False)
+    xb, xf = synth.acts(53, f"mx{K}", T, K)
+    dW, dS, _ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), None, N, K)
+    Y = host(qwq4.gemm(dW, dS, None, to_dev(xb, gpu), N, K, y_bf16=False))
+    r = np.random.default_rng(1)
+    toks = np.sort(np.unique(np.r_[0, T - 1, r.choice(T, 32, replace=False)]))
+    rows = np.sort(np.unique(np.r_[0, N - 1, r.choice(N, 512, replace=False)]))
+    ref = oracle.q4_linear(W[rows], S[rows], None, len(rows), K, xf[toks])
+    assert rel_err(Y[np.ix_(toks, rows)], ref) <= TOL
+
+
 # (E, H, F, k, T, zeros, bias): few tokens per expert (one partial tile each,
 # some experts empty); many per expert (several tiles, ragged last tile, F
 # not a multiple of 256); symmetric weights (no zero tensor).
