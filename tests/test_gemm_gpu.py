@@ -100,3 +100,31 @@ def test_grouped_full_config_sampled(gpu, oracle):
     idx[:2] = [0, T - 1]
     ref = oracle.moe(xf[idx], l[idx], k, *ex)
     assert rel_err(o[idx], ref) <= TOL
+
+
+def _random_gemm_shapes(n, seed=77):
+    r = np.random.default_rng(seed)
+    return [(int(r.integers(1, 4097)), 16 * int(r.integers(1, 769)), 128 * int(r.integers(1, 49)),
+             bool(r.integers(0, 2)), bool(r.integers(0, 2))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("T,N,K,zeros,y_bf16", _random_gemm_shapes(10))
+def test_gemm_random_shapes(gpu, oracle, T, N, K, zeros, y_bf16):
+    """Seeded random shapes (T up to 4096, N a multiple of 16 up to 12288, K a
+    multiple of 128 up to 6144, with and without zeros, fp32 or bf16 out):
+    the tile-shape choice and ragged tile edges, on sampled tokens and rows
+    (first and last included)."""
+    print(f"gemm random T={T} N={N} K={K} zeros={zeros} bf16={y_bf16}", flush=True)
+    W, S, Z = synth.q4_weights(T + N, f"r{N}x{K}", N, K, zeros)
+    xb, xf = synth.acts(T + K, f"rx{T}x{K}", T, K)
+    dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
+    Y = host(qwq4.gemm(dW, dS, dZ, to_dev(xb, gpu), N, K, y_bf16=y_bf16))
+    r = np.random.default_rng(T)
+    toks = np.sort(np.unique(np.r_[0, T - 1, r.choice(T, min(T, 24), replace=False)]))
+    rows = np.sort(np.unique(np.r_[0, N - 1, r.choice(N, min(N, 256), replace=False)]))
+    ref = oracle.q4_linear(W[rows], S[rows], Z[rows] if zeros else None, len(rows), K, xf[toks])
+    got = Y[np.ix_(toks, rows)]
+    if y_bf16:
+        assert bf16_err_ok(got, ref)
+    else:
+        assert rel_err(got, ref) <= TOL

@@ -104,3 +104,29 @@ def test_gemv_special_inputs(gpu, oracle):
     assert np.all(y[0] == 0)
     deq = oracle.q4_dequant(W, S, Z, N, K)
     assert np.array_equal(y[1], deq[:, 777])  # one-hot: a column, exactly
+
+
+def _random_shapes(n, seed=2024):
+    r = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        out.append((16 * int(r.integers(1, 641)), 128 * int(r.integers(1, 65)), int(r.integers(1, 33)),
+                    bool(r.integers(0, 2)), bool(r.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("N,K,M,zeros,y_bf16", _random_shapes(16))
+def test_gemv_random_shapes(gpu, oracle, N, K, M, zeros, y_bf16):
+    """Seeded random shapes (N a multiple of 16 up to 10240, K a multiple of
+    128 up to 8192, batch 1-32, with and without zeros, fp32 or bf16 out):
+    exercises the launch-shape choices (K split, block width, register or
+    direct staging, one round or persistent, row-split launches) against
+    the oracle."""
+    print(f"gemv random N={N} K={K} M={M} zeros={zeros} bf16={y_bf16}", flush=True)
+    (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M, zeros=zeros, seed=N + K + M)
+    y = host(qwq4.gemv(dW, dS, dZ, dx, N, K, M, y_bf16=y_bf16))
+    r = oracle.q4_linear(W, S, Z if zeros else None, N, K, xf)
+    if y_bf16:
+        assert bf16_err_ok(y, r)
+    else:
+        assert rel_err(y, r) <= TOL
