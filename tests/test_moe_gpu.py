@@ -148,3 +148,36 @@ def test_decode_and_prefill_experts_agree(gpu, oracle, T):
     assert np.array_equal(host(r1.tok_slot), host(r2.tok_slot))
     assert np.max(np.abs(o1 - o2)) <= 0.01 * np.max(np.abs(o1))
     assert rel_err(o1, out) <= TOL and rel_err(o2, out) <= TOL
+
+
+def _random_moe(n, seed=99):
+    r = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        E = int(r.integers(2, 65))
+        out.append((E, int(r.integers(1, min(E, 8) + 1)), 128 * int(r.integers(1, 17)), 128 * int(r.integers(1, 13)),
+                    int(r.integers(1, 33)), int(r.integers(33, 700)), bool(r.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("E,k,H,F,Td,Tp,zeros", _random_moe(6))
+def test_moe_random_shapes(gpu, oracle, E, k, H, F, Td, Tp, zeros):
+    """Seeded random expert counts, top-k, H, F, with and without zeros: a
+    decode batch (gathered GEMVs) and a prefill chunk (grouped GEMMs over
+    mixed tiles, skewed routing) against the oracle; routing bit-exact."""
+    print(f"moe random E={E} k={k} H={H} F={F} Td={Td} Tp={Tp} zeros={zeros}", flush=True)
+    ex = synth.experts(E + H + F, E, H, F, zeros=zeros)
+    (dg, du, dd), E, F = _experts_dev(gpu, ex)
+    for T, tm in ((Td, 0), (Tp, qwq4.moe_grouped_tile_m())):
+        xb, xf = synth.acts(T + E, f"rx{T}", T, H)
+        l = synth.router_logits(T + k, f"rl{T}", T, E, bias_sigma=0.5 if tm else 0.0)
+        out = oracle.moe(xf, l, k, *ex)
+        r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=tm)
+        te, _ = oracle.route(l, k)
+        assert np.array_equal(host(r.top_e), te)
+        if tm:
+            _, yp = qwq4.moe_experts_grouped(dg, du, dd, r, to_dev(xb, gpu), E, F)
+        else:
+            _, yp = qwq4.moe_experts_gemv(dg, du, dd, r, to_dev(xb, gpu), E, F)
+        o = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
+        assert rel_err(o, out) <= TOL
