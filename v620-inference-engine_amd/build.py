@@ -26,10 +26,17 @@ FLAGS = [
 ]
 
 
+# Kernel arguments preloaded into SGPRs at wave launch (gfx950): the first
+# weight request then does not wait on a scalar load of the argument block,
+# which the latency-bound GEMVs feel at every launch.
+PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
+SOURCE_FLAGS = {"q4_gemv.hip": PRELOAD}
+
+
 def _compile(src):
     obj = os.path.join(OBJ, src + ".o")
     lang = ["-x", "hip"] if src.endswith(".cpp") else []
-    cmd = [HIPCC] + FLAGS + lang + ["-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC] + FLAGS + SOURCE_FLAGS.get(src, []) + lang + ["-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:

@@ -47,11 +47,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 struct BF16 {
     static constexpr uint32_t HI = 0x43434343u;    // high byte of 128 + v
     static constexpr uint32_t NEG_BIAS = 0xC310C310u;  // two bf16 -144
+    static constexpr uint32_t ONE = 0x3F803F80u;       // two bf16 1.0
+    static constexpr float BASE = 128.f;               // value of the high byte alone
     typedef bf16x8 vec;
 };
 struct F16 {
     static constexpr uint32_t HI = 0x64646464u;    // high byte of 1024 + v
     static constexpr uint32_t NEG_BIAS = 0xE410E410u;  // two fp16 -1040
+    static constexpr uint32_t ONE = 0x3C003C00u;       // two fp16 1.0
+    static constexpr float BASE = 1024.f;
     typedef f16x8 vec;
 };
 
@@ -93,6 +97,21 @@ __device__ __forceinline__ uint4 unpack8(uint32_t w, uint32_t zb) {
     const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) + zb;
     uint4 r;
     // byte selectors: 0-3 pick from the second source (lo/hi), 4 picks a byte of T::HI
+    r.x = __builtin_amdgcn_perm(T::HI, lo, 0x04010400u);  // e0, e1
+    r.y = __builtin_amdgcn_perm(T::HI, lo, 0x04030402u);  // e2, e3
+    r.z = __builtin_amdgcn_perm(T::HI, hi, 0x04010400u);  // e4, e5
+    r.w = __builtin_amdgcn_perm(T::HI, hi, 0x04030402u);  // e6, e7
+    return r;
+}
+
+// One reordered word (8 nibbles) -> 8 operand elements BASE + q, K order
+// (the zero point is left to the accumulator's starting value): the
+// unpack8 scheme without the per-byte zero add.
+template <typename T>
+__device__ __forceinline__ uint4 unpack8_q(uint32_t w) {
+    const uint32_t lo = w & 0x0F0F0F0Fu;
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+    uint4 r;
     r.x = __builtin_amdgcn_perm(T::HI, lo, 0x04010400u);  // e0, e1
     r.y = __builtin_amdgcn_perm(T::HI, lo, 0x04030402u);  // e2, e3
     r.z = __builtin_amdgcn_perm(T::HI, hi, 0x04010400u);  // e4, e5

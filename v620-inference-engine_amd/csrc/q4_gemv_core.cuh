@@ -160,6 +160,12 @@ struct XRegs {
     __device__ __forceinline__ uint4 get(int j) const { return j == 0 ? v0 : j == 1 ? v1 : j == 2 ? v2 : v3; }
 };
 
+// i / d for 0 <= i < 2^20 and 1 <= d < 2^16 without an integer division
+// (a ~40-instruction sequence on the GPU): (i + 0.5) / d is at least 0.5 / d
+// away from an integer, and rd = rcp(d) (within 1 ulp) leaves a relative
+// error of a few 2^-24, far inside that margin.
+__device__ __forceinline__ int div_small(int i, float rd) { return int((float(i) + 0.5f) * rd); }
+
 // Activation rows through registers: thread t takes pieces t, t + nt, ...
 // of the M x K/8 pieces (XPT >= M * K / 8 / blockDim.x, XPT <= 4). Issued
 // before the weight loads; unlike direct-to-LDS loads (after which the
@@ -170,9 +176,10 @@ template <int XPT>
 __device__ __forceinline__ void stage_regs_issue(const uint16_t *x, int xs, int M, int K, XRegs &xv) {
     static_assert(XPT >= 1 && XPT <= 4, "up to 4 pieces per thread");
     const int kn = K / 8, P = M * kn, nt = blockDim.x;
+    const float rkn = __builtin_amdgcn_rcpf(float(kn));
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
-        const int i = min(int(threadIdx.x) + j * nt, P - 1), m = i / kn, c = i - m * kn;
+        const int i = min(int(threadIdx.x) + j * nt, P - 1), m = div_small(i, rkn), c = i - m * kn;
         xv.set(j, *reinterpret_cast<const uint4 *>(x + int64_t(m) * xs + c * 8));
     }
 }
@@ -181,12 +188,13 @@ __device__ __forceinline__ void stage_regs_issue(const uint16_t *x, int xs, int 
 template <int XPT>
 __device__ __forceinline__ void stage_regs_commit(const XRegs &xv, int M, int K, uint4 *xl) {
     const int kn = K / 8, kc = x_row_stride(K), P = M * kn, nt = blockDim.x;
+    const float rkn = __builtin_amdgcn_rcpf(float(kn));
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
         // unconditional store (a thread past the end rewrites the last piece
         // with the same value): a conditional one lets the compiler sink the
         // load down to it, behind the weight loads and their wait
-        const int i = min(int(threadIdx.x) + j * nt, P - 1), m = i / kn, c = i - m * kn;
+        const int i = min(int(threadIdx.x) + j * nt, P - 1), m = div_small(i, rkn), c = i - m * kn;
         xl[m * kc + c] = xv.get(j);
     }
 }
@@ -236,6 +244,104 @@ __device__ __forceinline__ void group_bias(const uint4 *const (&xr)[MB], XpFn xp
                     pc[c][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int t = 0; t < 4; ++t) pc[c][mb] = mfma16<T>(xr[mb][g * 16 + t], negb, pc[c][mb]);
+                }
+            }
+        }
+    }
+}
+
+// Sum of the activations over each of a wave's groups g0 .. g0 + n - 1
+// (n <= GW), per token row, for the zero-point start of the group's product
+// (compute_zq): an MFMA chain of the group's four 32-element slices against
+// a splat of 1 (exact products, fp32 sums), on the staged activations only,
+// so it runs while the weights are in flight. sums[c][mb] is in the MFMA
+// result layout (lane: rows 4 (l / 16) + r of row block mb).
+// P4 (at most 4 token rows, MB == 1): four groups share one chain. Row
+// 4c + m of such a tile holds token m of group gb + c (xp_of(gb): the lane's
+// fragment of the tile starting at group gb), so each row goes through
+// exactly the arithmetic it gets in a tile of its own, and 4 MFMAs serve what
+// would take 16; the sums of rows r < MR are read out per (group, token) into
+// element r of every lane (wave-uniform values).
+template <typename T, int MB, int GW, bool P4, int MR, class XpFn>
+__device__ __forceinline__ void group_sums(const uint4 *const (&xr)[MB], XpFn xp_of, int g0, int n,
+                                           f32x4 (&sums)[GW][MB]) {
+    const uint4 one = make_uint4(T::ONE, T::ONE, T::ONE, T::ONE);
+    if constexpr (P4) {
+        static_assert(MB == 1 && GW % 4 == 0, "packed sums: one row block, whole tiles of four groups");
+#pragma unroll
+        for (int tl = 0; tl < GW / 4; ++tl) {
+            if (4 * tl < n) {
+                const uint4 *xp = xp_of(g0 + 4 * tl);
+                f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) c = mfma16<T>(xp[t], one, c);
+                const float cv[4] = {c[0], c[1], c[2], c[3]};
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        sums[4 * tl + g][0][r] =
+                            r < MR ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv[r]), 16 * g))
+                                   : 0.f;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < GW; ++c) {
+            if (c < n) {
+                const int g = g0 + c;
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    sums[c][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) sums[c][mb] = mfma16<T>(xr[mb][g * 16 + t], one, sums[c][mb]);
+                }
+            }
+        }
+    }
+}
+
+// NS subtiles over the same groups (wr[j] fetched with equal g0 and n): per
+// group, as its weights arrive, the product of the activations with the
+// operands BASE + q (unpack8_q) onto a start of -(BASE + z) * sum(x), which
+// leaves sum x * (q - z) (every product exact in fp32), times the group
+// scale into acc. Only elements r < MR of the last row block are formed
+// (rows past the batch are never read).
+template <typename T, int MB, int NS, int GW, bool HAS_Z, bool CH4, int MR>
+__device__ __forceinline__ void compute_zq(const WaveRange<GW, HAS_Z, CH4> (&wr)[NS], const uint4 *const (&xr)[MB],
+                                           const f32x4 (&sums)[GW][MB], f32x4 (&acc)[NS][MB]) {
+    const int g0 = wr[0].g0, n = wr[0].n;
+#pragma unroll
+    for (int c = 0; c < GW; ++c) {
+        if (c < n) {
+            const int g = g0 + c;
+            uint4 a[MB][4];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) a[mb][t] = xr[mb][g * 16 + t];
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                const float nz = -(T::BASE + float(HAS_Z ? Q4Tile::zero_of(wr[j].zv[c], g) : 8u));
+                const uint32_t sbits = wr[j].sv[c];
+                uint4 b[4];
+                b[0] = unpack8_q<T>(wr[j].w[c].x);
+                b[1] = unpack8_q<T>(wr[j].w[c].y);
+                b[2] = unpack8_q<T>(wr[j].w[c].z);
+                b[3] = unpack8_q<T>(wr[j].w[c].w);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    constexpr int R = 4;
+                    const int rows = mb == MB - 1 ? MR : R;
+                    f32x4 p;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) p[r] = r < rows ? sums[c][mb][r] * nz : 0.f;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) p = mfma16<T>(a[mb][t], b[t], p);
+                    const float sc = f16_bits_to_f32(uint16_t(sbits));
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        if (r < rows) acc[j][mb][r] += sc * p[r];
                 }
             }
         }
