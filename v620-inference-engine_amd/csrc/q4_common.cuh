@@ -59,6 +59,16 @@ struct F16 {
     typedef f16x8 vec;
 };
 
+// Waits until at most N vector-memory loads of this wave are in flight
+// (loads complete in order: everything issued before the last N is done),
+// without waiting on LDS or scalar traffic. For direct-to-LDS loads followed
+// by loads that must stay in flight: a fence would wait for all of them.
+template <int N>
+__device__ __forceinline__ void wait_vm_below() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // LDS-only barrier: orders this block's LDS traffic without draining the
 // global-memory loads in flight.
 __device__ __forceinline__ void lds_barrier() {

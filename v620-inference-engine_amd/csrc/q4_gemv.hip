@@ -29,6 +29,9 @@ namespace qwq4 {
 // passes of GW.
 
 constexpr int DENSE_GW = 4;
+#ifndef XREG_STAGING
+#define XREG_STAGING 1
+#endif
 
 // partial sums: one slot per wave that is not a k-part 0, double-buffered
 __host__ __device__ inline int red_slots(int waves, int KS) { return waves - waves / KS; }
@@ -134,7 +137,11 @@ __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t
         stage_regs_commit<XPT>(xv, M, K, xl);
         lds_barrier();
     } else {
-        __syncthreads();
+        // the direct loads of the activations are this wave's oldest loads in
+        // flight: wait for them alone, then for every wave's
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm_below<WaveRange<GW, HAS_Z, CH4>::LOADS>();
+        __builtin_amdgcn_s_barrier();
     }
     const uint4 *xr[MB];
 #pragma unroll
@@ -230,7 +237,7 @@ static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
         // below (151936 rows at batch 4: 60 against 65 us; at batches 1-3
         // the register path stays ahead: 51 against 58 at batch 1, 57.5
         // against 59 at batch 3)
-        bool regs = xpt <= 4;
+        bool regs = xpt <= 4 && XREG_STAGING;
         if (regs && a.M >= 4 && gpk <= DENSE_GW) {
             auto pf = q4_gemv_block_kernel<NW, MB, HAS_Z, CH4, true, KSNW, 0, P4, MR>;
             const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);

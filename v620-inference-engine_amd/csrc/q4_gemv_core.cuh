@@ -97,6 +97,8 @@ __device__ __forceinline__ void dense_group(const uint4 &w, uint32_t zb, float s
 // the loads.)
 template <int GW, bool HAS_Z, bool CH4 = false>
 struct WaveRange {
+    // vector-memory instructions fetch() issues
+    static constexpr int LOADS = CH4 ? GW / 4 * (HAS_Z ? 2 : 1) + GW : GW * (HAS_Z ? 3 : 2);
     uint4 w[GW];
     uint32_t sv[GW], zv[GW];
     int g0, n;
