@@ -158,6 +158,14 @@ struct Q4Tile {
     }
     // lane's 16 bytes of group g, its row's scale and zero
     __device__ __forceinline__ uint4 word4(int g, int lane) const { return w[g * 64 + lane]; }
+    // the same as a streaming (non-temporal) load: weights are read once per
+    // launch, so they should not displace the activations (read by every
+    // block) from the caches
+    __device__ __forceinline__ uint4 word4_stream(int g, int lane) const {
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + g * 64 + lane));
+        return make_uint4(v[0], v[1], v[2], v[3]);
+    }
     __device__ __forceinline__ uint16_t scale(int g, int n) const { return s[(g >> 2) * 64 + n * 4 + (g & 3)]; }
     // the 16-bit zero word holding group g's zero (z must be non-null); the
     // zero itself is zero_of(word, g)

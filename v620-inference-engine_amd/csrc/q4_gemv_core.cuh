@@ -133,7 +133,7 @@ struct WaveRange {
             }
         }
 #pragma unroll
-        for (int c = 0; c < GW; ++c) w[c] = t.word4(g0 + min(c, n - 1), lane);
+        for (int c = 0; c < GW; ++c) w[c] = t.word4_stream(g0 + min(c, n - 1), lane);
     }
     template <typename T, int MB>
     __device__ __forceinline__ void compute(const uint4 *const (&xr)[MB], f32x4 (&acc)[MB]) const {
