@@ -31,9 +31,10 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
 L_LAYERS = 24
 BATCHES = (1, 2, 4, 6, 8)
-DOM_BATCHES = (1, 2, 4)
-# name prefix of the dominant launches' instantiations (batch 1 and batches 2/4)
-DOM_KERNEL = "q4_gemv_block_kernel<8, 1, true, true, false, true"
+DOM_BATCHES = BATCHES
+# name prefix of the dominant launches' instantiations (every batch: 8-wave
+# blocks, one 16-row tile of tokens, zero points, whole 4-group chunks)
+DOM_KERNEL = "q4_gemv_block_kernel<8, 1, true, true"
 H, QKV, FFN_DOWN_K, VOCAB = 4096, 12288, 6144, 151936
 
 
@@ -170,9 +171,7 @@ def bench_gemv(torch, qwq4, dev, steps, warmup):
         "per_batch": per_m,
         "bytes_per_step_weights": step_bytes_w,
         "launches_per_step": 2 * L_LAYERS + 1,
-        # roofline subset: batches 1, 2, 4 (one item per block; activations
-        # through registers at batch 1, direct to LDS at 2 and 4); 6 and 8 run
-        # the prefetching instantiation
+        # roofline over every batch of the sweep
         "dominant": {"shape": f"{H}->{QKV}", "batches": list(DOM_BATCHES),
                      "avg_launch_us": sum(dom_us[BATCHES.index(m)] for m in DOM_BATCHES) / len(DOM_BATCHES),
                      "avg_bytes_per_launch": sum(dom_bytes[BATCHES.index(m)] for m in DOM_BATCHES) / len(DOM_BATCHES),
@@ -341,27 +340,72 @@ def measured_traffic():
 
 
 # ------------------------------------------------------------ CPU baseline
-def cpu_baseline(budget_s=12.0):
-    """The C oracle (oracle/q4_oracle.c, the reference's expert_linear scheme) on
-    the host cores: decode step at M=1 on a 2-layer + LM-head sample."""
+def host_cores():
+    """CPUs this process may run on: the affinity mask, capped by the cgroup
+    CPU quota when one is set (a GPU box grants each GPU's job a share of the
+    host, whatever the machine-wide count says)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def cpu_baseline(runs=5):
+    """The C oracle (oracle/q4_oracle.c, the reference's expert_linear scheme,
+    threaded over N with a grain of 16 rows like src/core/threadpool.hpp:38-58)
+    on every host core this job has: one warm-up, then the median of `runs`
+    timed passes of (a) the decode step at M=1 on a 2-layer + LM-head sample
+    and (b) config 1 (4096x4096, M=1, fp32 x)."""
+    import statistics
     from oracle import oracle as o
     from qwq4 import synth
-    threads = min(os.cpu_count() or 1, 16)
+    threads = host_cores()
     mats = [(QKV, H), (H, FFN_DOWN_K)] * 2 + [(VOCAB, H)]
     ws = [synth.q4_weights(7, f"cpu{i}", N, K) for i, (N, K) in enumerate(mats)]
     xs = {K: synth.acts(7, f"cx{K}", 1, K)[1] for K in (H, FFN_DOWN_K)}
     nbytes = sum(q4_bytes(N, K) for N, K in mats)
-    runs, t0 = 0, time.perf_counter()
-    while True:
+
+    def one_step():
         for (N, K), (W, S, Z) in zip(mats, ws):
             o.q4_linear(W, S, Z, N, K, xs[K], threads=threads)
-        runs += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": nbytes * runs / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"oracle q4_linear, M=1, 2 layers (4096->12288, 6144->4096) + LM head 4096->151936, "
-                      f"{runs} passes in {dt:.1f} s"}
+
+    t0 = time.perf_counter()
+    one_step()
+    reps = max(1, int(2.0 / max(time.perf_counter() - t0, 1e-4)))  # ~2 s per timed run
+
+    def step_pass():
+        for _ in range(reps):
+            one_step()
+
+    W1, S1, Z1 = synth.q4_weights(7, "config1", H, H)
+    x1 = np.random.default_rng(7).standard_normal((1, H)).astype(np.float32)
+
+    def c1_pass():
+        for _ in range(200):
+            o.q4_linear(W1, S1, Z1, H, H, x1, threads=threads)
+
+    def median_s(fn):
+        fn()  # warm-up
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    t_step = median_s(step_pass) / reps
+    t_c1 = median_s(c1_pass) / 200
+    return {"value": nbytes / t_step / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle q4_linear on {threads} threads, M=1: one pass over 2 layers (4096->12288, "
+                      f"6144->4096) + LM head 4096->151936 ({nbytes / 1e6:.0f} MB of q4 weights); median of "
+                      f"{runs} runs of {reps} passes after 1 warm-up",
+            "config1": {"us": t_c1 * 1e6, "GB_s": q4_bytes(H, H) / t_c1 / 1e9,
+                        "sample": "4096x4096 q4 with zero points, M=1, fp32 x; median of "
+                                  f"{runs} runs of 200 calls after 1 warm-up"}}
 
 
 # ------------------------------------------------ HBM traffic (rocprofv3 PMC)
@@ -484,7 +528,7 @@ def main():
         ach = d["avg_bytes_per_launch"] / (d["avg_launch_us"] * 1e-6) / 1e9
         line["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                            "kernel": DOM_KERNEL + ", 1|2|4, true> (4096->12288, batch 1/2/4; the middle value is activation pieces per thread)",
+                            "kernel": DOM_KERNEL + ", ...> (4096->12288, every batch of the sweep)",
                             "avg_launch_us": round(d["avg_launch_us"], 3),
                             "algorithmic_bytes_per_launch": int(d["avg_bytes_per_launch"])}
     line["workloads"] = res

@@ -88,7 +88,12 @@ int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
  * q4 weights): Y[t][n] = sum_k X[t][k] * W[n][k], t < T. X bf16 rows of stride
  * ldx; Y fp32 or bf16 rows of stride ldy. `workspace` (device memory of at
  * least qw_q4_gemm_workspace_size(T, K) bytes, 256-byte aligned) is scratch
- * for the activation pre-pass; it holds nothing between calls. */
+ * for the activation pre-pass; it holds nothing between calls.
+ * Numerics: X runs through the MFMAs as fp16 (the reference's prefill rows
+ * are fp16, src/engine/prefill.hip): exact for |x| in the fp16 normal range;
+ * finite |x| > 65504 saturates to +-65504, infinities and NaN pass through
+ * (a NaN in row t makes row t of Y NaN); weights are fp16((q - z) * s);
+ * sums in fp32. */
 size_t qw_q4_gemm_workspace_size(int T, int K);
 int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *X, int ldx, int T, void *Y,
                int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream);
@@ -135,7 +140,8 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
  * tile_m = qw_moe_grouped_tile_m() (mixed tiles, -64: 256, 128 and 64
  * slots). workspace: at least
  * qw_moe_grouped_workspace_size(...) bytes (an fp16 copy of x),
- * 256-byte aligned. */
+ * 256-byte aligned. x and h pass through fp16 as in qw_q4_gemm (finite
+ * values beyond +-65504 saturate, infinities and NaN pass through). */
 int qw_moe_grouped_tile_m(void);
 size_t qw_moe_grouped_workspace_size(int T, int topk, int E, int H, int F);
 int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,

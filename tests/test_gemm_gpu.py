@@ -128,3 +128,27 @@ def test_gemm_random_shapes(gpu, oracle, T, N, K, zeros, y_bf16):
         assert bf16_err_ok(got, ref)
     else:
         assert rel_err(got, ref) <= TOL
+
+
+def test_gemm_saturation_and_nonfinite(gpu, oracle):
+    """Stated behaviour of the fp16 activation path: finite |x| > 65504
+    saturates to +-65504 (output equals the oracle on the clipped x), and NaN
+    or infinity in a row is carried into that row's outputs, not replaced."""
+    T, N, K = 8, 256, 512
+    W, S, Z = synth.q4_weights(57, "sat", N, K)
+    xf = np.random.default_rng(57).standard_normal((T, K)).astype(np.float32)
+    xf[1, 3] = 1.0e6
+    xf[2, 100] = -3.0e5
+    xb = synth.bf16_bits(xf)
+    xf = synth.bf16_to_f32(xb)
+    xb_bad = xb.copy()
+    xb_bad[5, 7] = 0x7fc0          # NaN
+    xb_bad[6, 9] = 0x7f80          # +inf
+    dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
+    Y = host(qwq4.gemm(dW, dS, dZ, to_dev(xb_bad, gpu), N, K))
+    clipped = np.clip(xf, -65504.0, 65504.0)
+    ok = [0, 1, 2, 3, 4, 7]
+    ref = oracle.q4_linear(W, S, Z, N, K, clipped[ok])
+    assert rel_err(Y[ok], ref) <= TOL
+    assert np.all(np.isnan(Y[5]))
+    assert np.all(~np.isfinite(Y[6]))

@@ -59,8 +59,13 @@ def test_gemv_bf16_out_is_rne_of_fp32(gpu, oracle):
     assert bf16_err_ok(host(y16), oracle.q4_linear(W, S, Z, N, K, xf))
 
 
-def test_gemv_lm_head(gpu, oracle):
-    N, K, M = 151936, 4096, 2
+@pytest.mark.parametrize("M", [1, 2, 4, 6, 8])
+def test_gemv_lm_head(gpu, oracle, M):
+    """The LM head at every benchmarked batch: batches 4-8 run the persistent
+    prefetching kernel (blocks take items grid-stride), 1-2 one item per
+    block over many rounds."""
+    N, K = 151936, 4096
+    print(f"gemv lm head M={M}", flush=True)
     (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M)
     y = host(qwq4.gemv(dW, dS, dZ, dx, N, K, M, y_bf16=True))
     r = oracle.q4_linear(W, S, Z, N, K, xf)

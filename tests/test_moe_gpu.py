@@ -29,9 +29,8 @@ def test_route_bit_exact(gpu, oracle, T, E, k):
     r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=32 if T > 64 else 0)
     te, tw = oracle.route(l, k)
     assert np.array_equal(host(r.top_e), te)
-    # weights are fp: the device exp is correctly rounded, the C library's expf
-    # (what the reference calls) is off by one ulp for ~0.1% of inputs
-    assert np.max(np.abs(host(r.top_w) - tw) / tw) <= 4 * 2.0**-24
+    # the device evaluates the C library's expf algorithm: weights bit-exact
+    assert np.array_equal(host(r.top_w).view(np.uint32), tw.view(np.uint32))
     counts, offsets, tok_slot, pair_tok = oracle.moe_slots(te, E)
     assert np.array_equal(host(r.counts), counts)
     assert np.array_equal(host(r.offsets), offsets)
@@ -44,6 +43,60 @@ def test_route_bit_exact(gpu, oracle, T, E, k):
         want = [(e, m0) for e in range(E) for m0 in range(0, counts[e], 32)]
         got = list(zip(host(r.tile_e)[:nt], host(r.tile_m0)[:nt]))
         assert got == want
+
+
+# Adjacent floats (d_small, d_large) = bit patterns (u, u - 1) in [-1, 0)
+# where the C library's expf and the correctly rounded exp disagree on
+# whether exp(d_small) == exp(d_large): a tie under one rounding and not under
+# the other, so the (p desc, index asc) order differs. An exhaustive
+# comparison of the two over [-4, 0) finds 127,332 such pairs, none below -1;
+# these are the first two of each binade from 2^-6 up (the tie flag is
+# glibc's). tests/test_oracle.py checks them against the host's expf.
+EXPF_TIE_PAIRS = [
+    (0xbc8000bf, True), (0xbc8000c0, False), (0xbd000aa1, True), (0xbd000aa2, False),
+    (0xbd801976, True), (0xbd801977, False), (0xbe0000d8, True), (0xbe0000d9, False),
+    (0xbe801e5d, True), (0xbe801e5e, False), (0xbf001f30, True), (0xbf001f31, False),
+]
+
+
+def _f32(u):
+    return np.array([u], np.uint32).view(np.float32)[0]
+
+
+@pytest.mark.parametrize("k", [2, 3])
+def test_route_expf_tie_order(gpu, oracle, k):
+    """Adversarial routing: the larger of two logits sits at the higher
+    index, and the two exponentials tie under the C library's expf but not
+    under the correctly rounded exp (or the reverse). The reference orders by
+    (p desc, index asc), so the pick depends on that rounding: the device must
+    choose what the CPU path (glibc's expf) chooses."""
+    rows = []
+    for u, _ in EXPF_TIE_PAIRS:
+        for lead in (0.0, 0.25):
+            row = np.full(16, -8.0, np.float32)
+            row[0] = lead            # the maximum (lead 0: d exact; 0.25: shifted copies)
+            row[5] = lead + _f32(u)        # d_small, lower index
+            row[9] = lead + _f32(u - 1)    # d_large, higher index
+            row[12] = lead + _f32(u)       # a third copy of d_small
+            rows.append(row)
+    l = np.stack(rows)
+    r = qwq4.moe_route(to_dev(l, gpu), k)
+    te, tw = oracle.route(l, k)
+    assert np.array_equal(host(r.top_e), te)
+    assert np.array_equal(host(r.top_w).view(np.uint32), tw.view(np.uint32))
+
+
+def test_route_weights_bit_exact_dense(gpu, oracle):
+    """Every expert selected (k = E) over logits near the maximum, where most
+    exponentials are computed: the weights p / sum p equal the CPU path's bit
+    for bit, so every p does."""
+    T, E = 512, 64
+    r0 = np.random.default_rng(5)
+    l = (r0.uniform(-4.0, 0.0, size=(T, E)) + r0.normal(0.0, 0.001, size=(T, 1))).astype(np.float32)
+    r = qwq4.moe_route(to_dev(l, gpu), E)
+    te, tw = oracle.route(l, E)
+    assert np.array_equal(host(r.top_e), te)
+    assert np.array_equal(host(r.top_w).view(np.uint32), tw.view(np.uint32))
 
 
 def _mixed_tiles(counts, g):

@@ -9,6 +9,7 @@ import pytest
 from qwq4 import synth
 
 GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz"))
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 # ---------------------------------------------------------------- numbers
@@ -207,3 +208,43 @@ def test_tile_against_numpy_restatement(oracle, N, K, zeros):
         z[:, :G] = synth.unpack_zeros(Z, G)
         zt = (z.reshape(N, GC, 4) << (4 * np.arange(4, dtype=np.uint16))).sum(-1).astype(np.uint16)
         assert np.array_equal(Zt, zt.reshape(N // 16, 16, GC).transpose(0, 2, 1).reshape(-1))
+
+
+def _libm_expf():
+    import ctypes
+    import ctypes.util
+    m = ctypes.CDLL(ctypes.util.find_library("m"))
+    m.expf.argtypes = [ctypes.c_float]
+    m.expf.restype = ctypes.c_float
+    return m.expf
+
+
+def test_expf_tie_pairs_are_rounding_conflicts():
+    """The adversarial routing pairs (test_moe_gpu.EXPF_TIE_PAIRS) really are
+    pairs of adjacent floats whose exponentials tie under the C library's
+    expf (what the reference's std::exp on a float calls) and not under the
+    correctly rounded exp, or the reverse."""
+    from test_moe_gpu import EXPF_TIE_PAIRS
+    expf = _libm_expf()
+    for u, glibc_tie in EXPF_TIE_PAIRS:
+        d_small, d_large = np.array([u, u - 1], np.uint32).view(np.float32)
+        g = (np.float32(expf(float(d_small))), np.float32(expf(float(d_large))))
+        c = (np.float32(np.exp(np.float64(d_small))), np.float32(np.exp(np.float64(d_large))))
+        assert (g[0] == g[1]) == glibc_tie
+        assert (c[0] == c[1]) != glibc_tie
+
+
+def test_device_expf_table_is_nearest_powers_of_two():
+    """The 32-entry table of the device's expf (csrc/moe_route.hip) holds the
+    doubles nearest 2^(i/32), i << 47 subtracted from their bits."""
+    import re
+    import struct
+    from decimal import Decimal, getcontext
+    src = open(os.path.join(ROOT, "v620-inference-engine_amd", "csrc", "moe_route.hip")).read()
+    body = src[src.index("kExp2Tab32[32] = {"):]
+    vals = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{16})ull", body[:body.index("};")])]
+    assert len(vals) == 32
+    getcontext().prec = 60
+    for i, v in enumerate(vals):
+        exact = float(Decimal(2) ** (Decimal(i) / Decimal(32)))
+        assert (v + (i << 47)) & (2**64 - 1) == struct.unpack("<Q", struct.pack("<d", exact))[0]

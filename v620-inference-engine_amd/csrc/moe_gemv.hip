@@ -29,9 +29,7 @@ __host__ __device__ inline size_t moe_lds_bytes(int R, int K) {
 }
 
 __device__ __forceinline__ uint16_t silu_mul_f16(float g, float u) {
-    float v = g / (1.f + __expf(-g)) * u;
-    v = fminf(fmaxf(v, -65504.f), 65504.f);
-    return __builtin_bit_cast(uint16_t, _Float16(v));
+    return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(g / (1.f + __expf(-g)) * u));
 }
 
 // Reads the block's expert: n_active and active[y] are requested together

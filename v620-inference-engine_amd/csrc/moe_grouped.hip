@@ -30,8 +30,7 @@ int moe_grouped_tile_m() { return GROUPED_TILE_M; }
 size_t moe_grouped_workspace_bytes(int T, int, int, int H, int) { return gemm_workspace_bytes(T, H); }
 
 static __device__ __forceinline__ uint16_t f32_to_f16_sat(float v) {
-    v = fminf(fmaxf(v, -65504.f), 65504.f);
-    return __builtin_bit_cast(uint16_t, _Float16(v));
+    return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(v));
 }
 
 static __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + __expf(-g)) * u; }

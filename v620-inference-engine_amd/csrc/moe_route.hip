@@ -7,19 +7,72 @@
 // moe_route.hip:28-58, fills slots with atomics and is nondeterministic; this
 // one is not).
 //
-//   p_e      = float(exp(l_e - max l))                      per token
+//   p_e      = expf(l_e - max l)                            per token
 //   top k    by (p descending, expert index ascending)
 //   w_i      = float(double(p_i) / sum_{j<k} double(p_j))    sum in selection order
 //   slots    experts ascending; within an expert, tokens ascending
 //
-// exp is evaluated in double and rounded once to float, i.e. the correctly
-// rounded expf the CPU path uses, so selection and weights match it bit for
-// bit.
+// expf is the C library's: the reference calls std::exp on a float
+// (ref_model.cpp:418), i.e. glibc's expf, which is not correctly rounded (it
+// returns the other neighbour of the exact value for ~74,000 of the floats in
+// [-4, 0)). Where two logits' exponentials are equal under one rounding and
+// not under the other, the (p, index) order picks different experts, so the
+// device evaluates glibc's algorithm itself (expf_glibc below) and matches the
+// CPU path bit for bit: selection, order and weights.
 
 #include "q4_common.cuh"
 #include "q4_kernels.hpp"
 
 namespace qwq4 {
+
+// ---- glibc's expf (glibc 2.28 and later; the algorithm of ARM's
+// optimized-routines expf): with N = 32, x * N / ln 2 = k + r, |r| <= 1/2,
+// exp(x) = 2^(k/N) * 2^(r/N), 2^(k/N) from a table of 2^(i/N) (i = k mod N,
+// the integer part of k / N added to the exponent bits), 2^(r/N) by the
+// cubic 1 + C2 r + C1 r^2 + C0 r^3, all in double, rounded to float once.
+// Table entry i is the double nearest 2^(i/32) with i << 47 subtracted from
+// its bits (so adding k << 47 scales it by 2^(k div 32)). The result equals
+// the C library's expf on every float in [-4, 0) and on a sample below (a
+// test compares them); for x below ln(2^-150) it is 0, as there.
+__device__ const uint64_t kExp2Tab32[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+struct ExpfGlibc {
+    uint32_t lo, hi;  // this lane's table entry, lane % 32
+    __device__ __forceinline__ void load(int lane) {
+        const uint64_t t = kExp2Tab32[lane & 31];
+        lo = uint32_t(t);
+        hi = uint32_t(t >> 32);
+    }
+    // every lane of the wave must call it (the table lookup is a cross-lane
+    // permute)
+    __device__ __forceinline__ float operator()(float x) const {
+#pragma clang fp contract(off)
+        constexpr double InvLn2N = 0x1.71547652b82fep+0 * 32, Shift = 0x1.8p+52;
+        constexpr double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                         C2 = 0x1.62e42ff0c52d6p-1 / 32;
+        const double z = InvLn2N * double(x);
+        double kd = z + Shift;
+        const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+        kd -= Shift;
+        const double r = z - kd;
+        const int src = int(ki & 31) * 4;
+        const uint64_t t = ((uint64_t(uint32_t(__builtin_amdgcn_ds_bpermute(src, int(hi)))) << 32) |
+                            uint32_t(__builtin_amdgcn_ds_bpermute(src, int(lo)))) +
+                           (ki << 47);
+        const double sc = __builtin_bit_cast(double, t);
+        const double zz = __builtin_fma(C0, r, C1), r2 = r * r;
+        const double y = __builtin_fma(zz, r2, __builtin_fma(C2, r, 1.0)) * sc;
+        return x < -0x1.9fe368p6f ? 0.f : float(y);
+    }
+};
 
 
 // ---- wave-wide reductions and scans on DPP (row-local lane permutes, no
@@ -105,6 +158,8 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t x) {
 // j < k ends with the j-th selection.
 template <int PER, class LogitFn>
 __device__ __forceinline__ void topk_wave(LogitFn logit, int E, int k, int lane, int32_t *te, float *tw) {
+    ExpfGlibc ex;
+    ex.load(lane);
     float v[PER];
     float mx = -INFINITY;
 #pragma unroll
@@ -118,7 +173,7 @@ __device__ __forceinline__ void topk_wave(LogitFn logit, int E, int k, int lane,
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int idx = lane + WAVE * i;
-        const float p = float(exp(double(v[i] - mx)));
+        const float p = ex(v[i] - mx);
         key[i] = idx < E ? (uint64_t(__builtin_bit_cast(uint32_t, p)) << 32) | uint32_t(~uint32_t(idx)) : 0ull;
     }
     double top = 0.0;

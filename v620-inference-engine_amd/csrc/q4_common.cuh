@@ -139,6 +139,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return uint16_t(u >> 16);
 }
 
+// fp32 -> fp16 for the fp16 MFMA operands and intermediates: finite values
+// beyond the fp16 range saturate to +-65504 (the reference's bf16_to_f16
+// rule, src/engine/weight_convert.cpp:19-26); infinities and NaN pass
+// through, so a diverging activation stays visible in the output.
+__device__ __forceinline__ _Float16 f32_to_f16_satfinite(float v) {
+    const bool finite = __builtin_isfinite(v);
+    return _Float16(finite ? fminf(fmaxf(v, -65504.f), 65504.f) : v);
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __builtin_bit_cast(float, uint32_t(b) << 16); }
 
 __device__ __forceinline__ int group_zero(const uint32_t *Z, int64_t row, int zw, int g) {

@@ -6,8 +6,8 @@
 // Numerics. Each weight is dequantised once, w = fp16((q - z) * s) (the
 // subtraction exact, one rounding for the product), the way the reference's
 // grouped expert GEMM does (src/kernels/moe_experts.hip:31-42). X is
-// converted to fp16 by a pre-pass (exact for |x| in the fp16 normal range,
-// saturated at +-65504). Products and sums run on the fp16 MFMA with fp32
+// converted to fp16 by a pre-pass (exact for |x| in the fp16 normal range;
+// finite values beyond it saturate at +-65504, infinities and NaN pass). Products and sums run on the fp16 MFMA with fp32
 // accumulation. Rounding the dequantised weights to bf16 instead would cost
 // ~1.4e-3 of max|y| (close to the 2e-3 bar); fp16 costs ~2e-4.
 //
@@ -25,7 +25,7 @@ size_t gemm_workspace_bytes(int T, int K) {
     return (xh + 255) & ~size_t(255);
 }
 
-// bf16 -> fp16 (saturating), 8 elements per thread.
+// bf16 -> fp16 (finite values saturate, inf and NaN pass), 8 elements per thread.
 __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t *__restrict__ X, int ldx, int T, int K,
                                                        uint16_t *__restrict__ Xh) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -38,11 +38,9 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t *__restric
     uint32_t o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        float a = bf16_bits_to_f32(uint16_t(w[j])), b = bf16_bits_to_f32(uint16_t(w[j] >> 16));
-        a = fminf(fmaxf(a, -65504.f), 65504.f);
-        b = fminf(fmaxf(b, -65504.f), 65504.f);
-        o[j] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(a))) |
-               (uint32_t(__builtin_bit_cast(uint16_t, _Float16(b))) << 16);
+        const float a = bf16_bits_to_f32(uint16_t(w[j])), b = bf16_bits_to_f32(uint16_t(w[j] >> 16));
+        o[j] = uint32_t(__builtin_bit_cast(uint16_t, f32_to_f16_satfinite(a))) |
+               (uint32_t(__builtin_bit_cast(uint16_t, f32_to_f16_satfinite(b))) << 16);
     }
     *reinterpret_cast<uint4 *>(Xh + t * K + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
 }
