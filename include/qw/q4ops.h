@@ -78,30 +78,35 @@ int qw_q4_untile(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt, int
 /* Decode GEMV (replaces gpu::gemv_rows, src/kernels/gemv.hpp:13-14), tiled
  * weights (Wt, St, Zt or NULL):
  *   y[m*ys + n] (+)= sum_k W[n][k] * x[m*xs + k],   m < M, n < N
- * x bf16 rows of stride xs (elements, a multiple of 8, x 16-byte aligned);
- * y fp32 (y_bf16 = 0) or bf16 (y_bf16 = 1, round to nearest even) rows of
- * stride ys; accumulate != 0 adds to y. 1 <= M <= 32. */
-int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *x, int xs, void *y, int ys,
-               int y_bf16, int N, int K, int M, int accumulate, void *stream);
+ * x rows of stride xs (elements, a multiple of 8, x 16-byte aligned): bf16
+ * (x_f16 = 0) or fp16 (x_f16 = 1, the engine's decode rows,
+ * src/kernels/gemv.hpp:11-14); y fp32 (y_bf16 = 0) or bf16 (y_bf16 = 1,
+ * round to nearest even) rows of stride ys; accumulate != 0 adds to y.
+ * 1 <= M <= 32. Every product is exact, sums in fp32. */
+int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *x, int x_f16, int xs, void *y,
+               int ys, int y_bf16, int N, int K, int M, int accumulate, void *stream);
 
 /* Prefill GEMM (replaces gpu::gemm, src/kernels/gemm.hpp:14-15, with tiled
- * q4 weights): Y[t][n] = sum_k X[t][k] * W[n][k], t < T. X bf16 rows of stride
- * ldx; Y fp32 or bf16 rows of stride ldy. `workspace` (device memory of at
- * least qw_q4_gemm_workspace_size(T, K) bytes, 256-byte aligned) is scratch
- * for the activation pre-pass; it holds nothing between calls.
+ * q4 weights): Y[t][n] = sum_k X[t][k] * W[n][k], t < T. X rows of stride
+ * ldx, bf16 (x_f16 = 0) or fp16 (x_f16 = 1, the reference's prefill rows);
+ * Y fp32 or bf16 rows of stride ldy. For bf16 rows, `workspace` (device
+ * memory of at least qw_q4_gemm_workspace_size(T, K) bytes, 256-byte
+ * aligned) is scratch for the fp16 pre-pass; it holds nothing between calls.
+ * fp16 rows need none (workspace may be NULL).
  * Numerics: X runs through the MFMAs as fp16 (the reference's prefill rows
  * are fp16, src/engine/prefill.hip): exact for |x| in the fp16 normal range;
  * finite |x| > 65504 saturates to +-65504, infinities and NaN pass through
  * (a NaN in row t makes row t of Y NaN); weights are fp16((q - z) * s);
  * sums in fp32. */
 size_t qw_q4_gemm_workspace_size(int T, int K);
-int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *X, int ldx, int T, void *Y,
-               int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream);
+int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *X, int x_f16, int ldx, int T,
+               void *Y, int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Routing of T tokens over E experts (replaces gpu::moe_route_B for decode
  * rows and gpu::moe_route_T + moe_scatter_T for prefill, moe.hpp:17-27; math
  * of ref::Model::moe, src/ref/ref_model.cpp:412-431):
- *   p = float(exp(l - max l)); top k by (p desc, index asc);
+ *   p = expf(l - max l) (the C library's expf, evaluated bit for bit on the
+ *   device); top k by (p desc, index asc);
  *   top_w = float(p / sum of the k selected p, in double)
  * Outputs (all device int32 unless noted):
  *   top_e [T][k], top_w [T][k] (fp32), counts [E], offsets [E+1],
@@ -125,22 +130,23 @@ int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_
  *   h[p]  = silu(G_e x[pair_tok[p]]) * (U_e x[pair_tok[p]])     fp16 [T*k][F]
  *   yp[p] = D_e h[p]                                            fp32 [T*k][H]
  * Weights are tiled (qw_q4_tile) over the stacked experts: gate and up as one
- * [E*F][H] matrix each, down as [E*H][F]; zeros may be NULL. x bf16 [T][H].
+ * [E*F][H] matrix each, down as [E*H][F]; zeros may be NULL. x [T][H], bf16
+ * (x_f16 = 0) or fp16 (x_f16 = 1).
  * F and H multiples of 128. 1 <= T <= 32. Each expert's weights are read
  * once per call however many of the batch's tokens chose it. */
 int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
                         const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                         const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
-                        const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int T, int topk,
-                        uint16_t *h, float *yp, void *stream);
+                        const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int x_f16, int T,
+                        int topk, uint16_t *h, float *yp, void *stream);
 
 /* Grouped per-expert GEMMs for prefill chunks (replaces gpu::moe_experts_T,
  * moe.hpp:29-32): the same outputs as qw_moe_experts_gemv for any T, over
  * the (expert, tile) list qw_moe_route writes when called with
  * tile_m = qw_moe_grouped_tile_m() (mixed tiles, -64: 256, 128 and 64
- * slots). workspace: at least
- * qw_moe_grouped_workspace_size(...) bytes (an fp16 copy of x),
- * 256-byte aligned. x and h pass through fp16 as in qw_q4_gemm (finite
+ * slots). x [T][H] bf16 (x_f16 = 0) or fp16 (x_f16 = 1). For bf16 x,
+ * workspace: at least qw_moe_grouped_workspace_size(...) bytes (an fp16
+ * copy of x), 256-byte aligned; fp16 x needs none. x and h pass through fp16 as in qw_q4_gemm (finite
  * values beyond +-65504 saturate, infinities and NaN pass through). */
 int qw_moe_grouped_tile_m(void);
 size_t qw_moe_grouped_workspace_size(int T, int topk, int E, int H, int F);
@@ -148,8 +154,8 @@ int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_
                            const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                            const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
                            const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
-                           int T, int topk, uint16_t *h, float *yp, void *workspace, size_t workspace_bytes,
-                           void *stream);
+                           int x_f16, int T, int topk, uint16_t *h, float *yp, void *workspace,
+                           size_t workspace_bytes, void *stream);
 
 /* Weighted combine (replaces gpu::moe_combine_B/T, moe.hpp:42-46):
  *   out[t][j] = shared[t][j] + sum_{i<k} tok_w[t][i] * yp[tok_slot[t][i]][j]
@@ -173,12 +179,12 @@ int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, 
  * The router GEMV and routing share a launch; up to T = 4 the combine runs
  * inside the down projection, above that in a launch of its own. Outputs: out, logits [T][E], top_e, top_w, tok_slot [T][k],
  * h, yp (as qw_moe_experts_gemv). shared fp32 [T][H] or NULL (e.g. the shared
- * expert's output). 1 <= T <= 32.
+ * expert's output). x [T][H] bf16 (x_f16 = 0) or fp16 (x_f16 = 1). 1 <= T <= 32.
  * workspace: qw_moe_decode_workspace_size(...) bytes, 256-byte aligned, filled
  * with zeros once before its first use (it holds completion counters that
  * every call leaves at zero); calls that share a workspace must not overlap. */
 size_t qw_moe_decode_workspace_size(int T, int E, int topk, int H, int F);
-int qw_moe_decode(const float *router_w, const uint16_t *x, int T, int E, int topk, const uint32_t *gw,
+int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
                   const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
                   const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
                   void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,

@@ -79,12 +79,12 @@ int check_ckpt(const char *fn, const uint32_t *W, const uint16_t *S, int64_t N, 
 
 extern "C" {
 
-int qw_q4_abi_version(void) { return 1; }
+int qw_q4_abi_version(void) { return 2; }
 
 const char *qw_q4_last_error(void) { return g_err.c_str(); }
 
-int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *x, int xs, void *y, int ys,
-               int y_bf16, int N, int K, int M, int accumulate, void *stream) {
+int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *x, int x_f16, int xs, void *y,
+               int ys, int y_bf16, int N, int K, int M, int accumulate, void *stream) {
     if (int r = check_q4("qw_q4_gemv", W, S, N, K)) return r;
     REQUIRE(x && y, "qw_q4_gemv: null x or y");
     REQUIRE(M >= 1 && M <= 32, "qw_q4_gemv: M = %d outside 1..32", M);
@@ -92,6 +92,7 @@ int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
     REQUIRE(ys >= N || M == 1, "qw_q4_gemv: y stride %d < N", ys);
     REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_q4_gemv: y misaligned");
     qwq4::GemvArgs a{W, S, Z, x, xs, y, ys, y_bf16 != 0, N, K, M, accumulate != 0};
+    a.x_f16 = x_f16 != 0;
     qwq4::launch_gemv(a, st(stream));
     return launched("qw_q4_gemv");
 }
@@ -101,8 +102,8 @@ size_t qw_q4_gemm_workspace_size(int T, int K) {
     return qwq4::gemm_workspace_bytes(T, K);
 }
 
-int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *X, int ldx, int T, void *Y,
-               int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream) {
+int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *X, int x_f16, int ldx, int T,
+               void *Y, int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream) {
     if (int r = check_q4("qw_q4_gemm", W, S, N, K)) return r;
     REQUIRE(X && Y, "qw_q4_gemm: null X or Y");
     REQUIRE(T >= 1, "qw_q4_gemm: T = %d must be >= 1", T);
@@ -110,10 +111,11 @@ int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
     REQUIRE(ldy >= N, "qw_q4_gemm: ldy %d < N", ldy);
     REQUIRE(aligned(Y, 16) && ldy % (y_bf16 ? 8 : 4) == 0,
             "qw_q4_gemm: Y must be 16-byte aligned with rows of a multiple of 16 bytes (ldy %d)", ldy);
-    const size_t need = qwq4::gemm_workspace_bytes(T, K);
-    REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256),
+    const size_t need = x_f16 ? 0 : qwq4::gemm_workspace_bytes(T, K);
+    REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
             "qw_q4_gemm: workspace needs %zu bytes, 256-byte aligned (got %zu)", need, workspace_bytes);
     qwq4::GemmArgs a{W, S, Z, X, ldx, T, Y, ldy, y_bf16 != 0, N, K, workspace};
+    a.x_f16 = x_f16 != 0;
     qwq4::launch_gemm(a, st(stream));
     return launched("qw_q4_gemm");
 }
@@ -139,8 +141,8 @@ int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_
 int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
                         const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                         const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
-                        const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int T, int topk,
-                        uint16_t *h, float *yp, void *stream) {
+                        const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int x_f16, int T,
+                        int topk, uint16_t *h, float *yp, void *stream) {
     if (int r = check_q4("qw_moe_experts_gemv(gate)", gw, gs, int64_t(E) * F, H)) return r;
     if (int r = check_q4("qw_moe_experts_gemv(up)", uw, us, int64_t(E) * F, H)) return r;
     if (int r = check_q4("qw_moe_experts_gemv(down)", dw, ds, int64_t(E) * H, F)) return r;
@@ -151,6 +153,7 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
     REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(yp, 4), "qw_moe_experts_gemv: x/h must be 16-byte aligned");
     qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, offsets, active, n_active, pair_tok,
                         x, T, topk, h, yp};
+    a.x_f16 = x_f16 != 0;
     qwq4::launch_moe_gemv(a, st(stream));
     return launched("qw_moe_experts_gemv");
 }
@@ -166,8 +169,8 @@ int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_
                            const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                            const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
                            const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
-                           int T, int topk, uint16_t *h, float *yp, void *workspace, size_t workspace_bytes,
-                           void *stream) {
+                           int x_f16, int T, int topk, uint16_t *h, float *yp, void *workspace,
+                           size_t workspace_bytes, void *stream) {
     if (int r = check_q4("qw_moe_experts_grouped(gate)", gw, gs, int64_t(E) * F, H)) return r;
     if (int r = check_q4("qw_moe_experts_grouped(up)", uw, us, int64_t(E) * F, H)) return r;
     if (int r = check_q4("qw_moe_experts_grouped(down)", dw, ds, int64_t(E) * H, F)) return r;
@@ -175,11 +178,12 @@ int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_
             "qw_moe_experts_grouped: null pointer");
     REQUIRE(T >= 1 && topk >= 1 && topk <= E, "qw_moe_experts_grouped: T = %d, topk = %d", T, topk);
     REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(yp, 4), "qw_moe_experts_grouped: x/h must be 16-byte aligned");
-    const size_t need = qwq4::moe_grouped_workspace_bytes(T, topk, E, H, F);
+    const size_t need = x_f16 ? 0 : qwq4::moe_grouped_workspace_bytes(T, topk, E, H, F);
     REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
             "qw_moe_experts_grouped: workspace needs %zu bytes, 256-byte aligned", need);
     qwq4::MoeGroupedArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, offsets, pair_tok, tile_e, tile_m0, n_tiles,
                            x, T, topk, h, yp, workspace};
+    a.x_f16 = x_f16 != 0;
     qwq4::launch_moe_grouped(a, st(stream));
     return launched("qw_moe_experts_grouped");
 }
@@ -381,7 +385,7 @@ size_t qw_moe_decode_workspace_size(int T, int E, int topk, int H, int F) {
     return decode_layout(T, E, topk, H, F).total;
 }
 
-int qw_moe_decode(const float *router_w, const uint16_t *x, int T, int E, int topk, const uint32_t *gw,
+int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
                   const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
                   const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
                   void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
@@ -403,6 +407,7 @@ int qw_moe_decode(const float *router_w, const uint16_t *x, int T, int E, int to
     qwq4::RouteArgs ra{logits, T, E, topk, 0, top_e, top_w, at(L.counts), at(L.offsets), tok_slot, at(L.pair_tok),
                        at(L.active), at(L.n_active), nullptr, nullptr, nullptr};
     qwq4::RouterArgs rr{router_w, x, H, L.kl, reinterpret_cast<float *>(w + L.part), logits, at(L.rcounter)};
+    rr.x_f16 = x_f16 != 0;
     qwq4::launch_router_route(ra, rr, st(stream));
     // up to 4 tokens the combine runs in the down projection's last blocks
     // (one launch less); from there on its own launch is faster than the
@@ -411,6 +416,7 @@ int qw_moe_decode(const float *router_w, const uint16_t *x, int T, int E, int to
     const qwq4::CombineArgs cmb{at(L.dcounters), tok_slot, top_w, shared, out, out_bf16};
     qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, at(L.offsets), at(L.active), at(L.n_active),
                         at(L.pair_tok), x, T, topk, h, yp, fold ? &cmb : nullptr};
+    a.x_f16 = x_f16 != 0;
     qwq4::launch_moe_gemv(a, st(stream));
     if (!fold) qwq4::launch_combine(yp, tok_slot, top_w, shared, T, topk, H, out, out_bf16, st(stream));
     return launched("qw_moe_decode");

@@ -39,7 +39,7 @@ __device__ __forceinline__ int block_expert(const int32_t *n_active, const int32
     return int(blockIdx.y) < na ? min(max(e, 0), E - 1) : -1;
 }
 
-template <int KS, int GW, bool HAS_Z, bool CH4>
+template <typename XT, int KS, int GW, bool HAS_Z, bool CH4>
 __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
     const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
         __syncthreads();
         const uint4 *xr[1] = {xl + min(n, mc - 1) * kc + q * 4};
         f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
-        wr.template compute<BF16, 1>(xr, acc);
+        wr.template compute<XT, 1>(xr, acc);
         red[wave * WAVE + lane] = acc[0];
         lds_barrier();
         if (mat == 0 && kp == 0 && lsub < fsub) {
@@ -206,7 +206,7 @@ static int down_ks(int G) {
 
 template <int KS, int GW, bool HAS_Z, bool CH4>
 static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
-    auto kern = moe_gate_up_gemv_kernel<KS, GW, HAS_Z, CH4>;
+    auto kern = a.x_f16 ? moe_gate_up_gemv_kernel<F16, KS, GW, HAS_Z, CH4> : moe_gate_up_gemv_kernel<BF16, KS, GW, HAS_Z, CH4>;
     const size_t lds = moe_lds_bytes(R, a.H);
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
     constexpr int SUB = 8 / (2 * KS);

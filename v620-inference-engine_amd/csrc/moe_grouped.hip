@@ -165,8 +165,13 @@ __global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
 }
 
 void launch_moe_grouped(const MoeGroupedArgs &a, hipStream_t s) {
-    uint16_t *xh = static_cast<uint16_t *>(a.ws);
-    launch_x_to_f16(a.x, a.H, a.T, a.H, xh, s);
+    // bf16 rows through the fp16 pre-pass into the workspace; fp16 rows as they are
+    const uint16_t *xh = a.x;
+    if (!a.x_f16) {
+        uint16_t *w = static_cast<uint16_t *>(a.ws);
+        launch_x_to_f16(a.x, a.H, a.T, a.H, w, s);
+        xh = w;
+    }
     const int max_tiles = a.T * a.topk / -GROUPED_TILE_M + a.E;
     const dim3 g1(unsigned((a.F + 127) / 128), unsigned(max_tiles)),
         g2(unsigned((a.H + GB_N - 1) / GB_N), unsigned(max_tiles));

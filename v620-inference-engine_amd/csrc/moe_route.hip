@@ -449,7 +449,7 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 
 template <int PER>
 __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterArgs r) {
-    extern __shared__ __align__(16) unsigned char smem[];  // x slice, [T][kl] bf16
+    extern __shared__ __align__(16) unsigned char smem[];  // x slice, [T][kl]
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int T = a.T, E = a.E, H = r.H, kc = r.kl / 8, k0 = blockIdx.y * r.kl;
     const int e = blockIdx.x * 16 + wave;
@@ -468,27 +468,31 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
         xs[i] = *reinterpret_cast<const uint4 *>(r.x + int64_t(t) * H + k0 + c * 8);
     }
     __syncthreads();
-    if (e < E) {
+    // x rows bf16 or fp16 (a block-uniform choice; both conversions are exact)
+    auto dots = [&](auto cvt) {
+        if (e >= E) return;
 #pragma unroll
         for (int t = 0; t < 64; ++t) {
             if (t < T) {
                 float s = 0.f;
                 if (mine) {
                     const uint4 v = xs[t * kc + lane];
-                    s = fmaf(w0.x, bf16_bits_to_f32(uint16_t(v.x)), s);
-                    s = fmaf(w0.y, bf16_bits_to_f32(uint16_t(v.x >> 16)), s);
-                    s = fmaf(w0.z, bf16_bits_to_f32(uint16_t(v.y)), s);
-                    s = fmaf(w0.w, bf16_bits_to_f32(uint16_t(v.y >> 16)), s);
-                    s = fmaf(w1.x, bf16_bits_to_f32(uint16_t(v.z)), s);
-                    s = fmaf(w1.y, bf16_bits_to_f32(uint16_t(v.z >> 16)), s);
-                    s = fmaf(w1.z, bf16_bits_to_f32(uint16_t(v.w)), s);
-                    s = fmaf(w1.w, bf16_bits_to_f32(uint16_t(v.w >> 16)), s);
+                    s = fmaf(w0.x, cvt(uint16_t(v.x)), s);
+                    s = fmaf(w0.y, cvt(uint16_t(v.x >> 16)), s);
+                    s = fmaf(w0.z, cvt(uint16_t(v.y)), s);
+                    s = fmaf(w0.w, cvt(uint16_t(v.y >> 16)), s);
+                    s = fmaf(w1.x, cvt(uint16_t(v.z)), s);
+                    s = fmaf(w1.y, cvt(uint16_t(v.z >> 16)), s);
+                    s = fmaf(w1.z, cvt(uint16_t(v.w)), s);
+                    s = fmaf(w1.w, cvt(uint16_t(v.w >> 16)), s);
                 }
                 const float v = wave_sum_f32(s);
                 if (lane == 0) st_agent(r.part + (int64_t(blockIdx.y) * T + t) * E + e, v);
             }
         }
-    }
+    };
+    if (r.x_f16) dots([](uint16_t b) { return f16_bits_to_f32(b); });
+    else dots([](uint16_t b) { return bf16_bits_to_f32(b); });
     // the last slice block of each group of 16 experts adds the group's
     // slices in slice order (up to 8 loads in flight per logit)
     if (!count_last_block(r.counter + 1 + blockIdx.x, int(gridDim.y))) return;

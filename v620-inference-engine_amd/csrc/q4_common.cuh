@@ -48,14 +48,15 @@ struct BF16 {
     static constexpr uint32_t HI = 0x43434343u;    // high byte of 128 + v
     static constexpr uint32_t NEG_BIAS = 0xC310C310u;  // two bf16 -144
     static constexpr uint32_t ONE = 0x3F803F80u;       // two bf16 1.0
-    static constexpr float BASE = 128.f;               // value of the high byte alone
+    // unpack8_q operands: BASE + UNIT * q
+    static constexpr float BASE = 128.f, UNIT = 1.f;
     typedef bf16x8 vec;
 };
 struct F16 {
     static constexpr uint32_t HI = 0x64646464u;    // high byte of 1024 + v
     static constexpr uint32_t NEG_BIAS = 0xE410E410u;  // two fp16 -1040
     static constexpr uint32_t ONE = 0x3C003C00u;       // two fp16 1.0
-    static constexpr float BASE = 1024.f;
+    static constexpr float BASE = 1024.f, UNIT = 16.f;
     typedef f16x8 vec;
 };
 
@@ -114,13 +115,23 @@ __device__ __forceinline__ uint4 unpack8(uint32_t w, uint32_t zb) {
     return r;
 }
 
-// One reordered word (8 nibbles) -> 8 operand elements BASE + q, K order
-// (the zero point is left to the accumulator's starting value): the
-// unpack8 scheme without the per-byte zero add.
+// One reordered word (8 nibbles) -> 8 operand elements BASE + UNIT * q, K
+// order (the zero point is left to the accumulator's starting value): the
+// unpack8 scheme without the per-byte zero add. bf16: 128 + q (q in the low
+// mantissa bits, the most a 7-bit mantissa allows). fp16: 1024 + 16 q (q in
+// mantissa bits 4-7 of 10): the product's cancelling part, BASE / UNIT = 64
+// times the wanted one, is 16 times smaller than with 1024 + q, at the same
+// instruction count.
 template <typename T>
 __device__ __forceinline__ uint4 unpack8_q(uint32_t w) {
-    const uint32_t lo = w & 0x0F0F0F0Fu;
-    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+    uint32_t lo, hi;
+    if constexpr (__is_same(T, F16)) {
+        lo = (w << 4) & 0xF0F0F0F0u;
+        hi = w & 0xF0F0F0F0u;
+    } else {
+        lo = w & 0x0F0F0F0Fu;
+        hi = (w >> 4) & 0x0F0F0F0Fu;
+    }
     uint4 r;
     r.x = __builtin_amdgcn_perm(T::HI, lo, 0x04010400u);  // e0, e1
     r.y = __builtin_amdgcn_perm(T::HI, lo, 0x04030402u);  // e2, e3

@@ -54,8 +54,8 @@ template <bool HAS_Z, bool Y_BF16, int GB_M, int BN = GB_N>
 __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
                                                             const uint16_t *St,
                                                             const uint16_t *Zt,
-                                                            const uint16_t *__restrict__ Xh, int T, void *__restrict__ Y,
-                                                            int ldy, int N, int K) {
+                                                            const uint16_t *__restrict__ Xh, int lda, int T,
+                                                            void *__restrict__ Y, int ldy, int N, int K) {
     using Sh = GemmShape<GB_M, BN>;
     const int tid = threadIdx.x, wave = tid / WAVE;
     // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs;
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
     const uint16_t *ap[GB_M / 32];
 #pragma unroll
-    for (int j = 0; j < GB_M / 32; ++j) ap[j] = Xh + int64_t(min(t0 + a_load_row(j), T - 1)) * K;
+    for (int j = 0; j < GB_M / 32; ++j) ap[j] = Xh + int64_t(min(t0 + a_load_row(j), T - 1)) * lda;
     gemm_tile<GB_M, HAS_Z, BN>(ap, b, K, acc);
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
@@ -94,17 +94,17 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
 }
 
 template <bool HAS_Z, bool Y_BF16, int GB_M, int BN = GB_N>
-static void launch_gemm_t(const GemmArgs &a, const uint16_t *Xh, hipStream_t s) {
+static void launch_gemm_t(const GemmArgs &a, const uint16_t *Xh, int lda, hipStream_t s) {
     auto kern = q4_gemm_kernel<HAS_Z, Y_BF16, GB_M, BN>;
     const dim3 grid(unsigned((a.N + BN - 1) / BN), unsigned((a.T + GB_M - 1) / GB_M));
-    kern<<<grid, G_THREADS, 0, s>>>(a.W, a.S, a.Z, Xh, a.T, a.Y, a.ldy, a.N, a.K);
+    kern<<<grid, G_THREADS, 0, s>>>(a.W, a.S, a.Z, Xh, lda, a.T, a.Y, a.ldy, a.N, a.K);
 }
 
 // 256 x 256 tiles when they fill whole rounds of the chip (or many rounds);
 // else 256 tokens x 128 weight rows when those do (the same dequant work per
 // MFMA, e.g. 2048-token micro-batches); else 128 x 256.
 template <bool HAS_Z, bool Y_BF16>
-static void launch_gemm_m(const GemmArgs &a, const uint16_t *Xh, hipStream_t s) {
+static void launch_gemm_m(const GemmArgs &a, const uint16_t *Xh, int lda, hipStream_t s) {
     int cus = 0, dev = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -114,20 +114,28 @@ static void launch_gemm_m(const GemmArgs &a, const uint16_t *Xh, hipStream_t s) 
         return rounds >= 4.0 || (rounds >= 1.0 && rounds - double(int64_t(rounds)) < 0.01);
     };
     const int64_t t256 = (a.T + 255) / 256;
-    if (whole(int64_t((a.N + 255) / 256) * t256)) launch_gemm_t<HAS_Z, Y_BF16, 256>(a, Xh, s);
-    else if (whole(int64_t((a.N + 127) / 128) * t256)) launch_gemm_t<HAS_Z, Y_BF16, 256, 128>(a, Xh, s);
-    else launch_gemm_t<HAS_Z, Y_BF16, 128>(a, Xh, s);
+    if (whole(int64_t((a.N + 255) / 256) * t256)) launch_gemm_t<HAS_Z, Y_BF16, 256>(a, Xh, lda, s);
+    else if (whole(int64_t((a.N + 127) / 128) * t256)) launch_gemm_t<HAS_Z, Y_BF16, 256, 128>(a, Xh, lda, s);
+    else launch_gemm_t<HAS_Z, Y_BF16, 128>(a, Xh, lda, s);
 }
 
+// bf16 rows go through the fp16 pre-pass into the workspace; fp16 rows
+// (x_f16) are the MFMA operand as they are.
 void launch_gemm(const GemmArgs &a, hipStream_t s) {
-    uint16_t *Xh = static_cast<uint16_t *>(a.ws);
-    launch_x_to_f16(a.X, a.ldx, a.T, a.K, Xh, s);
+    const uint16_t *Xh = a.X;
+    int lda = a.ldx;
+    if (!a.x_f16) {
+        uint16_t *w = static_cast<uint16_t *>(a.ws);
+        launch_x_to_f16(a.X, a.ldx, a.T, a.K, w, s);
+        Xh = w;
+        lda = a.K;
+    }
     if (a.Z) {
-        if (a.y_bf16) launch_gemm_m<true, true>(a, Xh, s);
-        else launch_gemm_m<true, false>(a, Xh, s);
+        if (a.y_bf16) launch_gemm_m<true, true>(a, Xh, lda, s);
+        else launch_gemm_m<true, false>(a, Xh, lda, s);
     } else {
-        if (a.y_bf16) launch_gemm_m<false, true>(a, Xh, s);
-        else launch_gemm_m<false, false>(a, Xh, s);
+        if (a.y_bf16) launch_gemm_m<false, true>(a, Xh, lda, s);
+        else launch_gemm_m<false, false>(a, Xh, lda, s);
     }
 }
 

@@ -305,9 +305,9 @@ __device__ __forceinline__ void group_sums(const uint4 *const (&xr)[MB], XpFn xp
 
 // NS subtiles over the same groups (wr[j] fetched with equal g0 and n): per
 // group, as its weights arrive, the product of the activations with the
-// operands BASE + q (unpack8_q) onto a start of -(BASE + z) * sum(x), which
-// leaves sum x * (q - z) (every product exact in fp32), times the group
-// scale into acc. Only elements r < MR of the last row block are formed
+// operands BASE + UNIT q (unpack8_q) onto a start of -(BASE + UNIT z) *
+// sum(x), which leaves UNIT * sum x * (q - z) (every product exact in fp32),
+// times the group scale / UNIT (a power of two) into acc. Only elements r < MR of the last row block are formed
 // (rows past the batch are never read).
 template <typename T, int MB, int NS, int GW, bool HAS_Z, bool CH4, int MR>
 __device__ __forceinline__ void compute_zq(const WaveRange<GW, HAS_Z, CH4> (&wr)[NS], const uint4 *const (&xr)[MB],
@@ -324,7 +324,7 @@ __device__ __forceinline__ void compute_zq(const WaveRange<GW, HAS_Z, CH4> (&wr)
                 for (int t = 0; t < 4; ++t) a[mb][t] = xr[mb][g * 16 + t];
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
-                const float nz = -(T::BASE + float(HAS_Z ? Q4Tile::zero_of(wr[j].zv[c], g) : 8u));
+                const float nz = -(T::BASE + T::UNIT * float(HAS_Z ? Q4Tile::zero_of(wr[j].zv[c], g) : 8u));
                 const uint32_t sbits = wr[j].sv[c];
                 uint4 b[4];
                 b[0] = unpack8_q<T>(wr[j].w[c].x);
@@ -340,7 +340,7 @@ __device__ __forceinline__ void compute_zq(const WaveRange<GW, HAS_Z, CH4> (&wr)
                     for (int r = 0; r < R; ++r) p[r] = r < rows ? sums[c][mb][r] * nz : 0.f;
 #pragma unroll
                     for (int t = 0; t < 4; ++t) p = mfma16<T>(a[mb][t], b[t], p);
-                    const float sc = f16_bits_to_f32(uint16_t(sbits));
+                    const float sc = f16_bits_to_f32(uint16_t(sbits)) * (1.f / T::UNIT);
 #pragma unroll
                     for (int r = 0; r < R; ++r)
                         if (r < rows) acc[j][mb][r] += sc * p[r];

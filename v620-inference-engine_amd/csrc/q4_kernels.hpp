@@ -25,6 +25,7 @@ struct GemvArgs {
     int xs;
     void *y;
     int ys, y_bf16, N, K, M, accumulate;
+    int x_f16 = 0;  // x rows are fp16 (else bf16)
 };
 void launch_gemv(const GemvArgs &a, hipStream_t s);
 
@@ -59,6 +60,7 @@ struct MoeGemvArgs {
     uint16_t *h;
     float *yp;
     const CombineArgs *cmb;  // null: yp only
+    int x_f16 = 0;           // x rows are fp16 (else bf16)
 };
 void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s);
 // Whether the expert GEMVs take these sizes (a wave holds <= 16 groups of its K range).
@@ -81,6 +83,7 @@ struct MoeGroupedArgs {
     uint16_t *h;
     float *yp;
     void *ws;
+    int x_f16 = 0;  // x rows are fp16 (no pre-pass)
 };
 // Tokens per tile the grouped kernels expect in the routing tile list.
 int moe_grouped_tile_m();
@@ -98,11 +101,12 @@ struct RouteArgs {
 // fp32 router GEMV fused with the decode routing (T <= 64).
 struct RouterArgs {
     const float *w;     // [E][H]
-    const uint16_t *x;  // bf16 [T][H]
+    const uint16_t *x;  // bf16 or fp16 [T][H]
     int H, kl;          // K slice per block (a multiple of 8 dividing H)
     float *part;        // [H / kl][T][E] partial logits
     float *logits;      // [T][E]
     int32_t *counter;   // [1 + ceil(E / 16)], zero between calls
+    int x_f16 = 0;      // x rows are fp16 (else bf16)
 };
 size_t router_lds_bytes(int T, int kl);
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
@@ -133,7 +137,8 @@ struct GemmArgs {
     int ldx, T;
     void *Y;
     int ldy, y_bf16, N, K;
-    void *ws;  // workspace: fp16 copy of X
+    void *ws;  // workspace: fp16 copy of X (bf16 rows only)
+    int x_f16 = 0;  // X rows are fp16 (else bf16)
 };
 size_t gemm_workspace_bytes(int T, int K);
 // bf16 [T][ldx] -> fp16 [T][K] (saturating), the GEMMs' A operand.

@@ -31,13 +31,13 @@ _SZ = ctypes.c_size_t
 _SIGS = {
     "qw_q4_abi_version": ([], _I),
     "qw_q4_last_error": ([], ctypes.c_char_p),
-    "qw_q4_gemv": ([_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_q4_gemv": ([_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_q4_gemm_workspace_size": ([_I, _I], _SZ),
-    "qw_q4_gemm": ([_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _SZ, _P], _I),
+    "qw_q4_gemm": ([_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _P, _SZ, _P], _I),
     "qw_moe_route": ([_P, _I, _I, _I, _I] + [_P] * 11 + [_P], _I),
-    "qw_moe_experts_gemv": ([_P] * 9 + [_I, _I, _I] + [_P] * 5 + [_I, _I, _P, _P, _P], _I),
+    "qw_moe_experts_gemv": ([_P] * 9 + [_I, _I, _I] + [_P] * 5 + [_I, _I, _I, _P, _P, _P], _I),
     "qw_moe_grouped_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
-    "qw_moe_experts_grouped": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _P, _P, _P, _SZ, _P], _I),
+    "qw_moe_experts_grouped": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _I, _P, _P, _P, _SZ, _P], _I),
     "qw_moe_grouped_tile_m": ([], _I),
     "qw_moe_combine": ([_P, _P, _P, _P, _I, _I, _I, _P, _I, _P], _I),
     "qw_q4_tiled_size": ([_I64, _I64, _P, _P, _P], None),
@@ -48,7 +48,7 @@ _SIGS = {
     "qw_q4_from_engine_order": ([_P, _P, _I64, _P], _I),
     "qw_bf16_to_f16": ([_P, _P, _I64, _P], _I),
     "qw_moe_decode_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
-    "qw_moe_decode": ([_P, _P, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
+    "qw_moe_decode": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
     "qw_st_close": ([_P], None),
     "qw_wcache_open": ([ctypes.c_char_p, ctypes.c_uint64, _P, _P], _I),
@@ -141,8 +141,16 @@ def tile_experts(W, S, Z, rows, K):
 
 
 # ---------------------------------------------------------------- operators
-def gemv(W, S, Z, x, N, K, M=None, y=None, y_bf16=False, accumulate=False, xs=None, ys=None):
-    """y[m][n] (+)= sum_k deq(W)[n][k] x[m][k]. x: bf16-bits int16/uint16 or bfloat16 tensor."""
+def _is_f16(x, x_f16):
+    """x_f16 given, else from the tensor: float16 -> fp16 rows, anything else
+    (bfloat16, or int16 bit patterns) -> bf16 rows."""
+    import torch
+    return bool(x_f16) if x_f16 is not None else x.dtype == torch.float16
+
+
+def gemv(W, S, Z, x, N, K, M=None, y=None, y_bf16=False, accumulate=False, xs=None, ys=None, x_f16=None):
+    """y[m][n] (+)= sum_k deq(W)[n][k] x[m][k]. x: bf16 rows (bfloat16, or int16 bit patterns) or fp16
+    rows (float16, or x_f16=True with int16 bit patterns)."""
     import torch
     M = M if M is not None else x.shape[0]
     xs = xs if xs is not None else x.stride(0) if x.dim() == 2 else K
@@ -150,8 +158,8 @@ def gemv(W, S, Z, x, N, K, M=None, y=None, y_bf16=False, accumulate=False, xs=No
         y = torch.zeros((M, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=x.device)
     ys = ys if ys is not None else (y.stride(0) if y.dim() == 2 else N)
     _dev(W, S, Z, x, y)
-    rc = lib().qw_q4_gemv(_ptr(W), _ptr(S), _ptr(Z), _ptr(x), xs, _ptr(y), ys, int(y_bf16), N, K, M,
-                          int(accumulate), _stream())
+    rc = lib().qw_q4_gemv(_ptr(W), _ptr(S), _ptr(Z), _ptr(x), int(_is_f16(x, x_f16)), xs, _ptr(y), ys, int(y_bf16),
+                          N, K, M, int(accumulate), _stream())
     _check(rc, "qw_q4_gemv")
     return y
 
@@ -160,16 +168,17 @@ def gemm_workspace_size(T, K):
     return lib().qw_q4_gemm_workspace_size(T, K)
 
 
-def gemm(W, S, Z, X, N, K, Y=None, y_bf16=False, workspace=None):
+def gemm(W, S, Z, X, N, K, Y=None, y_bf16=False, workspace=None, x_f16=None):
     import torch
     T = X.shape[0]
+    f16 = _is_f16(X, x_f16)
     if Y is None:
         Y = torch.empty((T, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=X.device)
-    if workspace is None:
+    if workspace is None and not f16:
         workspace = torch.empty(gemm_workspace_size(T, K), dtype=torch.uint8, device=X.device)
     _dev(W, S, Z, X, Y, workspace)
-    rc = lib().qw_q4_gemm(_ptr(W), _ptr(S), _ptr(Z), _ptr(X), X.stride(0), T, _ptr(Y), Y.stride(0), int(y_bf16), N, K,
-                          _ptr(workspace), workspace.numel(), _stream())
+    rc = lib().qw_q4_gemm(_ptr(W), _ptr(S), _ptr(Z), _ptr(X), int(f16), X.stride(0), T, _ptr(Y), Y.stride(0),
+                          int(y_bf16), N, K, _ptr(workspace), 0 if workspace is None else workspace.numel(), _stream())
     _check(rc, "qw_q4_gemm")
     return Y
 
@@ -206,7 +215,7 @@ def moe_route(logits, topk, tile_m=0, out=None):
     return r
 
 
-def moe_experts_gemv(gate, up, down, route, x, E, F, h=None, yp=None):
+def moe_experts_gemv(gate, up, down, route, x, E, F, h=None, yp=None, x_f16=None):
     """gate/up/down: tiled (Wt, St, Zt) of the stacked experts; returns (h fp16, yp fp32)."""
     import torch
     H = x.shape[1]
@@ -217,8 +226,8 @@ def moe_experts_gemv(gate, up, down, route, x, E, F, h=None, yp=None):
         yp = torch.empty((T * topk, H), dtype=torch.float32, device=x.device)
     _dev(x, h, yp, *gate, *up, *down)
     rc = lib().qw_moe_experts_gemv(*[_ptr(t) for t in (*gate, *up, *down)], E, H, F, _ptr(route.offsets),
-                                   _ptr(route.active), _ptr(route.n_active), _ptr(route.pair_tok), _ptr(x), T, topk,
-                                   _ptr(h), _ptr(yp), _stream())
+                                   _ptr(route.active), _ptr(route.n_active), _ptr(route.pair_tok), _ptr(x),
+                                   int(_is_f16(x, x_f16)), T, topk, _ptr(h), _ptr(yp), _stream())
     _check(rc, "qw_moe_experts_gemv")
     return h, yp
 
@@ -231,7 +240,7 @@ def moe_grouped_workspace_size(T, topk, E, H, F):
     return lib().qw_moe_grouped_workspace_size(T, topk, E, H, F)
 
 
-def moe_experts_grouped(gate, up, down, route, x, E, F, h=None, yp=None, workspace=None):
+def moe_experts_grouped(gate, up, down, route, x, E, F, h=None, yp=None, workspace=None, x_f16=None):
     import torch
     T, H = x.shape
     topk = route.topk
@@ -239,14 +248,15 @@ def moe_experts_grouped(gate, up, down, route, x, E, F, h=None, yp=None, workspa
         h = torch.empty((T * topk, F), dtype=torch.float16, device=x.device)
     if yp is None:
         yp = torch.empty((T * topk, H), dtype=torch.float32, device=x.device)
-    if workspace is None:
+    f16 = _is_f16(x, x_f16)
+    if workspace is None and not f16:
         workspace = torch.empty(max(moe_grouped_workspace_size(T, topk, E, H, F), 1), dtype=torch.uint8,
                                 device=x.device)
     _dev(x, h, yp, workspace, *gate, *up, *down)
     rc = lib().qw_moe_experts_grouped(*[_ptr(t) for t in (*gate, *up, *down)], E, H, F, _ptr(route.offsets),
                                       _ptr(route.pair_tok), _ptr(route.tile_e), _ptr(route.tile_m0),
-                                      _ptr(route.n_tiles), _ptr(x), T, topk, _ptr(h), _ptr(yp), _ptr(workspace),
-                                      workspace.numel(), _stream())
+                                      _ptr(route.n_tiles), _ptr(x), int(f16), T, topk, _ptr(h), _ptr(yp),
+                                      _ptr(workspace), 0 if workspace is None else workspace.numel(), _stream())
     _check(rc, "qw_moe_experts_grouped")
     return h, yp
 
@@ -301,7 +311,7 @@ class MoeDecode:
         self.ws = torch.zeros(lib().qw_moe_decode_workspace_size(T, E, topk, H, F), dtype=torch.uint8, device=device)
 
 
-def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, out=None, out_bf16=True):
+def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, out=None, out_bf16=True, x_f16=None):
     """Router GEMV + routing + experts + combine for a decode batch (3 launches; 4 above 4 tokens)."""
     import torch
     T, H = x.shape
@@ -309,7 +319,7 @@ def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, o
     if out is None:
         out = torch.empty((T, H), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=x.device)
     _dev(router_w, x, shared, out, *gate, *up, *down)
-    rc = lib().qw_moe_decode(_ptr(router_w), _ptr(x), T, E, topk, *map(_ptr, gate), *map(_ptr, up), *map(_ptr, down),
+    rc = lib().qw_moe_decode(_ptr(router_w), _ptr(x), int(_is_f16(x, x_f16)), T, E, topk, *map(_ptr, gate), *map(_ptr, up), *map(_ptr, down),
                              H, F, _ptr(shared), _ptr(out), int(out_bf16), _ptr(buf.logits), _ptr(buf.top_e),
                              _ptr(buf.top_w), _ptr(buf.tok_slot), _ptr(buf.h), _ptr(buf.yp), _ptr(buf.ws),
                              buf.ws.numel(), _stream())
