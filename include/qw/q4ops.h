@@ -190,6 +190,26 @@ int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, in
                   void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
                   uint16_t *h, float *yp, void *workspace, size_t workspace_bytes, void *stream);
 
+/* qw_moe_decode without a workspace argument: it allocates nothing and
+ * needs no caller scratch. No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops). The scratch (completion counters, partial router
+ * logits, routing arrays) is one library-held device array per GPU of
+ * qw_moe_decode_static_max_bytes() = 4 MiB, kept until the process ends;
+ * shapes needing more (about T * E * ceil(H / 512) * 4 bytes plus a few
+ * E-sized arrays) are rejected with QW_Q4_EINVAL. The counters start at zero
+ * (the array is zero when the library loads) and every call leaves them at
+ * zero. All calls on one GPU share the array: calls that overlap on one GPU
+ * (on different streams, or from different threads) race and must not be
+ * issued. */
+size_t qw_moe_decode_static_max_bytes(void);
+int qw_moe_decode_static(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk,
+                         const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                         const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                         const uint16_t *dz, int H, int F, const float *shared, void *out, int out_bf16,
+                         float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot, uint16_t *h, float *yp,
+                         void *stream);
+
 /* Scale conversion as the reference does it at load (weight_convert.cpp:19-26):
  * bf16 -> fp16 bits, magnitudes above 65504 saturated, round to nearest even. */
 int qw_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, void *stream);

@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -385,30 +386,41 @@ size_t qw_moe_decode_workspace_size(int T, int E, int topk, int H, int F) {
     return decode_layout(T, E, topk, H, F).total;
 }
 
-int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
-                  const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
-                  const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
-                  void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
-                  uint16_t *h, float *yp, void *workspace, size_t workspace_bytes, void *stream) {
-    if (int r = check_q4("qw_moe_decode(gate)", gw, gs, int64_t(E) * F, H)) return r;
-    if (int r = check_q4("qw_moe_decode(up)", uw, us, int64_t(E) * F, H)) return r;
-    if (int r = check_q4("qw_moe_decode(down)", dw, ds, int64_t(E) * H, F)) return r;
-    REQUIRE(router_w && x && out && logits && top_e && top_w && tok_slot && h && yp && workspace,
-            "qw_moe_decode: null pointer");
-    REQUIRE(T >= 1 && T <= 32, "qw_moe_decode: T = %d outside 1..32", T);
-    REQUIRE(E >= 1 && E <= 1024 && topk >= 1 && topk <= E && topk <= 64, "qw_moe_decode: E = %d, topk = %d", E, topk);
-    REQUIRE(qwq4::moe_gemv_supported(H, F), "qw_moe_decode: H = %d, F = %d too large", H, F);
-    REQUIRE(aligned(router_w, 16) && aligned(x, 16) && aligned(h, 16) && aligned(workspace, 256),
-            "qw_moe_decode: router_w, x, h must be 16-byte and workspace 256-byte aligned");
-    const DecodeLayout L = decode_layout(T, E, topk, H, F);
-    REQUIRE(workspace_bytes >= L.total, "qw_moe_decode: workspace needs %zu bytes", L.total);
-    unsigned char *w = static_cast<unsigned char *>(workspace);
+}  // extern "C"
+
+namespace {
+
+int moe_decode_check(const char *fn, const float *router_w, const uint16_t *x, int T, int E, int topk,
+                     const uint32_t *gw, const uint16_t *gs, const uint32_t *uw, const uint16_t *us,
+                     const uint32_t *dw, const uint16_t *ds, int H, int F, const void *out, const float *logits,
+                     const int32_t *top_e, const float *top_w, const int32_t *tok_slot, const uint16_t *h,
+                     const float *yp) {
+    if (int r = check_q4(fn, gw, gs, int64_t(E) * F, H)) return r;
+    if (int r = check_q4(fn, uw, us, int64_t(E) * F, H)) return r;
+    if (int r = check_q4(fn, dw, ds, int64_t(E) * H, F)) return r;
+    REQUIRE(router_w && x && out && logits && top_e && top_w && tok_slot && h && yp, "%s: null pointer", fn);
+    REQUIRE(T >= 1 && T <= 32, "%s: T = %d outside 1..32", fn, T);
+    REQUIRE(E >= 1 && E <= 1024 && topk >= 1 && topk <= E && topk <= 64, "%s: E = %d, topk = %d", fn, E, topk);
+    REQUIRE(qwq4::moe_gemv_supported(H, F), "%s: H = %d, F = %d too large", fn, H, F);
+    REQUIRE(aligned(router_w, 16) && aligned(x, 16) && aligned(h, 16), "%s: router_w, x, h must be 16-byte aligned",
+            fn);
+    return 0;
+}
+
+// Router GEMV + routing, the expert GEMVs, and the combine (folded into the
+// down projection up to 4 tokens), on the scratch w laid out as L.
+void moe_decode_launch(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
+                       const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
+                       const uint16_t *uz, const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F,
+                       const float *shared, void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w,
+                       int32_t *tok_slot, uint16_t *h, float *yp, unsigned char *w, const DecodeLayout &L,
+                       hipStream_t s) {
     auto at = [&](size_t off) { return reinterpret_cast<int32_t *>(w + off); };
     qwq4::RouteArgs ra{logits, T, E, topk, 0, top_e, top_w, at(L.counts), at(L.offsets), tok_slot, at(L.pair_tok),
                        at(L.active), at(L.n_active), nullptr, nullptr, nullptr};
     qwq4::RouterArgs rr{router_w, x, H, L.kl, reinterpret_cast<float *>(w + L.part), logits, at(L.rcounter)};
     rr.x_f16 = x_f16 != 0;
-    qwq4::launch_router_route(ra, rr, st(stream));
+    qwq4::launch_router_route(ra, rr, s);
     // up to 4 tokens the combine runs in the down projection's last blocks
     // (one launch less); from there on its own launch is faster than the
     // serial tail it adds to those blocks
@@ -417,9 +429,95 @@ int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, in
     qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, at(L.offsets), at(L.active), at(L.n_active),
                         at(L.pair_tok), x, T, topk, h, yp, fold ? &cmb : nullptr};
     a.x_f16 = x_f16 != 0;
-    qwq4::launch_moe_gemv(a, st(stream));
-    if (!fold) qwq4::launch_combine(yp, tok_slot, top_w, shared, T, topk, H, out, out_bf16, st(stream));
+    qwq4::launch_moe_gemv(a, s);
+    if (!fold) qwq4::launch_combine(yp, tok_slot, top_w, shared, T, topk, H, out, out_bf16, s);
+}
+
+// ---- the allocation-free variant's scratch: one array per GPU, held until
+// the process ends. The completion counters sit at fixed offsets at its
+// start (every call leaves them at zero, whatever its shape; the array starts
+// zeroed), the rest after them.
+constexpr size_t kStaticScratchBytes = size_t(4) << 20;
+constexpr size_t kStaticCounterBytes = 16384;  // 1 + E/16 router counters, then the down row counters
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kMaxDevices];
+
+// The device address of the current device's scratch (looked up once per
+// device, with that device current; the array's host-side name is not a
+// device address).
+int static_scratch(void **ptr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail("qw_moe_decode_static: no current device (or more than %d)", kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail("qw_moe_decode_static: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch[dev] = p;
+    }
+    *ptr = g_scratch[dev];
+    return 0;
+}
+
+// The workspace layout with the counters moved to the fixed region.
+DecodeLayout static_layout(int T, int E, int topk, int H, int F) {
+    DecodeLayout L = decode_layout(T, E, topk, H, F);
+    for (size_t *o : {&L.part, &L.counts, &L.offsets, &L.pair_tok, &L.active, &L.n_active}) *o += kStaticCounterBytes;
+    L.total += kStaticCounterBytes;
+    L.rcounter = 0;
+    L.dcounters = 4096;
+    return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
+                  const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
+                  const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
+                  void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
+                  uint16_t *h, float *yp, void *workspace, size_t workspace_bytes, void *stream) {
+    if (int r = moe_decode_check("qw_moe_decode", router_w, x, T, E, topk, gw, gs, uw, us, dw, ds, H, F, out, logits,
+                                 top_e, top_w, tok_slot, h, yp))
+        return r;
+    REQUIRE(workspace && aligned(workspace, 256), "qw_moe_decode: workspace null or not 256-byte aligned");
+    const DecodeLayout L = decode_layout(T, E, topk, H, F);
+    REQUIRE(workspace_bytes >= L.total, "qw_moe_decode: workspace needs %zu bytes", L.total);
+    moe_decode_launch(router_w, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_bf16,
+                      logits, top_e, top_w, tok_slot, h, yp, static_cast<unsigned char *>(workspace), L, st(stream));
     return launched("qw_moe_decode");
+}
+
+size_t qw_moe_decode_static_max_bytes(void) { return kStaticScratchBytes; }
+
+int qw_moe_decode_static(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk,
+                         const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                         const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                         const uint16_t *dz, int H, int F, const float *shared, void *out, int out_bf16,
+                         float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot, uint16_t *h, float *yp,
+                         void *stream) {
+    if (int r = moe_decode_check("qw_moe_decode_static", router_w, x, T, E, topk, gw, gs, uw, us, dw, ds, H, F, out,
+                                 logits, top_e, top_w, tok_slot, h, yp))
+        return r;
+    const DecodeLayout L = static_layout(T, E, topk, H, F);
+    REQUIRE(L.total <= kStaticScratchBytes,
+            "qw_moe_decode_static: T = %d, E = %d, k = %d, H = %d needs %zu bytes of scratch, more than the %zu "
+            "the library holds (use qw_moe_decode with a workspace)",
+            T, E, topk, H, L.total, kStaticScratchBytes);
+    REQUIRE(size_t(1 + (E + 15) / 16) * 4 <= 4096 && size_t(L.rows) * 4 <= kStaticCounterBytes - 4096,
+            "qw_moe_decode_static: E = %d or H = %d needs more completion counters than the scratch holds", E, H);
+    void *w = nullptr;
+    if (int r = static_scratch(&w)) return r;
+    moe_decode_launch(router_w, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_bf16,
+                      logits, top_e, top_w, tok_slot, h, yp, static_cast<unsigned char *>(w), L, st(stream));
+    return launched("qw_moe_decode_static");
 }
 
 }  // extern "C"

@@ -19,7 +19,7 @@ SYMBOLS = (
     "qw_q4_tiled_size", "qw_q4_tile", "qw_q4_untile", "qw_bf16_to_f16",
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
-    "qw_moe_decode_workspace_size", "qw_moe_decode",
+    "qw_moe_decode_workspace_size", "qw_moe_decode", "qw_moe_decode_static_max_bytes", "qw_moe_decode_static",
     "qw_wcache_open", "qw_wcache_put", "qw_wcache_get", "qw_wcache_finish", "qw_wcache_close",
 )
 
@@ -49,6 +49,8 @@ _SIGS = {
     "qw_bf16_to_f16": ([_P, _P, _I64, _P], _I),
     "qw_moe_decode_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "qw_moe_decode": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
+    "qw_moe_decode_static_max_bytes": ([], _SZ),
+    "qw_moe_decode_static": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
     "qw_st_close": ([_P], None),
     "qw_wcache_open": ([ctypes.c_char_p, ctypes.c_uint64, _P, _P], _I),
