@@ -10,6 +10,9 @@
  *   qw_moe_experts_gemv   gpu::moe_experts_P        src/kernels/moe.hpp:35-37
  *   qw_moe_experts_grouped gpu::moe_experts_T       src/kernels/moe.hpp:29-32
  *   qw_moe_combine        gpu::moe_combine_B/T      src/kernels/moe.hpp:42-46
+ *   qw_w16_gemv           gpu::gemv_rows (fp16 W)   src/kernels/gemv.hpp:13-14
+ *                         ref::Model::linear        src/ref/ref_model.cpp:86-97
+ *   qw_swiglu_gate        gpu::swiglu_T             src/kernels/moe_route.hip:187-197
  *   qw_q4_unpack / qw_q4_dequant                    src/ref/ref_model.cpp:108-114
  *   qw_q4_from_engine_order (inverse of pack_int4_words)
  *                                                   src/engine/weight_convert.cpp:61-71
@@ -85,6 +88,26 @@ int qw_q4_untile(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt, int
  * 1 <= M <= 32. Every product is exact, sums in fp32. */
 int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *x, int x_f16, int xs, void *y,
                int ys, int y_bf16, int N, int K, int M, int accumulate, void *stream);
+
+/* Dense GEMV on 16-bit weights (the role of gpu::gemv_rows with fp16
+ * weights, src/kernels/gemv.hpp:13-14, which the engine runs the shared
+ * expert's projections through, src/engine/decode.hip:99-101; and of
+ * ref::Model::linear on bf16 weights, src/ref/ref_model.cpp:86-97):
+ *   y[m*ys + n] (+)= sum_k W[n*ldw + k] * x[m*xs + k],   m < M, n < N
+ * f16 = 1: W and x fp16; f16 = 0: W and x bf16 (the MFMA takes matching
+ * types; every product is exact, sums in fp32). W row-major, ldw >= K a
+ * multiple of 8, 16-byte aligned; K a multiple of 32; any N >= 1; x rows of
+ * stride xs as in qw_q4_gemv; y fp32 or bf16 (y_bf16). 1 <= M <= 32. */
+int qw_w16_gemv(const uint16_t *W, int ldw, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N,
+                int K, int M, int accumulate, void *stream);
+
+/* The shared expert's activation (replaces gpu::swiglu_T,
+ * src/kernels/moe_route.hip:187-197; math of src/ref/ref_model.cpp:468-476):
+ *   h[t][j] = fp16(silu(v[t][j]) * v[t][n + j] * sigmoid(v[t][2n]))
+ * v fp32 [T][ldv] (ldv >= 2n + 1): the output of the fused gate / up /
+ * gate-logit projection; h fp16 [T][n], finite values beyond +-65504
+ * saturate. */
+int qw_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, void *stream);
 
 /* Prefill GEMM (replaces gpu::gemm, src/kernels/gemm.hpp:14-15, with tiled
  * q4 weights): Y[t][n] = sum_k X[t][k] * W[n][k], t < T. X rows of stride

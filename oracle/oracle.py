@@ -46,6 +46,8 @@ def lib():
         L.o_moe_slots.argtypes = [_i32p, _int, _int, _int, _i32p, _i32p, _i32p, _i32p]
         L.o_q4_tile.argtypes = [_u32p, _u16p, _vp, _i64, _i64, _u32p, _u16p, _vp]
         L.o_moe.argtypes = [_f32p, _int, _int, _int, _int, _int, _f32p] + [_u32p, _u16p, _vp] * 3 + [_f32p, _vp, _vp, _int]
+        L.o_linear_w16.argtypes = [_u16p, _int, _i64, _i64, _i64, _f32p, _int, _int, _f32p, _int, _int]
+        L.o_swiglu_gate.argtypes = [_f32p, _int, _int, _int, _f32p]
         for n in ("o_bf16_to_f32", "o_f16_to_f32"):
             getattr(L, n).argtypes = [ctypes.c_uint16]
             getattr(L, n).restype = ctypes.c_float
@@ -202,6 +204,36 @@ def moe(x, logits, topk, gate, up, down, threads=None, want_parts=False):
     if want_parts:
         return out, h, yp
     return out
+
+
+def linear_w16(W, x, f16=False, threads=None):
+    """y[t][o] = sum_i W[o][i] x[t][i], W 16-bit bits [N][K] (bf16, or fp16 with f16) widened
+    to fp32 (ref::Model::linear, src/ref/ref_model.cpp:86-97)."""
+    W = _c(W, np.uint16)
+    N, K = W.shape
+    x = _c(x, np.float32).reshape(-1, K)
+    T = x.shape[0]
+    y = np.empty((T, N), np.float32)
+    lib().o_linear_w16(W, int(f16), N, K, K, x, T, K, y, N, threads or nthreads())
+    return y
+
+
+def swiglu_gate(v, n):
+    """h[t][j] = silu(v[t][j]) * v[t][n + j] * sigmoid(v[t][2n]) for v [T][>= 2n + 1]."""
+    v = _c(v, np.float32)
+    T, ldv = v.shape
+    h = np.empty((T, n), np.float32)
+    lib().o_swiglu_gate(v, ldv, n, T, h)
+    return h
+
+
+def shared_expert(x, w_gu, w_down, f16_gu=False, f16_down=False):
+    """The shared expert's term of ref_model.cpp:465-478: w_gu [2n + 1][H] holds the gate
+    rows, the up rows and the gate-logit row (the engine's concatenation, decode.hip:99),
+    w_down [H][n]; returns sigmoid(gate logit) * down(silu(gate x) * up x), [T][H]."""
+    n = (w_gu.shape[0] - 1) // 2
+    v = linear_w16(w_gu, x, f16_gu)
+    return linear_w16(w_down, swiglu_gate(v, n), f16_down)
 
 
 def q4_tile(W, S, Z, N, K):

@@ -14,6 +14,8 @@
  *   - engine nibble order          src/engine/weight_convert.cpp:61-71
  *   - int4 g128 quantiser          src/engine/weight_convert.cpp:73-90
  *   - MoE routing and combine      src/ref/ref_model.cpp:406-463
+ *   - 16-bit dense linear          src/ref/ref_model.cpp:86-97
+ *   - shared expert (SwiGLU, gate) src/ref/ref_model.cpp:465-478
  *   - slot order                   src/kernels/moe_route.hip:149-160
  *   - parallel_for chunking        src/core/threadpool.hpp:38-58
  *
@@ -367,8 +369,9 @@ void o_moe_slots(const int32_t *top_e, int T, int E, int topk, int32_t *counts, 
 
 static float o_silu(float x) { return x * (1.f / (1.f + expf(-x))); }
 
-/* ref_model.cpp:406-463 without the shared expert (bf16 dense, not on the q4
- * path): route, then for each expert in ascending order gather its tokens,
+/* ref_model.cpp:406-463 (the routed experts; the shared expert is
+ * o_linear_w16 + o_swiglu_gate below, composed in oracle.py's
+ * shared_expert): route, then for each expert in ascending order gather its tokens,
  * g = gate x, u = up x, h = silu(g) u, y = down h, out[t] += w y.
  * Weights per expert are contiguous: gate/up [E][F][H/8], down [E][H][F/8].
  * Also returns h [T*k][F] and yp [T*k][H] in slot order when non-NULL. */
@@ -425,6 +428,52 @@ void o_moe(const float *x, int T, int H, int F, int E, int topk, const float *lo
     free(offsets);
     free(tok_slot);
     free(pair_tok);
+}
+
+/* ---------------------------------------------- 16-bit dense weights */
+
+typedef struct {
+    const uint16_t *W;
+    int f16;
+    int64_t K, ldw;
+    const float *x;
+    int T, ldx;
+    float *y;
+    int ldy;
+} lin16_ctx;
+
+static void lin16_range(void *vc, int64_t b, int64_t e) {
+    lin16_ctx *c = (lin16_ctx *)vc;
+    float *row = (float *)malloc(sizeof(float) * (size_t)c->K);
+    for (int64_t o = b; o < e; ++o) {
+        const uint16_t *w = c->W + (size_t)o * (size_t)c->ldw;
+        for (int64_t i = 0; i < c->K; ++i) row[i] = c->f16 ? o_f16_to_f32(w[i]) : o_bf16_to_f32(w[i]);
+        for (int t = 0; t < c->T; ++t) c->y[(size_t)t * c->ldy + o] = dot_f32(row, c->x + (size_t)t * c->ldx, c->K);
+    }
+    free(row);
+}
+
+/* ref::Model::linear (src/ref/ref_model.cpp:86-97): y[t][o] = sum_i W[o][i] x[t][i]
+ * with W 16-bit (bf16 there; fp16 as in gpu::gemv_rows, src/kernels/gemv.hip:7-42,
+ * when f16 != 0), each row widened to fp32 and dotted in fp32. */
+void o_linear_w16(const uint16_t *W, int f16, int64_t N, int64_t K, int64_t ldw, const float *x, int T, int ldx,
+                  float *y, int ldy, int threads) {
+    lin16_ctx c = {W, f16, K, ldw, x, T, ldx, y, ldy};
+    parallel_for(threads, N, 16, lin16_range, &c);
+}
+
+static float o_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+
+/* The shared expert's activation (ref_model.cpp:468-476 with the gate folded
+ * in, the role of gpu::swiglu_T, src/kernels/moe_route.hip:187-197):
+ *   h[t][j] = silu(v[t][j]) * v[t][n + j] * sigmoid(v[t][2n])
+ * for v [T][ldv] holding gate (n), up (n) and the gate logit (1) per row. */
+void o_swiglu_gate(const float *v, int ldv, int n, int T, float *h) {
+    for (int t = 0; t < T; ++t) {
+        const float *r = v + (size_t)t * ldv;
+        const float gsig = o_sigmoid(r[2 * n]);
+        for (int j = 0; j < n; ++j) h[(size_t)t * n + j] = o_silu(r[j]) * r[n + j] * gsig;
+    }
 }
 
 /* ------------------------------------------------- device tiled format */

@@ -248,3 +248,50 @@ def test_device_expf_table_is_nearest_powers_of_two():
     for i, v in enumerate(vals):
         exact = float(Decimal(2) ** (Decimal(i) / Decimal(32)))
         assert (v + (i << 47)) & (2**64 - 1) == struct.unpack("<Q", struct.pack("<d", exact))[0]
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_linear_w16_vs_fp64(oracle, f16):
+    """The 16-bit-weight linear (ref_model.cpp:86-97) against an fp64 numpy
+    product of the same widened weights, and exactly on integer data."""
+    r = np.random.default_rng(3)
+    W = (r.standard_normal((37, 384)) * 0.05).astype(np.float32)
+    bits = W.astype(np.float16).view(np.uint16) if f16 else synth.bf16_bits(W)
+    Wf = bits.view(np.float16).astype(np.float32) if f16 else synth.bf16_to_f32(bits)
+    x = r.standard_normal((3, 384)).astype(np.float32)
+    y = oracle.linear_w16(bits, x, f16)
+    ref = x.astype(np.float64) @ Wf.astype(np.float64).T
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
+    Wi = r.integers(-8, 8, size=(16, 256)).astype(np.float32)
+    xi = r.integers(-8, 8, size=(2, 256)).astype(np.float32)
+    bi = Wi.astype(np.float16).view(np.uint16) if f16 else synth.bf16_bits(Wi)
+    assert np.array_equal(oracle.linear_w16(bi, xi, f16), xi @ Wi.T)
+
+
+def test_swiglu_gate_vs_torch(oracle):
+    """h = silu(g) * u * sigmoid(gate logit), against torch's own silu and
+    sigmoid in fp64."""
+    import torch
+    r = np.random.default_rng(4)
+    n, T = 96, 5
+    v = (r.standard_normal((T, 2 * n + 3)) * 3).astype(np.float32)
+    h = oracle.swiglu_gate(v, n)
+    vt = torch.from_numpy(v.astype(np.float64))
+    ref = (torch.nn.functional.silu(vt[:, :n]) * vt[:, n:2 * n] * torch.sigmoid(vt[:, 2 * n:2 * n + 1])).numpy()
+    assert np.max(np.abs(h - ref)) <= 1e-6 * np.max(np.abs(ref))
+
+
+def test_shared_expert_vs_dense_numpy(oracle):
+    """The shared expert's term (ref_model.cpp:465-478) against a dense fp64
+    numpy evaluation of the same formula from the widened weights."""
+    r = np.random.default_rng(6)
+    H, n, T = 256, 128, 4
+    gu = synth.bf16_bits((r.standard_normal((2 * n + 1, H)) * 0.05).astype(np.float32))
+    dn = synth.bf16_bits((r.standard_normal((H, n)) * 0.05).astype(np.float32))
+    x = r.standard_normal((T, H)).astype(np.float32)
+    got = oracle.shared_expert(x, gu, dn)
+    v = x.astype(np.float64) @ synth.bf16_to_f32(gu).astype(np.float64).T
+    g, u, s = v[:, :n], v[:, n:2 * n], v[:, 2 * n:2 * n + 1]
+    h = g / (1 + np.exp(-g)) * u / (1 + np.exp(-s))
+    ref = h @ synth.bf16_to_f32(dn).astype(np.float64).T
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))

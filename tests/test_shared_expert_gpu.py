@@ -1,0 +1,93 @@
+"""The shared expert and the dense 16-bit linear: qw_w16_gemv (fp16 weights
+with fp16 rows, as the engine's gemv_rows; bf16 with bf16, as the reference's
+Model::linear) and qw_swiglu_gate (the engine's swiglu_T) against the oracle,
+and the whole MoE block (routed experts + shared expert, ref_model.cpp:406-478)
+composed from the entry points."""
+import numpy as np
+import pytest
+
+import qwq4
+from qwq4 import synth
+from _gpu_util import TOL, bf16_err_ok, host, rel_err, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def w16(seed, name, N, K, f16, scale=0.05):
+    """16-bit weight bits [N][K] and their exact fp32 values."""
+    w = (synth.rng(seed, name).normal(0.0, scale, size=(N, K))).astype(np.float32)
+    if f16:
+        b = w.astype(np.float16).view(np.uint16)
+        return b, b.view(np.float16).astype(np.float32)
+    b = synth.bf16_bits(w)
+    return b, synth.bf16_to_f32(b)
+
+
+def rows(seed, name, M, K, f16):
+    v = synth.rng(seed, name).normal(0.0, 1.0, size=(M, K)).astype(np.float32)
+    if f16:
+        b = v.astype(np.float16).view(np.uint16)
+        return b, b.view(np.float16).astype(np.float32)
+    b = synth.bf16_bits(v)
+    return b, synth.bf16_to_f32(b)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("N,K,M", [(3073, 4096, 1), (3073, 4096, 4), (3073, 4096, 8), (4096, 1536, 1), (4096, 1536, 8),
+                                   (100, 320, 3), (1024, 2048, 17), (256, 4096, 32)])
+def test_w16_gemv(gpu, oracle, f16, N, K, M):
+    print(f"w16 gemv f16={f16} N={N} K={K} M={M}", flush=True)
+    Wb, _ = w16(81, f"w{N}x{K}", N, K, f16)
+    xb, xf = rows(81, f"x{M}x{K}", M, K, f16)
+    y = host(qwq4.gemv_w16(to_dev(Wb, gpu), to_dev(xb, gpu), M, f16=f16))
+    assert rel_err(y, oracle.linear_w16(Wb, xf, f16)) <= TOL
+
+
+def test_w16_gemv_strides_bf16_out_and_accumulate(gpu, oracle):
+    import torch
+    N, K, M = 500, 1024, 5
+    Wb, _ = w16(82, "ws", N, K, True)
+    xb, xf = rows(82, "xs", M, K, True)
+    Wp = torch.zeros((N, K + 64), dtype=torch.int16, device=gpu)
+    Wp[:, :K] = to_dev(Wb, gpu)
+    y = torch.full((M, N + 8), 0.5, dtype=torch.float32, device=gpu)
+    qwq4.gemv_w16(Wp[:, :K], to_dev(xb, gpu), M, y=y, accumulate=True, f16=True, ys=N + 8)
+    yh = host(y)
+    assert np.all(yh[:, N:] == 0.5)
+    assert rel_err(yh[:, :N], oracle.linear_w16(Wb, xf, True) + 0.5) <= TOL
+    yb = host(qwq4.gemv_w16(to_dev(Wb, gpu), to_dev(xb, gpu), M, y_bf16=True, f16=True))
+    assert bf16_err_ok(yb, oracle.linear_w16(Wb, xf, True))
+
+
+def test_swiglu_gate(gpu, oracle):
+    n, T = 1536, 6
+    v = (np.random.default_rng(83).standard_normal((T, 2 * n + 1)) * 2).astype(np.float32)
+    h = host(qwq4.swiglu_gate(to_dev(v, gpu), n)).astype(np.float32)
+    r = oracle.swiglu_gate(v, n)
+    # fp16 output: the oracle's value rounded to fp16, within an ulp
+    assert np.all(np.abs(h - r) <= 2.0**-10 * np.abs(r) + 2.0**-24)
+
+
+@pytest.mark.parametrize("T", [1, 4, 8])
+def test_moe_block_with_shared_expert(gpu, oracle, T):
+    """The engine's decode MoE block (decode.hip:99-111): shared expert
+    (fused gate/up/gate-logit GEMV on bf16 weights, SwiGLU x sigmoid gate,
+    down GEMV on fp16 weights) into the routed block's combine; against the
+    oracle's routed experts plus its shared expert (ref_model.cpp:406-478)."""
+    E, H, F, k, SF = 64, 1024, 256, 4, 512
+    print(f"moe block + shared expert T={T}", flush=True)
+    ex = synth.experts(84, E, H, F)
+    xb, xf = synth.acts(84, f"bx{T}", T, H)
+    Wr = (np.random.default_rng(84).standard_normal((E, H)) * 0.05).astype(np.float32)
+    gu_b, _ = w16(85, "gu", 2 * SF + 1, H, False)
+    dn_b, _ = w16(86, "dn", H, SF, True)
+    from test_moe_gpu import _experts_dev
+    (g, u, d), _, _ = _experts_dev(gpu, ex)
+    dx = to_dev(xb, gpu)
+    v = qwq4.gemv_w16(to_dev(gu_b, gpu), dx, T, f16=False)          # [T][2 SF + 1] fp32
+    hs = qwq4.swiglu_gate(v, SF)                                     # [T][SF] fp16
+    sh = qwq4.gemv_w16(to_dev(dn_b, gpu), hs, T, f16=True)           # [T][H] fp32
+    out, buf = qwq4.moe_decode(to_dev(Wr, gpu), dx, k, g, u, d, E, F, shared=sh, out_bf16=False)
+    logits = host(buf.logits)
+    ref = oracle.moe(xf, logits, k, *ex) + oracle.shared_expert(xf, gu_b, dn_b, f16_gu=False, f16_down=True)
+    assert rel_err(host(out), ref) <= TOL

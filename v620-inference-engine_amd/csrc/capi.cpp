@@ -98,6 +98,30 @@ int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
     return launched("qw_q4_gemv");
 }
 
+int qw_w16_gemv(const uint16_t *W, int ldw, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N,
+                int K, int M, int accumulate, void *stream) {
+    REQUIRE(W && x && y, "qw_w16_gemv: null W, x or y");
+    REQUIRE(N >= 1 && K >= 32 && K % 32 == 0, "qw_w16_gemv: N = %d, K = %d (need N >= 1, K a positive multiple of 32)",
+            N, K);
+    REQUIRE(ldw >= K && ldw % 8 == 0 && aligned(W, 16), "qw_w16_gemv: ldw %d must be >= K, a multiple of 8, W 16-byte aligned", ldw);
+    REQUIRE(M >= 1 && M <= 32, "qw_w16_gemv: M = %d outside 1..32", M);
+    REQUIRE(xs >= K && xs % 8 == 0 && aligned(x, 16), "qw_w16_gemv: x stride %d must be >= K, a multiple of 8, x 16-byte aligned", xs);
+    REQUIRE(ys >= N || M == 1, "qw_w16_gemv: y stride %d < N", ys);
+    REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_w16_gemv: y misaligned");
+    qwq4::W16Args a{W, ldw, x, xs, y, ys, y_bf16 != 0, N, K, M, accumulate != 0, f16 != 0};
+    qwq4::launch_w16_gemv(a, st(stream));
+    return launched("qw_w16_gemv");
+}
+
+int qw_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, void *stream) {
+    REQUIRE(v && h, "qw_swiglu_gate: null v or h");
+    REQUIRE(n >= 1 && T >= 1 && ldv >= 2 * n + 1, "qw_swiglu_gate: n = %d, T = %d, ldv = %d (need ldv >= 2n + 1)", n, T,
+            ldv);
+    REQUIRE(T <= 65535, "qw_swiglu_gate: T = %d > 65535", T);
+    qwq4::launch_swiglu_gate(v, ldv, n, T, h, st(stream));
+    return launched("qw_swiglu_gate");
+}
+
 size_t qw_q4_gemm_workspace_size(int T, int K) {
     if (T < 1 || K < 128) return 0;
     return qwq4::gemm_workspace_bytes(T, K);

@@ -407,4 +407,76 @@ __device__ __forceinline__ void store_y(void *y, int64_t o, float v, int y_bf16,
     }
 }
 
+// ---- the row-block tail shared by the dense GEMVs: k-split partial sums
+// through LDS, then the output rows
+
+// partial sums: one slot per wave that is not a k-part 0, double-buffered
+__host__ __device__ inline int red_slots(int waves, int KS) { return waves - waves / KS; }
+
+// LDS: staged rows, then the partial-sum slots
+__host__ __device__ inline size_t dense_lds_bytes(int M, int K, int MB, int waves, int KS) {
+    return size_t(x_pieces(M, K)) * 16 + size_t(2) * red_slots(waves, KS) * MB * WAVE * 16;
+}
+
+__device__ __forceinline__ void stage_x_issue(const uint16_t *__restrict__ x, int xs, int M, int K, uint4 *xl) {
+    stage_rows_issue([&](int m) { return x + int64_t(m) * xs; }, M, K, xl);
+}
+
+// Accumulator elements a lane keeps: MR of the last row block, 4 of the others.
+template <int MB, int MR>
+constexpr int acc_elems() { return (MB - 1) * 4 + MR; }
+
+template <int MB, int MR>
+__device__ __forceinline__ void store_rows(const f32x4 (&acc)[MB], void *y, int ys, int y_bf16, int accumulate,
+                                           int M, int N, int sub, int lane) {
+    const int q = lane / 16, n = lane % 16;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < (mb == MB - 1 ? MR : 4); ++r) {
+            const int m = mb * 16 + 4 * q + r;
+            if (m < M && sub * 16 + n < N) store_y(y, int64_t(m) * ys + sub * 16 + n, acc[mb][r], y_bf16, accumulate);
+        }
+}
+
+// Sums the KS partials of each subtile into the k-part 0 wave's acc, in
+// k-part order. Buffer rb: one slot of acc_elems() x 64 floats (element-major,
+// so a wave's write of one element is 64 consecutive floats) per wave with
+// k-part != 0, red_slots of them.
+template <int MB, int MR>
+__device__ __forceinline__ void ksplit_sum(f32x4 (&acc)[MB], float *rb, int KS, int wave, int kp, int lane) {
+    if (KS == 1) return;
+    constexpr int PER = acc_elems<MB, MR>();
+    const int slot0 = (wave / KS) * (KS - 1);  // the subtile's first partial slot
+    if (kp != 0) {
+        float *d = rb + (slot0 + kp - 1) * PER * WAVE + lane;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < (mb == MB - 1 ? MR : 4); ++r) d[(mb * 4 + r) * WAVE] = acc[mb][r];
+    }
+    lds_barrier();
+    if (kp == 0) {
+        // four partials in flight per step (KS is a runtime value), added in
+        // k-part order
+        for (int i0 = 1; i0 < KS; i0 += 4) {
+            float part[4][PER];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float *p = rb + (slot0 + min(i0 + j, KS - 1) - 1) * PER * WAVE + lane;
+#pragma unroll
+                for (int e = 0; e < PER; ++e) part[j][e] = p[e * WAVE];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (i0 + j < KS) {
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                        for (int r = 0; r < (mb == MB - 1 ? MR : 4); ++r) acc[mb][r] += part[j][mb * 4 + r];
+                }
+        }
+    }
+}
+
 }  // namespace qwq4

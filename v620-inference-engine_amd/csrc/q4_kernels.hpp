@@ -129,6 +129,20 @@ void launch_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int
 void launch_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, hipStream_t s);
 void launch_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, hipStream_t s);
 
+// Dense GEMV on 16-bit weights (row-major [N][ldw]; fp16 weights with fp16
+// x, or bf16 with bf16).
+struct W16Args {
+    const uint16_t *W;
+    int ldw;
+    const uint16_t *x;
+    int xs;
+    void *y;
+    int ys, y_bf16, N, K, M, accumulate, f16;
+};
+bool w16_fits(int M, int K);
+void launch_w16_gemv(const W16Args &a, hipStream_t s);
+void launch_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, hipStream_t s);
+
 struct GemmArgs {
     const uint32_t *W;
     const uint16_t *S;

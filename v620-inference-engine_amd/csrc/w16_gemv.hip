@@ -1,0 +1,158 @@
+// Dense GEMV on 16-bit weights, and the shared expert's SwiGLU with its
+// sigmoid gate.
+//
+// Reference roles: gpu::gemv_rows with fp16 weights (src/kernels/gemv.hip:7-42;
+// the engine runs the shared expert's gate/up and down projections through
+// it, src/engine/decode.hip:99-101) and ref::Model::linear on bf16 weights
+// (src/ref/ref_model.cpp:86-97); gpu::swiglu_T (src/kernels/moe_route.hip:187-197).
+//
+// The weights are row-major [N][ldw] as the checkpoint holds them, fp16 with
+// fp16 activations or bf16 with bf16 ones: the 16x16x32 MFMA takes both as
+// they are, so a product needs no conversion and every product is exact
+// (fp32 sums). The kernel shape is the q4 GEMV's (q4_gemv_impl.cuh): a block
+// holds one 16-row tile, its KS waves split K, each wave requests its whole
+// range of weight rows (16 B per lane per 32-element MFMA step, up to
+// W16_STEPS steps at once) before anything waits, the activations are staged
+// in LDS, and the KS partial sums are added through LDS in k-part order.
+#include "q4_gemv_core.cuh"
+#include "q4_kernels.hpp"
+
+namespace qwq4 {
+
+constexpr int W16_STEPS = 16;  // 32-element MFMA steps in flight per wave (64 VGPRs)
+constexpr int W16_MAX_KS = 8;  // waves per block
+
+template <typename XT, int MB, int MR, int XPT>
+__global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16_t *W, int ldw, const uint16_t *x,
+                                                                    int xs, int M, int K, int N, void *__restrict__ y,
+                                                                    int ys, int y_bf16, int accumulate) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int KS = blockDim.x / WAVE;
+    const int tid = threadIdx.x, kp = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
+              n = lane % 16;
+    const int steps = K / 32, spw = (steps + KS - 1) / KS, s0 = kp * spw, ns = min(spw, steps - s0);
+    const int kc = x_row_stride(K);
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    float *red = reinterpret_cast<float *>(xl + x_pieces(M, K));
+    XRegs xv;
+    if constexpr (XPT > 0) stage_regs_issue<XPT>(x, xs, M, K, xv);
+    else stage_x_issue(x, xs, M, K, xl);
+    __builtin_amdgcn_sched_barrier(0);  // every activation load goes out before the weight loads
+    // lane (n, q): 8 weights of row n at K 32 s + 8 q, step s
+    const uint4 *wrow =
+        reinterpret_cast<const uint4 *>(W + int64_t(min(int(blockIdx.x) * 16 + n, N - 1)) * ldw + 8 * q);
+    f32x4 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    uint4 w[W16_STEPS];
+    auto fetch = [&](int p) {  // steps p .. p + W16_STEPS - 1 of the wave's range (clamped, no branches)
+#pragma unroll
+        for (int t = 0; t < W16_STEPS; ++t) {
+            const int s = min(s0 + min(p + t, max(ns - 1, 0)), steps - 1);
+            const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow + s * 4));
+            w[t] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    };
+    fetch(0);
+    if constexpr (XPT > 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        stage_regs_commit<XPT>(xv, M, K, xl);
+        lds_barrier();
+    } else {
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm_below<W16_STEPS>();  // this wave's activation loads (its oldest)
+        __builtin_amdgcn_s_barrier();
+    }
+    const uint4 *xr[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) xr[mb] = xl + min(mb * 16 + n, M - 1) * kc + q;
+    for (int p = 0; p < ns; p += W16_STEPS) {
+        if (p > 0) fetch(p);
+#pragma unroll
+        for (int t = 0; t < W16_STEPS; ++t)
+            if (p + t < ns) {
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16<XT>(xr[mb][(s0 + p + t) * 4], w[t], acc[mb]);
+            }
+    }
+    ksplit_sum<MB, MR>(acc, red, KS, kp, kp, lane);
+    if (kp == 0) store_rows<MB, MR>(acc, y, ys, y_bf16, accumulate, M, N, blockIdx.x, lane);
+}
+
+template <typename XT, int MB, int MR>
+static void launch_w16_t(const W16Args &a, int KS, hipStream_t s) {
+    const int threads = KS * WAVE;
+    const size_t lds = dense_lds_bytes(a.M, a.K, MB, KS, KS);
+    const int xpt = (a.M * (a.K / 8) + threads - 1) / threads;
+    const unsigned blocks = unsigned((a.N + 15) / 16);
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), threads, lds);
+        kern<<<blocks, threads, lds, s>>>(a.W, a.ldw, a.x, a.xs, a.M, a.K, a.N, a.y, a.ys, a.y_bf16, a.accumulate);
+    };
+    if (xpt <= 1) go(w16_gemv_kernel<XT, MB, MR, 1>);
+    else if (xpt <= 2) go(w16_gemv_kernel<XT, MB, MR, 2>);
+    else if (xpt <= 4) go(w16_gemv_kernel<XT, MB, MR, 4>);
+    else go(w16_gemv_kernel<XT, MB, MR, 0>);
+}
+
+template <typename XT>
+static void launch_w16_x(const W16Args &a, int KS, hipStream_t s) {
+    if (a.M > 16) launch_w16_t<XT, 2, 4>(a, KS, s);
+    else if (a.M == 1) launch_w16_t<XT, 1, 1>(a, KS, s);
+    else if (a.M == 2) launch_w16_t<XT, 1, 2>(a, KS, s);
+    else launch_w16_t<XT, 1, 4>(a, KS, s);
+}
+
+// K split: as many waves (up to 8) as the 32-element steps allow; fewer
+// steps per wave mean more loads in flight per weight byte.
+static int w16_ks(int K) { return K / 32 < W16_MAX_KS ? K / 32 : W16_MAX_KS; }
+
+bool w16_fits(int M, int K) {
+    const int KS = w16_ks(K), MB = M > 16 ? 2 : 1;
+    return dense_lds_bytes(M, K, MB, KS, KS) <= 160 * 1024;
+}
+
+static void launch_w16_fit(const W16Args &a, hipStream_t s) {
+    const int KS = w16_ks(a.K);
+    if (a.f16) launch_w16_x<F16>(a, KS, s);
+    else launch_w16_x<BF16>(a, KS, s);
+}
+
+// Batches whose activations exceed LDS run as several launches of fewer rows.
+void launch_w16_gemv(const W16Args &a, hipStream_t s) {
+    if (w16_fits(a.M, a.K)) {
+        launch_w16_fit(a, s);
+        return;
+    }
+    int mc = 16;
+    while (mc > 1 && !w16_fits(mc, a.K)) --mc;
+    const size_t ysz = a.y_bf16 ? 2 : 4;
+    for (int m0 = 0; m0 < a.M; m0 += mc) {
+        W16Args b = a;
+        b.M = a.M - m0 < mc ? a.M - m0 : mc;
+        b.x = a.x + int64_t(m0) * a.xs;
+        b.y = static_cast<char *>(a.y) + int64_t(m0) * a.ys * ysz;
+        launch_w16_fit(b, s);
+    }
+}
+
+// ---------------------------------------------------------- SwiGLU x gate
+// h[t][j] = fp16(silu(v[t][j]) * v[t][n + j] * sigmoid(v[t][2n])): the shared
+// expert's activation, v the output of its fused gate/up/gate-logit GEMV.
+// Finite values beyond the fp16 range saturate (f32_to_f16_satfinite).
+__global__ __launch_bounds__(256) void swiglu_gate_kernel(const float *__restrict__ v, int ldv, int n, int T,
+                                                          uint16_t *__restrict__ h) {
+    const int t = blockIdx.y, j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const float *r = v + int64_t(t) * ldv;
+    const float g = r[j], u = r[n + j], gl = r[2 * n];
+    const float silu = g / (1.f + expf(-g)), gate = 1.f / (1.f + expf(-gl));
+    h[int64_t(t) * n + j] = __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(silu * u * gate));
+}
+
+void launch_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, hipStream_t s) {
+    swiglu_gate_kernel<<<dim3(unsigned((n + 255) / 256), unsigned(T)), 256, 0, s>>>(v, ldv, n, T, h);
+}
+
+}  // namespace qwq4

@@ -20,6 +20,7 @@ SYMBOLS = (
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
     "qw_moe_decode_workspace_size", "qw_moe_decode", "qw_moe_decode_static_max_bytes", "qw_moe_decode_static",
+    "qw_w16_gemv", "qw_swiglu_gate",
     "qw_wcache_open", "qw_wcache_put", "qw_wcache_get", "qw_wcache_finish", "qw_wcache_close",
 )
 
@@ -50,6 +51,8 @@ _SIGS = {
     "qw_moe_decode_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "qw_moe_decode": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
     "qw_moe_decode_static_max_bytes": ([], _SZ),
+    "qw_w16_gemv": ([_P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_swiglu_gate": ([_P, _I, _I, _I, _P, _P], _I),
     "qw_moe_decode_static": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
     "qw_st_close": ([_P], None),
@@ -164,6 +167,35 @@ def gemv(W, S, Z, x, N, K, M=None, y=None, y_bf16=False, accumulate=False, xs=No
                           N, K, M, int(accumulate), _stream())
     _check(rc, "qw_q4_gemv")
     return y
+
+
+def gemv_w16(W, x, M=None, y=None, y_bf16=False, accumulate=False, f16=None, xs=None, ys=None):
+    """y[m][n] (+)= sum_k W[n][k] x[m][k] for 16-bit W [N][K] (row-major, stride W.stride(0)):
+    fp16 W with fp16 x (f16 True, the default for float16 tensors) or bf16 with bf16."""
+    import torch
+    N, K = W.shape
+    M = M if M is not None else x.shape[0]
+    f16 = _is_f16(x, f16)
+    xs = xs if xs is not None else x.stride(0) if x.dim() == 2 else K
+    if y is None:
+        y = torch.zeros((M, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=x.device)
+    ys = ys if ys is not None else (y.stride(0) if y.dim() == 2 else N)
+    _dev(W, x, y)
+    rc = lib().qw_w16_gemv(_ptr(W), W.stride(0), _ptr(x), xs, int(f16), _ptr(y), ys, int(y_bf16), N, K, M,
+                           int(accumulate), _stream())
+    _check(rc, "qw_w16_gemv")
+    return y
+
+
+def swiglu_gate(v, n, h=None):
+    """h[t][j] = fp16(silu(v[t][j]) * v[t][n + j] * sigmoid(v[t][2n])); v fp32 [T][>= 2n + 1]."""
+    import torch
+    T = v.shape[0]
+    if h is None:
+        h = torch.empty((T, n), dtype=torch.float16, device=v.device)
+    _dev(v, h)
+    _check(lib().qw_swiglu_gate(_ptr(v), v.stride(0), n, T, _ptr(h), _stream()), "qw_swiglu_gate")
+    return h
 
 
 def gemm_workspace_size(T, K):
