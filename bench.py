@@ -255,6 +255,43 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
     return out
 
 
+# ------------------------------------------------- shared expert (16-bit)
+SH_LAYERS, SH_FFN = 8, 1536
+
+
+def bench_shared(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8)):
+    """The shared expert as the engine runs it (src/engine/decode.hip:99-101):
+    fused gate/up/gate-logit GEMV [2F+1][H] on fp16 weights, SwiGLU x sigmoid
+    gate, down GEMV [H][F] on fp16 weights; SH_LAYERS layers of their own
+    weights (302 MB, past the Infinity Cache). Bytes: the 16-bit weights."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(500)
+    gu = [(torch.randn((2 * SH_FFN + 1, H), generator=g, device=dev) * 0.05).half() for _ in range(SH_LAYERS)]
+    dn = [(torch.randn((H, SH_FFN), generator=g, device=dev) * 0.05).half() for _ in range(SH_LAYERS)]
+    wbytes = SH_LAYERS * (gu[0].numel() + dn[0].numel()) * 2
+    out = {}
+    for M in batches:
+        x = torch.randn((M, H), generator=g, device=dev).half()
+        v = torch.empty((M, 2 * SH_FFN + 1), dtype=torch.float32, device=dev)
+        hs = torch.empty((M, SH_FFN), dtype=torch.float16, device=dev)
+        y = torch.empty((M, H), dtype=torch.float32, device=dev)
+
+        def launches():
+            for l in range(SH_LAYERS):
+                qwq4.gemv_w16(gu[l], x, M, y=v)
+                qwq4.swiglu_gate(v, SH_FFN, h=hs)
+                qwq4.gemv_w16(dn[l], hs, M, y=y)
+
+        step = graphed(torch, launches)
+        for _ in range(warmup):
+            step()
+        with Timer(torch) as t:
+            for _ in range(steps):
+                step()
+        out[M] = {"GB_s": wbytes * steps / (t.ms * 1e-3) / 1e9, "us_per_layer": t.ms * 1e3 / (steps * SH_LAYERS)}
+    return out
+
+
 # ---------------------------------------------------------------- config 4
 def bench_gemm(torch, qwq4, dev, steps, warmup):
     T = 4096
@@ -471,7 +508,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, gemm, moe_prefill; or traffic (launches for PMC runs), or dominant (the roofline kernel's launches alone)")
+    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, shared, gemm, moe_prefill; or traffic (launches for PMC runs), or dominant (the roofline kernel's launches alone)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parse-pmc", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT_JSON"),
                     help="reduce two rocprofv3 --pmc runs of --workload traffic to bytes per launch")
@@ -495,7 +532,7 @@ def main():
         return
     wl = set(a.workload.split(","))
     if "all" in wl:
-        wl = {"gemv", "moe", "gemm", "moe_prefill"}
+        wl = {"gemv", "moe", "shared", "gemm", "moe_prefill"}
     res = {}
     if "gemv" in wl:
         res["gemv"] = bench_gemv(torch, qwq4, dev, a.steps, a.warmup)
@@ -504,6 +541,10 @@ def main():
     if "moe" in wl:
         res["moe_decode"] = bench_moe(torch, qwq4, dev, a.steps, a.warmup)
         print("# moe decode done", file=sys.stderr, flush=True)
+    if "shared" in wl:
+        res["shared_expert"] = bench_shared(torch, qwq4, dev, a.steps, a.warmup)
+        print("# shared expert done", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
     if "gemm" in wl:
         res["prefill_gemm"] = bench_gemm(torch, qwq4, dev, max(4, a.steps), 1)
         print("# gemm done", file=sys.stderr, flush=True)
