@@ -510,6 +510,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, shared, gemm, moe_prefill; or traffic (launches for PMC runs), or dominant (the roofline kernel's launches alone)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--moe-batches", default="1,2,4,8,16,32",
+                    help="decode batches of the moe workload (comma list), e.g. one batch for a per-launch trace")
     ap.add_argument("--parse-pmc", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT_JSON"),
                     help="reduce two rocprofv3 --pmc runs of --workload traffic to bytes per launch")
     a = ap.parse_args()
@@ -539,7 +541,8 @@ def main():
         print(f"# gemv {res['gemv']['GB_s']:.1f} GB/s", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
     if "moe" in wl:
-        res["moe_decode"] = bench_moe(torch, qwq4, dev, a.steps, a.warmup)
+        res["moe_decode"] = bench_moe(torch, qwq4, dev, a.steps, a.warmup,
+                                      batches=tuple(int(b) for b in a.moe_batches.split(",")))
         print("# moe decode done", file=sys.stderr, flush=True)
     if "shared" in wl:
         res["shared_expert"] = bench_shared(torch, qwq4, dev, a.steps, a.warmup)

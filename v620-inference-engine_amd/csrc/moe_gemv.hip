@@ -75,7 +75,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
         __syncthreads();
         const uint4 *xr[1] = {xl + min(n, mc - 1) * kc + q * 4};
         f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
-        wr.template compute<XT, 1>(xr, acc);
+        compute_zq_inline<XT>(wr, xr[0], acc[0]);
         red[wave * WAVE + lane] = acc[0];
         lds_barrier();
         if (mat == 0 && kp == 0 && lsub < fsub) {
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
         __syncthreads();
         const uint4 *xr[1] = {xl + min(n, mc - 1) * kc + q * 4};
         f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
-        wr.template compute<F16, 1>(xr, acc);
+        compute_zq_inline<F16>(wr, xr[0], acc[0]);
         if constexpr (KS > 1) {
             red[wave * WAVE + lane] = acc[0];
             lds_barrier();

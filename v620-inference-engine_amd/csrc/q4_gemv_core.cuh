@@ -350,6 +350,36 @@ __device__ __forceinline__ void compute_zq(const WaveRange<GW, HAS_Z, CH4> (&wr)
     }
 }
 
+// compute_zq for one subtile and one row block with each group's sum of
+// activations formed just before its product (no per-group sums held across
+// the range: for kernels whose registers go to a longer weight range).
+template <typename T, int GW, bool HAS_Z, bool CH4>
+__device__ __forceinline__ void compute_zq_inline(const WaveRange<GW, HAS_Z, CH4> &wr, const uint4 *xr, f32x4 &acc) {
+    const uint4 one = make_uint4(T::ONE, T::ONE, T::ONE, T::ONE);
+#pragma unroll
+    for (int c = 0; c < GW; ++c) {
+        if (c < wr.n) {
+            const int g = wr.g0 + c;
+            uint4 a[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[t] = xr[g * 16 + t];
+            f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) sum = mfma16<T>(a[t], one, sum);
+            const float nz = -(T::BASE + T::UNIT * float(HAS_Z ? Q4Tile::zero_of(wr.zv[c], g) : 8u));
+            uint4 b[4];
+            b[0] = unpack8_q<T>(wr.w[c].x);
+            b[1] = unpack8_q<T>(wr.w[c].y);
+            b[2] = unpack8_q<T>(wr.w[c].z);
+            b[3] = unpack8_q<T>(wr.w[c].w);
+            f32x4 p = sum * nz;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) p = mfma16<T>(a[t], b[t], p);
+            acc += (f16_bits_to_f32(uint16_t(wr.sv[c])) * (1.f / T::UNIT)) * p;
+        }
+    }
+}
+
 // The lane's fragment of a packed correction tile (token n % 4 of group
 // gb + n / 4, groups past the last one clamped to it) in rows staged at xl
 // with row stride kc (pieces), M rows, G groups.
