@@ -341,7 +341,7 @@ def bench_moe_prefill(torch, qwq4, dev, steps, warmup):
     tm = qwq4.moe_grouped_tile_m()
     r = qwq4.Route(T, E, k, dev, tile_m=tm)
     h = torch.empty((T * k, F), dtype=torch.float16, device=dev)
-    yp = torch.empty((T * k, H), dtype=torch.float32, device=dev)
+    yp = torch.empty((T * k, H), dtype=torch.float16, device=dev)  # fp16 per-slot rows, as the reference keeps them
     o = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
     ws = torch.empty(max(qwq4.moe_grouped_workspace_size(T, k, E, H, F), 1), dtype=torch.uint8, device=dev)
 

@@ -170,21 +170,26 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
  * slots). x [T][H] bf16 (x_f16 = 0) or fp16 (x_f16 = 1). For bf16 x,
  * workspace: at least qw_moe_grouped_workspace_size(...) bytes (an fp16
  * copy of x), 256-byte aligned; fp16 x needs none. x and h pass through fp16 as in qw_q4_gemm (finite
- * values beyond +-65504 saturate, infinities and NaN pass through). */
+ * values beyond +-65504 saturate, infinities and NaN pass through). yp
+ * [T*k][H] (16-byte aligned) is fp32 (yp_f16 = 0) or fp16 (yp_f16 = 1, the
+ * reference's choice, src/kernels/moe.hpp:20-25: half the bytes written by
+ * the down GEMM and read by the combine; finite values beyond +-65504
+ * saturate). H a multiple of 8. */
 int qw_moe_grouped_tile_m(void);
 size_t qw_moe_grouped_workspace_size(int T, int topk, int E, int H, int F);
 int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
                            const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                            const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
                            const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
-                           int x_f16, int T, int topk, uint16_t *h, float *yp, void *workspace,
+                           int x_f16, int T, int topk, uint16_t *h, void *yp, int yp_f16, void *workspace,
                            size_t workspace_bytes, void *stream);
 
 /* Weighted combine (replaces gpu::moe_combine_B/T, moe.hpp:42-46):
  *   out[t][j] = shared[t][j] + sum_{i<k} tok_w[t][i] * yp[tok_slot[t][i]][j]
- * shared fp32 [T][H] or NULL; out fp32 or bf16 (out_bf16). H % 4 == 0. */
-int qw_moe_combine(const float *yp, const int32_t *tok_slot, const float *tok_w, const float *shared, int T, int topk,
-                   int H, void *out, int out_bf16, void *stream);
+ * yp fp32 (yp_f16 = 0) or fp16 (yp_f16 = 1); shared fp32 [T][H] or NULL;
+ * out fp32 or bf16 (out_bf16). H % 4 == 0. Sums in fp32, selection order. */
+int qw_moe_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared, int T,
+                   int topk, int H, void *out, int out_bf16, void *stream);
 
 /* Format surface (bit-exact): nibbles as bytes [N][K]; dequantised fp32
  * weights [N][K]; reference-engine word order -> checkpoint word order. */

@@ -27,7 +27,7 @@ def test_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert qwq4.lib().qw_q4_abi_version() == 2
+    assert qwq4.lib().qw_q4_abi_version() == 3
 
 
 @pytest.mark.parametrize("call", [
@@ -37,7 +37,7 @@ def test_abi_version():
     lambda L: L.qw_q4_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(256), 0, 4096,
                            ctypes.c_void_p(256), 4096, 0, 4096, 4096, 33, 0, None),
     lambda L: L.qw_moe_route(ctypes.c_void_p(256), 4, 256, 0, 0, *([ctypes.c_void_p(256)] * 11), None),
-    lambda L: L.qw_moe_combine(None, None, None, None, 1, 8, 4096, None, 1, None),
+    lambda L: L.qw_moe_combine(None, 0, None, None, None, 1, 8, 4096, None, 1, None),
     lambda L: L.qw_q4_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(256), 0, 4096,
                            ctypes.c_void_p(256), 4096, 0, 4008, 4096, 1, 0, None),  # N % 16
     lambda L: L.qw_q4_gemm(ctypes.c_void_p(256), ctypes.c_void_p(256), None, ctypes.c_void_p(256), 0, 4096, 4096,
@@ -48,7 +48,7 @@ def test_abi_version():
                                     0, 33, 8, ctypes.c_void_p(256), ctypes.c_void_p(256), None),  # T > 32
     lambda L: L.qw_moe_experts_grouped(*([ctypes.c_void_p(256)] * 9), 256, 4096, 1536,
                                        *([ctypes.c_void_p(256)] * 6), 0, 4096, 8, ctypes.c_void_p(256),
-                                       ctypes.c_void_p(256), ctypes.c_void_p(256), 0, None),  # workspace too small
+                                       ctypes.c_void_p(256), 0, ctypes.c_void_p(256), 0, None),  # workspace too small
     lambda L: L.qw_moe_decode(ctypes.c_void_p(256), ctypes.c_void_p(256), 0, 33, 256, 8,
                               *([ctypes.c_void_p(256)] * 9), 4096, 1536, None, ctypes.c_void_p(256), 1,
                               *([ctypes.c_void_p(256)] * 7), 1 << 30, None),  # T > 32

@@ -57,11 +57,12 @@ def test_gemm_microbatch_fp32_out(gpu, oracle):
 # (E, H, F, k, T, zeros, bias): few tokens per expert (one partial tile each,
 # some experts empty); many per expert (several tiles, ragged last tile, F
 # not a multiple of 256); symmetric weights (no zero tensor).
+@pytest.mark.parametrize("yp16", [False, True])
 @pytest.mark.parametrize("E,H,F,k,T,zeros,bias", [(16, 512, 256, 4, 300, True, 0.5),
                                                   (8, 256, 384, 2, 1100, True, 1.0),
                                                   (64, 384, 128, 6, 40, False, 0.0)])
-def test_grouped_matches_oracle_small(gpu, oracle, E, H, F, k, T, zeros, bias):
-    print(f"grouped E={E} H={H} F={F} k={k} T={T} zeros={zeros}", flush=True)
+def test_grouped_matches_oracle_small(gpu, oracle, E, H, F, k, T, zeros, bias, yp16):
+    print(f"grouped E={E} H={H} F={F} k={k} T={T} zeros={zeros} yp16={yp16}", flush=True)
     ex = synth.experts(61, E, H, F, zeros=zeros)
     xb, xf = synth.acts(61, "x", T, H)
     l = synth.router_logits(61, "l", T, E, bias_sigma=bias)
@@ -69,9 +70,9 @@ def test_grouped_matches_oracle_small(gpu, oracle, E, H, F, k, T, zeros, bias):
     from test_moe_gpu import _experts_dev
     (dg, du, dd), E, F = _experts_dev(gpu, ex)
     r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=qwq4.moe_grouped_tile_m())
-    h, yp = qwq4.moe_experts_grouped(dg, du, dd, r, to_dev(xb, gpu), E, F)
+    h, yp = qwq4.moe_experts_grouped(dg, du, dd, r, to_dev(xb, gpu), E, F, yp_f16=yp16)
     assert rel_err(host(h).astype(np.float32), h_ref) <= TOL
-    assert rel_err(host(yp), yp_ref) <= TOL
+    assert rel_err(host(yp).astype(np.float32), yp_ref) <= TOL
     o = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
     assert rel_err(o, out) <= TOL
 
@@ -91,7 +92,7 @@ def test_grouped_full_config_sampled(gpu, oracle):
     (dg, du, dd), E, F = _experts_dev(gpu, ex)
     g = -qwq4.moe_grouped_tile_m()
     r = qwq4.moe_route(to_dev(l, gpu), k, tile_m=-g)
-    _, yp = qwq4.moe_experts_grouped(dg, du, dd, r, to_dev(xb, gpu), E, F)
+    _, yp = qwq4.moe_experts_grouped(dg, du, dd, r, to_dev(xb, gpu), E, F, yp_f16=True)   # as the benchmark runs it
     o = host(qwq4.moe_combine(yp, r, H, out_bf16=False))
     counts = host(r.counts)
     rems = [int(c) - m0 for c in counts for m0 in range(0, int(c), g)]

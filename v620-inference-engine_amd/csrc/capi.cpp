@@ -80,7 +80,7 @@ int check_ckpt(const char *fn, const uint32_t *W, const uint16_t *S, int64_t N, 
 
 extern "C" {
 
-int qw_q4_abi_version(void) { return 2; }
+int qw_q4_abi_version(void) { return 3; }
 
 const char *qw_q4_last_error(void) { return g_err.c_str(); }
 
@@ -194,7 +194,7 @@ int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_
                            const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                            const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
                            const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
-                           int x_f16, int T, int topk, uint16_t *h, float *yp, void *workspace,
+                           int x_f16, int T, int topk, uint16_t *h, void *yp, int yp_f16, void *workspace,
                            size_t workspace_bytes, void *stream) {
     if (int r = check_q4("qw_moe_experts_grouped(gate)", gw, gs, int64_t(E) * F, H)) return r;
     if (int r = check_q4("qw_moe_experts_grouped(up)", uw, us, int64_t(E) * F, H)) return r;
@@ -202,25 +202,27 @@ int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_
     REQUIRE(offsets && pair_tok && tile_e && tile_m0 && n_tiles && x && h && yp,
             "qw_moe_experts_grouped: null pointer");
     REQUIRE(T >= 1 && topk >= 1 && topk <= E, "qw_moe_experts_grouped: T = %d, topk = %d", T, topk);
-    REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(yp, 4), "qw_moe_experts_grouped: x/h must be 16-byte aligned");
+    REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(yp, 16), "qw_moe_experts_grouped: x/h/yp must be 16-byte aligned");
+    REQUIRE(H % 8 == 0, "qw_moe_experts_grouped: H = %d must be a multiple of 8", H);
     const size_t need = x_f16 ? 0 : qwq4::moe_grouped_workspace_bytes(T, topk, E, H, F);
     REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
             "qw_moe_experts_grouped: workspace needs %zu bytes, 256-byte aligned", need);
     qwq4::MoeGroupedArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, offsets, pair_tok, tile_e, tile_m0, n_tiles,
                            x, T, topk, h, yp, workspace};
     a.x_f16 = x_f16 != 0;
+    a.yp_f16 = yp_f16 != 0;
     qwq4::launch_moe_grouped(a, st(stream));
     return launched("qw_moe_experts_grouped");
 }
 
-int qw_moe_combine(const float *yp, const int32_t *tok_slot, const float *tok_w, const float *shared, int T, int topk,
-                   int H, void *out, int out_bf16, void *stream) {
+int qw_moe_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared, int T,
+                   int topk, int H, void *out, int out_bf16, void *stream) {
     REQUIRE(yp && tok_slot && tok_w && out, "qw_moe_combine: null pointer");
     REQUIRE(T >= 1 && topk >= 1 && H >= 4 && H % 4 == 0, "qw_moe_combine: T = %d, topk = %d, H = %d (need H %% 4 == 0)", T,
             topk, H);
-    REQUIRE(aligned(yp, 16) && (!shared || aligned(shared, 16)) && aligned(out, out_bf16 ? 8 : 16),
+    REQUIRE(aligned(yp, yp_f16 ? 8 : 16) && (!shared || aligned(shared, 16)) && aligned(out, out_bf16 ? 8 : 16),
             "qw_moe_combine: misaligned yp/shared/out");
-    qwq4::launch_combine(yp, tok_slot, tok_w, shared, T, topk, H, out, out_bf16 != 0, st(stream));
+    qwq4::launch_combine(yp, yp_f16 != 0, tok_slot, tok_w, shared, T, topk, H, out, out_bf16 != 0, st(stream));
     return launched("qw_moe_combine");
 }
 
@@ -454,7 +456,7 @@ void moe_decode_launch(const float *router_w, const uint16_t *x, int x_f16, int 
                         at(L.pair_tok), x, T, topk, h, yp, fold ? &cmb : nullptr};
     a.x_f16 = x_f16 != 0;
     qwq4::launch_moe_gemv(a, s);
-    if (!fold) qwq4::launch_combine(yp, tok_slot, top_w, shared, T, topk, H, out, out_bf16, s);
+    if (!fold) qwq4::launch_combine(yp, 0, tok_slot, top_w, shared, T, topk, H, out, out_bf16, s);
 }
 
 // ---- the allocation-free variant's scratch: one array per GPU, held until

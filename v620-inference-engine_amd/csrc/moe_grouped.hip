@@ -124,9 +124,11 @@ __global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(GateUpTile 
 }
 
 // One down tile of BM slot rows (M real) starting at slot base.
-template <int BM, bool HAS_Z>
+// yp rows fp32 (YP16 false) or fp16 (finite values beyond +-65504 saturate,
+// as the reference keeps yp, src/kernels/moe.hpp:20-25).
+template <int BM, bool HAS_Z, bool YP16>
 __device__ __forceinline__ void down_tile(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int e,
-                                          int base, int M, const uint16_t *h, int H, int F, float *yp) {
+                                          int base, int M, const uint16_t *h, int H, int F, void *yp) {
     using Sh = GemmShape<BM>;
     const int tid = threadIdx.x, wave = tid / WAVE;
     const int n0 = blockIdx.x * GB_N;
@@ -142,26 +144,28 @@ __device__ __forceinline__ void down_tile(const uint32_t *dw, const uint16_t *ds
     gemm_tile<BM, HAS_Z>(ap, b, F, acc);
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
-    emit_tile<Sh::NJ, 4>(
-        epi_slot(wave), acc, [](float, int, int) { return uint16_t(0); },
+    constexpr int YB = YP16 ? 2 : 4;
+    emit_tile<Sh::NJ, YB>(
+        epi_slot(wave), acc, [](float v, int, int) { return f32_to_f16_sat(v); },
         [&](int tr, int c, uint4 v) {
             const int m = wm * 64 + tr, n = n0 + wn2 * Sh::WNR + c;
-            if (m < M && n < H) *reinterpret_cast<uint4 *>(yp + int64_t(base + m) * H + n) = v;
+            if (m < M && n < H)
+                *reinterpret_cast<uint4 *>(static_cast<unsigned char *>(yp) + (int64_t(base + m) * H + n) * YB) = v;
         });
 }
 
-template <bool HAS_Z>
+template <bool HAS_Z, bool YP16>
 __global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
     const uint32_t *__restrict__ dw, const uint16_t *__restrict__ ds, const uint16_t *__restrict__ dz,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ tile_e, const int32_t *__restrict__ tile_m0,
-    const int32_t *__restrict__ n_tiles, const uint16_t *__restrict__ h, int H, int F, float *__restrict__ yp) {
+    const int32_t *__restrict__ n_tiles, const uint16_t *__restrict__ h, int H, int F, void *__restrict__ yp) {
     const int tile = blockIdx.y;
     if (tile >= *n_tiles) return;
     const int e = tile_e[tile], m0 = tile_m0[tile], rem = offsets[e + 1] - offsets[e] - m0;
     const int base = offsets[e] + m0, rows = tile_rows(rem, GROUPED_TILE_M), M = min(rows, rem);
-    if (rows == 256) down_tile<256, HAS_Z>(dw, ds, dz, e, base, M, h, H, F, yp);
-    else if (rows == 128) down_tile<128, HAS_Z>(dw, ds, dz, e, base, M, h, H, F, yp);
-    else down_tile<64, HAS_Z>(dw, ds, dz, e, base, M, h, H, F, yp);
+    if (rows == 256) down_tile<256, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
+    else if (rows == 128) down_tile<128, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
+    else down_tile<64, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
 }
 
 void launch_moe_grouped(const MoeGroupedArgs &a, hipStream_t s) {
@@ -178,12 +182,15 @@ void launch_moe_grouped(const MoeGroupedArgs &a, hipStream_t s) {
     const GateUpTile gu{a.gw, a.uw, a.gs, a.gz, a.us, a.uz, a.pair_tok, xh, a.H, a.F, a.h};
     if (a.gz) moe_gate_up_gemm_kernel<true><<<g1, G_THREADS, 0, s>>>(gu, a.offsets, a.tile_e, a.tile_m0, a.n_tiles);
     else moe_gate_up_gemm_kernel<false><<<g1, G_THREADS, 0, s>>>(gu, a.offsets, a.tile_e, a.tile_m0, a.n_tiles);
+    auto down = [&](auto kern) {
+        kern<<<g2, G_THREADS, 0, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0, a.n_tiles, a.h, a.H, a.F, a.yp);
+    };
     if (a.dz) {
-        moe_down_gemm_kernel<true><<<g2, G_THREADS, 0, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0,
-                                                                   a.n_tiles, a.h, a.H, a.F, a.yp);
+        if (a.yp_f16) down(moe_down_gemm_kernel<true, true>);
+        else down(moe_down_gemm_kernel<true, false>);
     } else {
-        moe_down_gemm_kernel<false><<<g2, G_THREADS, 0, s>>>(a.dw, a.ds, a.dz, a.offsets, a.tile_e, a.tile_m0,
-                                                                    a.n_tiles, a.h, a.H, a.F, a.yp);
+        if (a.yp_f16) down(moe_down_gemm_kernel<false, true>);
+        else down(moe_down_gemm_kernel<false, false>);
     }
 }
 

@@ -572,7 +572,20 @@ void launch_route(const RouteArgs &a, hipStream_t s) {
 
 // out[t][j] = shared[t][j] + sum_i w[t][i] * yp[slot[t][i]][j], i in selection
 // order (src/kernels/moe_route.hip:168-185, 201-224). 4 columns per thread.
-__global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ yp, const int32_t *__restrict__ tok_slot,
+// yp rows fp32, or fp16 (YP16)
+template <bool YP16>
+__device__ __forceinline__ float4 yp_row4(const void *yp, int64_t row, int H, int j) {
+    if constexpr (YP16) {
+        const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(yp) + row * H + j);
+        return make_float4(f16_bits_to_f32(uint16_t(u.x)), f16_bits_to_f32(uint16_t(u.x >> 16)),
+                           f16_bits_to_f32(uint16_t(u.y)), f16_bits_to_f32(uint16_t(u.y >> 16)));
+    } else {
+        return *reinterpret_cast<const float4 *>(static_cast<const float *>(yp) + row * H + j);
+    }
+}
+
+template <bool YP16>
+__global__ __launch_bounds__(256) void combine_kernel(const void *__restrict__ yp, const int32_t *__restrict__ tok_slot,
                                                       const float *__restrict__ tok_w, const float *__restrict__ shared,
                                                       int k, int H, void *__restrict__ out, int out_bf16) {
     const int t = blockIdx.x, j = (blockIdx.y * 256 + threadIdx.x) * 4;
@@ -587,7 +600,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
         for (int u = 0; u < 8; ++u) {
             const int i = min(i0 + u, k - 1);
             w[u] = tok_w[t * k + i];
-            v[u] = *reinterpret_cast<const float4 *>(yp + int64_t(tok_slot[t * k + i]) * H + j);
+            v[u] = yp_row4<YP16>(yp, int64_t(tok_slot[t * k + i]), H, j);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -610,10 +623,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     }
 }
 
-void launch_combine(const float *yp, const int32_t *tok_slot, const float *tok_w, const float *shared, int T, int topk,
-                    int H, void *out, int out_bf16, hipStream_t s) {
+void launch_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared,
+                    int T, int topk, int H, void *out, int out_bf16, hipStream_t s) {
     const dim3 grid(unsigned(T), unsigned((H / 4 + 255) / 256));
-    combine_kernel<<<grid, 256, 0, s>>>(yp, tok_slot, tok_w, shared, topk, H, out, out_bf16);
+    if (yp_f16) combine_kernel<true><<<grid, 256, 0, s>>>(yp, tok_slot, tok_w, shared, topk, H, out, out_bf16);
+    else combine_kernel<false><<<grid, 256, 0, s>>>(yp, tok_slot, tok_w, shared, topk, H, out, out_bf16);
 }
 
 }  // namespace qwq4

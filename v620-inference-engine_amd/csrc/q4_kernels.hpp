@@ -81,9 +81,10 @@ struct MoeGroupedArgs {
     const uint16_t *x;
     int T, topk;
     uint16_t *h;
-    float *yp;
+    void *yp;       // fp32, or fp16 with yp_f16
     void *ws;
     int x_f16 = 0;  // x rows are fp16 (no pre-pass)
+    int yp_f16 = 0;
 };
 // Tokens per tile the grouped kernels expect in the routing tile list.
 int moe_grouped_tile_m();
@@ -114,8 +115,8 @@ void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s)
 size_t route_lds_bytes(int T, int E);
 void launch_route(const RouteArgs &a, hipStream_t s);
 
-void launch_combine(const float *yp, const int32_t *tok_slot, const float *tok_w, const float *shared, int T, int topk,
-                    int H, void *out, int out_bf16, hipStream_t s);
+void launch_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared,
+                    int T, int topk, int H, void *out, int out_bf16, hipStream_t s);
 
 // checkpoint order <-> tiled device format (q4_common.cuh)
 void launch_tile(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, uint32_t *Wt,

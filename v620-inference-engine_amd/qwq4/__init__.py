@@ -38,9 +38,9 @@ _SIGS = {
     "qw_moe_route": ([_P, _I, _I, _I, _I] + [_P] * 11 + [_P], _I),
     "qw_moe_experts_gemv": ([_P] * 9 + [_I, _I, _I] + [_P] * 5 + [_I, _I, _I, _P, _P, _P], _I),
     "qw_moe_grouped_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
-    "qw_moe_experts_grouped": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _I, _P, _P, _P, _SZ, _P], _I),
+    "qw_moe_experts_grouped": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _I, _P, _P, _I, _P, _SZ, _P], _I),
     "qw_moe_grouped_tile_m": ([], _I),
-    "qw_moe_combine": ([_P, _P, _P, _P, _I, _I, _I, _P, _I, _P], _I),
+    "qw_moe_combine": ([_P, _I, _P, _P, _P, _I, _I, _I, _P, _I, _P], _I),
     "qw_q4_tiled_size": ([_I64, _I64, _P, _P, _P], None),
     "qw_q4_tile": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P], _I),
     "qw_q4_untile": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P], _I),
@@ -274,14 +274,15 @@ def moe_grouped_workspace_size(T, topk, E, H, F):
     return lib().qw_moe_grouped_workspace_size(T, topk, E, H, F)
 
 
-def moe_experts_grouped(gate, up, down, route, x, E, F, h=None, yp=None, workspace=None, x_f16=None):
+def moe_experts_grouped(gate, up, down, route, x, E, F, h=None, yp=None, workspace=None, x_f16=None, yp_f16=False):
+    """Grouped expert GEMMs; yp fp32, or fp16 (yp_f16, or an fp16 yp tensor)."""
     import torch
     T, H = x.shape
     topk = route.topk
     if h is None:
         h = torch.empty((T * topk, F), dtype=torch.float16, device=x.device)
     if yp is None:
-        yp = torch.empty((T * topk, H), dtype=torch.float32, device=x.device)
+        yp = torch.empty((T * topk, H), dtype=torch.float16 if yp_f16 else torch.float32, device=x.device)
     f16 = _is_f16(x, x_f16)
     if workspace is None and not f16:
         workspace = torch.empty(max(moe_grouped_workspace_size(T, topk, E, H, F), 1), dtype=torch.uint8,
@@ -290,7 +291,8 @@ def moe_experts_grouped(gate, up, down, route, x, E, F, h=None, yp=None, workspa
     rc = lib().qw_moe_experts_grouped(*[_ptr(t) for t in (*gate, *up, *down)], E, H, F, _ptr(route.offsets),
                                       _ptr(route.pair_tok), _ptr(route.tile_e), _ptr(route.tile_m0),
                                       _ptr(route.n_tiles), _ptr(x), int(f16), T, topk, _ptr(h), _ptr(yp),
-                                      _ptr(workspace), 0 if workspace is None else workspace.numel(), _stream())
+                                      int(yp.dtype == torch.float16), _ptr(workspace),
+                                      0 if workspace is None else workspace.numel(), _stream())
     _check(rc, "qw_moe_experts_grouped")
     return h, yp
 
@@ -301,8 +303,8 @@ def moe_combine(yp, route, H, shared=None, out=None, out_bf16=True):
     if out is None:
         out = torch.empty((T, H), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=yp.device)
     _dev(yp, shared, out)
-    rc = lib().qw_moe_combine(_ptr(yp), _ptr(route.tok_slot), _ptr(route.top_w), _ptr(shared), T, topk, H, _ptr(out),
-                              int(out_bf16), _stream())
+    rc = lib().qw_moe_combine(_ptr(yp), int(yp.dtype == torch.float16), _ptr(route.tok_slot), _ptr(route.top_w),
+                              _ptr(shared), T, topk, H, _ptr(out), int(out_bf16), _stream())
     _check(rc, "qw_moe_combine")
     return out
 
