@@ -29,11 +29,16 @@ constexpr int TILE_BYTES = 256 * GB_K * 2;     // 32 KB: one operand of one stag
 constexpr size_t GEMM_LDS = 4 * size_t(TILE_BYTES);  // the stage buffers (static LDS)
 
 // byte offset of 16-byte chunk c (0..7) of row r in a [rows][64 fp16] tile.
-// gfx950 LDS serves 256 B (64 banks) per cycle: the 16 rows one pass of a
-// b128 access touches occupy two 128-byte halves (row parity), and within a
-// half the chunk is XORed with r/2, so those 16 accesses hit 16 distinct
-// 16-byte bank groups.
-__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+// The chunk is XORed with (r & 7) ^ bit 3 of r. Two access shapes use it:
+// the weight dequant writes one row per lane (64 consecutive rows, one
+// chunk), and the fragment reads take 32 consecutive rows at chunk c (lanes
+// 0-31) and c+1 (lanes 32-63). Measured with SQ_LDS_BANK_CONFLICT on gfx950
+// both are conflict-free under this XOR; the XOR with r/2 used before left
+// the reads clean but served the b128 writes at half rate (conflict cycles
+// = 1/2 of the active LDS cycles), and XOR with r & 7 alone does the same
+// to the reads.
+__device__ __forceinline__ int swz_x(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_x(r)) << 4); }
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
@@ -126,7 +131,7 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
 #pragma unroll
         for (int j = 0; j < GB_M / 8 / G_ROLE; ++j) {
             const int rb = (j * G_ROLE + wa) * 8;
-            const int r = rb + lane / 8, c = (lane % 8) ^ ((r >> 1) & 7);
+            const int r = rb + lane / 8, c = (lane % 8) ^ swz_x(r);
             __builtin_amdgcn_global_load_lds(ap[j] + k0 + c * 8, dst + rb * 128, 16, 0, 0);
         }
     };
