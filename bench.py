@@ -118,6 +118,28 @@ def time_dominant(torch, qwq4, wqs, x, y, M, steps, warmup):
     return td.ms * 1e3 / (steps * len(wqs))
 
 
+def launch_ceiling(torch, qwq4, wqs, steps, warmup):
+    """What one launch can reach at all: the graph-launched per-kernel floor
+    (an empty one-block kernel) and a kernel that only reads the dominant
+    launch's weight bytes with the GEMV's load shape (qw_read_probe), both back
+    to back over the same 24-layer pool as the dominant launches."""
+    def timed(fn):
+        g = graphed(torch, fn)
+        for _ in range(warmup):
+            g()
+        with Timer(torch) as t:
+            for _ in range(steps):
+                g()
+        return t.ms * 1e3 / (steps * len(wqs))
+
+    empty_us = timed(lambda: [qwq4.read_probe() for _ in wqs])
+    read_us = timed(lambda: [qwq4.read_probe(wq[0]) for wq in wqs])
+    wb = wqs[0][0].numel() * wqs[0][0].element_size()
+    return {"empty_launch_us": round(empty_us, 3), "read_only_us": round(read_us, 3), "read_bytes": wb,
+            "read_only_GB_s": round(wb / (read_us * 1e-6) / 1e9, 1),
+            "read_only_frac": round(wb / (read_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_dominant(torch, qwq4, dev, steps, warmup):
     """Only the dominant launches (the command whose kernel trace is compared
     with the bench line's roofline figures)."""
@@ -165,6 +187,7 @@ def bench_gemv(torch, qwq4, dev, steps, warmup):
 
         dom_us.append(time_dominant(torch, qwq4, [wq for (wq, _) in layers], x, y, M, steps, warmup))
         dom_bytes.append(q4_bytes(QKV, H) + M * H * 2 + M * QKV * 2)
+    ceiling = launch_ceiling(torch, qwq4, [wq for (wq, _) in layers], steps, warmup)
     return {
         "GB_s": tot_bytes / (tot_ms * 1e-3) / 1e9,
         "ms_per_step": tot_ms / (steps * len(BATCHES)),
@@ -175,7 +198,7 @@ def bench_gemv(torch, qwq4, dev, steps, warmup):
         "dominant": {"shape": f"{H}->{QKV}", "batches": list(DOM_BATCHES),
                      "avg_launch_us": sum(dom_us[BATCHES.index(m)] for m in DOM_BATCHES) / len(DOM_BATCHES),
                      "avg_bytes_per_launch": sum(dom_bytes[BATCHES.index(m)] for m in DOM_BATCHES) / len(DOM_BATCHES),
-                     "per_batch_us": dict(zip(BATCHES, dom_us))},
+                     "per_batch_us": dict(zip(BATCHES, dom_us)), "launch_ceiling": ceiling},
     }
 
 
@@ -574,7 +597,8 @@ def main():
                             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                             "kernel": DOM_KERNEL + ", ...> (4096->12288, every batch of the sweep)",
                             "avg_launch_us": round(d["avg_launch_us"], 3),
-                            "algorithmic_bytes_per_launch": int(d["avg_bytes_per_launch"])}
+                            "algorithmic_bytes_per_launch": int(d["avg_bytes_per_launch"]),
+                            "launch_ceiling": d["launch_ceiling"]}
     line["workloads"] = res
     if not a.no_cpu and "gemv" in wl:
         line["cpu_baseline"] = cpu_baseline()

@@ -242,6 +242,12 @@ int qw_moe_decode_static(const float *router_w, const uint16_t *x, int x_f16, in
  * bf16 -> fp16 bits, magnitudes above 65504 saturated, round to nearest even. */
 int qw_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, void *stream);
 
+/* Measurement aid, no counterpart in the reference: reads `bytes` (a multiple
+ * of 32768) at p with the dense GEMV's load shape and computes nothing; with
+ * bytes == 0 it launches one empty block. Benchmarks time it beside the GEMV
+ * to show the per-launch floor and the read-only ceiling of one launch. */
+int qw_read_probe(const void *p, int64_t bytes, void *stream);
+
 /* ---- Checkpoint loading (role of the reference's loader, src/core/safetensors.cpp
  * and src/engine/weights.hip:352-402).
  * A safetensors file, mapped read-only and indexed by tensor name. */

@@ -135,3 +135,16 @@ def test_gemv_random_shapes(gpu, oracle, N, K, M, zeros, y_bf16):
         assert bf16_err_ok(y, r)
     else:
         assert rel_err(y, r) <= TOL
+
+
+@pytest.mark.gpu
+def test_read_probe_runs():
+    """The measurement aid the bench times beside the GEMV: launches and
+    rejects sizes that are not whole 32 KB blocks."""
+    import torch
+    t = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    qwq4.read_probe(t)
+    qwq4.read_probe()
+    torch.cuda.synchronize()
+    with pytest.raises(RuntimeError):
+        qwq4.read_probe(t[:1000])

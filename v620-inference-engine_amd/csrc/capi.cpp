@@ -281,6 +281,13 @@ int qw_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, void *stream) {
     return launched("qw_bf16_to_f16");
 }
 
+int qw_read_probe(const void *p, int64_t bytes, void *stream) {
+    REQUIRE(bytes >= 0 && bytes % 32768 == 0 && (bytes == 0 || (p && aligned(p, 16))),
+            "qw_read_probe: bytes must be a multiple of 32768 and p 16-byte aligned");
+    qwq4::launch_read_probe(p, bytes, st(stream));
+    return launched("qw_read_probe");
+}
+
 int qw_st_open(const char *path, qw_st_file **out) {
     REQUIRE(path && out, "qw_st_open: null argument");
     *out = nullptr;

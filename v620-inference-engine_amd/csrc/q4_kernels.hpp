@@ -128,6 +128,7 @@ void launch_unpack(const uint32_t *W, int64_t N, int64_t K, uint8_t *out, hipStr
 void launch_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, float *out,
                     hipStream_t s);
 void launch_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, hipStream_t s);
+void launch_read_probe(const void *p, int64_t bytes, hipStream_t s);
 void launch_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, hipStream_t s);
 
 // Dense GEMV on 16-bit weights (row-major [N][ldw]; fp16 weights with fp16

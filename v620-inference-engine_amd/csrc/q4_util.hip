@@ -202,6 +202,29 @@ __global__ __launch_bounds__(256) void bf16_to_f16_kernel(const uint16_t *__rest
 
 static unsigned blocks(int64_t n, int b) { return unsigned((n + b - 1) / b); }
 
+// Measurement aid: a read of `bytes` and nothing else, shaped like the dense
+// GEMV's weight stream (512-thread blocks, each wave four 1 KB pieces of
+// non-temporal 16-byte loads, 32 KB per block). bytes == 0 launches one
+// empty block (the per-launch floor).
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(512) void read_probe_kernel(const u32x4 *__restrict__ p, int64_t n16) {
+    if (n16 == 0) return;
+    const int64_t wave = (int64_t(blockIdx.x) * 512 + threadIdx.x) / WAVE;
+    const u32x4 *q = p + wave * 4 * WAVE + threadIdx.x % WAVE;
+    u32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __builtin_nontemporal_load(q + i * WAVE);
+    unsigned a = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    asm volatile("" ::"v"(a));  // the value is consumed: the loads stay
+}
+
+void launch_read_probe(const void *p, int64_t bytes, hipStream_t s) {
+    const int64_t n16 = bytes / 16;
+    read_probe_kernel<<<bytes ? unsigned(bytes / 32768) : 1u, 512, 0, s>>>(static_cast<const u32x4 *>(p), n16);
+}
+
 void launch_bf16_to_f16(const uint16_t *in, uint16_t *out, int64_t n, hipStream_t s) {
     bf16_to_f16_kernel<<<blocks(n, 256), 256, 0, s>>>(in, n, out);
 }

@@ -16,7 +16,7 @@ SYMBOLS = (
     "qw_q4_abi_version", "qw_q4_last_error", "qw_q4_gemv", "qw_q4_gemm_workspace_size", "qw_q4_gemm",
     "qw_moe_route", "qw_moe_experts_gemv", "qw_moe_experts_grouped", "qw_moe_grouped_workspace_size", "qw_moe_grouped_tile_m",
     "qw_moe_combine", "qw_q4_unpack", "qw_q4_dequant", "qw_q4_from_engine_order",
-    "qw_q4_tiled_size", "qw_q4_tile", "qw_q4_untile", "qw_bf16_to_f16",
+    "qw_q4_tiled_size", "qw_q4_tile", "qw_q4_untile", "qw_bf16_to_f16", "qw_read_probe",
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
     "qw_moe_decode_workspace_size", "qw_moe_decode", "qw_moe_decode_static_max_bytes", "qw_moe_decode_static",
@@ -48,6 +48,7 @@ _SIGS = {
     "qw_q4_dequant": ([_P, _P, _P, _I64, _I64, _P, _P], _I),
     "qw_q4_from_engine_order": ([_P, _P, _I64, _P], _I),
     "qw_bf16_to_f16": ([_P, _P, _I64, _P], _I),
+    "qw_read_probe": ([_P, _I64, _P], _I),
     "qw_moe_decode_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "qw_moe_decode": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
     "qw_moe_decode_static_max_bytes": ([], _SZ),
@@ -372,6 +373,16 @@ def bf16_to_f16(x, out=None):
     _dev(x, out)
     _check(lib().qw_bf16_to_f16(_ptr(x), _ptr(out), x.numel(), _stream()), "qw_bf16_to_f16")
     return out
+
+
+def read_probe(t=None):
+    """Measurement aid: read tensor t's bytes (a multiple of 32768) with the
+    dense GEMV's load shape and nothing else; t=None launches one empty block."""
+    if t is None:
+        _check(lib().qw_read_probe(None, 0, _stream()), "qw_read_probe")
+        return
+    _dev(t)
+    _check(lib().qw_read_probe(_ptr(t), t.numel() * t.element_size(), _stream()), "qw_read_probe")
 
 
 class StFile:
