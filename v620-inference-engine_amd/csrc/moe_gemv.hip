@@ -32,10 +32,21 @@ __device__ __forceinline__ uint16_t silu_mul_f16(float g, float u) {
     return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(g / (1.f + __expf(-g)) * u));
 }
 
+// A wave-uniform read of routing data through the scalar cache (the
+// constant address space): counted apart from the vector loads, so waiting
+// for it does not wait for the weight requests issued before it (vector
+// loads complete in order: a vector load of a token index issued after the
+// weights would hold the activation rows back until every weight word had
+// arrived).
+__device__ __forceinline__ int ld_uniform(const int32_t *p, int i) {
+    typedef const __attribute__((address_space(4))) int32_t cint;
+    return ((cint *)(p))[__builtin_amdgcn_readfirstlane(i)];
+}
+
 // Reads the block's expert: n_active and active[y] are requested together
 // (one latency), and the weight loads need only e.
 __device__ __forceinline__ int block_expert(const int32_t *n_active, const int32_t *active, int E) {
-    const int na = *n_active, e = active[blockIdx.y];
+    const int na = ld_uniform(n_active, 0), e = ld_uniform(active, blockIdx.y);
     return int(blockIdx.y) < na ? min(max(e, 0), E - 1) : -1;
 }
 
@@ -60,7 +71,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     // active expert has at least one token)
     WaveRange<GW, HAS_Z, CH4> wr;
     wr.fetch(t, kp * gpk, gpk, opaque_lane());
-    const int base = offsets[e], M = offsets[e + 1] - base;
+    const int base = ld_uniform(offsets, e), M = ld_uniform(offsets, e + 1) - base;
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
     f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(R, H));
     int m0 = 0;
@@ -71,7 +82,15 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
             wr.fetch(t, kp * gpk, gpk, opaque_lane());
             lds_barrier();  // the previous chunk's rows and partials are consumed
         }  // the previous chunk's rows and partials are consumed
-        stage_rows_issue([&](int m) { return x + int64_t(pair_tok[base + m0 + m]) * H; }, mc, H, xl);
+        // (stage_rows_issue asks for one row at a time, wave-uniform, when a
+        // row is whole waves of 16-byte pieces; else per lane)
+        const bool rows_uniform = (H / 8) % WAVE == 0;
+        stage_rows_issue(
+            [&](int m) {
+                const int i = base + m0 + m;
+                return x + int64_t(rows_uniform ? ld_uniform(pair_tok, i) : pair_tok[i]) * H;
+            },
+            mc, H, xl);
         __syncthreads();
         const uint4 *xr[1] = {xl + min(n, mc - 1) * kc + q * 4};
         f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -117,7 +136,7 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
     const Q4Tile t(dw, ds, dz, int64_t(e) * hsub + min(lsub, hsub - 1), G);
     WaveRange<GW, HAS_Z, CH4> wr;
     wr.fetch(t, kp * gpk, gpk, opaque_lane());
-    const int base = offsets[e], M = offsets[e + 1] - base;
+    const int base = ld_uniform(offsets, e), M = ld_uniform(offsets, e + 1) - base;
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
     f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(R, F));
     int m0 = 0;

@@ -100,7 +100,19 @@ struct WaveRange {
     // vector-memory instructions fetch() issues
     static constexpr int LOADS = CH4 ? GW / 4 * (HAS_Z ? 2 : 1) + GW : GW * (HAS_Z ? 3 : 2);
     uint4 w[GW];
-    uint32_t sv[GW], zv[GW];
+    // scales and zero words as loaded: with whole chunks two fp16 scales per
+    // word and one zero word per chunk (unpacked where used: holding them
+    // one per group costs 1.5 registers a group)
+    static constexpr int NSV = CH4 ? GW / 2 : GW, NZV = CH4 ? GW / 4 : GW;
+    uint32_t sv[NSV], zv[NZV];
+    __device__ __forceinline__ uint32_t scale_bits(int c) const {
+        if constexpr (CH4) return (sv[c >> 1] >> ((c & 1) * 16)) & 0xffffu;
+        else return sv[c];
+    }
+    __device__ __forceinline__ uint32_t zero_word(int c) const {
+        if constexpr (CH4) return zv[c >> 2];
+        else return zv[c];
+    }
     int g0, n;
     __device__ __forceinline__ void fetch(const Q4Tile &t, int g0_, int n_, int lane) {
         g0 = g0_;
@@ -114,15 +126,9 @@ struct WaveRange {
             for (int j = 0; j < GW / 4; ++j) {
                 const int gc = (g0 >> 2) + min(j, n / 4 - 1);
                 const uint2 s4 = *reinterpret_cast<const uint2 *>(t.s + gc * 64 + r * 4);
-                sv[4 * j] = s4.x;
-                sv[4 * j + 1] = s4.x >> 16;
-                sv[4 * j + 2] = s4.y;
-                sv[4 * j + 3] = s4.y >> 16;
-                if constexpr (HAS_Z) {
-                    const uint32_t z4 = t.z[gc * 16 + r];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) zv[4 * j + i] = z4;
-                }
+                sv[2 * j] = s4.x;
+                sv[2 * j + 1] = s4.y;
+                if constexpr (HAS_Z) zv[j] = t.z[gc * 16 + r];
             }
         } else {
 #pragma unroll
@@ -141,8 +147,8 @@ struct WaveRange {
         for (int c = 0; c < GW; ++c) {
             if (c < n) {
                 const int g = g0 + c;
-                const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(zv[c], g) : 8u);
-                dense_group<T, MB>(w[c], zb, f16_bits_to_f32(uint16_t(sv[c])), xr, g, acc);
+                const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(zero_word(c), g) : 8u);
+                dense_group<T, MB>(w[c], zb, f16_bits_to_f32(uint16_t(scale_bits(c))), xr, g, acc);
             }
         }
     }
@@ -324,8 +330,8 @@ __device__ __forceinline__ void compute_zq(const WaveRange<GW, HAS_Z, CH4> (&wr)
                 for (int t = 0; t < 4; ++t) a[mb][t] = xr[mb][g * 16 + t];
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
-                const float nz = -(T::BASE + T::UNIT * float(HAS_Z ? Q4Tile::zero_of(wr[j].zv[c], g) : 8u));
-                const uint32_t sbits = wr[j].sv[c];
+                const float nz = -(T::BASE + T::UNIT * float(HAS_Z ? Q4Tile::zero_of(wr[j].zero_word(c), g) : 8u));
+                const uint32_t sbits = wr[j].scale_bits(c);
                 uint4 b[4];
                 b[0] = unpack8_q<T>(wr[j].w[c].x);
                 b[1] = unpack8_q<T>(wr[j].w[c].y);
@@ -351,8 +357,13 @@ __device__ __forceinline__ void compute_zq(const WaveRange<GW, HAS_Z, CH4> (&wr)
 }
 
 // compute_zq for one subtile and one row block with each group's sum of
-// activations formed just before its product (no per-group sums held across
-// the range: for kernels whose registers go to a longer weight range).
+// activations formed beside its product (no per-group sums held across the
+// range: for kernels whose registers go to a longer weight range). Per
+// 32-element slice the activation fragment feeds both MFMAs (the sum against
+// a splat of 1, the product against BASE + UNIT q) and the weight word is
+// unpacked just before its use, so one fragment and one unpacked word are
+// live at a time; the zero-point term -(BASE + UNIT z) * sum(x) is added to
+// the product at the end of the group.
 template <typename T, int GW, bool HAS_Z, bool CH4>
 __device__ __forceinline__ void compute_zq_inline(const WaveRange<GW, HAS_Z, CH4> &wr, const uint4 *xr, f32x4 &acc) {
     const uint4 one = make_uint4(T::ONE, T::ONE, T::ONE, T::ONE);
@@ -360,22 +371,16 @@ __device__ __forceinline__ void compute_zq_inline(const WaveRange<GW, HAS_Z, CH4
     for (int c = 0; c < GW; ++c) {
         if (c < wr.n) {
             const int g = wr.g0 + c;
-            uint4 a[4];
+            const uint32_t words[4] = {wr.w[c].x, wr.w[c].y, wr.w[c].z, wr.w[c].w};
+            f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f}, p = sum;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) a[t] = xr[g * 16 + t];
-            f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int t = 0; t < 4; ++t) sum = mfma16<T>(a[t], one, sum);
-            const float nz = -(T::BASE + T::UNIT * float(HAS_Z ? Q4Tile::zero_of(wr.zv[c], g) : 8u));
-            uint4 b[4];
-            b[0] = unpack8_q<T>(wr.w[c].x);
-            b[1] = unpack8_q<T>(wr.w[c].y);
-            b[2] = unpack8_q<T>(wr.w[c].z);
-            b[3] = unpack8_q<T>(wr.w[c].w);
-            f32x4 p = sum * nz;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) p = mfma16<T>(a[t], b[t], p);
-            acc += (f16_bits_to_f32(uint16_t(wr.sv[c])) * (1.f / T::UNIT)) * p;
+            for (int t = 0; t < 4; ++t) {
+                const uint4 a = xr[g * 16 + t];
+                sum = mfma16<T>(a, one, sum);
+                p = mfma16<T>(a, unpack8_q<T>(words[t]), p);
+            }
+            const float nz = -(T::BASE + T::UNIT * float(HAS_Z ? Q4Tile::zero_of(wr.zero_word(c), g) : 8u));
+            acc += (f16_bits_to_f32(uint16_t(wr.scale_bits(c))) * (1.f / T::UNIT)) * (p + sum * nz);
         }
     }
 }
@@ -406,8 +411,8 @@ __device__ __forceinline__ void compute_pc(const WaveRange<GW, HAS_Z, CH4> (&wr)
                 for (int t = 0; t < 4; ++t) a[mb][t] = xr[mb][g * 16 + t];
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
-                const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(wr[j].zv[c], g) : 8u);
-                const float sc = f16_bits_to_f32(uint16_t(wr[j].sv[c]));
+                const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(wr[j].zero_word(c), g) : 8u);
+                const float sc = f16_bits_to_f32(uint16_t(wr[j].scale_bits(c)));
                 uint4 b[4];
                 b[0] = unpack8<T>(wr[j].w[c].x, zb);
                 b[1] = unpack8<T>(wr[j].w[c].y, zb);
