@@ -431,8 +431,10 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
 // Block (g, ks) computes the fp32 logits of experts 16g .. 16g + 15 (one per
 // wave) over K slice ks for every token and writes them as partial sums. The
 // last block of group g to finish adds its slices into the logits; the last
-// group to finish routes. Counters (device scope) are cleared for the next
-// call by the blocks that count last.
+// group to finish routes. With at most two logits per thread of a block
+// (T * E <= 2048) the last block of the whole grid does both instead.
+// Counters (device scope) are cleared for the next call by the blocks that
+// count last.
 __device__ __forceinline__ float wave_sum_f32(float v) {
 #define QW_FSUM_STEP(ctrl) v += __builtin_bit_cast(float, QW_DPP(__builtin_bit_cast(uint32_t, v), ctrl, 0xf, 0xf, false));
     QW_FSUM_STEP(DPP_XOR1)
@@ -493,12 +495,9 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
     };
     if (r.x_f16) dots([](uint16_t b) { return f16_bits_to_f32(b); });
     else dots([](uint16_t b) { return bf16_bits_to_f32(b); });
-    // the last slice block of each group of 16 experts adds the group's
-    // slices in slice order (up to 8 loads in flight per logit)
-    if (!count_last_block(r.counter + 1 + blockIdx.x, int(gridDim.y))) return;
-    const int e0 = blockIdx.x * 16, ng = min(16, E - e0), ksplit = gridDim.y, TE = T * E;
-    for (int i = tid; i < T * ng; i += blockDim.x) {
-        const int t = i / ng, o = t * E + e0 + (i - t * ng);
+    const int ksplit = gridDim.y, TE = T * E;
+    // the sum of a logit's slices, in slice order (up to 8 loads in flight)
+    auto slice_sum = [&](int o) {
         float v = 0.f;
         for (int j0 = 0; j0 < ksplit; j0 += 8) {
             float pv[8];
@@ -507,14 +506,36 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
 #pragma unroll
             for (int j = 0; j < 8; ++j) v += pv[j];
         }
-        st_agent(r.logits + o, v);
+        return v;
+    };
+    auto route = [&]() {
+        route_small_body<PER>(a, [&](int t) {
+            const float *l = r.logits + int64_t(t) * E;
+            return [l](int i) { return ld_agent(l + i); };
+        });
+    };
+    if (T * E <= 2 * int(blockDim.x)) {
+        // few logits (decode batches): the last block of the whole grid sums
+        // every logit's slices (the same additions in the same order as the
+        // per-group sums below) and routes, one hand-off instead of two
+        if (!count_last_block(r.counter, int(gridDim.x * gridDim.y))) return;
+        for (int o = tid; o < TE; o += blockDim.x) st_agent(r.logits + o, slice_sum(o));
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        route();
+        return;
+    }
+    // the last slice block of each group of 16 experts adds the group's
+    // slices in slice order
+    if (!count_last_block(r.counter + 1 + blockIdx.x, int(gridDim.y))) return;
+    const int e0 = blockIdx.x * 16, ng = min(16, E - e0);
+    for (int i = tid; i < T * ng; i += blockDim.x) {
+        const int t = i / ng, o = t * E + e0 + (i - t * ng);
+        st_agent(r.logits + o, slice_sum(o));
     }
     // and the last group to finish routes
     if (!count_last_block(r.counter, int(gridDim.x))) return;
-    route_small_body<PER>(a, [&](int t) {
-        const float *l = r.logits + int64_t(t) * E;
-        return [l](int i) { return ld_agent(l + i); };
-    });
+    route();
 }
 
 size_t router_lds_bytes(int T, int kl) { return size_t(T) * kl * 2; }
