@@ -34,7 +34,7 @@ BATCHES = (1, 2, 4, 6, 8)
 DOM_BATCHES = BATCHES
 # name prefix of the dominant launches' instantiations (every batch: 8-wave
 # blocks, one 16-row tile of tokens, zero points, whole 4-group chunks)
-DOM_KERNEL = "q4_gemv_block_kernel<8, 1, true, true"
+DOM_KERNEL = "q4_gemv_block_kernel<qwq4::BF16, 8, 1, true, true"
 H, QKV, FFN_DOWN_K, VOCAB = 4096, 12288, 6144, 151936
 
 
