@@ -143,7 +143,8 @@ int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
  *   tile_m > 0: tiles of tile_m slots. tile_m = -g (mixed): the tile starting
  *   rem slots before the end of the expert's range has 4g slots when rem > 3g,
  *   2g when rem > g, else g.
- * Limits: 1 <= k <= min(E, 64), E <= 1024, T <= 8192 for E <= 256 (LDS). */
+ * Limits: 1 <= k <= min(E, 64), E <= 1024, T * k < 2^30. Above 16 tokens the
+ * slots are assigned by one block per 64 tokens. */
 int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_t *top_e, float *top_w,
                  int32_t *counts, int32_t *offsets, int32_t *tok_slot, int32_t *pair_tok, int32_t *active,
                  int32_t *n_active, int32_t *tile_e, int32_t *tile_m0, int32_t *n_tiles, void *stream);

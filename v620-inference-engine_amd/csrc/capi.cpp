@@ -155,8 +155,6 @@ int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_
     REQUIRE(tile_m > -4096 && tile_m < 4096, "qw_moe_route: |tile_m| >= 4096");
     REQUIRE(tile_m == 0 || (tile_e && tile_m0 && n_tiles), "qw_moe_route: tile_m != 0 needs the tile outputs");
     REQUIRE(int64_t(T) * topk < (1 << 30), "qw_moe_route: too many pairs");
-    const size_t lds = T <= 64 ? 0 : qwq4::route_lds_bytes(T, E);
-    REQUIRE(lds <= 160 * 1024, "qw_moe_route: T = %d, E = %d needs %zu bytes of LDS (> 160 KiB)", T, E, lds);
     qwq4::RouteArgs a{logits, T, E, topk, tile_m, top_e, top_w, counts, offsets, tok_slot, pair_tok, active,
                       n_active, tile_e, tile_m0, n_tiles};
     qwq4::launch_route(a, st(stream));

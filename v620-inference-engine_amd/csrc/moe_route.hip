@@ -209,150 +209,82 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict
     topk_wave<PER>([&](int i) { return l[i]; }, E, k, lane, top_e + int64_t(t) * k, top_w + int64_t(t) * k);
 }
 
-struct SlotLds {
-    int32_t *cnt, *off;
-    unsigned long long *mask;  // [16 waves][E]
-    uint16_t *cc;              // [chunks][E]
-    uint16_t *te;              // [T][k] copy of the selections, or null (see slot_lds_bytes)
-};
+// ---- slots of a larger batch: one block per 64-token chunk
+// Every block counts the selections of all tokens (totals) and of the tokens
+// before its chunk (prefix) from top_e with LDS atomics, scans the totals over
+// the experts (offsets), and gives each of its chunk's pairs the slot
+// offsets[e] + prefix[e] + (its token's rank among the chunk's tokens of e,
+// a popcount below its bit in the expert's 64-bit chunk mask). Block 0 also
+// writes counts, offsets, the active list and the tile list. No block reads
+// what another writes, so one launch needs no hand-off between blocks.
+constexpr int SLOT_CHUNK = 64;
 
-// P16: also a 16-bit copy of the T x k selections (the chunk passes then read
-// LDS instead of strided global words).
-__host__ __device__ inline size_t slot_lds_layout(int T, int E, SlotLds *p, unsigned char *base, int P16 = 0) {
-    const size_t n_chunks = size_t(T + WAVE - 1) / WAVE;
-    size_t o = 0;
-    const size_t cnt = o;
-    o += size_t(E) * 4;
-    const size_t off = o;
-    o += size_t(E + 1) * 4;
-    o = (o + 7) & ~size_t(7);
-    const size_t mask = o;
-    o += size_t(16) * E * 8;
-    const size_t cc = o;
-    o += n_chunks * E * 2;
-    o = (o + 15) & ~size_t(15);
-    const size_t te = o;
-    o += size_t(P16) * 2;
-    if (p) {
-        p->cnt = reinterpret_cast<int32_t *>(base + cnt);
-        p->off = reinterpret_cast<int32_t *>(base + off);
-        p->mask = reinterpret_cast<unsigned long long *>(base + mask);
-        p->cc = reinterpret_cast<uint16_t *>(base + cc);
-        p->te = P16 ? reinterpret_cast<uint16_t *>(base + te) : nullptr;
-    }
-    return o;
-}
-
-size_t route_lds_bytes(int T, int E) { return slot_lds_layout(T, E, nullptr, nullptr); }
-
-// The slots launch's LDS and whether it holds the selection copy (when that
-// fits the 160 KB of a CU and E fits 16 bits).
-static size_t slot_lds_bytes(int T, int E, int k, int &P16) {
-    P16 = E <= 65535 ? T * k : 0;
-    if (P16 && slot_lds_layout(T, E, nullptr, nullptr, P16) > 160 * 1024) P16 = 0;
-    return slot_lds_layout(T, E, nullptr, nullptr, P16);
-}
-
-// counts, offsets, active list, tile list and slots from the selections te
-// (LDS or global). Whole block (1024 threads) participates.
-__device__ void route_slots(const int32_t *te, const RouteArgs &a, SlotLds L) {
+// exclusive scan over the first E threads' values (1024-thread block); the
+// total is returned in every thread
+__device__ __forceinline__ int block_scan_excl(int v, int E, int *s_w, int &total) {
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
-    const int T = a.T, E = a.E, k = a.topk, P = T * k;
-    for (int e = tid; e < E; e += blockDim.x) L.cnt[e] = 0;
-    for (int i = tid; i < 16 * E; i += blockDim.x) L.mask[i] = 0ull;
+    const uint32_t inc = wave_scan_incl(uint32_t(tid < E ? v : 0));
+    if (lane == WAVE - 1) s_w[wave] = int(inc);
+    __syncthreads();
+    int before = 0, all = 0;
+    for (int w = 0; w < int(blockDim.x) / WAVE; ++w) {
+        before += w < wave ? s_w[w] : 0;
+        all += s_w[w];
+    }
+    __syncthreads();
+    total = all;
+    return before + int(inc) - (tid < E ? v : 0);
+}
+
+__global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a) {
+    __shared__ int s_all[1024], s_pre[1024], s_base[1024], s_w[16];
+    __shared__ unsigned long long s_mask[1024];
+    const int tid = threadIdx.x, T = a.T, E = a.E, k = a.topk, P = T * k;
+    const int t0 = int(blockIdx.x) * SLOT_CHUNK, nt = min(SLOT_CHUNK, T - t0), pk = t0 * k;
+    if (tid < E) {
+        s_all[tid] = 0;
+        s_pre[tid] = 0;
+        s_mask[tid] = 0ull;
+    }
     __syncthreads();
     for (int i = tid; i < P; i += blockDim.x) {
-        const int e = te[i];
-        if (L.te) L.te[i] = uint16_t(e);
-        atomicAdd(&L.cnt[e], 1);
+        const int e = a.top_e[i];
+        atomicAdd(&s_all[e], 1);
+        if (i < pk) atomicAdd(&s_pre[e], 1);
     }
     __syncthreads();
-    auto sel = [&](int i) { return L.te ? int(L.te[i]) : te[i]; };
-    if (wave == 0) {  // three exclusive scans over the experts: pairs, non-empty experts, tiles
-        const int per = (E + WAVE - 1) / WAVE, e0 = lane * per;
-        int c_pairs = 0, c_act = 0, c_tiles = 0;
-        for (int i = 0; i < per; ++i) {
-            const int e = e0 + i;
-            if (e < E) {
-                const int c = L.cnt[e];
-                c_pairs += c;
-                c_act += c > 0;
-                c_tiles += a.tile_m != 0 ? tile_count(c, a.tile_m) : 0;
+    const int c = tid < E ? s_all[tid] : 0;
+    int total;
+    const int off = block_scan_excl(c, E, s_w, total);
+    if (tid < E) s_base[tid] = off + s_pre[tid];
+    if (blockIdx.x == 0) {
+        int n_act, n_tiles = 0;
+        const int act = block_scan_excl(c > 0, E, s_w, n_act);
+        const int ntl = a.tile_m != 0 && tid < E ? tile_count(c, a.tile_m) : 0;
+        const int tile0 = a.tile_m != 0 ? block_scan_excl(ntl, E, s_w, n_tiles) : 0;
+        if (tid < E) {
+            a.offsets[tid] = off;
+            a.counts[tid] = c;
+            if (c > 0) a.active[act] = tid;
+            for (int j = 0, m0 = 0; j < ntl; ++j, m0 += tile_rows(c - m0, a.tile_m)) {
+                a.tile_e[tile0 + j] = tid;
+                a.tile_m0[tile0 + j] = m0;
             }
         }
-        int ip = c_pairs, ia = c_act, it = c_tiles;
-#pragma unroll
-        for (int o = 1; o < WAVE; o <<= 1) {
-            const int np = __shfl_up(ip, o, WAVE), na = __shfl_up(ia, o, WAVE), nt = __shfl_up(it, o, WAVE);
-            if (lane >= o) {
-                ip += np;
-                ia += na;
-                it += nt;
-            }
-        }
-        int rp = ip - c_pairs, ra = ia - c_act, rt = it - c_tiles;
-        for (int i = 0; i < per; ++i) {
-            const int e = e0 + i;
-            if (e >= E) break;
-            const int c = L.cnt[e];
-            L.off[e] = rp;
-            a.offsets[e] = rp;
-            a.counts[e] = c;
-            if (c > 0) a.active[ra++] = e;
-            if (a.tile_m != 0)
-                for (int m0 = 0; m0 < c; m0 += tile_rows(c - m0, a.tile_m)) {
-                    a.tile_e[rt] = e;
-                    a.tile_m0[rt] = m0;
-                    ++rt;
-                }
-            rp += c;
-        }
-        if (lane == WAVE - 1) {
-            L.off[E] = rp;
-            a.offsets[E] = rp;
-            *a.n_active = ra;
-            if (a.tile_m != 0) *a.n_tiles = rt;
+        if (tid == 0) {
+            a.offsets[E] = total;
+            *a.n_active = n_act;
+            if (a.tile_m != 0) *a.n_tiles = n_tiles;
         }
     }
+    // the chunk's pairs: token bits per expert, then ranks
+    for (int i = tid; i < nt * k; i += blockDim.x) atomicOr(&s_mask[a.top_e[pk + i]], 1ull << (i / k));
     __syncthreads();
-    // per-chunk (64 tokens) counts of every expert, then their exclusive
-    // prefix over chunks, then each pair's rank inside its chunk from a bitmask
-    const int n_chunks = (T + WAVE - 1) / WAVE, rounds = (n_chunks + 15) / 16;
-    unsigned long long *M = L.mask + size_t(wave) * E;
-    for (int pass = 0; pass < 2; ++pass) {
-        for (int r = 0; r < rounds; ++r) {
-            const int c = r * 16 + wave, t = c * WAVE + lane;
-            if (c < n_chunks && t < T)
-                for (int j = 0; j < k; ++j) atomicOr(&M[sel(t * k + j)], 1ull << lane);
-            __syncthreads();
-            if (c < n_chunks) {
-                if (pass == 0) {
-                    for (int e = lane; e < E; e += WAVE) L.cc[size_t(c) * E + e] = uint16_t(__popcll(M[e]));
-                } else if (t < T) {
-                    const unsigned long long below = (1ull << lane) - 1ull;
-                    for (int j = 0; j < k; ++j) {
-                        const int e = sel(t * k + j);
-                        const int slot = L.off[e] + L.cc[size_t(c) * E + e] + __popcll(M[e] & below);
-                        a.tok_slot[t * k + j] = slot;
-                        a.pair_tok[slot] = t;
-                    }
-                }
-            }
-            __syncthreads();
-            for (int e = lane; e < E; e += WAVE) M[e] = 0ull;
-            __syncthreads();
-        }
-        if (pass == 0) {
-            for (int e = tid; e < E; e += blockDim.x) {
-                int run = 0;
-                for (int c = 0; c < n_chunks; ++c) {
-                    const int v = L.cc[size_t(c) * E + e];
-                    L.cc[size_t(c) * E + e] = uint16_t(run);
-                    run += v;
-                }
-            }
-            __syncthreads();
-        }
+    for (int i = tid; i < nt * k; i += blockDim.x) {
+        const int e = a.top_e[pk + i], tl = i / k;
+        const int slot = s_base[e] + __popcll(s_mask[e] & ((1ull << tl) - 1ull));
+        a.tok_slot[pk + i] = slot;
+        a.pair_tok[slot] = t0 + tl;
     }
 }
 
@@ -558,16 +490,7 @@ void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s)
     else go(router_route_kernel<16>);
 }
 
-__global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a, int P16) {
-    extern __shared__ unsigned char smem[];
-    SlotLds L;
-    slot_lds_layout(a.T, a.E, &L, smem, P16);
-    route_slots(a.top_e, a, L);
-}
-
 void launch_route(const RouteArgs &a, hipStream_t s) {
-    int P16 = 0;
-    const size_t lds = slot_lds_bytes(a.T, a.E, a.topk, P16);
     // one block while each of its 16 waves routes at most one token; beyond,
     // top-k in parallel blocks and the slots in a second launch (32 tokens:
     // 9.8 against 12.1 us)
@@ -579,15 +502,12 @@ void launch_route(const RouteArgs &a, hipStream_t s) {
         else if (per <= 8) route_small_kernel<8><<<1, 1024, 0, s>>>(a);
         else route_small_kernel<16><<<1, 1024, 0, s>>>(a);
     } else {
-        if (lds > 48 * 1024)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(route_slots_kernel),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         const int per = (a.E + WAVE - 1) / WAVE;
         const unsigned g = unsigned((a.T + 3) / 4);
         if (per <= 4) route_topk_kernel<4><<<g, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
         else if (per <= 8) route_topk_kernel<8><<<g, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
         else route_topk_kernel<16><<<g, 256, 0, s>>>(a.logits, a.T, a.E, a.topk, a.top_e, a.top_w);
-        route_slots_kernel<<<1, 1024, lds, s>>>(a, P16);
+        route_slots_kernel<<<unsigned((a.T + SLOT_CHUNK - 1) / SLOT_CHUNK), 1024, 0, s>>>(a);
     }
 }
 

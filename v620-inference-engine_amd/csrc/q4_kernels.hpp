@@ -112,7 +112,6 @@ struct RouterArgs {
 size_t router_lds_bytes(int T, int kl);
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
 // LDS bytes the slot pass needs for (T, E); the C-ABI rejects larger inputs.
-size_t route_lds_bytes(int T, int E);
 void launch_route(const RouteArgs &a, hipStream_t s);
 
 void launch_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared,
