@@ -19,7 +19,7 @@ def _experts_dev(dev, ex):
 
 
 @pytest.mark.parametrize("T,E,k", [(1, 256, 8), (7, 256, 8), (32, 256, 8), (64, 128, 4), (100, 512, 10),
-                                   (4096, 256, 8)])
+                                   (4096, 256, 8), (9001, 256, 8), (130, 1024, 64)])
 def test_route_bit_exact(gpu, oracle, T, E, k):
     print(f"route T={T} E={E} k={k}", flush=True)
     l = synth.router_logits(31, f"l{T}", T, E, bias_sigma=0.5 if T > 64 else 0.0)
