@@ -50,7 +50,7 @@ __device__ __forceinline__ int block_expert(const int32_t *n_active, const int32
     return int(blockIdx.y) < na ? min(max(e, 0), E - 1) : -1;
 }
 
-template <typename XT, int KS, int GW, bool HAS_Z, bool CH4>
+template <typename XT, int KS, int GW, bool HAS_Z, bool CH4, bool MULTI>
 __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
     const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
@@ -74,14 +74,9 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     const int base = ld_uniform(offsets, e), M = ld_uniform(offsets, e + 1) - base;
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
     f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(R, H));
-    int m0 = 0;
-    do {  // M >= 1: the first chunk always runs (its weights are already requested)
+    // one chunk of mc rows from slot base + m0 (weights in wr)
+    auto chunk = [&](int m0) {
         const int mc = min(R, M - m0);
-        if (m0 > 0) {
-            // later chunks refetch (from L2): nothing stays live across chunks
-            wr.fetch(t, kp * gpk, gpk, opaque_lane());
-            lds_barrier();  // the previous chunk's rows and partials are consumed
-        }  // the previous chunk's rows and partials are consumed
         // (stage_rows_issue asks for one row at a time, wave-uniform, when a
         // row is whole waves of 16-byte pieces; else per lane)
         const bool rows_uniform = (H / 8) % WAVE == 0;
@@ -110,14 +105,26 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
                 if (m < mc) h[int64_t(base + m0 + m) * F + lsub * 16 + n] = silu_mul_f16(g[r], u[r]);
             }
         }
-        m0 += R;
-    } while (m0 < M);
+    };
+    // the first chunk (its weights are already requested; M >= 1), then,
+    // when an expert can have more than R tokens (MULTI), further ones, each
+    // refetching its weights (from L2). Without that loop the kernel needs 72
+    // VGPRs instead of 88, so a batch-1 grid (768 blocks) is resident in one
+    // round.
+    chunk(0);
+    if constexpr (MULTI) {
+        for (int m0 = R; m0 < M; m0 += R) {
+            wr.fetch(t, kp * gpk, gpk, opaque_lane());
+            lds_barrier();  // the previous chunk's rows and partials are consumed
+            chunk(m0);
+        }
+    }
 }
 
 // CMB: the last block of each row block (over the active experts, counted
 // on a device-scope counter) also forms the combined output of those rows
 // for every token, in the fixed selection order, then clears the counter.
-template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB>
+template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB, bool MULTI>
 __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz,
                                                             const int32_t *__restrict__ offsets,
                                                             const int32_t *__restrict__ active,
@@ -139,13 +146,8 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
     const int base = ld_uniform(offsets, e), M = ld_uniform(offsets, e + 1) - base;
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
     f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(R, F));
-    int m0 = 0;
-    do {  // M >= 1: the first chunk always runs (its weights are already requested)
+    auto chunk = [&](int m0) {
         const int mc = min(R, M - m0);
-        if (m0 > 0) {
-            wr.fetch(t, kp * gpk, gpk, opaque_lane());
-            lds_barrier();
-        }
         stage_rows_issue([&](int m) { return h + int64_t(base + m0 + m) * F; }, mc, F, xl);
         __syncthreads();
         const uint4 *xr[1] = {xl + min(n, mc - 1) * kc + q * 4};
@@ -170,8 +172,17 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
                 }
             }
         }
-        m0 += R;
-    } while (m0 < M);
+    };
+    // the first chunk, then (MULTI) further ones refetching their weights, as
+    // in the gate/up kernel
+    chunk(0);
+    if constexpr (MULTI) {
+        for (int m0 = R; m0 < M; m0 += R) {
+            wr.fetch(t, kp * gpk, gpk, opaque_lane());
+            lds_barrier();
+            chunk(m0);
+        }
+    }
     if constexpr (CMB) {
         if (!count_last_block(&c.counters[blockIdx.x], *n_active)) return;
         // The combine of rows r0 .. r0 + nr - 1 for every token, in the
@@ -225,7 +236,11 @@ static int down_ks(int G) {
 
 template <int KS, int GW, bool HAS_Z, bool CH4>
 static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
-    auto kern = a.x_f16 ? moe_gate_up_gemv_kernel<F16, KS, GW, HAS_Z, CH4> : moe_gate_up_gemv_kernel<BF16, KS, GW, HAS_Z, CH4>;
+    // an expert has at most T tokens: one chunk of R rows holds them when R >= T
+    auto kern = a.T <= R ? (a.x_f16 ? moe_gate_up_gemv_kernel<F16, KS, GW, HAS_Z, CH4, false>
+                                    : moe_gate_up_gemv_kernel<BF16, KS, GW, HAS_Z, CH4, false>)
+                         : (a.x_f16 ? moe_gate_up_gemv_kernel<F16, KS, GW, HAS_Z, CH4, true>
+                                    : moe_gate_up_gemv_kernel<BF16, KS, GW, HAS_Z, CH4, true>);
     const size_t lds = moe_lds_bytes(R, a.H);
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
     constexpr int SUB = 8 / (2 * KS);
@@ -236,7 +251,7 @@ static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStrea
 
 template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB>
 static void launch_down_c(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
-    auto kern = moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB>;
+    auto kern = a.T <= R ? moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB, false> : moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB, true>;
     const size_t lds = moe_lds_bytes(R, a.F);
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
     constexpr int SUB = 8 / KS;
