@@ -3,6 +3,7 @@
 // reference engine's repacked word order. These are the bit-exact parity
 // surface of the q4 format (reference: src/ref/ref_model.cpp:108-114,
 // src/engine/weight_convert.cpp:61-71).
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -72,14 +73,20 @@ LaunchShape persistent_shape(const void *kernel, int threads, size_t lds) {
     };
     static std::mutex mu;
     static std::vector<Entry> cache;
+    static std::vector<std::pair<const void *, int>> raised;  // (kernel, device) with the LDS limit at its maximum
     int dev = 0;
     (void)hipGetDevice(&dev);
     std::lock_guard<std::mutex> lk(mu);
+    // the dynamic-LDS limit is a per-kernel attribute: set once to the CU's
+    // 160 KiB, so a launch with less never lowers it under one with more
+    if (lds > 64 * 1024 && std::find(raised.begin(), raised.end(), std::make_pair(kernel, dev)) == raised.end()) {
+        (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        raised.emplace_back(kernel, dev);
+    }
     for (const Entry &e : cache)
         if (e.k == kernel && e.dev == dev && e.threads == threads && e.lds == lds) return e.shape;
     int cus = 0, per_cu = 0;
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (lds > 64 * 1024) (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds);
     if (cus < 1) cus = 1;
     if (per_cu < 1) per_cu = 1;
