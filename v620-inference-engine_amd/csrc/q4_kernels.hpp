@@ -140,7 +140,7 @@ struct W16Args {
     void *y;
     int ys, y_bf16, N, K, M, accumulate, f16;
 };
-bool w16_fits(int M, int K);
+bool w16_fits(int M, int K, int N);
 void launch_w16_gemv(const W16Args &a, hipStream_t s);
 void launch_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, hipStream_t s);
 

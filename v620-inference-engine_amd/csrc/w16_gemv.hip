@@ -14,15 +14,20 @@
 // range of weight rows (16 B per lane per 32-element MFMA step, up to
 // W16_STEPS steps at once) before anything waits, the activations are staged
 // in LDS, and the KS partial sums are added through LDS in k-part order.
+#include <type_traits>
+
 #include "q4_gemv_core.cuh"
 #include "q4_kernels.hpp"
 
 namespace qwq4 {
 
-constexpr int W16_STEPS = 16;  // 32-element MFMA steps in flight per wave (64 VGPRs)
 constexpr int W16_MAX_KS = 8;  // waves per block
 
-template <typename XT, int MB, int MR, int XPT>
+// WS: 32-element MFMA steps a wave keeps in flight (8 or 16: 32 or 64 VGPRs),
+// the smallest that holds its range where one does (the shared expert's down
+// projection, 6 steps per wave: 16 held 81-97 VGPRs, 4-5 waves per SIMD;
+// 8 make it 10% faster per layer)
+template <typename XT, int MB, int MR, int XPT, int WS>
 __global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16_t *W, int ldw, const uint16_t *x,
                                                                     int xs, int M, int K, int N, void *__restrict__ y,
                                                                     int ys, int y_bf16, int accumulate) {
@@ -45,10 +50,10 @@ __global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-    uint4 w[W16_STEPS];
-    auto fetch = [&](int p) {  // steps p .. p + W16_STEPS - 1 of the wave's range (clamped, no branches)
+    uint4 w[WS];
+    auto fetch = [&](int p) {  // steps p .. p + WS - 1 of the wave's range (clamped, no branches)
 #pragma unroll
-        for (int t = 0; t < W16_STEPS; ++t) {
+        for (int t = 0; t < WS; ++t) {
             const int s = min(s0 + min(p + t, max(ns - 1, 0)), steps - 1);
             const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow + s * 4));
             w[t] = make_uint4(v[0], v[1], v[2], v[3]);
@@ -61,16 +66,16 @@ __global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16
         lds_barrier();
     } else {
         __builtin_amdgcn_sched_barrier(0);
-        wait_vm_below<W16_STEPS>();  // this wave's activation loads (its oldest)
+        wait_vm_below<WS>();  // this wave's activation loads (its oldest)
         __builtin_amdgcn_s_barrier();
     }
     const uint4 *xr[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) xr[mb] = xl + min(mb * 16 + n, M - 1) * kc + q;
-    for (int p = 0; p < ns; p += W16_STEPS) {
+    for (int p = 0; p < ns; p += WS) {
         if (p > 0) fetch(p);
 #pragma unroll
-        for (int t = 0; t < W16_STEPS; ++t)
+        for (int t = 0; t < WS; ++t)
             if (p + t < ns) {
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16<XT>(xr[mb][(s0 + p + t) * 4], w[t], acc[mb]);
@@ -90,10 +95,16 @@ static void launch_w16_t(const W16Args &a, int KS, hipStream_t s) {
         if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), threads, lds);
         kern<<<blocks, threads, lds, s>>>(a.W, a.ldw, a.x, a.xs, a.M, a.K, a.N, a.y, a.ys, a.y_bf16, a.accumulate);
     };
-    if (xpt <= 1) go(w16_gemv_kernel<XT, MB, MR, 1>);
-    else if (xpt <= 2) go(w16_gemv_kernel<XT, MB, MR, 2>);
-    else if (xpt <= 4) go(w16_gemv_kernel<XT, MB, MR, 4>);
-    else go(w16_gemv_kernel<XT, MB, MR, 0>);
+    const int spw = (a.K / 32 + KS - 1) / KS;
+    auto pick = [&](auto ws) {
+        constexpr int W = decltype(ws)::value;
+        if (xpt <= 1) go(w16_gemv_kernel<XT, MB, MR, 1, W>);
+        else if (xpt <= 2) go(w16_gemv_kernel<XT, MB, MR, 2, W>);
+        else if (xpt <= 4) go(w16_gemv_kernel<XT, MB, MR, 4, W>);
+        else go(w16_gemv_kernel<XT, MB, MR, 0, W>);
+    };
+    if (spw <= 8) pick(std::integral_constant<int, 8>());
+    else pick(std::integral_constant<int, 16>());
 }
 
 template <typename XT>
@@ -105,28 +116,29 @@ static void launch_w16_x(const W16Args &a, int KS, hipStream_t s) {
 }
 
 // K split: as many waves (up to 8) as the 32-element steps allow; fewer
-// steps per wave mean more loads in flight per weight byte.
-static int w16_ks(int K) { return K / 32 < W16_MAX_KS ? K / 32 : W16_MAX_KS; }
+// steps per wave mean more loads in flight per weight byte. (16 waves of 8
+// steps for shapes with fewer row blocks than CUs measured slower.)
+static int w16_ks(int K, int) { return K / 32 < W16_MAX_KS ? K / 32 : W16_MAX_KS; }
 
-bool w16_fits(int M, int K) {
-    const int KS = w16_ks(K), MB = M > 16 ? 2 : 1;
+bool w16_fits(int M, int K, int N) {
+    const int KS = w16_ks(K, N), MB = M > 16 ? 2 : 1;
     return dense_lds_bytes(M, K, MB, KS, KS) <= 160 * 1024;
 }
 
 static void launch_w16_fit(const W16Args &a, hipStream_t s) {
-    const int KS = w16_ks(a.K);
+    const int KS = w16_ks(a.K, a.N);
     if (a.f16) launch_w16_x<F16>(a, KS, s);
     else launch_w16_x<BF16>(a, KS, s);
 }
 
 // Batches whose activations exceed LDS run as several launches of fewer rows.
 void launch_w16_gemv(const W16Args &a, hipStream_t s) {
-    if (w16_fits(a.M, a.K)) {
+    if (w16_fits(a.M, a.K, a.N)) {
         launch_w16_fit(a, s);
         return;
     }
     int mc = 16;
-    while (mc > 1 && !w16_fits(mc, a.K)) --mc;
+    while (mc > 1 && !w16_fits(mc, a.K, a.N)) --mc;
     const size_t ysz = a.y_bf16 ? 2 : 4;
     for (int m0 = 0; m0 < a.M; m0 += mc) {
         W16Args b = a;
