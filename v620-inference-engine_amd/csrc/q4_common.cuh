@@ -46,7 +46,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // (the expert down projection, whose input h is kept in fp16).
 struct BF16 {
     static constexpr uint32_t HI = 0x43434343u;    // high byte of 128 + v
-    static constexpr uint32_t NEG_BIAS = 0xC310C310u;  // two bf16 -144
     static constexpr uint32_t ONE = 0x3F803F80u;       // two bf16 1.0
     // unpack8_q operands: BASE + UNIT * q
     static constexpr float BASE = 128.f, UNIT = 1.f;
@@ -54,7 +53,6 @@ struct BF16 {
 };
 struct F16 {
     static constexpr uint32_t HI = 0x64646464u;    // high byte of 1024 + v
-    static constexpr uint32_t NEG_BIAS = 0xE410E410u;  // two fp16 -1040
     static constexpr uint32_t ONE = 0x3C003C00u;       // two fp16 1.0
     static constexpr float BASE = 1024.f, UNIT = 16.f;
     typedef f16x8 vec;

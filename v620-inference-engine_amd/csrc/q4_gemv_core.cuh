@@ -64,31 +64,6 @@ __device__ __forceinline__ int opaque_lane() {
     return l;
 }
 
-// One group of one subtile: acc[mb] += s * (x . (q - z)) for the lane's rows.
-// xr[mb] points at the lane's activation row (LDS) at K quarter q.
-template <typename T, int MB>
-__device__ __forceinline__ void dense_group(const uint4 &w, uint32_t zb, float s, const uint4 *const (&xr)[MB], int g,
-                                            f32x4 (&acc)[MB]) {
-    const uint4 negb = make_uint4(T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS);
-    uint4 b[4];
-    b[0] = unpack8<T>(w.x, zb);
-    b[1] = unpack8<T>(w.y, zb);
-    b[2] = unpack8<T>(w.z, zb);
-    b[3] = unpack8<T>(w.w, zb);
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-        uint4 a[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) a[t] = xr[mb][g * 16 + t];
-        f32x4 p = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) p = mfma16<T>(a[t], negb, p);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) p = mfma16<T>(a[t], b[t], p);
-        acc[mb] += s * p;
-    }
-}
-
 // A wave's whole K range of one subtile (groups g0 .. g0 + n - 1, n <= GW),
 // requested up front into registers. CH4: the range is whole 4-group chunks
 // (g0 and n multiples of 4), so each chunk's scales are one 8-byte load and
@@ -140,17 +115,6 @@ struct WaveRange {
         }
 #pragma unroll
         for (int c = 0; c < GW; ++c) w[c] = t.word4_stream(g0 + min(c, n - 1), lane);
-    }
-    template <typename T, int MB>
-    __device__ __forceinline__ void compute(const uint4 *const (&xr)[MB], f32x4 (&acc)[MB]) const {
-#pragma unroll
-        for (int c = 0; c < GW; ++c) {
-            if (c < n) {
-                const int g = g0 + c;
-                const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(zero_word(c), g) : 8u);
-                dense_group<T, MB>(w[c], zb, f16_bits_to_f32(uint16_t(scale_bits(c))), xr, g, acc);
-            }
-        }
     }
 };
 
@@ -204,57 +168,6 @@ __device__ __forceinline__ void stage_regs_commit(const XRegs &xv, int M, int K,
         // load down to it, behind the weight loads and their wait
         const int i = min(int(threadIdx.x) + j * nt, P - 1), m = div_small(i, rkn), c = i - m * kn;
         xl[m * kc + c] = xv.get(j);
-    }
-}
-
-// The -BIAS * sum(x) correction of each of a wave's groups g0 .. g0 + n - 1
-// (n <= GW) for its token rows: the starting accumulator of that group's
-// product (MFMAs on the staged activations only, so they run while the
-// weights are still in flight). Per group, an MFMA chain over its four
-// 32-element slices against a splat of -BIAS.
-// P4 (at most 4 token rows, MB == 1): four groups share one chain. Row
-// 4c + m of such a tile holds token m of group gb + c (xp_of(gb): the lane's
-// fragment of the tile starting at group gb), so each row goes through
-// exactly the arithmetic it gets in a tile of its own, and 4 MFMAs serve
-// what would take 16; the results, equal across a row's 16 columns, are
-// read out per (group, token).
-template <typename T, int MB, int GW, bool P4, class XpFn>
-__device__ __forceinline__ void group_bias(const uint4 *const (&xr)[MB], XpFn xp_of, int g0, int n,
-                                           f32x4 (&pc)[GW][MB]) {
-    const uint4 negb = make_uint4(T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS, T::NEG_BIAS);
-    if constexpr (P4) {
-        static_assert(MB == 1 && GW % 4 == 0, "packed correction: one row block, whole tiles of four groups");
-#pragma unroll
-        for (int tl = 0; tl < GW / 4; ++tl) {
-            if (4 * tl < n) {
-                const uint4 *xp = xp_of(g0 + 4 * tl);
-                f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int t = 0; t < 4; ++t) c = mfma16<T>(xp[t], negb, c);
-                // (each element copied out first: a bit cast of the subscript
-                // c[r] itself reads element 0)
-                const float cv[4] = {c[0], c[1], c[2], c[3]};
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        pc[4 * tl + g][0][r] =
-                            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv[r]), 16 * g));
-            }
-        }
-    } else {
-#pragma unroll
-        for (int c = 0; c < GW; ++c) {
-            if (c < n) {
-                const int g = g0 + c;
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    pc[c][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) pc[c][mb] = mfma16<T>(xr[mb][g * 16 + t], negb, pc[c][mb]);
-                }
-            }
-        }
     }
 }
 
@@ -391,43 +304,6 @@ __device__ __forceinline__ void compute_zq_inline(const WaveRange<GW, HAS_Z, CH4
 __device__ __forceinline__ const uint4 *packed_fragment(const uint4 *xl, int kc, int M, int G, int gb, int lane) {
     const int n = lane % 16, q = lane / 16;
     return xl + min(n & 3, M - 1) * kc + min(gb + (n >> 2), G - 1) * 16 + q * 4;
-}
-
-// NS subtiles over the same groups (wr[j] fetched with equal g0 and n): per
-// group, as its weights arrive, the 4 MFMAs of the product onto the group's
-// correction pc; the activation fragments are read once for all NS.
-template <typename T, int MB, int NS, int GW, bool HAS_Z, bool CH4>
-__device__ __forceinline__ void compute_pc(const WaveRange<GW, HAS_Z, CH4> (&wr)[NS], const uint4 *const (&xr)[MB],
-                                           const f32x4 (&pc)[GW][MB], f32x4 (&acc)[NS][MB]) {
-    const int g0 = wr[0].g0, n = wr[0].n;
-#pragma unroll
-    for (int c = 0; c < GW; ++c) {
-        if (c < n) {
-            const int g = g0 + c;
-            uint4 a[MB][4];
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) a[mb][t] = xr[mb][g * 16 + t];
-#pragma unroll
-            for (int j = 0; j < NS; ++j) {
-                const uint32_t zb = zero_bytes(HAS_Z ? Q4Tile::zero_of(wr[j].zero_word(c), g) : 8u);
-                const float sc = f16_bits_to_f32(uint16_t(wr[j].scale_bits(c)));
-                uint4 b[4];
-                b[0] = unpack8<T>(wr[j].w[c].x, zb);
-                b[1] = unpack8<T>(wr[j].w[c].y, zb);
-                b[2] = unpack8<T>(wr[j].w[c].z, zb);
-                b[3] = unpack8<T>(wr[j].w[c].w, zb);
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    f32x4 p = pc[c][mb];
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) p = mfma16<T>(a[mb][t], b[t], p);
-                    acc[j][mb] += sc * p;
-                }
-            }
-        }
-    }
 }
 
 __device__ __forceinline__ void store_y(void *y, int64_t o, float v, int y_bf16, int accumulate) {

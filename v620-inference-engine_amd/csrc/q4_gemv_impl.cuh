@@ -32,9 +32,6 @@ namespace qwq4 {
 // passes of GW.
 
 constexpr int DENSE_GW = 4;
-#ifndef XREG_STAGING
-#define XREG_STAGING 1
-#endif
 
 template <typename XT, int NW, int MB, bool HAS_Z, bool CH4, bool PF, bool KSNW, int XPT, bool P4, int MR>
 // Argument order: what the weight and activation requests need first (the
@@ -171,7 +168,7 @@ static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
         // below (151936 rows at batch 4: 60 against 65 us; at batches 1-3
         // the register path stays ahead: 51 against 58 at batch 1, 57.5
         // against 59 at batch 3)
-        bool regs = xpt <= 4 && XREG_STAGING;
+        bool regs = xpt <= 4;
         if (regs && a.M >= 4 && gpk <= DENSE_GW) {
             auto pf = q4_gemv_block_kernel<XT, NW, MB, HAS_Z, CH4, true, KSNW, 0, P4, MR>;
             const size_t lds = dense_lds_bytes(a.M, a.K, MB, waves, KS);
