@@ -48,6 +48,8 @@ def lib():
         L.o_moe.argtypes = [_f32p, _int, _int, _int, _int, _int, _f32p] + [_u32p, _u16p, _vp] * 3 + [_f32p, _vp, _vp, _int]
         L.o_linear_w16.argtypes = [_u16p, _int, _i64, _i64, _i64, _f32p, _int, _int, _f32p, _int, _int]
         L.o_swiglu_gate.argtypes = [_f32p, _int, _int, _int, _f32p]
+        L.o_quantize_rows_i8.argtypes = [_u16p, _i64, _i64, _i64, _vp, _f32p]
+        L.o_i8_linear_f64.argtypes = [_vp, _f32p, _i64, _i64, _int, _u16p, _int, _int, _int, _f64p, _int, _int]
         for n in ("o_bf16_to_f32", "o_f16_to_f32"):
             getattr(L, n).argtypes = [ctypes.c_uint16]
             getattr(L, n).restype = ctypes.c_float
@@ -225,6 +227,30 @@ def swiglu_gate(v, n):
     h = np.empty((T, n), np.float32)
     lib().o_swiglu_gate(v, ldv, n, T, h)
     return h
+
+
+def quantize_rows_i8(w16, group=32):
+    """fp16 weight bits [N][K] -> (int8 [N][K], fp32 scales [N][K/group]) as
+    quantize_rows_i8 (src/engine/weight_convert.cpp:92-108)."""
+    w16 = _c(w16, np.uint16)
+    N, K = w16.shape
+    q = np.empty((N, K), np.int8)
+    s = np.empty((N, K // group), np.float32)
+    lib().o_quantize_rows_i8(w16, N, K, group, q.ctypes.data, s)
+    return q, s
+
+
+def i8_linear_f64(W8, scale, x16, M, xs=None, rpg=0, group=32, threads=None):
+    """fp64 y [M][N] of gemv_rows_i8 (src/kernels/gemv.hip:75-136): int8 W8 [N][K] times
+    its group scales times fp16 rows x16 (stride xs; row n reads block n // rpg when rpg)."""
+    W8 = np.ascontiguousarray(W8, np.int8)
+    N, K = W8.shape
+    x16 = _c(x16, np.uint16).ravel()
+    xs = xs or K
+    y = np.empty((M, N), np.float64)
+    lib().o_i8_linear_f64(W8.ctypes.data, _c(scale, np.float32), N, K, group, x16, xs, M, rpg, y, N,
+                          threads or nthreads())
+    return y
 
 
 def shared_expert(x, w_gu, w_down, f16_gu=False, f16_down=False):

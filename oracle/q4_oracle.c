@@ -462,6 +462,65 @@ void o_linear_w16(const uint16_t *W, int f16, int64_t N, int64_t K, int64_t ldw,
     parallel_for(threads, N, 16, lin16_range, &c);
 }
 
+/* weight_convert.cpp:92-108 (quantize_rows_i8): per row and group of `group`
+ * weights along K, s = amax / 127 over the group's fp16 weights widened to
+ * fp32 (1 when amax is 0), q = lrint(clamp(w / s, -127, 127)) (round to
+ * nearest even, the default rounding mode). */
+void o_quantize_rows_i8(const uint16_t *w16, int64_t N, int64_t K, int64_t group, int8_t *q, float *scale) {
+    const int64_t G = K / group;
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t g = 0; g < G; ++g) {
+            const uint16_t *w = w16 + n * K + g * group;
+            float amax = 0.f;
+            for (int64_t k = 0; k < group; ++k) amax = fmaxf(amax, fabsf(o_f16_to_f32(w[k])));
+            const float s = amax > 0.f ? amax / 127.f : 1.f;
+            scale[n * G + g] = s;
+            for (int64_t k = 0; k < group; ++k) {
+                float v = o_f16_to_f32(w[k]) / s;
+                v = v < -127.f ? -127.f : v > 127.f ? 127.f : v;
+                q[n * K + g * group + k] = (int8_t)lrintf(v);
+            }
+        }
+}
+
+typedef struct {
+    const int8_t *W8;
+    const float *scale;
+    int64_t K;
+    int group;
+    const uint16_t *x;
+    int xs, M, rpg;
+    double *y;
+    int ys;
+} i8_ctx;
+
+static void i8_range(void *vc, int64_t b, int64_t e) {
+    i8_ctx *c = (i8_ctx *)vc;
+    const int64_t G = c->K / c->group;
+    for (int64_t n = b; n < e; ++n) {
+        const int8_t *w = c->W8 + n * c->K;
+        const float *s = c->scale + n * G;
+        const int64_t off = c->rpg > 0 ? (n / c->rpg) * c->K : 0;
+        for (int m = 0; m < c->M; ++m) {
+            const uint16_t *x = c->x + (int64_t)m * c->xs + off;
+            double acc = 0.0;
+            for (int64_t k = 0; k < c->K; ++k) acc += (double)w[k] * (double)s[k / c->group] * (double)o_f16_to_f32(x[k]);
+            c->y[(int64_t)m * c->ys + n] = acc;
+        }
+    }
+}
+
+/* gpu::gemv_rows_i8 (src/kernels/gemv.hip:75-136, declared gemv.hpp:15-23):
+ *   y[m*ys + n] = sum_k W8[n][k] * scale[n][k / group] * x[m*xs + off(n) + k]
+ * with off(n) = (n / rpg) * K for rpg > 0 (rows grouped over activation
+ * blocks), x fp16 bits; the sum in fp64, as the reference's own test forms
+ * its expected values (tests/gpu/test_gemv.hip:93-104). */
+void o_i8_linear_f64(const int8_t *W8, const float *scale, int64_t N, int64_t K, int group, const uint16_t *x, int xs,
+                     int M, int rpg, double *y, int ys, int threads) {
+    i8_ctx c = {W8, scale, K, group, x, xs, M, rpg, y, ys};
+    parallel_for(threads, N, 16, i8_range, &c);
+}
+
 static float o_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
 
 /* The shared expert's activation (ref_model.cpp:468-476 with the gate folded

@@ -15,6 +15,9 @@ The output holds inputs and the reference's outputs only:
   qsrc         uint16 [groups*128] bf16 weights (random + edge groups)
   q_words      uint32              ref quantize_int4_g128 words
   q_scales     uint16              ref quantize_int4_g128 fp16 scales
+  i8_src       uint16 [12][256]    fp16 weights (random + edge rows) for quantize_rows_i8
+  i8_q32, i8_s32                   ref quantize_rows_i8 (group 32): int8 [12][256], fp32 [12][8]
+  i8_q16, i8_s16                   the same with group 16
 """
 import ctypes
 import os
@@ -71,10 +74,37 @@ def main():
     L.ref_quantize_int4_g128(qsrc.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(ng),
                              q_words.ctypes.data_as(ctypes.c_void_p), q_scales.ctypes.data_as(ctypes.c_void_p))
 
+    # int8 rows (quantize_rows_i8, weight_convert.cpp:92-108): fp16 weights,
+    # random rows plus a zero group, a constant group, a symmetric ramp (ties
+    # of w / s at half steps), an outlier row and large magnitudes
+    rows = [rng.normal(0, 0.05, 256) for _ in range(6)]
+    r = rng.normal(0, 1, 256)
+    r[32:64] = 0.0
+    r[64:96] = -2.5
+    rows.append(r)
+    rows.append(np.tile(np.linspace(-127, 127, 32), 8) * 0.01)
+    r = rng.normal(0, 1e-3, 256)
+    r[5] = 300.0
+    rows.append(r)
+    rows.append(rng.normal(0, 1, 256) * 1e4)
+    rows.append(rng.uniform(-1, 1, 256))
+    rows.append(-np.abs(rng.normal(0, 1, 256)))
+    i8_f32 = np.stack(rows).astype(np.float32)
+    i8_src = np.array([L.ref_f32_to_f16(float(v)) for v in i8_f32.ravel()], np.uint16).reshape(i8_f32.shape)
+    N8, K8 = i8_src.shape
+    L.ref_quantize_rows_i8.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_int64]
+    i8 = {}
+    for g in (32, 16):
+        q = np.empty((N8, K8), np.int8)
+        sc = np.empty((N8, K8 // g), np.float32)
+        L.ref_quantize_rows_i8(i8_src.ctypes.data, N8, K8, q.ctypes.data, sc.ctypes.data, g)
+        i8[f"i8_q{g}"], i8[f"i8_s{g}"] = q, sc
+
     out = os.path.join(HERE, "ref_vectors.npz")
     np.savez_compressed(out, f16_all=f16_all, f16_all_f32=f16_all_f32, f32_in=f32_in, f32_to_f16=f32_to_f16,
                         bf16_in=bf16_in, bf16_to_f16=bf16_to_f16, words_in=words_in, words_eng=words_eng, qsrc=qsrc,
-                        q_words=q_words, q_scales=q_scales)
+                        q_words=q_words, q_scales=q_scales, i8_src=i8_src, **i8)
     print(out, os.path.getsize(out))
 
 

@@ -295,3 +295,37 @@ def test_shared_expert_vs_dense_numpy(oracle):
     h = g / (1 + np.exp(-g)) * u / (1 + np.exp(-s))
     ref = h @ synth.bf16_to_f32(dn).astype(np.float64).T
     assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("group", [32, 16])
+def test_quantize_rows_i8_matches_reference(oracle, group):
+    """The int8 row quantiser against the reference's own quantize_rows_i8
+    (weight_convert.cpp:92-108, run from oracle/_ref): int8 values and fp32
+    scales bit for bit, over random rows, a zero group, a constant group, a
+    symmetric ramp, an outlier and large magnitudes."""
+    q, s = oracle.quantize_rows_i8(GOLD["i8_src"], group)
+    assert np.array_equal(q, GOLD[f"i8_q{group}"])
+    assert np.array_equal(s.view(np.uint32), GOLD[f"i8_s{group}"].view(np.uint32))
+
+
+def test_i8_linear_vs_numpy_and_one_hot(oracle):
+    """The int8 GEMV's oracle against a numpy fp64 restatement (with row groups
+    over activation blocks, rpg) and the closed form of a one-hot row."""
+    r = np.random.default_rng(8)
+    N, K, M, rpg, g = 50, 160, 3, 20, 32
+    W8 = r.integers(-127, 128, size=(N, K)).astype(np.int8)
+    S = np.abs(r.standard_normal((N, K // g))).astype(np.float32) * 0.01
+    nb = (N + rpg - 1) // rpg
+    xs = nb * K + 8
+    x = r.standard_normal((M, xs)).astype(np.float16)
+    y = oracle.i8_linear_f64(W8, S, x.view(np.uint16), M, xs=xs, rpg=rpg, group=g)
+    Wf = W8.astype(np.float64) * np.repeat(S.astype(np.float64), g, axis=1)
+    ref = np.empty((M, N))
+    for n in range(N):
+        blk = x[:, (n // rpg) * K:(n // rpg) * K + K].astype(np.float64)
+        ref[:, n] = blk @ Wf[n]
+    assert np.allclose(y, ref, rtol=1e-12, atol=1e-12)
+    oh = np.zeros((1, K), np.float16)
+    oh[0, 37] = 1.0
+    y1 = oracle.i8_linear_f64(W8, S, oh.view(np.uint16), 1, group=g)
+    assert np.array_equal(y1[0], W8[:, 37].astype(np.float64) * S[:, 37 // g].astype(np.float64))
