@@ -1,6 +1,6 @@
 """Benchmark of the q4 matmul path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|gemv|moe|gemm|moe_prefill]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|gemv|moe|shared|i8|gemm|moe_prefill]
 
 Prints ONE JSON line. The headline (`value`) is the q4 decode GEMV of
 a "step" is one decode pass over the dense projections of
@@ -315,6 +315,41 @@ def bench_shared(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8)):
     return out
 
 
+def bench_i8(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8)):
+    """The int8 dense GEMV (the engine's QW_INT8_DENSE copy, gpu::gemv_rows_i8,
+    src/engine/decode.hip:64-70) on config 2's decode projections: L_LAYERS x
+    (4096->12288, 6144->4096), int8 weights with an fp32 scale per 32 along K
+    (1.125 B a weight, 2.04 GB of layers, past the Infinity Cache), fp16 rows,
+    fp32 out, one graph per step, weights tiled at load (qw_i8_tile). Bytes:
+    weights + scales + rows in and out."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(600)
+    shapes = ((QKV, H), (H, FFN_DOWN_K))
+    ws = [[qwq4.i8_tile(torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8),
+                        torch.rand((N, K // 32), generator=g, device=dev) * 1e-3) for N, K in shapes]
+          for _ in range(L_LAYERS)]
+    out = {}
+    for M in batches:
+        xs = {K: torch.randn((M, K), generator=g, device=dev).half() for _, K in shapes}
+        ys = {N: torch.empty((M, N), dtype=torch.float32, device=dev) for N, _ in shapes}
+        nbytes = L_LAYERS * sum(N * K * 1.125 + M * K * 2 + M * N * 4 for N, K in shapes)
+
+        def launches():
+            for layer in ws:
+                for (Wt, St), (N, K) in zip(layer, shapes):
+                    qwq4.gemv_i8(Wt, St, N, K, xs[K], M, y=ys[N])
+
+        step = graphed(torch, launches)
+        for _ in range(warmup):
+            step()
+        with Timer(torch) as t:
+            for _ in range(steps):
+                step()
+        out[M] = {"GB_s": nbytes * steps / (t.ms * 1e-3) / 1e9,
+                  "us_per_launch": t.ms * 1e3 / (steps * L_LAYERS * len(shapes))}
+    return out
+
+
 # ---------------------------------------------------------------- config 4
 def bench_gemm(torch, qwq4, dev, steps, warmup):
     T = 4096
@@ -531,7 +566,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, shared, gemm, moe_prefill; or traffic (launches for PMC runs), or dominant (the roofline kernel's launches alone)")
+    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, shared, i8, gemm, moe_prefill; or traffic (launches for PMC runs), or dominant (the roofline kernel's launches alone)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--moe-batches", default="1,2,4,8,16,32",
                     help="decode batches of the moe workload (comma list), e.g. one batch for a per-launch trace")
@@ -557,7 +592,7 @@ def main():
         return
     wl = set(a.workload.split(","))
     if "all" in wl:
-        wl = {"gemv", "moe", "shared", "gemm", "moe_prefill"}
+        wl = {"gemv", "moe", "shared", "i8", "gemm", "moe_prefill"}
     res = {}
     if "gemv" in wl:
         res["gemv"] = bench_gemv(torch, qwq4, dev, a.steps, a.warmup)
@@ -570,6 +605,10 @@ def main():
     if "shared" in wl:
         res["shared_expert"] = bench_shared(torch, qwq4, dev, a.steps, a.warmup)
         print("# shared expert done", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+    if "i8" in wl:
+        res["i8_gemv"] = bench_i8(torch, qwq4, dev, a.steps, a.warmup)
+        print("# int8 gemv done", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
     if "gemm" in wl:
         res["prefill_gemm"] = bench_gemm(torch, qwq4, dev, max(4, a.steps), 1)

@@ -12,6 +12,7 @@
  *   qw_moe_combine        gpu::moe_combine_B/T      src/kernels/moe.hpp:42-46
  *   qw_w16_gemv           gpu::gemv_rows (fp16 W)   src/kernels/gemv.hpp:13-14
  *                         ref::Model::linear        src/ref/ref_model.cpp:86-97
+ *   qw_i8_gemv            gpu::gemv_rows_i8         src/kernels/gemv.hpp:15-23
  *   qw_swiglu_gate        gpu::swiglu_T             src/kernels/moe_route.hip:187-197
  *   qw_q4_unpack / qw_q4_dequant                    src/ref/ref_model.cpp:108-114
  *   qw_q4_from_engine_order (inverse of pack_int4_words)
@@ -100,6 +101,31 @@ int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
  * stride xs as in qw_q4_gemv; y fp32 or bf16 (y_bf16). 1 <= M <= 32. */
 int qw_w16_gemv(const uint16_t *W, int ldw, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N,
                 int K, int M, int accumulate, void *stream);
+
+/* Dense GEMV on int8 weights (replaces gpu::gemv_rows_i8,
+ * src/kernels/gemv.hpp:15-23, src/kernels/gemv.hip:75-136; the engine's int8
+ * copy of its dense weights, src/engine/decode.hip:52-70,119-125):
+ *   y[m*ys + n] (+)= sum_g scale[n][g] * sum_{k in group g} W8[n][k] * x[m*xs + off(n) + k]
+ * off(n) = (n / rpg) * K when rpg > 0 (row n reads activation slice n / rpg),
+ * else 0. Wt / St: the weights and scales in the kernel format written by
+ * qw_i8_tile, both 16-byte aligned; group 16 or 32 (the reference's
+ * I8_GROUP); K a multiple of 64; any N >= 1; rpg 0 or >= 16; x fp16 rows of
+ * stride xs (a multiple of 8, covering every slice when M > 1), 16-byte
+ * aligned; y fp32 or bf16 (y_bf16). 1 <= M <= 32. Each group's int8 x fp16
+ * products are exact and summed in fp32, then scaled, as in the reference. */
+int qw_i8_gemv(const void *Wt, const float *St, int group, const uint16_t *x, int xs, void *y, int ys, int y_bf16,
+               int N, int K, int M, int rpg, int accumulate, void *stream);
+
+/* Bytes of the kernel format of an int8 [N][K] matrix: weights (Wt) and
+ * scales (St). N is padded to a multiple of 16 rows. */
+void qw_i8_tiled_size(int N, int K, int group, size_t *w_bytes, size_t *s_bytes);
+
+/* Load-time conversion (the role pack_int4_words plays for q4,
+ * src/engine/weight_convert.cpp:61-71): W8 int8 row-major [N][K] and scale
+ * fp32 [N][K / group], as quantize_rows_i8 writes them
+ * (src/engine/weight_convert.cpp:92-108), into Wt / St (sizes from
+ * qw_i8_tiled_size). Device buffers; W8 8-byte aligned, Wt 16-byte aligned. */
+int qw_i8_tile(const int8_t *W8, const float *scale, int N, int K, int group, void *Wt, float *St, void *stream);
 
 /* The shared expert's activation (replaces gpu::swiglu_T,
  * src/kernels/moe_route.hip:187-197; math of src/ref/ref_model.cpp:468-476):

@@ -52,6 +52,16 @@ def test_abi_version():
     lambda L: L.qw_moe_decode(ctypes.c_void_p(256), ctypes.c_void_p(256), 0, 33, 256, 8,
                               *([ctypes.c_void_p(256)] * 9), 4096, 1536, None, ctypes.c_void_p(256), 1,
                               *([ctypes.c_void_p(256)] * 7), 1 << 30, None),  # T > 32
+    lambda L: L.qw_i8_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), 32, ctypes.c_void_p(256), 96,
+                           ctypes.c_void_p(256), 64, 0, 64, 96, 1, 0, 0, None),  # K % 64
+    lambda L: L.qw_i8_tile(ctypes.c_void_p(256), ctypes.c_void_p(256), 64, 4096, 64, ctypes.c_void_p(256),
+                           ctypes.c_void_p(256), None),  # group 64
+    lambda L: L.qw_i8_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), 64, ctypes.c_void_p(256), 128,
+                           ctypes.c_void_p(256), 64, 0, 64, 128, 1, 0, 0, None),  # group 64
+    lambda L: L.qw_i8_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), 32, ctypes.c_void_p(256), 128,
+                           ctypes.c_void_p(256), 64, 0, 64, 128, 1, 8, 0, None),  # rpg < 16
+    lambda L: L.qw_i8_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), 32, ctypes.c_void_p(256), 1024,
+                           ctypes.c_void_p(256), 1296, 0, 1296, 1024, 2, 324, 0, None),  # xs < 4 slices
 ])
 def test_bad_arguments_are_rejected(call):
     L = qwq4.lib()

@@ -16,7 +16,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libqwq4.so")
 OBJ = os.path.join(HERE, "_build")
-SOURCES = ["q4_gemv.hip", "q4_gemv_f16.hip", "moe_gemv.hip", "q4_gemm.hip", "w16_gemv.hip", "moe_route.hip", "q4_util.hip", "moe_grouped.hip", "st_loader.cpp", "wcache.cpp", "capi.cpp"]
+SOURCES = ["q4_gemv.hip", "q4_gemv_f16.hip", "moe_gemv.hip", "q4_gemm.hip", "w16_gemv.hip", "i8_gemv.hip", "moe_route.hip", "q4_util.hip", "moe_grouped.hip", "st_loader.cpp", "wcache.cpp", "capi.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -30,7 +30,7 @@ FLAGS = [
 # weight request then does not wait on a scalar load of the argument block,
 # which the latency-bound GEMVs feel at every launch.
 PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
-SOURCE_FLAGS = {"q4_gemv.hip": PRELOAD, "q4_gemv_f16.hip": PRELOAD, "w16_gemv.hip": PRELOAD}
+SOURCE_FLAGS = {"q4_gemv.hip": PRELOAD, "q4_gemv_f16.hip": PRELOAD, "w16_gemv.hip": PRELOAD, "i8_gemv.hip": PRELOAD}
 
 
 def _compile(src):

@@ -113,6 +113,46 @@ int qw_w16_gemv(const uint16_t *W, int ldw, const uint16_t *x, int xs, int f16, 
     return launched("qw_w16_gemv");
 }
 
+void qw_i8_tiled_size(int N, int K, int group, size_t *w_bytes, size_t *s_bytes) {
+    const size_t tiles = N > 0 ? size_t((N + 15) / 16) : 0, k = K > 0 ? size_t(K) : 0;
+    if (w_bytes) *w_bytes = tiles * 16 * k;
+    if (s_bytes) *s_bytes = group > 0 ? tiles * 16 * (k / size_t(group)) * 4 : 0;
+}
+
+static int i8_shape(const char *fn, int N, int K, int group) {
+    REQUIRE(group == 16 || group == 32, "%s: group %d (need 16 or 32)", fn, group);
+    REQUIRE(N >= 1 && K >= 64 && K % 64 == 0, "%s: N = %d, K = %d (need N >= 1, K a positive multiple of 64)", fn, N,
+            K);
+    return 0;
+}
+
+int qw_i8_tile(const int8_t *W8, const float *scale, int N, int K, int group, void *Wt, float *St, void *stream) {
+    REQUIRE(W8 && scale && Wt && St, "qw_i8_tile: null pointer");
+    if (int rc = i8_shape("qw_i8_tile", N, K, group)) return rc;
+    REQUIRE(aligned(W8, 8) && aligned(Wt, 16) && aligned(St, 4) && aligned(scale, 4), "qw_i8_tile: misaligned buffer");
+    qwq4::launch_i8_tile(W8, scale, N, K, group, static_cast<uint4 *>(Wt), St, st(stream));
+    return launched("qw_i8_tile");
+}
+
+int qw_i8_gemv(const void *Wt, const float *St, int group, const uint16_t *x, int xs, void *y, int ys, int y_bf16, int N,
+               int K, int M, int rpg, int accumulate, void *stream) {
+    REQUIRE(Wt && St && x && y, "qw_i8_gemv: null Wt, St, x or y");
+    if (int rc = i8_shape("qw_i8_gemv", N, K, group)) return rc;
+    REQUIRE(aligned(Wt, 16) && aligned(St, 16), "qw_i8_gemv: Wt and St must be 16-byte aligned");
+    REQUIRE(M >= 1 && M <= 32, "qw_i8_gemv: M = %d outside 1..32", M);
+    REQUIRE(rpg == 0 || rpg >= 16, "qw_i8_gemv: rpg = %d (need 0 or >= 16)", rpg);
+    const int64_t slices = rpg > 0 ? (int64_t(N) + rpg - 1) / rpg : 1;
+    REQUIRE(xs % 8 == 0 && aligned(x, 16) && (M == 1 || int64_t(xs) >= slices * K),
+            "qw_i8_gemv: x stride %d must be a multiple of 8 and cover %lld slices of K = %d, x 16-byte aligned", xs,
+            (long long)slices, K);
+    REQUIRE(ys >= N || M == 1, "qw_i8_gemv: y stride %d < N", ys);
+    REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_i8_gemv: y misaligned");
+    REQUIRE(qwq4::i8_fits(1, K, N, group, rpg), "qw_i8_gemv: K = %d too large for one staged row", K);
+    qwq4::I8Args a{static_cast<const uint4 *>(Wt), St, group, x, xs, y, ys, y_bf16 != 0, N, K, M, rpg, accumulate != 0};
+    qwq4::launch_i8_gemv(a, st(stream));
+    return launched("qw_i8_gemv");
+}
+
 int qw_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, void *stream) {
     REQUIRE(v && h, "qw_swiglu_gate: null v or h");
     REQUIRE(n >= 1 && T >= 1 && ldv >= 2 * n + 1, "qw_swiglu_gate: n = %d, T = %d, ldv = %d (need ldv >= 2n + 1)", n, T,

@@ -142,6 +142,22 @@ struct W16Args {
 };
 bool w16_fits(int M, int K, int N);
 void launch_w16_gemv(const W16Args &a, hipStream_t s);
+// Dense GEMV on int8 weights (tiled by launch_i8_tile from row-major [N][K])
+// with an fp32 scale per group of `group` (16 or 32) along K; fp16
+// activation rows, row slices of rpg rows (0: none) as in gpu::gemv_rows_i8.
+struct I8Args {
+    const uint4 *W;
+    const float *S;
+    int group;
+    const uint16_t *x;
+    int xs;
+    void *y;
+    int ys, y_bf16, N, K, M, rpg, accumulate;
+};
+size_t i8_lds_bytes(int M, int K, int N, int group, int rpg);
+bool i8_fits(int M, int K, int N, int group, int rpg);
+void launch_i8_tile(const int8_t *W8, const float *S, int N, int K, int group, uint4 *Wt, float *St, hipStream_t s);
+void launch_i8_gemv(const I8Args &a, hipStream_t s);
 void launch_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, hipStream_t s);
 
 struct GemmArgs {

@@ -20,7 +20,7 @@ SYMBOLS = (
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
     "qw_moe_decode_workspace_size", "qw_moe_decode", "qw_moe_decode_static_max_bytes", "qw_moe_decode_static",
-    "qw_w16_gemv", "qw_swiglu_gate",
+    "qw_w16_gemv", "qw_i8_gemv", "qw_i8_tiled_size", "qw_i8_tile", "qw_swiglu_gate",
     "qw_wcache_open", "qw_wcache_put", "qw_wcache_get", "qw_wcache_finish", "qw_wcache_close",
 )
 
@@ -53,6 +53,9 @@ _SIGS = {
     "qw_moe_decode": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
     "qw_moe_decode_static_max_bytes": ([], _SZ),
     "qw_w16_gemv": ([_P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_i8_gemv": ([_P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_i8_tiled_size": ([_I, _I, _I, _P, _P], None),
+    "qw_i8_tile": ([_P, _P, _I, _I, _I, _P, _P, _P], _I),
     "qw_swiglu_gate": ([_P, _I, _I, _I, _P, _P], _I),
     "qw_moe_decode_static": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
@@ -185,6 +188,37 @@ def gemv_w16(W, x, M=None, y=None, y_bf16=False, accumulate=False, f16=None, xs=
     rc = lib().qw_w16_gemv(_ptr(W), W.stride(0), _ptr(x), xs, int(f16), _ptr(y), ys, int(y_bf16), N, K, M,
                            int(accumulate), _stream())
     _check(rc, "qw_w16_gemv")
+    return y
+
+
+def i8_tile(W8, scale, group=32):
+    """int8 W8 [N][K] and fp32 scale [N][K/group] (row-major, as quantize_rows_i8 writes
+    them) -> the kernel format (Wt uint8 bytes, St fp32) qw_i8_gemv reads."""
+    import torch
+    N, K = W8.shape
+    wb, sb = ctypes.c_size_t(), ctypes.c_size_t()
+    lib().qw_i8_tiled_size(N, K, group, ctypes.byref(wb), ctypes.byref(sb))
+    Wt = torch.empty(wb.value, dtype=torch.uint8, device=W8.device)
+    St = torch.empty(sb.value // 4, dtype=torch.float32, device=W8.device)
+    _dev(W8, scale)
+    _check(lib().qw_i8_tile(_ptr(W8), _ptr(scale), N, K, group, _ptr(Wt), _ptr(St), _stream()), "qw_i8_tile")
+    return Wt, St
+
+
+def gemv_i8(Wt, St, N, K, x, M=None, group=32, rpg=0, y=None, y_bf16=False, accumulate=False, xs=None, ys=None):
+    """y[m][n] (+)= sum_g scale[n][g] sum_{k in g} W8[n][k] x[m][off(n) + k] (gpu::gemv_rows_i8) on
+    the kernel format (i8_tile) of an int8 [N][K] matrix; fp16 rows x (row n reads slice
+    n // rpg when rpg)."""
+    import torch
+    M = M if M is not None else x.shape[0]
+    xs = xs if xs is not None else x.stride(0) if x.dim() == 2 else K
+    if y is None:
+        y = torch.zeros((M, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=x.device)
+    ys = ys if ys is not None else (y.stride(0) if y.dim() == 2 else N)
+    _dev(Wt, St, x, y)
+    rc = lib().qw_i8_gemv(_ptr(Wt), _ptr(St), group, _ptr(x), xs, _ptr(y), ys, int(y_bf16), N, K, M, rpg,
+                          int(accumulate), _stream())
+    _check(rc, "qw_i8_gemv")
     return y
 
 
