@@ -418,8 +418,32 @@ def bench_moe_prefill(torch, qwq4, dev, steps, warmup):
         for _ in range(steps):
             gstep()
     flops = 2.0 * (k * T) * (2 * F * H + H * F)
-    return {"TFLOP_s": flops * steps / (t.ms * 1e-3) / 1e12, "us_per_step": t.ms * 1e3 / steps,
-            "tokens_s": T * steps / (t.ms * 1e-3)}
+    res = {"TFLOP_s": flops * steps / (t.ms * 1e-3) / 1e12, "us_per_step": t.ms * 1e3 / steps,
+           "tokens_s": T * steps / (t.ms * 1e-3)}
+
+    # the reference's opt-in W4A8 path (int8 activations, lossy) on the same
+    # experts and routing: 64-slot tiles, fp16 rows as the engine passes them
+    tm8 = qwq4.moe_w4a8_tile_m()
+    r8 = qwq4.Route(T, E, k, dev, tile_m=tm8)
+    xh = x.half()
+    ws8 = torch.empty(qwq4.lib().qw_moe_w4a8_workspace_size(T, k, H, F), dtype=torch.uint8, device=dev)
+
+    def step8():
+        qwq4.moe_route(logits, k, tile_m=tm8, out=r8)
+        qwq4.moe_experts_w4a8(gate, up, down, r8, xh, E, F, h=h, yp=yp, workspace=ws8)
+        qwq4.moe_combine(yp, r8, H, out=o)
+
+    g8 = graphed(torch, step8)
+    t_end = time.perf_counter() + 1.0
+    while time.perf_counter() < t_end:
+        g8()
+        torch.cuda.synchronize()
+    with Timer(torch) as t8:
+        for _ in range(steps):
+            g8()
+    res["w4a8"] = {"TOP_s": flops * steps / (t8.ms * 1e-3) / 1e12, "us_per_step": t8.ms * 1e3 / steps,
+                   "note": "int8 activations per (row, 128-group), int8 MFMA, lossy (the reference's opt-in path)"}
+    return res
 
 
 def measured_traffic():

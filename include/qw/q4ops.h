@@ -9,6 +9,8 @@
  *                                                   src/kernels/moe.hpp:17-27
  *   qw_moe_experts_gemv   gpu::moe_experts_P        src/kernels/moe.hpp:35-37
  *   qw_moe_experts_grouped gpu::moe_experts_T       src/kernels/moe.hpp:29-32
+ *   qw_moe_experts_w4a8   gpu::moe_experts_w4a8     src/kernels/moe_tiling.hpp:14-20
+ *   qw_quant_rows_i8      quant_rows_kernel         src/kernels/moe_w4a8.hip:17-36
  *   qw_moe_combine        gpu::moe_combine_B/T      src/kernels/moe.hpp:42-46
  *   qw_w16_gemv           gpu::gemv_rows (fp16 W)   src/kernels/gemv.hpp:13-14
  *                         ref::Model::linear        src/ref/ref_model.cpp:86-97
@@ -210,6 +212,38 @@ int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_
                            const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
                            int x_f16, int T, int topk, uint16_t *h, void *yp, int yp_f16, void *workspace,
                            size_t workspace_bytes, void *stream);
+
+/* W4A8 grouped expert GEMMs (replaces gpu::moe_experts_w4a8,
+ * src/kernels/moe_tiling.hpp:14-20, src/kernels/moe_w4a8.hip:13-215: the
+ * reference's opt-in int8-activation path, lossy by design). Activation rows
+ * are quantised per (row, 128-group) as qw_quant_rows_i8 does; weights are
+ * widened exactly to int8 q - z; per 64-wide K step the products are summed
+ * in int32 and added as fp32 float(I) * s_w * s_x. Gate/up write
+ *   h[p] = fp16(silu(g) * u)                     fp16 [T*k][F]
+ * and the down projection, on h quantised the same way,
+ *   yp[p] = fp16(D_e . h[p])                     fp16 [T*k][H]
+ * (finite values beyond +-65504 saturate). Weights tiled as for
+ * qw_moe_experts_grouped; tile list from qw_moe_route with
+ * tile_m = qw_moe_w4a8_tile_m() (64-slot tiles). x [T][H] fp16 (x_f16 = 1,
+ * the reference's rows) or bf16. H and F multiples of 128. workspace: at
+ * least qw_moe_w4a8_workspace_size(T, topk, H, F) bytes, 256-byte aligned
+ * (the quantised rows and their scales, the reference's q8 / q8s). */
+int qw_moe_w4a8_tile_m(void);
+size_t qw_moe_w4a8_workspace_size(int T, int topk, int H, int F);
+int qw_moe_experts_w4a8(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                        const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                        const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
+                        const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
+                        int x_f16, int T, int topk, uint16_t *h, uint16_t *yp, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
+/* The W4A8 activation quantiser (quant_rows_kernel,
+ * src/kernels/moe_w4a8.hip:17-36): per row and group of 128 along K,
+ *   scale[r][g] = max|x| / 127 (1 for an all-zero group),
+ *   q[r][k] = rint(x[r][k] * (1 / scale[r][g]))   (round half to even)
+ * x rows of stride ldx (elements), fp16 (x_f16 = 1) or bf16; q int8 [rows][K],
+ * scale fp32 [rows][K / 128]. K a multiple of 128. */
+int qw_quant_rows_i8(const uint16_t *x, int x_f16, int rows, int K, int ldx, int8_t *q, float *scale, void *stream);
 
 /* Weighted combine (replaces gpu::moe_combine_B/T, moe.hpp:42-46):
  *   out[t][j] = shared[t][j] + sum_{i<k} tok_w[t][i] * yp[tok_slot[t][i]][j]

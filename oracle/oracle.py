@@ -50,6 +50,8 @@ def lib():
         L.o_swiglu_gate.argtypes = [_f32p, _int, _int, _int, _f32p]
         L.o_quantize_rows_i8.argtypes = [_u16p, _i64, _i64, _i64, _vp, _f32p]
         L.o_i8_linear_f64.argtypes = [_vp, _f32p, _i64, _i64, _int, _u16p, _int, _int, _int, _f64p, _int, _int]
+        L.o_quant_rows_i8.argtypes = [_u16p, _int, _i64, _i64, _i64, _vp, _f32p]
+        L.o_w4a8_linear.argtypes = [_vp, _f32p, _vp, _i64, _i64, _u32p, _u16p, _vp, _i64, _f32p, _int]
         for n in ("o_bf16_to_f32", "o_f16_to_f32"):
             getattr(L, n).argtypes = [ctypes.c_uint16]
             getattr(L, n).restype = ctypes.c_float
@@ -273,3 +275,71 @@ def q4_tile(W, S, Z, N, K):
     Zc = None if Z is None else _c(Z, np.uint32)
     lib().o_q4_tile(W, S, _zp(Zc), N, K, Wt, St, None if Zt is None else Zt.ctypes.data_as(ctypes.c_void_p))
     return Wt, St, Zt
+
+
+# ---- W4A8 (the reference's opt-in int8-activation expert GEMMs)
+def quant_rows_i8(x16, f16=True):
+    """16-bit rows [R][K] (fp16 bits when f16, else bf16) -> (int8 [R][K], fp32 [R][K/128])
+    as moe_w4a8.hip's quant_rows_kernel (src/kernels/moe_w4a8.hip:17-36)."""
+    x16 = _c(x16, np.uint16)
+    R, K = x16.shape
+    q = np.empty((R, K), np.int8)
+    sc = np.empty((R, K // 128), np.float32)
+    lib().o_quant_rows_i8(x16, int(f16), R, K, K, q.ctypes.data, sc)
+    return q, sc
+
+
+def w4a8_linear(q8, sx, W, S, Z, N, rowmap=None, threads=None):
+    """y[p][n]: the W4A8 product of quantised rows q8[rowmap[p]] (or q8[p]) with q4 weight
+    rows (moe_w4a8.hip:62-183): int32 per 64-wide K step, rescaled per step in fp32."""
+    q8 = np.ascontiguousarray(q8, np.int8)
+    R, K = q8.shape
+    rm = None if rowmap is None else _c(rowmap, np.int32)
+    P = R if rm is None else rm.size
+    y = np.empty((P, N), np.float32)
+    W, S = _c(W, np.uint32).reshape(N, K // 8), _c(S, np.uint16).reshape(N, K // 128)
+    Z = None if Z is None else _c(Z, np.uint32).reshape(N, -1)
+    lib().o_w4a8_linear(q8.ctypes.data, _c(sx, np.float32), None if rm is None else rm.ctypes.data, P, K, W, S, _zp(Z),
+                        N, y, threads or nthreads())
+    return y
+
+
+def _silu(g):
+    g = np.asarray(g, np.float32)
+    return g * (np.float32(1) / (np.float32(1) + np.exp(-g)))
+
+
+def moe_w4a8(x16, f16, gate, up, down, offsets, pair_tok, E, slots=None):
+    """The reference's W4A8 routed experts (gpu::moe_experts_w4a8,
+    src/kernels/moe_w4a8.hip:186-215) over the slots of qw_moe_route: x rows quantised
+    per 128-group; per expert e and slot p of it, h[p] = fp16(silu(g) * u) with g, u the
+    W4A8 products of x[pair_tok[p]]; h rows quantised; yp[p] = fp16(down W4A8 product).
+    gate/up/down: (W [E][rows][K/8], S, Z or None). slots: the slots to form (default
+    all). Returns h, yp as fp32 arrays of the fp16 values, rows = slots."""
+    qx, sx = quant_rows_i8(x16, f16)
+    F, H = gate[0].shape[1], gate[0].shape[2] * 8
+    P = int(offsets[E])
+    slots = np.arange(P) if slots is None else np.asarray(slots)
+    h = np.zeros((P, F), np.float16)
+    need = np.zeros(P, bool)
+    need[slots] = True
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        ps = np.arange(lo, hi)[need[lo:hi]]
+        if ps.size == 0:
+            continue
+        Zg = None if gate[2] is None else gate[2][e]
+        Zu = None if up[2] is None else up[2][e]
+        g = w4a8_linear(qx, sx, gate[0][e], gate[1][e], Zg, F, rowmap=pair_tok[ps])
+        u = w4a8_linear(qx, sx, up[0][e], up[1][e], Zu, F, rowmap=pair_tok[ps])
+        h[ps] = (_silu(g) * u).astype(np.float16)
+    qh, sh = quant_rows_i8(h.view(np.uint16), True)
+    yp = np.zeros((P, H), np.float16)
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        ps = np.arange(lo, hi)[need[lo:hi]]
+        if ps.size == 0:
+            continue
+        Zd = None if down[2] is None else down[2][e]
+        yp[ps] = w4a8_linear(qh, sh, down[0][e], down[1][e], Zd, H, rowmap=ps).astype(np.float16)
+    return h[slots].astype(np.float32), yp[slots].astype(np.float32)

@@ -17,6 +17,9 @@
  *   - 16-bit dense linear          src/ref/ref_model.cpp:86-97
  *   - shared expert (SwiGLU, gate) src/ref/ref_model.cpp:465-478
  *   - slot order                   src/kernels/moe_route.hip:149-160
+ *   - W4A8 expert GEMMs (opt-in)   src/kernels/moe_w4a8.hip:13-215
+ *   - int8 dense rows (i8 GEMV)    src/engine/weight_convert.cpp:92-108,
+ *                                  src/kernels/gemv.hip:75-136
  *   - parallel_for chunking        src/core/threadpool.hpp:38-58
  *
  * Formats used throughout (the device formats of this build):
@@ -579,4 +582,84 @@ void o_q4_tile(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t 
                 }
                 if (Zt) Zt[(sub * GC + gc) * 16 + n] = zt;
             }
+}
+
+/* ----------------------------------------------------------------- W4A8 */
+
+/* gpu::moe_experts_w4a8's activation quantiser, quant_rows_kernel
+ * (src/kernels/moe_w4a8.hip:17-36): per row and group of 128 along K,
+ * sc = max|x| / 127 (1 when the group is all zero), inv = 1 / sc (fp32
+ * division), q = int8(rint(x * inv)) (round half to even; |x * inv| <= 127
+ * up to an ulp, so no clamp is needed). x holds 16-bit bits: fp16 when
+ * f16 != 0 (the reference's rows), else bf16. */
+void o_quant_rows_i8(const uint16_t *x, int f16, int64_t rows, int64_t K, int64_t ldx, int8_t *q, float *scale) {
+    const int64_t G = K / QGROUP;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t g = 0; g < G; ++g) {
+            const uint16_t *xg = x + r * ldx + g * QGROUP;
+            float v[QGROUP], mx = 0.f;
+            for (int i = 0; i < QGROUP; ++i) {
+                v[i] = f16 ? o_f16_to_f32(xg[i]) : o_bf16_to_f32(xg[i]);
+                mx = fmaxf(mx, fabsf(v[i]));
+            }
+            const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
+            for (int i = 0; i < QGROUP; ++i) q[r * K + g * QGROUP + i] = (int8_t)(int)rintf(v[i] * inv);
+            scale[r * G + g] = sc;
+        }
+}
+
+typedef struct {
+    const int8_t *q8;
+    const float *sx;
+    const int32_t *rowmap;
+    int64_t K;
+    const uint32_t *W;
+    const uint16_t *S;
+    const uint32_t *Z;
+    int64_t N;
+    float *y;
+} w4a8_ctx;
+
+static void w4a8_range(void *vc, int64_t b, int64_t e) {
+    const w4a8_ctx *c = (const w4a8_ctx *)vc;
+    const int64_t K = c->K, G = K / QGROUP;
+    int8_t *wq = (int8_t *)malloc((size_t)K);
+    for (int64_t n = 0; n < c->N; ++n) {
+        /* the row widened exactly: q - z (moe_w4a8.hip:38-56 with z = 8) */
+        for (int64_t k = 0; k < K; ++k) {
+            const uint32_t word = c->W[n * (K / 8) + k / 8];
+            wq[k] = (int8_t)((int)((word >> (4 * (k % 8))) & 0xfu) - zero_of(c->Z, n, G, k / QGROUP));
+        }
+        for (int64_t p = b; p < e; ++p) {
+            const int64_t r = c->rowmap ? c->rowmap[p] : p;
+            const int8_t *a = c->q8 + r * K;
+            float acc = 0.f;
+            /* int32 per 64-wide K step, then the step's group scales in
+             * fp32, steps in order: acc += float(dot) * s_w * s_x, the
+             * last multiply-add fused as the HIP compiler contracts it
+             * (moe_w4a8.hip:98-116, :161-176) */
+            for (int64_t k0 = 0; k0 < K; k0 += 64) {
+                int32_t dot = 0;
+                for (int k = 0; k < 64; ++k) dot += (int32_t)a[k0 + k] * (int32_t)wq[k0 + k];
+                const int64_t g = k0 / QGROUP;
+                const float sw = o_f16_to_f32(c->S[n * G + g]);
+                acc = fmaf((float)dot * sw, c->sx[r * G + g], acc);
+            }
+            c->y[p * c->N + n] = acc;
+        }
+    }
+    free(wq);
+}
+
+/* One W4A8 projection of the grouped expert GEMMs (moe_w4a8.hip:62-118,
+ * :120-183): for P activation rows (row p of the product reads quantised row
+ * rowmap[p], or p when rowmap is NULL: the gathered token of a slot for
+ * gate / up, the slot itself for down) and N weight rows,
+ *   y[p][n] = sum over 64-wide K steps, in order, of float(I) * s_w * s_x
+ * with I the exact int32 dot of the step. q8 / sx as o_quant_rows_i8 writes
+ * them (row stride K); W, S, Z in this build's checkpoint formats. */
+void o_w4a8_linear(const int8_t *q8, const float *sx, const int32_t *rowmap, int64_t P, int64_t K, const uint32_t *W,
+                   const uint16_t *S, const uint32_t *Z, int64_t N, float *y, int threads) {
+    w4a8_ctx c = {q8, sx, rowmap, K, W, S, Z, N, y};
+    parallel_for(threads, P, 4, w4a8_range, &c);
 }

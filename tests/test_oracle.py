@@ -329,3 +329,83 @@ def test_i8_linear_vs_numpy_and_one_hot(oracle):
     oh[0, 37] = 1.0
     y1 = oracle.i8_linear_f64(W8, S, oh.view(np.uint16), 1, group=g)
     assert np.array_equal(y1[0], W8[:, 37].astype(np.float64) * S[:, 37 // g].astype(np.float64))
+
+
+@pytest.mark.parametrize("f16", [True, False])
+def test_quant_rows_i8_properties(oracle, f16):
+    """The W4A8 activation quantiser (moe_w4a8.hip:17-36): per 128-group the
+    largest magnitude maps to +-127, every value to within half a step of its
+    q * scale, an all-zero group to q = 0 with scale 1; and the values agree
+    bit for bit with IEEE fp32 numpy arithmetic of the same steps."""
+    r = np.random.default_rng(11)
+    R, K = 6, 512
+    v = r.standard_normal((R, K)).astype(np.float32) * np.float32(3.0)
+    v[1, 128:256] = 0.0                    # a zero group
+    v[2, 0:128] = 0.0
+    v[2, 5] = -1e-3                        # one nonzero value
+    v[3, 256:384] = np.linspace(-2, 2, 128, dtype=np.float32)  # symmetric ramp
+    bits = v.astype(np.float16).view(np.uint16) if f16 else synth.bf16_bits(v)
+    x = bits.view(np.float16).astype(np.float32) if f16 else synth.bf16_to_f32(bits)
+    q, sc = oracle.quant_rows_i8(bits, f16)
+    xg = x.reshape(R, K // 128, 128)
+    qg = q.reshape(R, K // 128, 128).astype(np.int32)
+    amax = np.abs(xg).max(-1)
+    zero = amax == 0
+    assert np.all(sc[zero] == 1.0) and np.all(qg[zero] == 0)
+    nz = ~zero
+    assert np.all(np.abs(qg).max(-1)[nz] == 127)
+    assert np.all(np.abs(qg) <= 127)
+    err = np.abs(qg * sc[..., None] - xg)
+    assert np.all(err <= sc[..., None] * (0.5 + 1e-5))
+    assert q[2, 5] == -127
+    # IEEE fp32 steps: scale = amax / 127, inv = 1 / scale, q = rint(x * inv)
+    s32 = np.where(zero, np.float32(1), (amax / np.float32(127)).astype(np.float32)).astype(np.float32)
+    inv = (np.float32(1) / s32).astype(np.float32)
+    ref = np.rint((xg * inv[..., None]).astype(np.float32)).astype(np.int32)
+    assert np.array_equal(sc.view(np.uint32), s32.view(np.uint32))
+    assert np.array_equal(qg, ref)
+
+
+def test_w4a8_linear_vs_numpy_and_exact(oracle):
+    """The W4A8 product (moe_w4a8.hip:62-183): against numpy (exact int64 dots per
+    64-wide K step, fp64 sums of the per-step fp32 terms), and bit-exact where every
+    term is exact (power-of-two scales, small values)."""
+    r = np.random.default_rng(12)
+    N, K, P = 24, 384, 9
+    W, S, Z = synth.q4_weights(12, "w4a8", N, K, zeros=True)
+    q8 = r.integers(-127, 128, size=(P + 3, K)).astype(np.int8)
+    sx = np.abs(r.standard_normal((P + 3, K // 128))).astype(np.float32) * 0.02
+    rowmap = r.integers(0, P + 3, size=P).astype(np.int32)
+    y = oracle.w4a8_linear(q8, sx, W, S, Z, N, rowmap=rowmap)
+    wq = oracle.q4_unpack(W, N, K).astype(np.int64) - np.repeat(synth.unpack_zeros(Z, K // 128), 128, 1)
+    sw = S.view(np.float16).astype(np.float32)
+    ref = np.zeros((P, N))
+    for s in range(K // 64):
+        d = q8[rowmap][:, 64 * s:64 * s + 64].astype(np.int64) @ wq[:, 64 * s:64 * s + 64].T
+        g = s // 2
+        ref += (d.astype(np.float32) * sw[None, :, g]).astype(np.float64) * sx[rowmap][:, g:g + 1]
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
+    # exact: scales 2^-4 .. 2^-1 and 1, small activations: every term and sum is an exact fp32
+    S2 = (np.float16(2.0) ** -r.integers(0, 5, size=(N, K // 128))).astype(np.float16).view(np.uint16)
+    q2 = r.integers(-3, 4, size=(P, K)).astype(np.int8)
+    sx2 = (np.float32(2.0) ** -r.integers(0, 4, size=(P, K // 128))).astype(np.float32)
+    y2 = oracle.w4a8_linear(q2, sx2, W, S2, Z, N)
+    w2 = wq.astype(np.float64) * np.repeat(S2.view(np.float16).astype(np.float64), 128, 1)
+    a2 = q2.astype(np.float64) * np.repeat(sx2.astype(np.float64), 128, 1)
+    assert np.array_equal(y2, (a2 @ w2.T).astype(np.float32))
+
+
+def test_moe_w4a8_close_to_the_unquantised_moe(oracle):
+    """The W4A8 experts (oracle restatement of moe_experts_w4a8) stay close to the
+    unquantised fp32 MoE (o_moe) on the same routing: int8 activations cost a few
+    1e-3 of max|y| (the reference's documented loss), nothing structural."""
+    E, H, F, k, T = 8, 256, 128, 2, 12
+    ex = synth.experts(13, E, H, F, zeros=True)
+    xb, xf = synth.acts(13, "x", T, H)
+    l = synth.router_logits(13, "l", T, E)
+    out, h_ref, yp_ref = oracle.moe(xf, l, k, *ex, want_parts=True)
+    te, _ = oracle.route(l, k)
+    counts, offsets, tok_slot, pair_tok = oracle.moe_slots(te, E)
+    h, yp = oracle.moe_w4a8(xb, False, *ex, offsets, pair_tok, E)
+    assert np.max(np.abs(h - h_ref)) <= 2e-2 * np.max(np.abs(h_ref))
+    assert np.max(np.abs(yp - yp_ref)) <= 3e-2 * np.max(np.abs(yp_ref))

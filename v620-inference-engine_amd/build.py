@@ -16,7 +16,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libqwq4.so")
 OBJ = os.path.join(HERE, "_build")
-SOURCES = ["q4_gemv.hip", "q4_gemv_f16.hip", "moe_gemv.hip", "q4_gemm.hip", "w16_gemv.hip", "i8_gemv.hip", "moe_route.hip", "q4_util.hip", "moe_grouped.hip", "st_loader.cpp", "wcache.cpp", "capi.cpp"]
+SOURCES = ["q4_gemv.hip", "q4_gemv_f16.hip", "moe_gemv.hip", "q4_gemm.hip", "w16_gemv.hip", "i8_gemv.hip", "moe_w4a8.hip", "moe_route.hip", "q4_util.hip", "moe_grouped.hip", "st_loader.cpp", "wcache.cpp", "capi.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -253,6 +253,46 @@ int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_
     return launched("qw_moe_experts_grouped");
 }
 
+int qw_moe_w4a8_tile_m(void) { return qwq4::moe_w4a8_tile_m(); }
+
+size_t qw_moe_w4a8_workspace_size(int T, int topk, int H, int F) {
+    if (T < 1 || topk < 1 || H < 1 || F < 1) return 0;
+    return qwq4::moe_w4a8_workspace_bytes(T, topk, H, F);
+}
+
+int qw_quant_rows_i8(const uint16_t *x, int x_f16, int rows, int K, int ldx, int8_t *q, float *scale, void *stream) {
+    REQUIRE(x && q && scale, "qw_quant_rows_i8: null pointer");
+    REQUIRE(rows >= 1 && K >= 128 && K % 128 == 0, "qw_quant_rows_i8: rows = %d, K = %d (need K a multiple of 128)",
+            rows, K);
+    REQUIRE(ldx >= K && ldx % 2 == 0 && aligned(x, 4) && aligned(q, 2) && aligned(scale, 4),
+            "qw_quant_rows_i8: row stride %d (>= K, even) or misaligned buffers", ldx);
+    qwq4::launch_quant_rows(x, x_f16 != 0, ldx, rows, K, q, scale, st(stream));
+    return launched("qw_quant_rows_i8");
+}
+
+int qw_moe_experts_w4a8(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                        const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                        const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *pair_tok,
+                        const int32_t *tile_e, const int32_t *tile_m0, const int32_t *n_tiles, const uint16_t *x,
+                        int x_f16, int T, int topk, uint16_t *h, uint16_t *yp, void *workspace, size_t workspace_bytes,
+                        void *stream) {
+    if (int r = check_q4("qw_moe_experts_w4a8(gate)", gw, gs, int64_t(E) * F, H)) return r;
+    if (int r = check_q4("qw_moe_experts_w4a8(up)", uw, us, int64_t(E) * F, H)) return r;
+    if (int r = check_q4("qw_moe_experts_w4a8(down)", dw, ds, int64_t(E) * H, F)) return r;
+    REQUIRE(offsets && pair_tok && tile_e && tile_m0 && n_tiles && x && h && yp, "qw_moe_experts_w4a8: null pointer");
+    REQUIRE(T >= 1 && topk >= 1 && topk <= E, "qw_moe_experts_w4a8: T = %d, topk = %d", T, topk);
+    REQUIRE(int64_t(T) * topk < (int64_t(1) << 30), "qw_moe_experts_w4a8: T * topk too large");
+    REQUIRE(F % 128 == 0 && H % 128 == 0, "qw_moe_experts_w4a8: H = %d, F = %d (need multiples of 128)", H, F);
+    REQUIRE(aligned(x, 4) && aligned(h, 4) && aligned(yp, 2), "qw_moe_experts_w4a8: misaligned x/h/yp");
+    const size_t need = qwq4::moe_w4a8_workspace_bytes(T, topk, H, F);
+    REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256),
+            "qw_moe_experts_w4a8: workspace needs %zu bytes, 256-byte aligned", need);
+    qwq4::W8Args a{gw, uw, dw, gs, gz, us, uz, ds, dz, E, H, F, offsets, pair_tok, tile_e, tile_m0, n_tiles, h, yp,
+                   workspace, nullptr, nullptr, nullptr, nullptr};
+    qwq4::launch_moe_w4a8(a, x, x_f16 != 0, T, topk, st(stream));
+    return launched("qw_moe_experts_w4a8");
+}
+
 int qw_moe_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared, int T,
                    int topk, int H, void *out, int out_bf16, void *stream) {
     REQUIRE(yp && tok_slot && tok_w && out, "qw_moe_combine: null pointer");

@@ -160,6 +160,25 @@ void launch_i8_tile(const int8_t *W8, const float *S, int N, int K, int group, u
 void launch_i8_gemv(const I8Args &a, hipStream_t s);
 void launch_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, hipStream_t s);
 
+// W4A8 grouped expert GEMMs (moe_w4a8.hip): tiled q4 weights as for the
+// grouped fp16 path, the routing tile list with 64-slot tiles, fp16 h and yp.
+// qx / sx / qh / sh point into the workspace (set by launch_moe_w4a8).
+struct W8Args {
+    const uint32_t *gw, *uw, *dw;
+    const uint16_t *gs, *gz, *us, *uz, *ds, *dz;
+    int E, H, F;
+    const int32_t *offsets, *pair_tok, *tile_e, *tile_m0, *n_tiles;
+    uint16_t *h, *yp;
+    void *ws;
+    const int8_t *qx, *qh;
+    const float *sx, *sh;
+};
+int moe_w4a8_tile_m();
+size_t moe_w4a8_workspace_bytes(int T, int topk, int H, int F);
+void launch_moe_w4a8(W8Args a, const uint16_t *x, int x_f16, int T, int topk, hipStream_t s);
+void launch_quant_rows(const uint16_t *x, int x_f16, int64_t ldx, int rows, int K, int8_t *q, float *scale,
+                       hipStream_t s);
+
 struct GemmArgs {
     const uint32_t *W;
     const uint16_t *S;

@@ -20,7 +20,8 @@ SYMBOLS = (
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
     "qw_moe_decode_workspace_size", "qw_moe_decode", "qw_moe_decode_static_max_bytes", "qw_moe_decode_static",
-    "qw_w16_gemv", "qw_i8_gemv", "qw_i8_tiled_size", "qw_i8_tile", "qw_swiglu_gate",
+    "qw_w16_gemv", "qw_i8_gemv", "qw_i8_tiled_size", "qw_i8_tile",
+    "qw_moe_w4a8_tile_m", "qw_moe_w4a8_workspace_size", "qw_moe_experts_w4a8", "qw_quant_rows_i8", "qw_swiglu_gate",
     "qw_wcache_open", "qw_wcache_put", "qw_wcache_get", "qw_wcache_finish", "qw_wcache_close",
 )
 
@@ -56,6 +57,10 @@ _SIGS = {
     "qw_i8_gemv": ([_P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_i8_tiled_size": ([_I, _I, _I, _P, _P], None),
     "qw_i8_tile": ([_P, _P, _I, _I, _I, _P, _P, _P], _I),
+    "qw_moe_w4a8_tile_m": ([], _I),
+    "qw_moe_w4a8_workspace_size": ([_I, _I, _I, _I], _SZ),
+    "qw_moe_experts_w4a8": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _I, _P, _P, _P, _SZ, _P], _I),
+    "qw_quant_rows_i8": ([_P, _I, _I, _I, _I, _P, _P, _P], _I),
     "qw_swiglu_gate": ([_P, _I, _I, _I, _P, _P], _I),
     "qw_moe_decode_static": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
@@ -329,6 +334,43 @@ def moe_experts_grouped(gate, up, down, route, x, E, F, h=None, yp=None, workspa
                                       int(yp.dtype == torch.float16), _ptr(workspace),
                                       0 if workspace is None else workspace.numel(), _stream())
     _check(rc, "qw_moe_experts_grouped")
+    return h, yp
+
+
+def moe_w4a8_tile_m():
+    return lib().qw_moe_w4a8_tile_m()
+
+
+def quant_rows_i8(x, x_f16=None):
+    """16-bit rows [R][K] -> (int8 [R][K], fp32 scales [R][K/128]) (the W4A8 quantiser)."""
+    import torch
+    R, K = x.shape
+    q = torch.empty((R, K), dtype=torch.int8, device=x.device)
+    sc = torch.empty((R, K // 128), dtype=torch.float32, device=x.device)
+    _dev(x)
+    _check(lib().qw_quant_rows_i8(_ptr(x), int(_is_f16(x, x_f16)), R, K, x.stride(0), _ptr(q), _ptr(sc), _stream()),
+           "qw_quant_rows_i8")
+    return q, sc
+
+
+def moe_experts_w4a8(gate, up, down, route, x, E, F, h=None, yp=None, workspace=None, x_f16=None):
+    """The W4A8 grouped expert GEMMs (route made with tile_m = moe_w4a8_tile_m());
+    returns (h fp16 [T*k][F], yp fp16 [T*k][H])."""
+    import torch
+    T, H = x.shape
+    topk = route.topk
+    if h is None:
+        h = torch.empty((T * topk, F), dtype=torch.float16, device=x.device)
+    if yp is None:
+        yp = torch.empty((T * topk, H), dtype=torch.float16, device=x.device)
+    if workspace is None:
+        workspace = torch.empty(lib().qw_moe_w4a8_workspace_size(T, topk, H, F), dtype=torch.uint8, device=x.device)
+    _dev(x, h, yp, workspace, *gate, *up, *down)
+    rc = lib().qw_moe_experts_w4a8(*[_ptr(t) for t in (*gate, *up, *down)], E, H, F, _ptr(route.offsets),
+                                   _ptr(route.pair_tok), _ptr(route.tile_e), _ptr(route.tile_m0), _ptr(route.n_tiles),
+                                   _ptr(x), int(_is_f16(x, x_f16)), T, topk, _ptr(h), _ptr(yp), _ptr(workspace),
+                                   workspace.numel(), _stream())
+    _check(rc, "qw_moe_experts_w4a8")
     return h, yp
 
 
