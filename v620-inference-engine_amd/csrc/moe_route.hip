@@ -20,7 +20,10 @@
 // device evaluates glibc's algorithm itself (expf_glibc below) and matches the
 // CPU path bit for bit: selection, order and weights.
 
+#include <type_traits>
+
 #include "q4_common.cuh"
+
 #include "q4_kernels.hpp"
 
 namespace qwq4 {
@@ -156,10 +159,11 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t x) {
 // they order like p) over the complement of the expert index, so one 64-bit
 // maximum picks the largest p and, among equal p, the lowest index. Lane
 // j < k ends with the j-th selection.
+// ex: the lane's expf table entry, loaded by the caller at kernel start (its
+// memory latency then overlaps the logits' instead of following them).
 template <int PER, class LogitFn>
-__device__ __forceinline__ void topk_wave(LogitFn logit, int E, int k, int lane, int32_t *te, float *tw) {
-    ExpfGlibc ex;
-    ex.load(lane);
+__device__ __forceinline__ void topk_wave(const ExpfGlibc &ex, LogitFn logit, int E, int k, int lane, int32_t *te,
+                                          float *tw) {
     float v[PER];
     float mx = -INFINITY;
 #pragma unroll
@@ -205,8 +209,10 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict
                                                          int32_t *__restrict__ top_e, float *__restrict__ top_w) {
     const int t = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     if (t >= T) return;
+    ExpfGlibc ex;
+    ex.load(lane);
     const float *l = logits + int64_t(t) * E;
-    topk_wave<PER>([&](int i) { return l[i]; }, E, k, lane, top_e + int64_t(t) * k, top_w + int64_t(t) * k);
+    topk_wave<PER>(ex, [&](int i) { return l[i]; }, E, k, lane, top_e + int64_t(t) * k, top_w + int64_t(t) * k);
 }
 
 // ---- slots of a larger batch: one block per 64-token chunk
@@ -294,7 +300,7 @@ __global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a) {
 // The whole routing of a decode batch by one block of 1024 threads; logit(t)
 // gives token t's row loader (expert index -> logit).
 template <int PER, class RowFn>
-__device__ __forceinline__ void route_small_body(const RouteArgs &a, RowFn logit_row) {
+__device__ __forceinline__ void route_small_body(const RouteArgs &a, const ExpfGlibc &ex, RowFn logit_row) {
     __shared__ int32_t s_te[64 * 64];
     __shared__ unsigned long long s_mask[1024];
     __shared__ int32_t s_off[1024];
@@ -303,7 +309,7 @@ __device__ __forceinline__ void route_small_body(const RouteArgs &a, RowFn logit
     const int T = a.T, E = a.E, k = a.topk, P = T * k;
     if (tid < E) s_mask[tid] = 0ull;
     for (int t = wave; t < T; t += 16)
-        topk_wave<PER>(logit_row(t), E, k, lane, s_te + t * k, a.top_w + int64_t(t) * k);
+        topk_wave<PER>(ex, logit_row(t), E, k, lane, s_te + t * k, a.top_w + int64_t(t) * k);
     __syncthreads();
     for (int i = tid; i < P; i += blockDim.x) {
         a.top_e[i] = s_te[i];
@@ -353,7 +359,9 @@ __device__ __forceinline__ void route_small_body(const RouteArgs &a, RowFn logit
 
 template <int PER>
 __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
-    route_small_body<PER>(a, [&](int t) {
+    ExpfGlibc ex;
+    ex.load(threadIdx.x % WAVE);
+    route_small_body<PER>(a, ex, [&](int t) {
         const float *l = a.logits + int64_t(t) * a.E;
         return [l](int i) { return l[i]; };
     });
@@ -385,6 +393,8 @@ template <int PER>
 __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterArgs r) {
     extern __shared__ __align__(16) unsigned char smem[];  // x slice, [T][kl]
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    ExpfGlibc ex;
+    ex.load(lane);
     const int T = a.T, E = a.E, H = r.H, kc = r.kl / 8, k0 = blockIdx.y * r.kl;
     const int e = blockIdx.x * 16 + wave;
     // kl <= 512: each lane owns at most one run of 8 weights of its expert's
@@ -441,7 +451,7 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
         return v;
     };
     auto route = [&]() {
-        route_small_body<PER>(a, [&](int t) {
+        route_small_body<PER>(a, ex, [&](int t) {
             const float *l = r.logits + int64_t(t) * E;
             return [l](int i) { return ld_agent(l + i); };
         });
@@ -470,9 +480,118 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
     route();
 }
 
+// ---- decode batches (T <= 8): full-K router blocks, one hand-off
+// Block b computes the complete fp32 logits of experts EPB b .. EPB b + EPB - 1
+// for every token: WPE waves per expert split K into WPE contiguous parts,
+// each lane sums runs of 8 weights (all of its weight loads requested before
+// the activations are staged), the wave reduces, and the WPE part sums are
+// added in part order. With no K split across blocks there is no partial-sum
+// pass, and only E / EPB blocks count into the hand-off counter (device-scope
+// atomics on one counter serialise at about 18 ns each). The last block reads
+// every logit once into LDS and routes from there.
+template <int PER, int EPB, int WPE, int NCH>
+__global__ __launch_bounds__(EPB *WPE *WAVE) void router_full_kernel(RouteArgs a, RouterArgs r) {
+    extern __shared__ __align__(16) unsigned char smem[];  // x [T][H] | part sums [T][EPB][WPE] | logits [T][E]
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int T = a.T, E = a.E, H = r.H, kw = H / WPE, nch = kw / 8;
+    const int el = wave / WPE, wp = wave % WPE, e = min(int(blockIdx.x) * EPB + el, E - 1);
+    ExpfGlibc ex;
+    ex.load(lane);
+    // the lane's runs of 8 weights: chunks lane, lane + 64, .. of its part
+    float4 w[NCH][2];
+    const float *wr = r.w + int64_t(e) * H + wp * kw;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        const int c = min(lane + j * WAVE, nch - 1);
+        w[j][0] = *reinterpret_cast<const float4 *>(wr + c * 8);
+        w[j][1] = *reinterpret_cast<const float4 *>(wr + c * 8 + 4);
+    }
+    uint4 *xs = reinterpret_cast<uint4 *>(smem);
+    const int xc = H / 8;
+    for (int i = tid; i < T * xc; i += blockDim.x) {
+        const int t = i / xc, c = i - t * xc;
+        xs[i] = *reinterpret_cast<const uint4 *>(r.x + int64_t(t) * H + c * 8);
+    }
+    float *part = reinterpret_cast<float *>(xs + T * xc);  // [T][EPB][WPE]
+    float *sl = part + T * EPB * WPE;                     // [T][E] (last block)
+    __syncthreads();
+    auto dots = [&](auto cvt) {
+        for (int t = 0; t < T; ++t) {
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < NCH; ++j) {
+                if (lane + j * WAVE < nch) {
+                    const uint4 v = xs[t * xc + wp * (kw / 8) + lane + j * WAVE];
+                    s = fmaf(w[j][0].x, cvt(uint16_t(v.x)), s);
+                    s = fmaf(w[j][0].y, cvt(uint16_t(v.x >> 16)), s);
+                    s = fmaf(w[j][0].z, cvt(uint16_t(v.y)), s);
+                    s = fmaf(w[j][0].w, cvt(uint16_t(v.y >> 16)), s);
+                    s = fmaf(w[j][1].x, cvt(uint16_t(v.z)), s);
+                    s = fmaf(w[j][1].y, cvt(uint16_t(v.z >> 16)), s);
+                    s = fmaf(w[j][1].z, cvt(uint16_t(v.w)), s);
+                    s = fmaf(w[j][1].w, cvt(uint16_t(v.w >> 16)), s);
+                }
+            }
+            const float v = wave_sum_f32(s);
+            if (lane == 0) part[(t * EPB + el) * WPE + wp] = v;
+        }
+    };
+    if (r.x_f16) dots([](uint16_t b) { return f16_bits_to_f32(b); });
+    else dots([](uint16_t b) { return bf16_bits_to_f32(b); });
+    __syncthreads();
+    for (int i = tid; i < T * EPB; i += blockDim.x) {
+        const int t = i / EPB, j = i - t * EPB, ee = int(blockIdx.x) * EPB + j;
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < WPE; ++q) v += part[i * WPE + q];
+        if (ee < E) st_agent(r.logits + int64_t(t) * E + ee, v);
+    }
+    if (!count_last_block(r.counter, int(gridDim.x))) return;
+    for (int i = tid; i < T * E; i += blockDim.x) sl[i] = ld_agent(r.logits + i);
+    __syncthreads();
+    route_small_body<PER>(a, ex, [&](int t) {
+        const float *l = sl + t * E;
+        return [l](int i) { return l[i]; };
+    });
+}
+
+// The full-K router serves T <= 8 (activations staged whole) and H up to
+// 8192 (runs of 8 weights: at most 8 per lane with 2 waves per expert)
+// (E <= 512: the routing's per-lane logits then fit the 1024-thread block's
+// registers)
+bool router_full_ok(int T, int E, int H) { return T <= 8 && H % 1024 == 0 && H <= 8192 && E <= 512 && E % 8 == 0; }
+
+static void launch_router_full(const RouteArgs &a, const RouterArgs &r, hipStream_t s) {
+    constexpr int EPB = 8, WPE = 2;
+    const int per = (a.E + WAVE - 1) / WAVE;
+    const size_t lds = size_t(a.T) * r.H * 2 + size_t(a.T) * EPB * WPE * 4 + size_t(a.T) * a.E * 4;
+    const unsigned grid = unsigned((a.E + EPB - 1) / EPB);
+    const int nch = r.H / WPE / 8;  // runs of 8 per wave
+    auto go = [&](auto kern) {
+        if (lds > 48 * 1024)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      int(lds));
+        kern<<<grid, EPB * WPE * WAVE, lds, s>>>(a, r);
+    };
+    auto pick = [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+        if (per <= 1) go(router_full_kernel<1, EPB, WPE, NC>);
+        else if (per <= 2) go(router_full_kernel<2, EPB, WPE, NC>);
+        else if (per <= 4) go(router_full_kernel<4, EPB, WPE, NC>);
+        else go(router_full_kernel<8, EPB, WPE, NC>);
+    };
+    if (nch <= 2 * WAVE) pick(std::integral_constant<int, 2>());
+    else if (nch <= 4 * WAVE) pick(std::integral_constant<int, 4>());
+    else pick(std::integral_constant<int, 8>());
+}
+
 size_t router_lds_bytes(int T, int kl) { return size_t(T) * kl * 2; }
 
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s) {
+    if (router_full_ok(a.T, a.E, r.H)) {
+        launch_router_full(a, r, s);
+        return;
+    }
     // callers guarantee kl in {128, 512}, H % kl == 0 and T <= 64
     const int per = (a.E + WAVE - 1) / WAVE;
     const dim3 grid(unsigned((a.E + 15) / 16), unsigned(r.H / r.kl));
