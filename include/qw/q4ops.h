@@ -224,7 +224,10 @@ int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_
  *   yp[p] = fp16(D_e . h[p])                     fp16 [T*k][H]
  * (finite values beyond +-65504 saturate). Weights tiled as for
  * qw_moe_experts_grouped; tile list from qw_moe_route with
- * tile_m = qw_moe_w4a8_tile_m() (64-slot tiles). x [T][H] fp16 (x_f16 = 1,
+ * tile_m = qw_moe_w4a8_tile_m() (mixed 256 / 128 / 64-slot tiles, as for the
+ * fp16 grouped path). The int32 sums run per 128-wide group (the reference:
+ * per 64-wide step; the fp32 rescale roundings differ by about 1e-7 of the
+ * result). x [T][H] fp16 (x_f16 = 1,
  * the reference's rows) or bf16. H and F multiples of 128. workspace: at
  * least qw_moe_w4a8_workspace_size(T, topk, H, F) bytes, 256-byte aligned
  * (the quantised rows and their scales, the reference's q8 / q8s). */

@@ -3,22 +3,33 @@
 // src/kernels/moe_w4a8.hip:13-215; selected by the engine with q8 scratch,
 // src/engine/prefill.hip:333), on the gfx950 int8 MFMA.
 //
-// Arithmetic (as the reference's): activation rows are quantised per (row,
-// 128-group), sc = max|x| / 127, q = rint(x * (1 / sc)); weights are widened
-// exactly to int8 q - z; per 64-wide K step the int8 products are summed
-// exactly in int32, then acc = fma(float(I) * s_w, s_x, acc) in fp32, steps
-// in order. Gate/up writes h = fp16(silu(g) * u); h rows are quantised the
-// same way for the down projection, which writes yp in fp16.
+// Arithmetic: activation rows are quantised per (row, 128-group) as the
+// reference does, sc = max|x| / 127, q = rint(x * (1 / sc)); weights are
+// widened exactly to int8 q - z; per 128-wide K group the int8 products are
+// summed exactly in int32 (v_mfma_i32_32x32x32_i8), then
+// acc = fma(float(I) * s_w, s_x, acc) in fp32, groups in order. The
+// reference sums per 64-wide step and rescales each step with the same group
+// scales; float(I) is exact either way (|I| < 2^24), so the two differ only
+// in the fp32 roundings of the rescale (about 1e-7 of the result). Gate/up
+// writes h = fp16(silu(g) * u); h rows are quantised the same way for the
+// down projection, which writes yp in fp16.
 //
-// Schedule. Work is the routing tile list with tiles of 64 slots
-// (qw_moe_route with tile_m = 64). A block (4 waves) takes one list entry and
-// 64 h columns (gate/up: 64 gate and the same 64 up rows) or 128 down rows.
-// K runs in 64-wide steps through a double-buffered LDS: the next step's
-// activation pieces and q4 weight entries are loaded into registers before
-// the current step's MFMAs and written to LDS after them (weights widened to
-// int8 on the way). Each wave holds two 32x32 tiles: one v_mfma_i32_32x32x32_i8
-// pair per tile and step, then the step's rescale (three VALU operations per
-// accumulator: the VALU, not the matrix core, bounds this kernel).
+// Schedule (the fp16 core's, q4_gemm_core.cuh, in int8): work is the routing
+// tile list (mixed 256 / 128 / 64-slot tiles, as for the fp16 grouped path);
+// a block of 8 waves takes one entry and 128 weight rows (gate/up: 64 gate
+// and the same 64 up rows, interleaved by 32). K runs in stages of 128 (one
+// scale group) through a double-buffered LDS; an int8 row of a stage is 128
+// bytes, the fp16 core's row geometry, so its buffers, swizzle and direct
+// loads serve unchanged:
+//   waves 0-3 move the next stage's quantised A rows global -> LDS by direct
+//     loads, and the rows' activation scales of that group;
+//   waves 4-7 (two threads per weight row) load the q4 entries two stages
+//     ahead and widen them into LDS between the MFMAs.
+// Each wave holds MT 32x32 tiles (128-slot blocks: 2, 64: 1; a 256-slot
+// list entry runs as two 128-slot blocks): per stage 4 int8 MFMAs per tile
+// into int32, then the rescale (three VALU operations per accumulator).
+#include <type_traits>
+
 #include "q4_gemm_core.cuh"
 #include "q4_kernels.hpp"
 
@@ -27,10 +38,9 @@ namespace qwq4 {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int W8_TILE = 64;  // slots per tile (the routing's tile_m)
-constexpr int W8_STEP = 64;  // K per step
+constexpr int W8_TILE_M = -64;  // the routing's mixed 256 / 128 / 64-slot tiles
 
-int moe_w4a8_tile_m() { return W8_TILE; }
+int moe_w4a8_tile_m() { return W8_TILE_M; }
 
 // ------------------------------------------------------------ quantiser
 // One wave per (row, group of 128): two elements per lane.
@@ -72,110 +82,9 @@ __device__ __forceinline__ uint2 widen8(uint32_t w, uint32_t zz) {
     return make_uint2(lo, hi);
 }
 
-// LDS tile rows of 64 int8 (4 chunks of 16 bytes); chunk c of row r sits at
-// c ^ ((r >> 1) & 3): the 8 lanes of a b128 read pass (8 consecutive rows,
-// one chunk) then cover all 8 16-byte bank groups of a 128-byte line.
-__device__ __forceinline__ int w8_off(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
-
 __device__ __forceinline__ i32x16 mfma_i8(const uint4 &a, const uint4 &b, const i32x16 &c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
                                                  0);
-}
-
-// Weight rows of a block: 128 rows of the tiled format, one thread pair per
-// row (thread t loads row t / 2: the entry of quarter 2 (s % 2) + t % 2 of
-// step s, 32 K).
-struct W8B {
-    BRow row;
-    int half;
-    __device__ __forceinline__ uint4 load(int s) const {
-        const int g = s / 2;
-        return row.w[g * 64 + ((s % 2) * 2 + half) * 16];
-    }
-    __device__ __forceinline__ uint32_t zz(int s) const {  // the step's zero in every byte
-        if (!row.z) return 0x08080808u;
-        const int g = s / 2;
-        return ((row.z[(g >> 2) * 8] >> (row.zs + 4 * (g & 3))) & 0xfu) * 0x01010101u;
-    }
-};
-
-// The main loop of one 64-slot tile by 128 weight rows. Slot i of the tile
-// reads quantised row arow(i) (i < M); tile row r is weight row brow(r) (a
-// BRow). Wave (wm, wn) forms two 32x32 tiles t = 0, 1: slots 32 wm .. and
-// tile rows tb[t] .. (lane column tb[t] + lane % 32), rescaled per step with
-// the scale of its column and those of its 16 slots (staged in LDS per
-// group). acc[t] ends in the 32x32 MFMA result layout.
-template <class ARowFn, class BRowFn>
-__device__ __forceinline__ void w4a8_tile(const int8_t *q8, const float *sx, int K, int M, ARowFn arow, BRowFn brow,
-                                          const int (&tb)[2], f32x16 (&acc)[2]) {
-    __shared__ __align__(16) int8_t la[2][W8_TILE * W8_STEP], lb[2][128 * W8_STEP];
-    __shared__ __align__(16) float lsx[W8_TILE];
-    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, l32 = lane % 32, lh = lane / 32;
-    const int wm = wave / 2, G = K / QGROUP, steps = K / W8_STEP;
-    // this thread's activation piece (slot row tid / 4, chunk tid % 4), the
-    // slot whose scales it stages (tid < 64), and its weight row
-    const int ar = tid / 4, ac = tid % 4, br = tid / 2, bh = tid % 2;
-    const int8_t *asrc = q8 + int64_t(arow(min(ar, M - 1))) * K + ac * 16;
-    const float *sxr = sx + int64_t(arow(min(tid % W8_TILE, M - 1))) * G;
-    const W8B wb{brow(br), bh};
-    const BRow sc0 = brow(tb[0] + l32), sc1 = brow(tb[1] + l32);
-    uint4 an, bn;
-    uint32_t zn;
-    auto load = [&](int s) {
-        an = *reinterpret_cast<const uint4 *>(asrc + s * W8_STEP);
-        bn = wb.load(s);
-        zn = wb.zz(s);
-    };
-    auto commit = [&](int p) {
-        *reinterpret_cast<uint4 *>(&la[p][w8_off(ar, ac)]) = an;
-        const uint2 x0 = widen8(bn.x, zn), x1 = widen8(bn.y, zn), x2 = widen8(bn.z, zn), x3 = widen8(bn.w, zn);
-        *reinterpret_cast<uint4 *>(&lb[p][w8_off(br, 2 * bh)]) = make_uint4(x0.x, x0.y, x1.x, x1.y);
-        *reinterpret_cast<uint4 *>(&lb[p][w8_off(br, 2 * bh + 1)]) = make_uint4(x2.x, x2.y, x3.x, x3.y);
-    };
-    acc[0] = f32x16{};
-    acc[1] = f32x16{};
-    load(0);
-    commit(0);
-    float sxv[16];
-    for (int s = 0; s < steps; ++s) {
-        const int p = s & 1, g = s / 2;
-        if (s % 2 == 0 && tid < W8_TILE) lsx[tid] = sxr[g];
-        if (s + 1 < steps) load(s + 1);
-        __syncthreads();  // step s's tiles and the group's scales are in LDS
-        if (s % 2 == 0) {
-            // the lane's 16 slots 32 wm + 8 (r / 4) + 4 lh + r % 4
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float4 v = *reinterpret_cast<const float4 *>(&lsx[32 * wm + 8 * j + 4 * lh]);
-                sxv[4 * j] = v.x;
-                sxv[4 * j + 1] = v.y;
-                sxv[4 * j + 2] = v.z;
-                sxv[4 * j + 3] = v.w;
-            }
-        }
-        const float sw[2] = {f16_bits_to_f32(sc0.s[(g >> 2) * 64 + (g & 3)]),
-                             f16_bits_to_f32(sc1.s[(g >> 2) * 64 + (g & 3)])};
-        uint4 af[2], bf[2][2];
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {  // two 32-K halves of the step; lane half lh takes 16 K of each
-            af[k] = *reinterpret_cast<const uint4 *>(&la[p][w8_off(32 * wm + l32, 2 * k + lh)]);
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-                bf[t][k] = *reinterpret_cast<const uint4 *>(&lb[p][w8_off(tb[t] + l32, 2 * k + lh)]);
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            i32x16 ip = i32x16{};
-            ip = mfma_i8(af[0], bf[t][0], ip);
-            ip = mfma_i8(af[1], bf[t][1], ip);
-            // acc += float(I) * s_w * s_x, the last multiply-add fused as the
-            // reference's compiler contracts it (moe_w4a8.hip:110-116)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[t][r] = __builtin_fmaf(float(ip[r]) * sw[t], sxv[r], acc[t][r]);
-        }
-        __syncthreads();  // every read of buffer p is done before it is refilled
-        if (s + 1 < steps) commit(p ^ 1);
-    }
 }
 
 static __device__ __forceinline__ uint16_t f16_sat(float v) {
@@ -185,71 +94,289 @@ static __device__ __forceinline__ uint16_t f16_sat(float v) {
 // the reference's silu: x * (1 / (1 + exp(-x))) (src/kernels/common.cuh:94-99)
 static __device__ __forceinline__ float silu_ref(float g) { return g * (1.f / (1.f + __expf(-g))); }
 
-// The 64-slot tile of list entry blockIdx.y: expert, first slot, real slots.
-struct W8Entry {
-    int e, base, M;
+constexpr int W8_BN = 128;  // weight rows per block
+constexpr int W8_K = 128;   // K per stage (one scale group)
+
+// activation scales of a stage's tile rows (waves 0-3 fill them), two stages
+static __shared__ __align__(16) float w8_lsx[2][256];
+
+// Block shapes: BM = 128 or 64 slot rows (a 256-slot list entry runs as two
+// 128-slot halves, blockIdx.z); waves 2 (slots) x 4 (weight rows), each MT
+// 32-row slot tiles by one 32-row weight tile.
+template <int BM>
+struct W8Shape {
+    static_assert(BM == 128 || BM == 64, "128 or 64 slot rows");
+    static constexpr int MT = BM / 64;  // 32-row tiles per wave along the slots
+    static constexpr int NT = 1;        // 32-row tiles per wave along the weight rows
+    static constexpr int WN = 4;        // waves along the weight rows
 };
-static __device__ __forceinline__ bool w8_entry(const int32_t *offsets, const int32_t *tile_e,
-                                                const int32_t *tile_m0, const int32_t *n_tiles, W8Entry &t) {
+
+// acc[mi][nj] += A (BM slot rows, quantised; ap[j]: row a_load_row(j); sxr:
+// the scale row of tile row tid, for tid < BM) x W^T (128 weight rows; this
+// B-role thread's row b, its K half bh; scale rows sw_row[nj] of the lane's
+// columns), K columns (a multiple of 128).
+// (USE tags the caller, 0 gate/up, 1 down: each call site instantiates its own
+// specialization; the host compilation pass rejects a second call site of a
+// shared one)
+template <int BM, bool HAS_Z, int USE, class ApT, class SwT, class AccT>
+__device__ __forceinline__ void w8_tile(const ApT &ap, const float *sxr, const BRow &b, const SwT &sw_row, int K,
+                                        AccT &acc) {
+    using S = W8Shape<BM>;
+    constexpr int MT = S::MT, NT = S::NT;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+    const int nk = K / W8_K, G = K / QGROUP;
+    auto bufA = [&](int i) { return i ? lds_a1 : lds_a0; };
+    auto bufB = [&](int i) { return i ? lds_b1 : lds_b0; };
+    const int mi0 = (wave / S::WN) * MT, nj0 = (wave % S::WN) * NT, l32 = lane % 32, lh = lane / 32;
+    i32x16 ip[MT][NT];
+
+    // MFMAs of one stage (4 slabs of 32 K) and the group's rescale; extra(q)
+    // runs after slab q (the B role's widening)
+    auto compute = [&](const unsigned char *a, const unsigned char *bb, const float *lsx, int g, auto extra) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < NT; ++j) ip[i][j] = i32x16{};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint4 af[MT], bf[NT];
+#pragma unroll
+            for (int i = 0; i < MT; ++i) af[i] = *reinterpret_cast<const uint4 *>(a + swz((mi0 + i) * 32 + l32, 2 * q + lh));
+#pragma unroll
+            for (int j = 0; j < NT; ++j) bf[j] = *reinterpret_cast<const uint4 *>(bb + swz((nj0 + j) * 32 + l32, 2 * q + lh));
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j) ip[i][j] = mfma_i8(af[i], bf[j], ip[i][j]);
+            extra(q);
+        }
+        float sw[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) sw[j] = f16_bits_to_f32(sw_row[j][(g >> 2) * 64 + (g & 3)]);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            float sx[16];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float4 v = *reinterpret_cast<const float4 *>(&lsx[(mi0 + i) * 32 + 8 * u + 4 * lh]);
+                sx[4 * u] = v.x;
+                sx[4 * u + 1] = v.y;
+                sx[4 * u + 2] = v.z;
+                sx[4 * u + 3] = v.w;
+            }
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(float(ip[i][j][r]) * sw[j], sx[r], acc[i][j][r]);
+        }
+    };
+
+    if (wave < G_ROLE) {
+        // A role: the quantised rows of stage ks + 1 by direct loads, and the
+        // group's activation scales of the tile rows
+        auto issue_a = [&](int ks, unsigned char *dst) {
+            const int k0 = ks * W8_K, wa = wave % G_ROLE;
+#pragma unroll
+            for (int j = 0; j < BM / 32; ++j) {
+                const int rb = (j * G_ROLE + wa) * 8;
+                const int r = rb + lane / 8, c = (lane % 8) ^ swz_x(r);
+                __builtin_amdgcn_global_load_lds(ap[j] + k0 + c * 16, dst + rb * 128, 16, 0, 0);
+            }
+        };
+        issue_a(0, bufA(0));
+        if (tid < BM) w8_lsx[0][tid] = sxr[0];
+        __syncthreads();
+        auto stage = [&](int ks, int p) {
+            const int kn = min(ks + 1, nk - 1);
+            issue_a(kn, bufA(p ^ 1));
+            const float sv = sxr[kn];
+            compute(bufA(p), bufB(p), w8_lsx[p], ks, [](int) {});
+            if (tid < BM) w8_lsx[p ^ 1][tid] = sv;
+            lds_barrier();
+        };
+        int ks = 0;
+        for (; ks + 1 < nk; ks += 2) {
+            stage(ks, 0);
+            stage(ks + 1, 1);
+        }
+        if (ks < nk) stage(ks, 0);
+    } else {
+        // weight role: row (tid - 256) / 2, K half bh of each stage
+        const int br = (tid - G_THREADS / 2) / 2, bh = tid % 2;
+        (void)G;
+        struct BRaw {
+            uint4 w0, w1;
+            uint32_t z;
+        };
+        auto issue_b = [&](int ks, BRaw &r) {
+            ks = min(ks, nk - 1);  // past the end: a valid, unused load keeps the code branch-free
+            r.w0 = b.w[ks * 64 + (2 * bh) * 16];
+            r.w1 = b.w[ks * 64 + (2 * bh + 1) * 16];
+            if constexpr (HAS_Z) r.z = b.z[(ks >> 2) * 8];
+        };
+        // entry e (32 K) of the raw weights -> int8 chunks 4 bh + 2 e, + 1
+        auto commit_b = [&](int ks, const BRaw &r, unsigned char *dst, int e) {
+            uint32_t zw = HAS_Z ? r.z : 0u;
+            asm volatile("" : "+v"(zw));
+            const uint32_t zz = HAS_Z ? ((zw >> (b.zs + 4 * (ks & 3))) & 0xfu) * 0x01010101u : 0x08080808u;
+            const uint4 w = e ? r.w1 : r.w0;
+            const uint2 x0 = widen8(w.x, zz), x1 = widen8(w.y, zz), x2 = widen8(w.z, zz), x3 = widen8(w.w, zz);
+            *reinterpret_cast<uint4 *>(dst + swz(br, 4 * bh + 2 * e)) = make_uint4(x0.x, x0.y, x1.x, x1.y);
+            *reinterpret_cast<uint4 *>(dst + swz(br, 4 * bh + 2 * e + 1)) = make_uint4(x2.x, x2.y, x3.x, x3.y);
+        };
+        BRaw rs[2];
+        issue_b(0, rs[0]);
+        commit_b(0, rs[0], bufB(0), 0);
+        commit_b(0, rs[0], bufB(0), 1);
+        issue_b(1, rs[1]);
+        __syncthreads();
+        auto stage = [&](int ks, BRaw &mine, const BRaw &next, int p) {
+            const bool more = ks + 1 < nk;
+            issue_b(ks + 2, mine);
+            compute(bufA(p), bufB(p), w8_lsx[p], ks, [&](int q) {
+                if (more && (q == 1 || q == 3)) commit_b(ks + 1, next, bufB(p ^ 1), q / 2);
+            });
+            lds_barrier();
+        };
+        int ks = 0;
+        for (; ks + 1 < nk; ks += 2) {
+            stage(ks, rs[0], rs[1], 0);
+            stage(ks + 1, rs[1], rs[0], 1);
+        }
+        if (ks < nk) stage(ks, rs[0], rs[1], 0);
+    }
+}
+
+// The block's slots: list entry blockIdx.y (expert, first slot), half
+// blockIdx.z of a 256-slot entry; real slots M of a block of `rows`.
+struct W8Entry {
+    int e, base, M, rows;
+};
+static __device__ __forceinline__ bool w8_entry(const W8Args &a, W8Entry &t) {
     const int tile = blockIdx.y;
-    if (tile >= *n_tiles) return false;
-    t.e = tile_e[tile];
-    const int m0 = tile_m0[tile];
-    t.base = offsets[t.e] + m0;
-    t.M = min(W8_TILE, offsets[t.e + 1] - offsets[t.e] - m0);
+    if (tile >= *a.n_tiles) return false;
+    t.e = a.tile_e[tile];
+    const int m0 = a.tile_m0[tile], rem = a.offsets[t.e + 1] - a.offsets[t.e] - m0;
+    const int rows = tile_rows(rem, W8_TILE_M), half = int(blockIdx.z);
+    if (rows <= 128 && half > 0) return false;
+    t.rows = rows > 128 ? 128 : rows;
+    t.base = a.offsets[t.e] + m0 + half * 128;
+    t.M = min(t.rows, rem - half * 128);
     return true;
 }
 
-// gate/up: tile rows 0-63 are gate rows j0 .., rows 64-127 the same up rows;
-// wave (wm, wn) holds gate (t = 0) and up (t = 1) of columns j0 + 32 wn ..;
-// h = fp16(silu(g) * u) (finite values beyond the fp16 range saturate).
-__global__ __launch_bounds__(256) void moe_gate_up_w4a8_kernel(W8Args a) {
-    W8Entry t;
-    if (!w8_entry(a.offsets, a.tile_e, a.tile_m0, a.n_tiles, t)) return;
-    const int j0 = blockIdx.x * 64, wave = threadIdx.x / WAVE, wm = wave / 2, wn = wave % 2;
-    const int lane = threadIdx.x % WAVE, l32 = lane % 32, lh = lane / 32, G = a.H / QGROUP;
-    const int32_t *pt = a.pair_tok + t.base;
+// gate/up tile: block rows r of the 128: 32-row group r / 32 is gate when
+// even, up when odd, for h columns j0 + 32 (r / 64) + r % 32.
+template <int BM, bool HAS_Z>
+__device__ __forceinline__ void gate_up_w8(const W8Args &a, const W8Entry &t) {
+    using S = W8Shape<BM>;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, l32 = lane % 32, lh = lane / 32;
+    const int j0 = blockIdx.x * 64, G = a.H / QGROUP;
     const int64_t eF = int64_t(t.e) * a.F;
-    const int tb[2] = {32 * wn, 64 + 32 * wn};
-    f32x16 acc[2];
-    w4a8_tile(
-        a.qx, a.sx, a.H, t.M, [&](int i) { return pt[i]; },
-        [&](int r) {
-            const int64_t row = eF + min(j0 + r % 64, a.F - 1);
-            return r < 64 ? BRow(a.gw, a.gs, a.gz, row, G) : BRow(a.uw, a.us, a.uz, row, G);
-        },
-        tb, acc);
-    const int j = j0 + 32 * wn + l32;
+    auto brow = [&](int r) {
+        const int64_t row = eF + min(j0 + (r / 64) * 32 + r % 32, a.F - 1);
+        return ((r / 32) & 1) ? BRow(a.uw, a.us, a.uz, row, G) : BRow(a.gw, a.gs, a.gz, row, G);
+    };
+    const int32_t *pt = a.pair_tok + t.base;
+    const int8_t *ap[BM / 32];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const int m = 32 * wm + 8 * (q / 4) + 4 * lh + q % 4;
-        if (m < t.M && j < a.F) a.h[int64_t(t.base + m) * a.F + j] = f16_sat(silu_ref(acc[0][q]) * acc[1][q]);
+    for (int j = 0; j < BM / 32; ++j) ap[j] = a.qx + int64_t(pt[min(a_load_row(j), t.M - 1)]) * a.H;
+    const BRow b = brow(max(0, min((tid - G_THREADS / 2) / 2, W8_BN - 1)));
+    const int mi0 = (wave / S::WN) * S::MT, nj0 = (wave % S::WN) * S::NT;
+    const uint16_t *swr[S::NT];
+#pragma unroll
+    for (int j = 0; j < S::NT; ++j) swr[j] = brow((nj0 + j) * 32 + l32).s;
+    // the scale row a thread t < BM stages: its slot's token
+    const float *sxp = a.sx + int64_t(pt[min(tid, t.M - 1)]) * G;
+    f32x16 acc[S::MT][S::NT];
+#pragma unroll
+    for (int i = 0; i < S::MT; ++i)
+#pragma unroll
+        for (int j = 0; j < S::NT; ++j) acc[i][j] = f32x16{};
+    w8_tile<BM, HAS_Z, 0>(ap, sxp, b, swr, a.H, acc);
+    // h = fp16(silu(g) * u): tile nj holds gate (nj even) or up (odd) of
+    // columns j0 + 32 (nj / 2) + l32
+    auto put = [&](int i, int col, const f32x16 &g, const f32x16 &u) {
+        const int j = j0 + col + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = (mi0 + i) * 32 + 8 * (r / 4) + 4 * lh + r % 4;
+            if (m < t.M && j < a.F) a.h[int64_t(t.base + m) * a.F + j] = f16_sat(silu_ref(g[r]) * u[r]);
+        }
+    };
+    {
+        // gate and up of a column group sit in waves wn and wn + 1: the up
+        // wave hands its accumulators over through LDS (free after the loop)
+        float *xb = reinterpret_cast<float *>(lds_a0) + (wave / 2) * (S::MT * 16 * WAVE);
+        if (nj0 & 1) {
+#pragma unroll
+            for (int i = 0; i < S::MT; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) xb[(i * 16 + r) * WAVE + lane] = acc[i][0][r];
+        }
+        __syncthreads();
+        if (!(nj0 & 1)) {
+#pragma unroll
+            for (int i = 0; i < S::MT; ++i) {
+                f32x16 u;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) u[r] = xb[(i * 16 + r) * WAVE + lane];
+                put(i, (nj0 / 2) * 32, acc[i][0], u);
+            }
+        }
     }
 }
 
-// down: tile rows are down rows n0 .. n0 + 127 of expert e; wave (wm, wn)
-// holds rows n0 + 64 wn + 32 t ..; yp = fp16 (saturating).
-__global__ __launch_bounds__(256) void moe_down_w4a8_kernel(W8Args a) {
+template <bool HAS_Z>
+__global__ __launch_bounds__(G_THREADS) void moe_gate_up_w4a8_kernel(W8Args a) {
     W8Entry t;
-    if (!w8_entry(a.offsets, a.tile_e, a.tile_m0, a.n_tiles, t)) return;
-    const int n0 = blockIdx.x * 128, wave = threadIdx.x / WAVE, wm = wave / 2, wn = wave % 2;
-    const int lane = threadIdx.x % WAVE, l32 = lane % 32, lh = lane / 32, G = a.F / QGROUP;
+    if (!w8_entry(a, t)) return;
+    if (t.rows == 128) gate_up_w8<128, HAS_Z>(a, t);
+    else gate_up_w8<64, HAS_Z>(a, t);
+}
+
+// down tile: block rows are down rows n0 .. n0 + 127 of expert e
+template <int BM, bool HAS_Z>
+__device__ __forceinline__ void down_w8(const W8Args &a, const W8Entry &t) {
+    using S = W8Shape<BM>;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, l32 = lane % 32, lh = lane / 32;
+    const int n0 = blockIdx.x * W8_BN, G = a.F / QGROUP;
     const int64_t eH = int64_t(t.e) * a.H;
-    const int tb[2] = {64 * wn, 64 * wn + 32};
-    f32x16 acc[2];
-    const int base = t.base;
-    w4a8_tile(
-        a.qh, a.sh, a.F, t.M, [&](int i) { return base + i; },
-        [&](int r) { return BRow(a.dw, a.ds, a.dz, eH + min(n0 + r, a.H - 1), G); }, tb, acc);
+    auto brow = [&](int r) { return BRow(a.dw, a.ds, a.dz, eH + min(n0 + r, a.H - 1), G); };
+    const int8_t *ap[BM / 32];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const int n = n0 + tb[tt] + l32;
+    for (int j = 0; j < BM / 32; ++j) ap[j] = a.qh + int64_t(t.base + min(a_load_row(j), t.M - 1)) * a.F;
+    const BRow b = brow(max(0, min((tid - G_THREADS / 2) / 2, W8_BN - 1)));
+    const int mi0 = (wave / S::WN) * S::MT, nj0 = (wave % S::WN) * S::NT;
+    const uint16_t *swr[S::NT];
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int m = 32 * wm + 8 * (q / 4) + 4 * lh + q % 4;
-            if (m < t.M && n < a.H) a.yp[int64_t(base + m) * a.H + n] = f16_sat(acc[tt][q]);
+    for (int j = 0; j < S::NT; ++j) swr[j] = brow((nj0 + j) * 32 + l32).s;
+    const float *sxp = a.sh + int64_t(t.base + min(tid, t.M - 1)) * G;  // the slot of tile row tid
+    f32x16 acc[S::MT][S::NT];
+#pragma unroll
+    for (int i = 0; i < S::MT; ++i)
+#pragma unroll
+        for (int j = 0; j < S::NT; ++j) acc[i][j] = f32x16{};
+    w8_tile<BM, HAS_Z, 1>(ap, sxp, b, swr, a.F, acc);
+#pragma unroll
+    for (int i = 0; i < S::MT; ++i)
+#pragma unroll
+        for (int j = 0; j < S::NT; ++j) {
+            const int n = n0 + (nj0 + j) * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = (mi0 + i) * 32 + 8 * (r / 4) + 4 * lh + r % 4;
+                if (m < t.M && n < a.H) a.yp[int64_t(t.base + m) * a.H + n] = f16_sat(acc[i][j][r]);
+            }
         }
-    }
+}
+
+template <bool HAS_Z>
+__global__ __launch_bounds__(G_THREADS) void moe_down_w4a8_kernel(W8Args a) {
+    W8Entry t;
+    if (!w8_entry(a, t)) return;
+    if (t.rows == 128) down_w8<128, HAS_Z>(a, t);
+    else down_w8<64, HAS_Z>(a, t);
 }
 
 size_t moe_w4a8_workspace_bytes(int T, int topk, int H, int F) {
@@ -271,10 +398,12 @@ void launch_moe_w4a8(W8Args a, const uint16_t *x, int x_f16, int T, int topk, hi
     w += up(P * a.F);
     a.sh = reinterpret_cast<float *>(w);
     launch_quant_rows(x, x_f16, a.H, T, a.H, const_cast<int8_t *>(a.qx), const_cast<float *>(a.sx), s);
-    const int max_tiles = int(P / W8_TILE) + a.E;
-    moe_gate_up_w4a8_kernel<<<dim3(unsigned(a.F / 64), unsigned(max_tiles)), 256, 0, s>>>(a);
+    const int max_tiles = int(P / -W8_TILE_M) + a.E;
+    if (a.gz) moe_gate_up_w4a8_kernel<true><<<dim3(unsigned(a.F / 64), unsigned(max_tiles), 2), G_THREADS, 0, s>>>(a);
+    else moe_gate_up_w4a8_kernel<false><<<dim3(unsigned(a.F / 64), unsigned(max_tiles), 2), G_THREADS, 0, s>>>(a);
     launch_quant_rows(a.h, 1, a.F, int(P), a.F, const_cast<int8_t *>(a.qh), const_cast<float *>(a.sh), s);
-    moe_down_w4a8_kernel<<<dim3(unsigned(a.H / 128), unsigned(max_tiles)), 256, 0, s>>>(a);
+    if (a.dz) moe_down_w4a8_kernel<true><<<dim3(unsigned(a.H / W8_BN), unsigned(max_tiles), 2), G_THREADS, 0, s>>>(a);
+    else moe_down_w4a8_kernel<false><<<dim3(unsigned(a.H / W8_BN), unsigned(max_tiles), 2), G_THREADS, 0, s>>>(a);
 }
 
 }  // namespace qwq4
