@@ -286,12 +286,15 @@ def bench_shared(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8)):
     """The shared expert as the engine runs it (src/engine/decode.hip:99-101):
     fused gate/up/gate-logit GEMV [2F+1][H] on fp16 weights, SwiGLU x sigmoid
     gate, down GEMV [H][F] on fp16 weights; SH_LAYERS layers of their own
-    weights (302 MB, past the Infinity Cache). Bytes: the 16-bit weights."""
+    weights (302 MB, past the Infinity Cache), tiled once at load (qw_w16_tile,
+    outside the timed region). Bytes: the 16-bit weights."""
     g = torch.Generator(device=dev)
     g.manual_seed(500)
     gu = [(torch.randn((2 * SH_FFN + 1, H), generator=g, device=dev) * 0.05).half() for _ in range(SH_LAYERS)]
     dn = [(torch.randn((H, SH_FFN), generator=g, device=dev) * 0.05).half() for _ in range(SH_LAYERS)]
     wbytes = SH_LAYERS * (gu[0].numel() + dn[0].numel()) * 2
+    gu = [qwq4.w16_tile(w) for w in gu]
+    dn = [qwq4.w16_tile(w) for w in dn]
     out = {}
     for M in batches:
         x = torch.randn((M, H), generator=g, device=dev).half()
@@ -301,9 +304,9 @@ def bench_shared(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8)):
 
         def launches():
             for l in range(SH_LAYERS):
-                qwq4.gemv_w16(gu[l], x, M, y=v)
+                qwq4.gemv_w16_tiled(gu[l], 2 * SH_FFN + 1, H, x, M, y=v)
                 qwq4.swiglu_gate(v, SH_FFN, h=hs)
-                qwq4.gemv_w16(dn[l], hs, M, y=y)
+                qwq4.gemv_w16_tiled(dn[l], H, SH_FFN, hs, M, y=y)
 
         step = graphed(torch, launches)
         for _ in range(warmup):

@@ -13,6 +13,7 @@
  *   qw_quant_rows_i8      quant_rows_kernel         src/kernels/moe_w4a8.hip:17-36
  *   qw_moe_combine        gpu::moe_combine_B/T      src/kernels/moe.hpp:42-46
  *   qw_w16_gemv           gpu::gemv_rows (fp16 W)   src/kernels/gemv.hpp:13-14
+ *   qw_w16_gemv_tiled     gpu::gemv_rows (fp16 W)   src/kernels/gemv.hpp:13-14 (weights tiled at load)
  *                         ref::Model::linear        src/ref/ref_model.cpp:86-97
  *   qw_i8_gemv            gpu::gemv_rows_i8         src/kernels/gemv.hpp:15-23
  *   qw_swiglu_gate        gpu::swiglu_T             src/kernels/moe_route.hip:187-197
@@ -103,6 +104,26 @@ int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
  * stride xs as in qw_q4_gemv; y fp32 or bf16 (y_bf16). 1 <= M <= 32. */
 int qw_w16_gemv(const uint16_t *W, int ldw, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N,
                 int K, int M, int accumulate, void *stream);
+
+/* Bytes of the tiled layout of a 16-bit [N][K] matrix (N padded to a
+ * multiple of 16 rows). */
+size_t qw_w16_tiled_size(int N, int K);
+
+/* Load-time conversion of a 16-bit row-major [N][ldw] matrix (fp16 or bf16,
+ * the bits are moved unchanged) into the tiled layout qw_w16_gemv_tiled
+ * reads: each 32-element step of a 16-row tile is one contiguous 1 KB piece,
+ * so every wave load of the GEMV is contiguous (the row-major GEMV's loads
+ * take 64 bytes from each of 16 rows). No counterpart in the reference, whose
+ * gemv_rows reads the row-major matrix (src/kernels/gemv.hip:7-42); the
+ * engine's loader would call it once per matrix, as it converts q4 weights
+ * (src/engine/weight_convert.cpp:61-71). Device buffers, 16-byte aligned;
+ * ldw >= K a multiple of 8, K a multiple of 32, N >= 1. */
+int qw_w16_tile(const uint16_t *W, int ldw, int N, int K, void *Wt, void *stream);
+
+/* qw_w16_gemv on weights in the tiled layout (qw_w16_tile); the same
+ * arguments and results, bit for bit, without ldw. */
+int qw_w16_gemv_tiled(const void *Wt, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N, int K,
+                      int M, int accumulate, void *stream);
 
 /* Dense GEMV on int8 weights (replaces gpu::gemv_rows_i8,
  * src/kernels/gemv.hpp:15-23, src/kernels/gemv.hip:75-136; the engine's int8

@@ -62,6 +62,12 @@ def test_abi_version():
                            ctypes.c_void_p(256), 64, 0, 64, 128, 1, 8, 0, None),  # rpg < 16
     lambda L: L.qw_i8_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), 32, ctypes.c_void_p(256), 1024,
                            ctypes.c_void_p(256), 1296, 0, 1296, 1024, 2, 324, 0, None),  # xs < 4 slices
+    lambda L: L.qw_w16_tile(ctypes.c_void_p(256), 96, 64, 48, ctypes.c_void_p(256), None),  # K % 32
+    lambda L: L.qw_w16_tile(ctypes.c_void_p(256), 64, 64, 96, ctypes.c_void_p(256), None),  # ldw < K
+    lambda L: L.qw_w16_gemv_tiled(ctypes.c_void_p(256), ctypes.c_void_p(256), 4096, 1, ctypes.c_void_p(256), 64, 0,
+                                  64, 4096, 33, 0, None),  # M > 32
+    lambda L: L.qw_w16_gemv_tiled(ctypes.c_void_p(264), ctypes.c_void_p(256), 4096, 1, ctypes.c_void_p(256), 64, 0,
+                                  64, 4096, 1, 0, None),  # Wt not 16-byte aligned
 ])
 def test_bad_arguments_are_rejected(call):
     L = qwq4.lib()
@@ -70,5 +76,6 @@ def test_bad_arguments_are_rejected(call):
 
 
 def test_workspace_sizes():
+    assert qwq4.lib().qw_w16_tiled_size(3073, 4096) == 3088 * 4096 * 2
     assert qwq4.gemm_workspace_size(4096, 4096) >= 4096 * 4096 * 2
     assert qwq4.lib().qw_q4_gemm_workspace_size(0, 4096) == 0

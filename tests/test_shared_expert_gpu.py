@@ -59,6 +59,54 @@ def test_w16_gemv_strides_bf16_out_and_accumulate(gpu, oracle):
     assert bf16_err_ok(yb, oracle.linear_w16(Wb, xf, True))
 
 
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("N,K,M", [(3073, 4096, 1), (3073, 4096, 8), (4096, 1536, 4), (100, 320, 3), (1024, 2048, 17),
+                                   (256, 4096, 32), (40, 32, 2)])
+def test_w16_gemv_tiled(gpu, oracle, f16, N, K, M):
+    """The tiled layout gives the row-major GEMV's results bit for bit (the same
+    products summed in the same order), and the oracle's."""
+    print(f"w16 gemv tiled f16={f16} N={N} K={K} M={M}", flush=True)
+    Wb, _ = w16(87, f"wt{N}x{K}", N, K, f16)
+    xb, xf = rows(87, f"xt{M}x{K}", M, K, f16)
+    W, x = to_dev(Wb, gpu), to_dev(xb, gpu)
+    y = host(qwq4.gemv_w16_tiled(qwq4.w16_tile(W), N, K, x, M, f16=f16))
+    assert np.array_equal(y.view(np.uint32), host(qwq4.gemv_w16(W, x, M, f16=f16)).view(np.uint32))
+    assert rel_err(y, oracle.linear_w16(Wb, xf, f16)) <= TOL
+
+
+def test_w16_gemv_tiled_strides_bf16_out_and_accumulate(gpu, oracle):
+    import torch
+    N, K, M = 500, 1024, 5
+    Wb, _ = w16(88, "wts", N, K, True)
+    xb, xf = rows(88, "xts", M, K, True)
+    Wp = torch.zeros((N, K + 64), dtype=torch.int16, device=gpu)
+    Wp[:, :K] = to_dev(Wb, gpu)
+    Wt = qwq4.w16_tile(Wp[:, :K])  # from a padded row stride
+    xp = torch.zeros((M, K + 32), dtype=torch.int16, device=gpu)
+    xp[:, :K] = to_dev(xb, gpu)
+    y = torch.full((M, N + 8), 0.5, dtype=torch.float32, device=gpu)
+    qwq4.gemv_w16_tiled(Wt, N, K, xp, M, y=y, accumulate=True, f16=True, xs=K + 32, ys=N + 8)
+    yh = host(y)
+    assert np.all(yh[:, N:] == 0.5)
+    assert rel_err(yh[:, :N], oracle.linear_w16(Wb, xf, True) + 0.5) <= TOL
+    yb = host(qwq4.gemv_w16_tiled(Wt, N, K, to_dev(xb, gpu), M, y_bf16=True, f16=True))
+    assert bf16_err_ok(yb, oracle.linear_w16(Wb, xf, True))
+
+
+def test_w16_tile_layout(gpu):
+    """qw_w16_tile against a numpy restatement of the layout: entry (sub, s, 16 q + n)
+    = row 16 sub + n, K 32 s + 8 q .. +8; rows past N zero (ragged last tile)."""
+    rng = np.random.default_rng(89)
+    N, K = 37, 96
+    Wb = rng.integers(0, 1 << 16, size=(N, K), dtype=np.uint16)
+    Wt = host(qwq4.w16_tile(to_dev(Wb, gpu))).view(np.uint16)
+    tiles = (N + 15) // 16
+    Wp = np.zeros((tiles * 16, K), np.uint16)
+    Wp[:N] = Wb
+    want = Wp.reshape(tiles, 16, K // 32, 4, 8).transpose(0, 2, 3, 1, 4)  # [sub][s][q][n][8]
+    assert np.array_equal(Wt.reshape(want.shape), want)
+
+
 def test_swiglu_gate(gpu, oracle):
     n, T = 1536, 6
     v = (np.random.default_rng(83).standard_normal((T, 2 * n + 1)) * 2).astype(np.float32)
@@ -68,8 +116,8 @@ def test_swiglu_gate(gpu, oracle):
     assert np.all(np.abs(h - r) <= 2.0**-10 * np.abs(r) + 2.0**-24)
 
 
-@pytest.mark.parametrize("T", [1, 4, 8])
-def test_moe_block_with_shared_expert(gpu, oracle, T):
+@pytest.mark.parametrize("T,tiled", [(1, False), (4, False), (8, False), (1, True), (8, True)])
+def test_moe_block_with_shared_expert(gpu, oracle, T, tiled):
     """The engine's decode MoE block (decode.hip:99-111): shared expert
     (fused gate/up/gate-logit GEMV on bf16 weights, SwiGLU x sigmoid gate,
     down GEMV on fp16 weights) into the routed block's combine; against the
@@ -84,9 +132,14 @@ def test_moe_block_with_shared_expert(gpu, oracle, T):
     from test_moe_gpu import _experts_dev
     (g, u, d), _, _ = _experts_dev(gpu, ex)
     dx = to_dev(xb, gpu)
-    v = qwq4.gemv_w16(to_dev(gu_b, gpu), dx, T, f16=False)          # [T][2 SF + 1] fp32
-    hs = qwq4.swiglu_gate(v, SF)                                     # [T][SF] fp16
-    sh = qwq4.gemv_w16(to_dev(dn_b, gpu), hs, T, f16=True)           # [T][H] fp32
+    if tiled:  # weights tiled at load (qw_w16_tile)
+        v = qwq4.gemv_w16_tiled(qwq4.w16_tile(to_dev(gu_b, gpu)), 2 * SF + 1, H, dx, T, f16=False)
+        hs = qwq4.swiglu_gate(v, SF)
+        sh = qwq4.gemv_w16_tiled(qwq4.w16_tile(to_dev(dn_b, gpu)), H, SF, hs, T, f16=True)
+    else:
+        v = qwq4.gemv_w16(to_dev(gu_b, gpu), dx, T, f16=False)          # [T][2 SF + 1] fp32
+        hs = qwq4.swiglu_gate(v, SF)                                     # [T][SF] fp16
+        sh = qwq4.gemv_w16(to_dev(dn_b, gpu), hs, T, f16=True)           # [T][H] fp32
     out, buf = qwq4.moe_decode(to_dev(Wr, gpu), dx, k, g, u, d, E, F, shared=sh, out_bf16=False)
     logits = host(buf.logits)
     ref = oracle.moe(xf, logits, k, *ex) + oracle.shared_expert(xf, gu_b, dn_b, f16_gu=False, f16_down=True)

@@ -108,9 +108,40 @@ int qw_w16_gemv(const uint16_t *W, int ldw, const uint16_t *x, int xs, int f16, 
     REQUIRE(xs >= K && xs % 8 == 0 && aligned(x, 16), "qw_w16_gemv: x stride %d must be >= K, a multiple of 8, x 16-byte aligned", xs);
     REQUIRE(ys >= N || M == 1, "qw_w16_gemv: y stride %d < N", ys);
     REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_w16_gemv: y misaligned");
-    qwq4::W16Args a{W, ldw, x, xs, y, ys, y_bf16 != 0, N, K, M, accumulate != 0, f16 != 0};
+    qwq4::W16Args a{W, ldw, x, xs, y, ys, y_bf16 != 0, N, K, M, accumulate != 0, f16 != 0, 0};
     qwq4::launch_w16_gemv(a, st(stream));
     return launched("qw_w16_gemv");
+}
+
+size_t qw_w16_tiled_size(int N, int K) {
+    return N > 0 && K > 0 ? size_t((N + 15) / 16) * 16 * size_t(K) * 2 : 0;
+}
+
+int qw_w16_tile(const uint16_t *W, int ldw, int N, int K, void *Wt, void *stream) {
+    REQUIRE(W && Wt, "qw_w16_tile: null W or Wt");
+    REQUIRE(N >= 1 && K >= 32 && K % 32 == 0, "qw_w16_tile: N = %d, K = %d (need N >= 1, K a positive multiple of 32)",
+            N, K);
+    REQUIRE(ldw >= K && ldw % 8 == 0 && aligned(W, 16) && aligned(Wt, 16),
+            "qw_w16_tile: ldw %d must be >= K, a multiple of 8; W and Wt 16-byte aligned", ldw);
+    qwq4::launch_w16_tile(W, ldw, N, K, Wt, st(stream));
+    return launched("qw_w16_tile");
+}
+
+int qw_w16_gemv_tiled(const void *Wt, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N, int K,
+                      int M, int accumulate, void *stream) {
+    REQUIRE(Wt && x && y, "qw_w16_gemv_tiled: null Wt, x or y");
+    REQUIRE(N >= 1 && K >= 32 && K % 32 == 0,
+            "qw_w16_gemv_tiled: N = %d, K = %d (need N >= 1, K a positive multiple of 32)", N, K);
+    REQUIRE(aligned(Wt, 16), "qw_w16_gemv_tiled: Wt must be 16-byte aligned");
+    REQUIRE(M >= 1 && M <= 32, "qw_w16_gemv_tiled: M = %d outside 1..32", M);
+    REQUIRE(xs >= K && xs % 8 == 0 && aligned(x, 16),
+            "qw_w16_gemv_tiled: x stride %d must be >= K, a multiple of 8, x 16-byte aligned", xs);
+    REQUIRE(ys >= N || M == 1, "qw_w16_gemv_tiled: y stride %d < N", ys);
+    REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_w16_gemv_tiled: y misaligned");
+    qwq4::W16Args a{static_cast<const uint16_t *>(Wt), K, x, xs, y, ys, y_bf16 != 0, N, K, M, accumulate != 0,
+                    f16 != 0, 1};
+    qwq4::launch_w16_gemv(a, st(stream));
+    return launched("qw_w16_gemv_tiled");
 }
 
 void qw_i8_tiled_size(int N, int K, int group, size_t *w_bytes, size_t *s_bytes) {

@@ -139,9 +139,11 @@ struct W16Args {
     int xs;
     void *y;
     int ys, y_bf16, N, K, M, accumulate, f16;
+    int tiled;  // W in the layout of launch_w16_tile (ldw unused)
 };
 bool w16_fits(int M, int K, int N);
 void launch_w16_gemv(const W16Args &a, hipStream_t s);
+void launch_w16_tile(const uint16_t *W, int64_t ldw, int N, int K, void *Wt, hipStream_t s);
 // Dense GEMV on int8 weights (tiled by launch_i8_tile from row-major [N][K])
 // with an fp32 scale per group of `group` (16 or 32) along K; fp16
 // activation rows, row slices of rpg rows (0: none) as in gpu::gemv_rows_i8.

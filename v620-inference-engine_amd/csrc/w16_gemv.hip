@@ -6,7 +6,8 @@
 // it, src/engine/decode.hip:99-101) and ref::Model::linear on bf16 weights
 // (src/ref/ref_model.cpp:86-97); gpu::swiglu_T (src/kernels/moe_route.hip:187-197).
 //
-// The weights are row-major [N][ldw] as the checkpoint holds them, fp16 with
+// The weights are row-major [N][ldw] as the checkpoint holds them, or in the
+// tiled layout qw_w16_tile writes once at load (below), fp16 with
 // fp16 activations or bf16 with bf16 ones: the 16x16x32 MFMA takes both as
 // they are, so a product needs no conversion and every product is exact
 // (fp32 sums). The kernel shape is the q4 GEMV's (q4_gemv_impl.cuh): a block
@@ -27,7 +28,7 @@ constexpr int W16_MAX_KS = 8;  // waves per block
 // the smallest that holds its range where one does (the shared expert's down
 // projection, 6 steps per wave: 16 held 81-97 VGPRs, 4-5 waves per SIMD;
 // 8 make it 10% faster per layer)
-template <typename XT, int MB, int MR, int XPT, int WS>
+template <typename XT, int MB, int MR, int XPT, int WS, bool TILED>
 __global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16_t *W, int ldw, const uint16_t *x,
                                                                     int xs, int M, int K, int N, void *__restrict__ y,
                                                                     int ys, int y_bf16, int accumulate) {
@@ -43,9 +44,12 @@ __global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16
     if constexpr (XPT > 0) stage_regs_issue<XPT>(x, xs, M, K, xv);
     else stage_x_issue(x, xs, M, K, xl);
     __builtin_amdgcn_sched_barrier(0);  // every activation load goes out before the weight loads
-    // lane (n, q): 8 weights of row n at K 32 s + 8 q, step s
+    // lane (n, q): 8 weights of row n at K 32 s + 8 q, step s. Row-major: 64
+    // bytes of each of 16 rows per wave load; tiled: the step's 1 KB entry.
     const uint4 *wrow =
-        reinterpret_cast<const uint4 *>(W + int64_t(min(int(blockIdx.x) * 16 + n, N - 1)) * ldw + 8 * q);
+        TILED ? reinterpret_cast<const uint4 *>(W) + int64_t(blockIdx.x) * steps * 64 + lane
+              : reinterpret_cast<const uint4 *>(W + int64_t(min(int(blockIdx.x) * 16 + n, N - 1)) * ldw + 8 * q);
+    constexpr int STEP = TILED ? 64 : 4;  // uint4 entries from one step to the next
     f32x4 acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -55,7 +59,7 @@ __global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16
 #pragma unroll
         for (int t = 0; t < WS; ++t) {
             const int s = min(s0 + min(p + t, max(ns - 1, 0)), steps - 1);
-            const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow + s * 4));
+            const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow + s * STEP));
             w[t] = make_uint4(v[0], v[1], v[2], v[3]);
         }
     };
@@ -85,7 +89,7 @@ __global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16
     if (kp == 0) store_rows<MB, MR>(acc, y, ys, y_bf16, accumulate, M, N, blockIdx.x, lane);
 }
 
-template <typename XT, int MB, int MR>
+template <typename XT, int MB, int MR, bool TILED>
 static void launch_w16_t(const W16Args &a, int KS, hipStream_t s) {
     const int threads = KS * WAVE;
     const size_t lds = dense_lds_bytes(a.M, a.K, MB, KS, KS);
@@ -98,21 +102,21 @@ static void launch_w16_t(const W16Args &a, int KS, hipStream_t s) {
     const int spw = (a.K / 32 + KS - 1) / KS;
     auto pick = [&](auto ws) {
         constexpr int W = decltype(ws)::value;
-        if (xpt <= 1) go(w16_gemv_kernel<XT, MB, MR, 1, W>);
-        else if (xpt <= 2) go(w16_gemv_kernel<XT, MB, MR, 2, W>);
-        else if (xpt <= 4) go(w16_gemv_kernel<XT, MB, MR, 4, W>);
-        else go(w16_gemv_kernel<XT, MB, MR, 0, W>);
+        if (xpt <= 1) go(w16_gemv_kernel<XT, MB, MR, 1, W, TILED>);
+        else if (xpt <= 2) go(w16_gemv_kernel<XT, MB, MR, 2, W, TILED>);
+        else if (xpt <= 4) go(w16_gemv_kernel<XT, MB, MR, 4, W, TILED>);
+        else go(w16_gemv_kernel<XT, MB, MR, 0, W, TILED>);
     };
     if (spw <= 8) pick(std::integral_constant<int, 8>());
     else pick(std::integral_constant<int, 16>());
 }
 
-template <typename XT>
+template <typename XT, bool TILED>
 static void launch_w16_x(const W16Args &a, int KS, hipStream_t s) {
-    if (a.M > 16) launch_w16_t<XT, 2, 4>(a, KS, s);
-    else if (a.M == 1) launch_w16_t<XT, 1, 1>(a, KS, s);
-    else if (a.M == 2) launch_w16_t<XT, 1, 2>(a, KS, s);
-    else launch_w16_t<XT, 1, 4>(a, KS, s);
+    if (a.M > 16) launch_w16_t<XT, 2, 4, TILED>(a, KS, s);
+    else if (a.M == 1) launch_w16_t<XT, 1, 1, TILED>(a, KS, s);
+    else if (a.M == 2) launch_w16_t<XT, 1, 2, TILED>(a, KS, s);
+    else launch_w16_t<XT, 1, 4, TILED>(a, KS, s);
 }
 
 // K split: as many waves (up to 8) as the 32-element steps allow; fewer
@@ -127,8 +131,13 @@ bool w16_fits(int M, int K, int N) {
 
 static void launch_w16_fit(const W16Args &a, hipStream_t s) {
     const int KS = w16_ks(a.K, a.N);
-    if (a.f16) launch_w16_x<F16>(a, KS, s);
-    else launch_w16_x<BF16>(a, KS, s);
+    if (a.tiled) {
+        if (a.f16) launch_w16_x<F16, true>(a, KS, s);
+        else launch_w16_x<BF16, true>(a, KS, s);
+    } else {
+        if (a.f16) launch_w16_x<F16, false>(a, KS, s);
+        else launch_w16_x<BF16, false>(a, KS, s);
+    }
 }
 
 // Batches whose activations exceed LDS run as several launches of fewer rows.
@@ -147,6 +156,25 @@ void launch_w16_gemv(const W16Args &a, hipStream_t s) {
         b.y = static_cast<char *>(a.y) + int64_t(m0) * a.ys * ysz;
         launch_w16_fit(b, s);
     }
+}
+
+// ------------------------------------------------------------ tiled layout
+// Wt uint4 [ceil(N/16)][K/32][64]: entry (sub, s, 16 q + n) holds the 8
+// elements of row 16 sub + n at K 32 s + 8 q .. +8 (zero past row N - 1),
+// which is what lane 16 q + n feeds the 16x16x32 MFMA at step s; one step of
+// a subtile is one contiguous 1 KB wave load. One thread per entry.
+__global__ __launch_bounds__(256) void w16_tile_kernel(const uint16_t *__restrict__ W, int64_t ldw, int N, int K,
+                                                       uint4 *__restrict__ Wt) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x, steps = K / 32;
+    if (i >= (int64_t(N) + 15) / 16 * steps * 64) return;
+    const int l = int(i % 64), q = l / 16, n = l % 16;
+    const int64_t s = i / 64 % steps, sub = i / 64 / steps, row = sub * 16 + n;
+    Wt[i] = row < N ? *reinterpret_cast<const uint4 *>(W + row * ldw + s * 32 + q * 8) : make_uint4(0, 0, 0, 0);
+}
+
+void launch_w16_tile(const uint16_t *W, int64_t ldw, int N, int K, void *Wt, hipStream_t s) {
+    const int64_t n = (int64_t(N) + 15) / 16 * (K / 32) * 64;
+    w16_tile_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(W, ldw, N, K, static_cast<uint4 *>(Wt));
 }
 
 // ---------------------------------------------------------- SwiGLU x gate

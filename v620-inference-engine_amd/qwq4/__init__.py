@@ -20,7 +20,7 @@ SYMBOLS = (
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
     "qw_moe_decode_workspace_size", "qw_moe_decode", "qw_moe_decode_static_max_bytes", "qw_moe_decode_static",
-    "qw_w16_gemv", "qw_i8_gemv", "qw_i8_tiled_size", "qw_i8_tile",
+    "qw_w16_gemv", "qw_w16_tiled_size", "qw_w16_tile", "qw_w16_gemv_tiled", "qw_i8_gemv", "qw_i8_tiled_size", "qw_i8_tile",
     "qw_moe_w4a8_tile_m", "qw_moe_w4a8_workspace_size", "qw_moe_experts_w4a8", "qw_quant_rows_i8", "qw_swiglu_gate",
     "qw_wcache_open", "qw_wcache_put", "qw_wcache_get", "qw_wcache_finish", "qw_wcache_close",
 )
@@ -54,6 +54,9 @@ _SIGS = {
     "qw_moe_decode": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
     "qw_moe_decode_static_max_bytes": ([], _SZ),
     "qw_w16_gemv": ([_P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_w16_tiled_size": ([_I, _I], _SZ),
+    "qw_w16_tile": ([_P, _I, _I, _I, _P, _P], _I),
+    "qw_w16_gemv_tiled": ([_P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_i8_gemv": ([_P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_i8_tiled_size": ([_I, _I, _I, _P, _P], None),
     "qw_i8_tile": ([_P, _P, _I, _I, _I, _P, _P, _P], _I),
@@ -193,6 +196,33 @@ def gemv_w16(W, x, M=None, y=None, y_bf16=False, accumulate=False, f16=None, xs=
     rc = lib().qw_w16_gemv(_ptr(W), W.stride(0), _ptr(x), xs, int(f16), _ptr(y), ys, int(y_bf16), N, K, M,
                            int(accumulate), _stream())
     _check(rc, "qw_w16_gemv")
+    return y
+
+
+def w16_tile(W):
+    """16-bit W [N][K] (row-major, stride W.stride(0)) -> the tiled layout qw_w16_gemv_tiled
+    reads (a flat tensor of W's dtype, rows padded to a multiple of 16)."""
+    import torch
+    N, K = W.shape
+    Wt = torch.empty(lib().qw_w16_tiled_size(N, K) // 2, dtype=W.dtype, device=W.device)
+    _dev(W)
+    _check(lib().qw_w16_tile(_ptr(W), W.stride(0), N, K, _ptr(Wt), _stream()), "qw_w16_tile")
+    return Wt
+
+
+def gemv_w16_tiled(Wt, N, K, x, M=None, y=None, y_bf16=False, accumulate=False, f16=None, xs=None, ys=None):
+    """gemv_w16 on the tiled layout (w16_tile) of a 16-bit [N][K] matrix."""
+    import torch
+    M = M if M is not None else x.shape[0]
+    f16 = _is_f16(x, f16)
+    xs = xs if xs is not None else x.stride(0) if x.dim() == 2 else K
+    if y is None:
+        y = torch.zeros((M, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=x.device)
+    ys = ys if ys is not None else (y.stride(0) if y.dim() == 2 else N)
+    _dev(Wt, x, y)
+    rc = lib().qw_w16_gemv_tiled(_ptr(Wt), _ptr(x), xs, int(f16), _ptr(y), ys, int(y_bf16), N, K, M,
+                                 int(accumulate), _stream())
+    _check(rc, "qw_w16_gemv_tiled")
     return y
 
 
