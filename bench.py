@@ -285,7 +285,8 @@ SH_LAYERS, SH_FFN = 8, 1536
 def bench_shared(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8)):
     """The shared expert as the engine runs it (src/engine/decode.hip:99-101):
     fused gate/up/gate-logit GEMV [2F+1][H] on fp16 weights, SwiGLU x sigmoid
-    gate, down GEMV [H][F] on fp16 weights; SH_LAYERS layers of their own
+    gate folded into the down GEMV [H][F] on fp16 weights (and, for comparison,
+    as the reference's separate swiglu_T launch); SH_LAYERS layers of their own
     weights (302 MB, past the Infinity Cache), tiled once at load (qw_w16_tile,
     outside the timed region). Bytes: the 16-bit weights."""
     g = torch.Generator(device=dev)
@@ -302,19 +303,27 @@ def bench_shared(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8)):
         hs = torch.empty((M, SH_FFN), dtype=torch.float16, device=dev)
         y = torch.empty((M, H), dtype=torch.float32, device=dev)
 
-        def launches():
+        def launches(fused):
             for l in range(SH_LAYERS):
                 qwq4.gemv_w16_tiled(gu[l], 2 * SH_FFN + 1, H, x, M, y=v)
-                qwq4.swiglu_gate(v, SH_FFN, h=hs)
-                qwq4.gemv_w16_tiled(dn[l], H, SH_FFN, hs, M, y=y)
+                if fused:  # swiglu_T folded into the down projection (two launches per layer)
+                    qwq4.swiglu_gemv_w16_tiled(dn[l], H, v, SH_FFN, M, y=y)
+                else:      # the reference's three launches
+                    qwq4.swiglu_gate(v, SH_FFN, h=hs)
+                    qwq4.gemv_w16_tiled(dn[l], H, SH_FFN, hs, M, y=y)
 
-        step = graphed(torch, launches)
-        for _ in range(warmup):
-            step()
-        with Timer(torch) as t:
-            for _ in range(steps):
+        for fused in (True, False):
+            step = graphed(torch, lambda: launches(fused))
+            for _ in range(warmup):
                 step()
-        out[M] = {"GB_s": wbytes * steps / (t.ms * 1e-3) / 1e9, "us_per_layer": t.ms * 1e3 / (steps * SH_LAYERS)}
+            with Timer(torch) as t:
+                for _ in range(steps):
+                    step()
+            r = {"GB_s": wbytes * steps / (t.ms * 1e-3) / 1e9, "us_per_layer": t.ms * 1e3 / (steps * SH_LAYERS)}
+            if fused:
+                out[M] = r
+            else:
+                out[M]["three_launches"] = r
     return out
 
 

@@ -14,6 +14,7 @@
  *   qw_moe_combine        gpu::moe_combine_B/T      src/kernels/moe.hpp:42-46
  *   qw_w16_gemv           gpu::gemv_rows (fp16 W)   src/kernels/gemv.hpp:13-14
  *   qw_w16_gemv_tiled     gpu::gemv_rows (fp16 W)   src/kernels/gemv.hpp:13-14 (weights tiled at load)
+ *   qw_w16_swiglu_gemv_tiled  gpu::swiglu_T + gemv_rows  src/kernels/moe_route.hip:187-197, gemv.hpp:13-14
  *                         ref::Model::linear        src/ref/ref_model.cpp:86-97
  *   qw_i8_gemv            gpu::gemv_rows_i8         src/kernels/gemv.hpp:15-23
  *   qw_swiglu_gate        gpu::swiglu_T             src/kernels/moe_route.hip:187-197
@@ -124,6 +125,21 @@ int qw_w16_tile(const uint16_t *W, int ldw, int N, int K, void *Wt, void *stream
  * arguments and results, bit for bit, without ldw. */
 int qw_w16_gemv_tiled(const void *Wt, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N, int K,
                       int M, int accumulate, void *stream);
+
+/* The shared expert's SwiGLU x gate folded into its down projection: the
+ * result of qw_swiglu_gate(v, ldv, n, M, h) followed by
+ * qw_w16_gemv_tiled(Wt, h, n, 1, y, ys, y_bf16, N, n, M, accumulate), bit for
+ * bit, in one launch and without h:
+ *   h[m][j] = fp16(silu(v[m][j]) * v[m][n + j] * sigmoid(v[m][2n]))
+ *   y[m*ys + i] (+)= sum_j Wt[i][j] * h[m][j],   i < N, m < M
+ * Replaces swiglu_T + gemv_rows (src/kernels/moe_route.hip:187-197,
+ * src/engine/decode.hip:99-101), which the reference runs as two launches.
+ * Wt: fp16 [N][n] tiled by qw_w16_tile (16-byte aligned); v fp32 [M][ldv]
+ * (ldv >= 2n + 1); n a multiple of 32; y fp32 or bf16; 1 <= M <= 32. Every
+ * block forms all of h, so this is the faster form up to about 4 rows; with
+ * more rows the two launches (h formed once) are faster. */
+int qw_w16_swiglu_gemv_tiled(const void *Wt, const float *v, int ldv, int n, void *y, int ys, int y_bf16, int N, int M,
+                             int accumulate, void *stream);
 
 /* Dense GEMV on int8 weights (replaces gpu::gemv_rows_i8,
  * src/kernels/gemv.hpp:15-23, src/kernels/gemv.hip:75-136; the engine's int8

@@ -68,6 +68,12 @@ def test_abi_version():
                                   64, 4096, 33, 0, None),  # M > 32
     lambda L: L.qw_w16_gemv_tiled(ctypes.c_void_p(264), ctypes.c_void_p(256), 4096, 1, ctypes.c_void_p(256), 64, 0,
                                   64, 4096, 1, 0, None),  # Wt not 16-byte aligned
+    lambda L: L.qw_w16_swiglu_gemv_tiled(ctypes.c_void_p(256), ctypes.c_void_p(256), 97, 48, ctypes.c_void_p(256),
+                                         64, 0, 64, 1, 0, None),  # n % 32
+    lambda L: L.qw_w16_swiglu_gemv_tiled(ctypes.c_void_p(256), ctypes.c_void_p(256), 3073, 1536, ctypes.c_void_p(256),
+                                         4096, 0, 4096, 33, 0, None),  # M > 32
+    lambda L: L.qw_w16_swiglu_gemv_tiled(ctypes.c_void_p(256), ctypes.c_void_p(256), 3000, 1536, ctypes.c_void_p(256),
+                                         4096, 0, 4096, 2, 0, None),  # ldv < 2n + 1
 ])
 def test_bad_arguments_are_rejected(call):
     L = qwq4.lib()

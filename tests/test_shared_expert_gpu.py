@@ -107,6 +107,46 @@ def test_w16_tile_layout(gpu):
     assert np.array_equal(Wt.reshape(want.shape), want)
 
 
+@pytest.mark.parametrize("N,n,M", [(4096, 1536, 1), (4096, 1536, 2), (4096, 1536, 3), (4096, 1536, 5),
+                                   (4096, 1536, 8), (4096, 1536, 10), (4096, 1536, 11), (4096, 1536, 32), (100, 64, 4),
+                                   (1024, 512, 17), (40, 32, 1)])
+def test_w16_swiglu_gemv_tiled(gpu, N, n, M):
+    """The SwiGLU x gate folded into the down GEMV gives, bit for bit, what
+    qw_swiglu_gate followed by qw_w16_gemv_tiled gives (register staging up to two
+    pieces per thread, the staging loop beyond); v scaled so that some h values
+    saturate at the fp16 limit."""
+    import torch
+    print(f"w16 swiglu gemv N={N} n={n} M={M}", flush=True)
+    Wb, _ = w16(90, f"dn{N}x{n}", N, n, True)
+    v = (np.random.default_rng(91 + M).standard_normal((M, 2 * n + 1)) * 3).astype(np.float32)
+    v[:, : n // 8] *= 200.0  # silu(g) * u beyond 65504 for some
+    Wt = qwq4.w16_tile(to_dev(Wb, gpu))
+    dv = to_dev(v, gpu)
+    y = host(qwq4.swiglu_gemv_w16_tiled(Wt, N, dv, n, M))
+    h = qwq4.swiglu_gate(dv, n)
+    ref = host(qwq4.gemv_w16_tiled(Wt, N, n, h, M, f16=True))
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+    assert np.all(np.isfinite(y))
+
+
+def test_w16_swiglu_gemv_tiled_strides_bf16_out_and_accumulate(gpu, oracle):
+    import torch
+    N, n, M = 300, 256, 6
+    Wb, _ = w16(92, "dns", N, n, True)
+    v = (np.random.default_rng(92).standard_normal((M, 2 * n + 7)) * 2).astype(np.float32)  # ldv = 2n + 7
+    Wt = qwq4.w16_tile(to_dev(Wb, gpu))
+    dv = to_dev(v, gpu)
+    h = oracle.swiglu_gate(np.ascontiguousarray(v[:, : 2 * n + 1]), n)
+    ref = oracle.linear_w16(Wb, h, True)
+    y = torch.full((M, N + 8), 0.5, dtype=torch.float32, device=gpu)
+    qwq4.swiglu_gemv_w16_tiled(Wt, N, dv, n, M, y=y, accumulate=True, ys=N + 8)
+    yh = host(y)
+    assert np.all(yh[:, N:] == 0.5)
+    assert rel_err(yh[:, :N], ref + 0.5) <= TOL
+    yb = host(qwq4.swiglu_gemv_w16_tiled(Wt, N, dv, n, M, y_bf16=True))
+    assert bf16_err_ok(yb, ref)
+
+
 def test_swiglu_gate(gpu, oracle):
     n, T = 1536, 6
     v = (np.random.default_rng(83).standard_normal((T, 2 * n + 1)) * 2).astype(np.float32)
@@ -116,7 +156,8 @@ def test_swiglu_gate(gpu, oracle):
     assert np.all(np.abs(h - r) <= 2.0**-10 * np.abs(r) + 2.0**-24)
 
 
-@pytest.mark.parametrize("T,tiled", [(1, False), (4, False), (8, False), (1, True), (8, True)])
+@pytest.mark.parametrize("T,tiled", [(1, False), (4, False), (8, False), (1, True), (8, True), (1, "fused"),
+                                     (4, "fused"), (8, "fused")])
 def test_moe_block_with_shared_expert(gpu, oracle, T, tiled):
     """The engine's decode MoE block (decode.hip:99-111): shared expert
     (fused gate/up/gate-logit GEMV on bf16 weights, SwiGLU x sigmoid gate,
@@ -132,7 +173,10 @@ def test_moe_block_with_shared_expert(gpu, oracle, T, tiled):
     from test_moe_gpu import _experts_dev
     (g, u, d), _, _ = _experts_dev(gpu, ex)
     dx = to_dev(xb, gpu)
-    if tiled:  # weights tiled at load (qw_w16_tile)
+    if tiled == "fused":  # tiled weights, SwiGLU x gate folded into the down GEMV
+        v = qwq4.gemv_w16_tiled(qwq4.w16_tile(to_dev(gu_b, gpu)), 2 * SF + 1, H, dx, T, f16=False)
+        sh = qwq4.swiglu_gemv_w16_tiled(qwq4.w16_tile(to_dev(dn_b, gpu)), H, v, SF, T)
+    elif tiled:  # weights tiled at load (qw_w16_tile)
         v = qwq4.gemv_w16_tiled(qwq4.w16_tile(to_dev(gu_b, gpu)), 2 * SF + 1, H, dx, T, f16=False)
         hs = qwq4.swiglu_gate(v, SF)
         sh = qwq4.gemv_w16_tiled(qwq4.w16_tile(to_dev(dn_b, gpu)), H, SF, hs, T, f16=True)

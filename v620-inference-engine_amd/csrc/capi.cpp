@@ -144,6 +144,22 @@ int qw_w16_gemv_tiled(const void *Wt, const uint16_t *x, int xs, int f16, void *
     return launched("qw_w16_gemv_tiled");
 }
 
+int qw_w16_swiglu_gemv_tiled(const void *Wt, const float *v, int ldv, int n, void *y, int ys, int y_bf16, int N, int M,
+                             int accumulate, void *stream) {
+    REQUIRE(Wt && v && y, "qw_w16_swiglu_gemv_tiled: null Wt, v or y");
+    REQUIRE(N >= 1 && n >= 32 && n % 32 == 0,
+            "qw_w16_swiglu_gemv_tiled: N = %d, n = %d (need N >= 1, n a positive multiple of 32)", N, n);
+    REQUIRE(M >= 1 && M <= 32, "qw_w16_swiglu_gemv_tiled: M = %d outside 1..32", M);
+    REQUIRE(aligned(Wt, 16) && aligned(v, 4) && (M == 1 || ldv >= 2 * n + 1),
+            "qw_w16_swiglu_gemv_tiled: ldv %d must be >= 2n + 1; Wt 16-byte, v 4-byte aligned", ldv);
+    REQUIRE(ys >= N || M == 1, "qw_w16_swiglu_gemv_tiled: y stride %d < N", ys);
+    REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_w16_swiglu_gemv_tiled: y misaligned");
+    REQUIRE(qwq4::w16_swiglu_fits(M, n, N), "qw_w16_swiglu_gemv_tiled: %d rows of n = %d exceed the staging LDS", M, n);
+    qwq4::W16SwigluArgs a{static_cast<const uint16_t *>(Wt), v, ldv, n, y, ys, y_bf16 != 0, N, M, accumulate != 0};
+    qwq4::launch_w16_swiglu(a, st(stream));
+    return launched("qw_w16_swiglu_gemv_tiled");
+}
+
 void qw_i8_tiled_size(int N, int K, int group, size_t *w_bytes, size_t *s_bytes) {
     const size_t tiles = N > 0 ? size_t((N + 15) / 16) : 0, k = K > 0 ? size_t(K) : 0;
     if (w_bytes) *w_bytes = tiles * 16 * k;

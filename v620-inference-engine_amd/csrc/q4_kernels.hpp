@@ -144,6 +144,18 @@ struct W16Args {
 bool w16_fits(int M, int K, int N);
 void launch_w16_gemv(const W16Args &a, hipStream_t s);
 void launch_w16_tile(const uint16_t *W, int64_t ldw, int N, int K, void *Wt, hipStream_t s);
+// y = W h, h[m][j] = fp16(silu(v[m][j]) v[m][n + j] sigmoid(v[m][2n])) formed
+// while staging (the shared expert's swiglu_T folded into its down GEMV); W
+// fp16 [N][n] in the tiled layout of launch_w16_tile.
+struct W16SwigluArgs {
+    const uint16_t *Wt;
+    const float *v;
+    int ldv, n;
+    void *y;
+    int ys, y_bf16, N, M, accumulate;
+};
+bool w16_swiglu_fits(int M, int n, int N);
+void launch_w16_swiglu(const W16SwigluArgs &a, hipStream_t s);
 // Dense GEMV on int8 weights (tiled by launch_i8_tile from row-major [N][K])
 // with an fp32 scale per group of `group` (16 or 32) along K; fp16
 // activation rows, row slices of rpg rows (0: none) as in gpu::gemv_rows_i8.

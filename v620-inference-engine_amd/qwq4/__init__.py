@@ -20,7 +20,7 @@ SYMBOLS = (
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
     "qw_moe_decode_workspace_size", "qw_moe_decode", "qw_moe_decode_static_max_bytes", "qw_moe_decode_static",
-    "qw_w16_gemv", "qw_w16_tiled_size", "qw_w16_tile", "qw_w16_gemv_tiled", "qw_i8_gemv", "qw_i8_tiled_size", "qw_i8_tile",
+    "qw_w16_gemv", "qw_w16_tiled_size", "qw_w16_tile", "qw_w16_gemv_tiled", "qw_w16_swiglu_gemv_tiled", "qw_i8_gemv", "qw_i8_tiled_size", "qw_i8_tile",
     "qw_moe_w4a8_tile_m", "qw_moe_w4a8_workspace_size", "qw_moe_experts_w4a8", "qw_quant_rows_i8", "qw_swiglu_gate",
     "qw_wcache_open", "qw_wcache_put", "qw_wcache_get", "qw_wcache_finish", "qw_wcache_close",
 )
@@ -57,6 +57,7 @@ _SIGS = {
     "qw_w16_tiled_size": ([_I, _I], _SZ),
     "qw_w16_tile": ([_P, _I, _I, _I, _P, _P], _I),
     "qw_w16_gemv_tiled": ([_P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_w16_swiglu_gemv_tiled": ([_P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P], _I),
     "qw_i8_gemv": ([_P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_i8_tiled_size": ([_I, _I, _I, _P, _P], None),
     "qw_i8_tile": ([_P, _P, _I, _I, _I, _P, _P, _P], _I),
@@ -223,6 +224,22 @@ def gemv_w16_tiled(Wt, N, K, x, M=None, y=None, y_bf16=False, accumulate=False, 
     rc = lib().qw_w16_gemv_tiled(_ptr(Wt), _ptr(x), xs, int(f16), _ptr(y), ys, int(y_bf16), N, K, M,
                                  int(accumulate), _stream())
     _check(rc, "qw_w16_gemv_tiled")
+    return y
+
+
+def swiglu_gemv_w16_tiled(Wt, N, v, n, M=None, y=None, y_bf16=False, accumulate=False, ldv=None, ys=None):
+    """y = W h with h = fp16(silu(v[:, :n]) v[:, n:2n] sigmoid(v[:, 2n])) (swiglu_gate followed by
+    gemv_w16_tiled, in one launch); Wt: fp16 [N][n] tiled by w16_tile, v fp32 [M][>= 2n + 1]."""
+    import torch
+    M = M if M is not None else v.shape[0]
+    ldv = ldv if ldv is not None else v.stride(0) if v.dim() == 2 else 2 * n + 1
+    if y is None:
+        y = torch.zeros((M, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=v.device)
+    ys = ys if ys is not None else (y.stride(0) if y.dim() == 2 else N)
+    _dev(Wt, v, y)
+    rc = lib().qw_w16_swiglu_gemv_tiled(_ptr(Wt), _ptr(v), ldv, n, _ptr(y), ys, int(y_bf16), N, M, int(accumulate),
+                                        _stream())
+    _check(rc, "qw_w16_swiglu_gemv_tiled")
     return y
 
 
