@@ -43,6 +43,11 @@ __device__ __forceinline__ int ld_uniform(const int32_t *p, int i) {
     return ((cint *)(p))[__builtin_amdgcn_readfirstlane(i)];
 }
 
+__device__ __forceinline__ float ld_uniform_f32(const float *p, int i) {
+    typedef const __attribute__((address_space(4))) float cfloat;
+    return ((cfloat *)(p))[__builtin_amdgcn_readfirstlane(i)];
+}
+
 // Reads the block's expert: n_active and active[y] are requested together
 // (one latency), and the weight loads need only e.
 __device__ __forceinline__ int block_expert(const int32_t *n_active, const int32_t *active, int E) {
@@ -217,6 +222,74 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
     }
 }
 
+// Batch 1 with the combine (T = 1, k <= 8, the down K split in 2): block b
+// holds output rows 16 b .. 16 b + 15 of all k selected experts; wave
+// (y, kp) computes the y-th active expert (ascending; at T = 1 that is slot
+// y) over K half kp, exactly as the general kernel's subtile does. The k
+// results meet in LDS and the block forms its 16 outputs itself, in the
+// combine's order (shared row, then the selections in order): no yp round
+// trip through memory and no cross-block count before the combine. yp is
+// still written (an output of the decode block).
+template <int GW, bool HAS_Z, bool CH4>
+__global__ __launch_bounds__(1024) void moe_down_t1_kernel(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz,
+                                                           const int32_t *__restrict__ active,
+                                                           const int32_t *__restrict__ n_active,
+                                                           const uint16_t *__restrict__ h, int E, int H, int F,
+                                                           float *__restrict__ yp, CombineArgs c, int topk) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
+              n = lane % 16;
+    const int y = wave / 2, kp = wave % 2;
+    // n_active and active[y] requested together (one latency); the weight
+    // loads need only e
+    const int na = ld_uniform(n_active, 0), ea = ld_uniform(active, y);
+    const int rows = min(na, topk);
+    const bool live = y < rows;  // wave-uniform
+    const int e = live ? min(max(ea, 0), E - 1) : 0;
+    const int G = F / QGROUP, gpk = G / 2, hsub = H / 16, kc = x_row_stride(F);
+    const Q4Tile t(dw, ds, dz, int64_t(e) * hsub + blockIdx.x, G);
+    WaveRange<GW, HAS_Z, CH4> wr;
+    wr.fetch(t, kp * gpk, gpk, opaque_lane());
+    // the combine's inputs, requested now so that their latency is hidden:
+    // the selections' slots and weights (block-uniform, scalar loads) and
+    // the shared row's values (wave 0)
+    int slot_q[8];
+    float w_q[8];
+#pragma unroll
+    for (int qq = 0; qq < 8; ++qq) {
+        slot_q[qq] = qq < topk ? ld_uniform(c.tok_slot, qq) : 0;
+        w_q[qq] = qq < topk ? ld_uniform_f32(c.tok_w, qq) : 0.f;
+    }
+    const float shv = c.shared && tid < 16 ? c.shared[blockIdx.x * 16 + tid] : 0.f;
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(8, F));
+    float *yb = reinterpret_cast<float *>(red + 8 * WAVE);  // [8][16]
+    stage_rows_issue([&](int m) { return h + int64_t(m) * F; }, max(rows, 1), F, xl);
+    __syncthreads();
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (live) compute_zq_inline<F16>(wr, xl + y * kc + q * 4, acc);
+    if (kp == 1) red[y * WAVE + lane] = acc;
+    lds_barrier();
+    if (kp == 0 && live) {
+        acc += red[y * WAVE + lane];
+        if (q == 0) {
+            yb[y * 16 + n] = acc[0];
+            yp[int64_t(y) * H + blockIdx.x * 16 + n] = acc[0];
+        }
+    }
+    __syncthreads();
+    if (tid < 16) {
+        const int j = blockIdx.x * 16 + tid;
+        float v = 0.f;
+        if (c.shared) v = shv;
+#pragma unroll
+        for (int qq = 0; qq < 8; ++qq)
+            if (qq < topk) v += w_q[qq] * yb[slot_q[qq] * 16 + tid];
+        if (c.out_bf16) static_cast<uint16_t *>(c.out)[j] = f32_to_bf16_rne(v);
+        else static_cast<float *>(c.out)[j] = v;
+    }
+}
+
 // K split: the largest power of two <= kmax dividing G with at most 16 groups
 // per wave; GW: the register budget for a wave's groups.
 static int pick_ks(int G, int kmax) {
@@ -251,6 +324,14 @@ static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStrea
 
 template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB>
 static void launch_down_c(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
+    if constexpr (CMB && KS == 2 && GW <= 8) {  // GW 16 would spill at 1024 threads
+        if (a.T == 1 && a.topk <= 8) {
+            const size_t lds = size_t(x_pieces(8, a.F)) * 16 + size_t(8) * WAVE * 16 + 8 * 16 * 4;
+            moe_down_t1_kernel<GW, HAS_Z, CH4><<<unsigned(a.H / 16), 1024, lds, s>>>(
+                a.dw, a.ds, a.dz, a.active, a.n_active, a.h, a.E, a.H, a.F, a.yp, *a.cmb, a.topk);
+            return;
+        }
+    }
     auto kern = a.T <= R ? moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB, false> : moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB, true>;
     const size_t lds = moe_lds_bytes(R, a.F);
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
