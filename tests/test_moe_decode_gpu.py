@@ -79,3 +79,26 @@ def test_moe_decode_matches_unfused_path(gpu, T, E, H, F, k):
     assert np.array_equal(host(r.top_e), host(buf.top_e))
     assert np.array_equal(host(yp), host(buf.yp))
     assert np.array_equal(host(out).view(np.uint32), host(o2).view(np.uint32))
+
+
+@pytest.mark.parametrize("T,E", [(6, 64), (8, 64), (8, 256)])
+def test_moe_decode_router_lds_limit(gpu, oracle, T, E):
+    """H = 8192: the full-K router stages the token rows (T x 16 KB) in LDS
+    beside the routing's static arrays. T = 6 and 8 at E = 64 fit the CU's
+    160 KiB (the second within 2 KB); T = 8 at E = 256 does not and takes the
+    K-sliced router. Logits against the fp64 product, routing bit-exact with
+    the oracle, output bit-identical to the unfused calls."""
+    H, F, k = 8192, 128, 8
+    print(f"moe_decode router LDS T={T} E={E} H={H}", flush=True)
+    ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 95 + T + E, T, E, H, F, k, True)
+    out, buf = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
+                               out_bf16=False)
+    logits = host(buf.logits)
+    assert rel_err(logits, xf.astype(np.float64) @ Wr.astype(np.float64).T) <= 1e-5
+    te, tw = oracle.route(logits, k)
+    assert np.array_equal(host(buf.top_e), te)
+    assert np.array_equal(host(buf.top_w).view(np.uint32), tw.view(np.uint32))
+    r = qwq4.moe_route(buf.logits, k)
+    h, yp = qwq4.moe_experts_gemv(g, u, d, r, to_dev(xb, gpu), E, F)
+    o2 = qwq4.moe_combine(yp, r, H, shared=to_dev(sh, gpu), out_bf16=False)
+    assert np.array_equal(host(out).view(np.uint32), host(o2).view(np.uint32))

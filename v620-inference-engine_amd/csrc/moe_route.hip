@@ -299,12 +299,17 @@ __global__ __launch_bounds__(1024) void route_slots_kernel(RouteArgs a) {
 // one 64-bit mask; a pair's rank among them is a popcount below its bit.
 // The whole routing of a decode batch by one block of 1024 threads; logit(t)
 // gives token t's row loader (expert index -> logit).
+// Static LDS of the routing body (in every kernel that routes): its top-k,
+// mask, offset and scan arrays. Launchers count it against the CU's 160 KiB.
+constexpr size_t ROUTE_STATIC_LDS = 64 * 64 * 4 + 1024 * 8 + 1024 * 4 + 16 * 2 * 4;
+
 template <int PER, class RowFn>
 __device__ __forceinline__ void route_small_body(const RouteArgs &a, const ExpfGlibc &ex, RowFn logit_row) {
     __shared__ int32_t s_te[64 * 64];
     __shared__ unsigned long long s_mask[1024];
     __shared__ int32_t s_off[1024];
     __shared__ uint32_t s_sum[16][2];
+    static_assert(sizeof(s_te) + sizeof(s_mask) + sizeof(s_off) + sizeof(s_sum) == ROUTE_STATIC_LDS, "static LDS");
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int T = a.T, E = a.E, k = a.topk, P = T * k;
     if (tid < E) s_mask[tid] = 0ull;
@@ -559,18 +564,26 @@ __global__ __launch_bounds__(EPB *WPE *WAVE) void router_full_kernel(RouteArgs a
 // 8192 (runs of 8 weights: at most 8 per lane with 2 waves per expert)
 // (E <= 512: the routing's per-lane logits then fit the 1024-thread block's
 // registers)
-bool router_full_ok(int T, int E, int H) { return T <= 8 && H % 1024 == 0 && H <= 8192 && E <= 512 && E % 8 == 0; }
+// (and its activations, part sums and logits in LDS beside the routing's
+// static arrays fit the CU's 160 KiB: at H = 8192 and T = 8 only E <= 64 fits,
+// at H = 4096 every E up to 512 does)
+static size_t router_full_lds(int T, int E, int H) {
+    constexpr int EPB = 8, WPE = 2;
+    return size_t(T) * H * 2 + size_t(T) * EPB * WPE * 4 + size_t(T) * E * 4;
+}
+bool router_full_ok(int T, int E, int H) {
+    return T <= 8 && H % 1024 == 0 && H <= 8192 && E <= 512 && E % 8 == 0 &&
+           router_full_lds(T, E, H) + ROUTE_STATIC_LDS <= 160 * 1024;
+}
 
 static void launch_router_full(const RouteArgs &a, const RouterArgs &r, hipStream_t s) {
     constexpr int EPB = 8, WPE = 2;
     const int per = (a.E + WAVE - 1) / WAVE;
-    const size_t lds = size_t(a.T) * r.H * 2 + size_t(a.T) * EPB * WPE * 4 + size_t(a.T) * a.E * 4;
+    const size_t lds = router_full_lds(a.T, a.E, r.H);
     const unsigned grid = unsigned((a.E + EPB - 1) / EPB);
     const int nch = r.H / WPE / 8;  // runs of 8 per wave
     auto go = [&](auto kern) {
-        if (lds > 48 * 1024)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      int(lds));
+        if (lds > 48 * 1024) raise_lds_limit(reinterpret_cast<const void *>(kern));
         kern<<<grid, EPB * WPE * WAVE, lds, s>>>(a, r);
     };
     auto pick = [&](auto nc) {
@@ -597,9 +610,7 @@ void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s)
     const dim3 grid(unsigned((a.E + 15) / 16), unsigned(r.H / r.kl));
     const size_t lds = router_lds_bytes(a.T, r.kl);
     auto go = [&](auto kern) {
-        if (lds > 48 * 1024)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      int(lds));
+        if (lds > 48 * 1024) raise_lds_limit(reinterpret_cast<const void *>(kern));
         kern<<<grid, 1024, lds, s>>>(a, r);
     };
     if (per <= 1) go(router_route_kernel<1>);

@@ -16,6 +16,9 @@ struct LaunchShape {
     int max_blocks, cus;
 };
 LaunchShape persistent_shape(const void *kernel, int threads, size_t lds);
+// Raises a kernel's dynamic-LDS limit (once per kernel and device) to what the
+// CU's 160 KiB leave beside its static LDS.
+void raise_lds_limit(const void *kernel);
 
 struct GemvArgs {
     const uint32_t *W;

@@ -64,6 +64,22 @@ __global__ void from_engine_kernel(const uint32_t *__restrict__ in, uint32_t *__
     out[i] = r;
 }
 
+void raise_lds_limit(const void *kernel) {
+    static std::mutex mu;
+    static std::vector<std::pair<const void *, int>> raised;  // (kernel, device) with the limit at its maximum
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(mu);
+    if (std::find(raised.begin(), raised.end(), std::make_pair(kernel, dev)) != raised.end()) return;
+    // the dynamic-LDS limit is a per-kernel attribute: set once to what the
+    // CU's 160 KiB leave beside the kernel's static LDS, so a launch with less
+    // never lowers it under one with more (also across threads)
+    hipFuncAttributes fa{};
+    const size_t st = hipFuncGetAttributes(&fa, kernel) == hipSuccess ? fa.sharedSizeBytes : 0;
+    (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(160 * 1024 - st));
+    raised.emplace_back(kernel, dev);
+}
+
 LaunchShape persistent_shape(const void *kernel, int threads, size_t lds) {
     struct Entry {
         const void *k;
@@ -73,16 +89,10 @@ LaunchShape persistent_shape(const void *kernel, int threads, size_t lds) {
     };
     static std::mutex mu;
     static std::vector<Entry> cache;
-    static std::vector<std::pair<const void *, int>> raised;  // (kernel, device) with the LDS limit at its maximum
+    if (lds > 64 * 1024) raise_lds_limit(kernel);
     int dev = 0;
     (void)hipGetDevice(&dev);
     std::lock_guard<std::mutex> lk(mu);
-    // the dynamic-LDS limit is a per-kernel attribute: set once to the CU's
-    // 160 KiB, so a launch with less never lowers it under one with more
-    if (lds > 64 * 1024 && std::find(raised.begin(), raised.end(), std::make_pair(kernel, dev)) == raised.end()) {
-        (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        raised.emplace_back(kernel, dev);
-    }
     for (const Entry &e : cache)
         if (e.k == kernel && e.dev == dev && e.threads == threads && e.lds == lds) return e.shape;
     int cus = 0, per_cu = 0;
