@@ -3,8 +3,9 @@ whole decode step into a graph, src/engine/decode.hip:166-181).
 
 One decode layer: QKV projection, routing, gathered experts, combine and the
 down projection, the fused MoE block (router GEMV, routing, experts and the
-combine, whose cross-block counters must be left at zero by every call), plus
-a prefill GEMM, captured once and replayed several times with the program's own eager work and synchronisations in between.
+combine, whose cross-block counters must be left at zero by every call) at
+batches 4 and 1, the shared expert on tiled fp16 weights (SwiGLU x gate folded
+into the down GEMV, and as two launches), plus a prefill GEMM, captured once and replayed several times with the program's own eager work and synchronisations in between.
 Every replay must reproduce the eager results bit for bit (all kernels are
 deterministic), and the eager results must match the oracle.
 """
@@ -50,6 +51,21 @@ def test_decode_layer_graph_replays(gpu, oracle):
     router_w = to_dev(Wr, gpu)
     mdb = qwq4.MoeDecode(M, E, k, H, F, gpu)
     mout = torch.empty((M, H), dtype=torch.bfloat16, device=gpu)
+    # batch 1 of the fused block (down projection and combine in one kernel)
+    x1 = x[:1].contiguous()
+    mdb1 = qwq4.MoeDecode(1, E, k, H, F, gpu)
+    mout1 = torch.empty((1, H), dtype=torch.float32, device=gpu)
+    # the shared expert on fp16 weights tiled at load: gate/up/gate-logit GEMV,
+    # then the SwiGLU x gate folded into the down GEMV, and as two launches
+    SF = 256
+    gu16 = (torch.randn((2 * SF + 1, H), generator=torch.Generator(device=gpu).manual_seed(72), device=gpu) * 0.05).half()
+    dn16 = (torch.randn((H, SF), generator=torch.Generator(device=gpu).manual_seed(73), device=gpu) * 0.05).half()
+    gu16t, dn16t = qwq4.w16_tile(gu16), qwq4.w16_tile(dn16)
+    xh = x.float().half()
+    v = torch.empty((M, 2 * SF + 1), dtype=torch.float32, device=gpu)
+    hs16 = torch.empty((M, SF), dtype=torch.float16, device=gpu)
+    sh = torch.empty((M, H), dtype=torch.float32, device=gpu)
+    sh3 = torch.empty((M, H), dtype=torch.float32, device=gpu)
 
     def layer():
         qwq4.gemv(*dq, x, QKV, H, M, y=yq, y_bf16=True)
@@ -59,8 +75,13 @@ def test_decode_layer_graph_replays(gpu, oracle):
         qwq4.gemv(*dd, h2, H, F * 2, M, y=yd)
         qwq4.gemm(*dq, X, QKV, H, Y=Y, workspace=ws)
         qwq4.moe_decode(router_w, x, k, eg, eu, ed, E, F, buf=mdb, out=mout)
+        qwq4.moe_decode(router_w, x1, k, eg, eu, ed, E, F, buf=mdb1, out=mout1, out_bf16=False)
+        qwq4.gemv_w16_tiled(gu16t, 2 * SF + 1, H, xh, M, y=v)
+        qwq4.swiglu_gemv_w16_tiled(dn16t, H, v, SF, M, y=sh)
+        qwq4.swiglu_gate(v, SF, h=hs16)
+        qwq4.gemv_w16_tiled(dn16t, H, SF, hs16, M, y=sh3)
 
-    outs = (yq, yd, out, Y, r.top_e, r.pair_tok, h, mout, mdb.logits, mdb.top_e)
+    outs = (yq, yd, out, Y, r.top_e, r.pair_tok, h, mout, mdb.logits, mdb.top_e, mout1, mdb1.top_e, v, hs16, sh, sh3)
     layer()
     torch.cuda.synchronize()
     eager = [o.clone() for o in outs]
@@ -72,6 +93,11 @@ def test_decode_layer_graph_replays(gpu, oracle):
     assert rel_err(host(Y), oracle.q4_linear(*Wq, QKV, H, Xf)) <= TOL
     ml = host(mdb.logits)
     assert bf16_err_ok(host(mout), oracle.moe(xf, ml, k, *ex))
+    assert rel_err(host(mout1), oracle.moe(xf[:1], host(mdb1.logits), k, *ex)) <= TOL
+    assert torch.equal(sh.view(torch.uint8), sh3.view(torch.uint8))
+    hsb = host(hs16.view(torch.int16)).view(np.uint16)
+    assert rel_err(host(sh), oracle.linear_w16(host(dn16.view(torch.int16)).view(np.uint16),
+                                               hsb.view(np.float16).astype(np.float32), True)) <= TOL
 
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
