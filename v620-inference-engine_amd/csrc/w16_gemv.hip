@@ -13,7 +13,7 @@
 // (fp32 sums). The kernel shape is the q4 GEMV's (q4_gemv_impl.cuh): a block
 // holds one 16-row tile, its KS waves split K, each wave requests its whole
 // range of weight rows (16 B per lane per 32-element MFMA step, up to
-// W16_STEPS steps at once) before anything waits, the activations are staged
+// 8 or 16 steps at once, WS below) before anything waits, the activations are staged
 // in LDS, and the KS partial sums are added through LDS in k-part order.
 #include <type_traits>
 
