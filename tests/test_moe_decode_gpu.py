@@ -33,6 +33,7 @@ def _case(gpu, seed, T, E, H, F, k, with_shared):
                                                    # config 3's full size at batches 1, 4 (combine folded
                                                    # into the down projection) and 32 (separate combine)
                                                    (1, 256, 4096, 1536, 8, True, True),
+                                                   (2, 256, 4096, 1536, 8, True, False),
                                                    (4, 256, 4096, 1536, 8, False, False),
                                                    (32, 256, 4096, 1536, 8, True, True)])
 def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
@@ -61,14 +62,16 @@ def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
         assert rel_err(outs[0], ref) <= TOL
 
 
-@pytest.mark.parametrize("T,E,H,F,k", [(1, 64, 1024, 256, 4), (3, 64, 1024, 512, 4), (4, 64, 1024, 256, 4),
+@pytest.mark.parametrize("T,E,H,F,k", [(1, 64, 1024, 256, 4), (2, 64, 1024, 256, 4), (2, 16, 1024, 256, 8),
+                                       (3, 64, 1024, 512, 4), (4, 64, 1024, 256, 4),
                                        (6, 64, 1024, 256, 4), (6, 64, 1024, 512, 4), (1, 256, 4096, 1536, 8),
-                                       (4, 256, 4096, 1536, 8)])
+                                       (2, 256, 4096, 1536, 8), (4, 256, 4096, 1536, 8)])
 def test_moe_decode_matches_unfused_path(gpu, T, E, H, F, k):
     """The block against routing + experts + combine as separate calls: yp
     bit-identical, on both sides of the switch that folds the combine into
-    the down projection (up to 4 tokens) and at config 3's full size (down
-    projection with 6 groups per wave)."""
+    the down projection (up to 4 tokens; batches 1 and 2 in one block per 16
+    output rows), with experts chosen by both tokens (E = 16, k = 8), and at
+    config 3's full size (down projection with 6 groups per wave)."""
     print(f"moe_decode vs unfused T={T} E={E} H={H} F={F}", flush=True)
     ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 77 + T, T, E, H, F, k, True)
     out, buf = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
