@@ -105,3 +105,30 @@ def test_moe_decode_router_lds_limit(gpu, oracle, T, E):
     h, yp = qwq4.moe_experts_gemv(g, u, d, r, to_dev(xb, gpu), E, F)
     o2 = qwq4.moe_combine(yp, r, H, shared=to_dev(sh, gpu), out_bf16=False)
     assert np.array_equal(host(out).view(np.uint32), host(o2).view(np.uint32))
+
+
+def _random_moe(n, seed):
+    r = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        E = 8 * int(r.integers(2, 33))
+        out.append((int(r.integers(1, 3)), E, 1024 * int(r.integers(1, 5)), 128 * int(r.integers(1, 17)),
+                    int(r.integers(1, min(E, 10) + 1))))
+    return out
+
+
+@pytest.mark.parametrize("T,E,H,F,k", _random_moe(10, 2033))
+def test_moe_decode_random_small_batches(gpu, T, E, H, F, k):
+    """Seeded random shapes at batches 1 and 2 (E 16-256, H 1024-4096, F
+    128-2048, k 1-10): the fused block (one-block-per-row-range down kernels
+    where they apply, the folded combine elsewhere) against the unfused calls,
+    bit for bit."""
+    print(f"moe_decode random T={T} E={E} H={H} F={F} k={k}", flush=True)
+    ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 300 + T + E + F, T, E, H, F, k, True)
+    out, buf = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
+                               out_bf16=False)
+    r = qwq4.moe_route(buf.logits, k)
+    h, yp = qwq4.moe_experts_gemv(g, u, d, r, to_dev(xb, gpu), E, F)
+    o2 = qwq4.moe_combine(yp, r, H, shared=to_dev(sh, gpu), out_bf16=False)
+    assert np.array_equal(host(yp), host(buf.yp))
+    assert np.array_equal(host(out).view(np.uint32), host(o2).view(np.uint32))

@@ -188,3 +188,49 @@ def test_moe_block_with_shared_expert(gpu, oracle, T, tiled):
     logits = host(buf.logits)
     ref = oracle.moe(xf, logits, k, *ex) + oracle.shared_expert(xf, gu_b, dn_b, f16_gu=False, f16_down=True)
     assert rel_err(host(out), ref) <= TOL
+
+
+def _random_w16(n, seed):
+    r = np.random.default_rng(seed)
+    return [(int(r.integers(1, 5000)), 32 * int(r.integers(1, 257)), int(r.integers(1, 33)), bool(r.integers(0, 2)))
+            for _ in range(n)]
+
+
+@pytest.mark.parametrize("N,K,M,f16", _random_w16(12, 2031))
+def test_w16_gemv_tiled_random_shapes(gpu, oracle, N, K, M, f16):
+    """Seeded random shapes (any N, K a multiple of 32 up to 8192, batch 1-32,
+    fp16 or bf16): the tiled GEMV equals the row-major one bit for bit (every
+    launch-shape choice: K split, steps in flight, register or direct staging,
+    row-split launches) and the oracle."""
+    print(f"w16 tiled random N={N} K={K} M={M} f16={f16}", flush=True)
+    Wb, _ = w16(N + K, f"wr{N}x{K}", N, K, f16)
+    xb, xf = rows(N + K, f"xr{M}x{K}", M, K, f16)
+    W, x = to_dev(Wb, gpu), to_dev(xb, gpu)
+    y = host(qwq4.gemv_w16_tiled(qwq4.w16_tile(W), N, K, x, M, f16=f16))
+    assert np.array_equal(y.view(np.uint32), host(qwq4.gemv_w16(W, x, M, f16=f16)).view(np.uint32))
+    assert rel_err(y, oracle.linear_w16(Wb, xf, f16)) <= TOL
+
+
+def _random_swiglu(n, seed):
+    r = np.random.default_rng(seed)
+    return [(int(r.integers(1, 5000)), 32 * int(r.integers(1, 129)), int(r.integers(1, 33))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("N,n,M", _random_swiglu(12, 2032))
+def test_w16_swiglu_gemv_tiled_random_shapes(gpu, N, n, M):
+    """Seeded random shapes (any N, n a multiple of 32 up to 4096, batch 1-32): the
+    SwiGLU x gate folded into the down GEMV equals qw_swiglu_gate followed by
+    qw_w16_gemv_tiled bit for bit, or is rejected when the rows exceed the staging
+    LDS (as the two-launch form, which splits them, is not)."""
+    print(f"w16 swiglu random N={N} n={n} M={M}", flush=True)
+    Wb, _ = w16(N + n, f"dr{N}x{n}", N, n, True)
+    v = (np.random.default_rng(N + n + M).standard_normal((M, 2 * n + 1)) * 2).astype(np.float32)
+    Wt = qwq4.w16_tile(to_dev(Wb, gpu))
+    dv = to_dev(v, gpu)
+    ref = host(qwq4.gemv_w16_tiled(Wt, N, n, qwq4.swiglu_gate(dv, n), M, f16=True))
+    try:
+        y = host(qwq4.swiglu_gemv_w16_tiled(Wt, N, dv, n, M))
+    except RuntimeError as err:
+        assert "staging LDS" in str(err) and M * n * 2 > 96 * 1024
+        return
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
