@@ -22,8 +22,8 @@ def test_gemm_small_full_check(gpu, oracle, T, N, K):
 @pytest.mark.parametrize("N,K", [(12288, 4096), (4096, 6144)])
 @pytest.mark.parametrize("T", [4096, 2048])
 def test_gemm_prefill_chunk_sampled(gpu, oracle, N, K, T):
-    """4096-token chunk (256 x 256 tiles) and a 2048-token micro-batch (256
-    tokens x 128 weight rows), bf16 out; checked on sampled tokens and rows
+    """4096-token chunk (256 x 256 tiles) and a 2048-token micro-batch (256 x
+    256 tiles and 256 x 128 halves, or 256 x 128 only for 6144->4096), bf16 out; checked on sampled tokens and rows
     (fp64 oracle), first and last included."""
     print(f"gemm sampled T={T} N={N} K={K}", flush=True)
     W, S, Z = synth.q4_weights(52, f"p{N}x{K}", N, K)
@@ -35,6 +35,23 @@ def test_gemm_prefill_chunk_sampled(gpu, oracle, N, K, T):
     rows = np.sort(np.unique(np.r_[0, N - 1, r.choice(N, 512, replace=False)]))
     ref = oracle.q4_linear(W[rows], S[rows], Z[rows], len(rows), K, xf[toks])
     assert bf16_err_ok(Y[np.ix_(toks, rows)], ref)
+
+
+@pytest.mark.parametrize("T", [2048, 3072, 2304])
+def test_gemm_tile_shapes_bit_identical(gpu, T):
+    """A token row's result does not depend on the tile shape that computed it:
+    2048 and 3072 tokens of 4096->12288 (whole 256 x 256 rounds plus 256 x 128
+    halves in one launch) and 2304 (128 x 256 tiles) against the same rows of a
+    4096-token run (256 x 256 tiles only), bit for bit."""
+    N, K = 12288, 4096
+    print(f"gemm tile shapes T={T}", flush=True)
+    W, S, Z = synth.q4_weights(53, f"m{N}x{K}", N, K)
+    xb, _ = synth.acts(53, f"mx{K}", 4096, K)
+    dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
+    X = to_dev(xb, gpu)
+    Y4 = host(qwq4.gemm(dW, dS, dZ, X, N, K))
+    YT = host(qwq4.gemm(dW, dS, dZ, X[:T].contiguous(), N, K))
+    assert np.array_equal(YT.view(np.uint32), Y4[:T].view(np.uint32))
 
 
 def test_gemm_microbatch_fp32_out(gpu, oracle):

@@ -50,27 +50,13 @@ void launch_x_to_f16(const uint16_t *X, int ldx, int T, int K, uint16_t *Xh, hip
     x_to_f16_kernel<<<unsigned((n8 + 255) / 256), 256, 0, s>>>(X, ldx, T, K, Xh);
 }
 
-template <bool HAS_Z, bool Y_BF16, int GB_M, int BN = GB_N>
-__global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
-                                                            const uint16_t *St,
-                                                            const uint16_t *Zt,
-                                                            const uint16_t *__restrict__ Xh, int lda, int T,
-                                                            void *__restrict__ Y, int ldy, int N, int K) {
+// One GB_M x BN output tile at tokens t0.., weight rows n0..
+template <bool HAS_Z, bool Y_BF16, int GB_M, int BN>
+__device__ __forceinline__ void gemm_tile_at(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt,
+                                             const uint16_t *__restrict__ Xh, int lda, int T, void *__restrict__ Y,
+                                             int ldy, int N, int K, int t0, int n0) {
     using Sh = GemmShape<GB_M, BN>;
     const int tid = threadIdx.x, wave = tid / WAVE;
-    // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs;
-    // give each XCD a contiguous, token-major range of tiles so the blocks
-    // sharing an X tile run together and hit the same L2
-    int bx = blockIdx.x, by = blockIdx.y;
-    {
-        const int nb = gridDim.x * gridDim.y, w = blockIdx.y * gridDim.x + blockIdx.x;
-        if (nb % 8 == 0) {
-            const int lin = (w % 8) * (nb / 8) + w / 8;
-            by = lin / gridDim.x;
-            bx = lin % gridDim.x;
-        }
-    }
-    const int t0 = by * GB_M, n0 = bx * BN;
     const BRow b(Wt, St, Zt, min(n0 + b_tile_row<BN>(), N - 1), K / QGROUP);
     f32x16 acc[2][Sh::NJ];
 #pragma unroll
@@ -93,6 +79,45 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
         });
 }
 
+// XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; give each
+// XCD a contiguous range of the nb items so that the blocks sharing an X tile
+// run together and hit the same L2
+__device__ __forceinline__ int xcd_item(int w, int nb) { return nb % 8 == 0 ? (w % 8) * (nb / 8) + w / 8 : w; }
+
+template <bool HAS_Z, bool Y_BF16, int GB_M, int BN = GB_N>
+__global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
+                                                            const uint16_t *St,
+                                                            const uint16_t *Zt,
+                                                            const uint16_t *__restrict__ Xh, int lda, int T,
+                                                            void *__restrict__ Y, int ldy, int N, int K) {
+    // token-major tile order (consecutive items share their X rows)
+    const int lin = xcd_item(int(blockIdx.y * gridDim.x + blockIdx.x), int(gridDim.x * gridDim.y));
+    const int by = lin / gridDim.x, bx = lin % gridDim.x;
+    gemm_tile_at<HAS_Z, Y_BF16, GB_M, BN>(Wt, St, Zt, Xh, lda, T, Y, ldy, N, K, by * GB_M, bx * BN);
+}
+
+// 256 x 256 tiles that do not fill whole rounds of the chip: the first nbig
+// (whole rounds) run as they are; each remaining tile runs as two 256 x 128
+// halves, so the last round has twice the blocks at half the work each
+// instead of a partly idle round of whole tiles. Tiles are numbered
+// token-major over the 256 x 256 grid of nbx tiles per row.
+template <bool HAS_Z, bool Y_BF16>
+__global__ __launch_bounds__(G_THREADS) void q4_gemm_mixed_kernel(const uint32_t *Wt, const uint16_t *St,
+                                                                  const uint16_t *Zt,
+                                                                  const uint16_t *__restrict__ Xh, int lda, int T,
+                                                                  void *__restrict__ Y, int ldy, int N, int K,
+                                                                  int nbx, int nbig, int nhalf) {
+    const int w = blockIdx.x;
+    if (w < nbig) {
+        const int lin = xcd_item(w, nbig);
+        gemm_tile_at<HAS_Z, Y_BF16, 256, 256>(Wt, St, Zt, Xh, lda, T, Y, ldy, N, K, lin / nbx * 256, lin % nbx * 256);
+    } else {
+        const int hw = xcd_item(w - nbig, nhalf), lin = nbig + hw / 2;
+        gemm_tile_at<HAS_Z, Y_BF16, 256, 128>(Wt, St, Zt, Xh, lda, T, Y, ldy, N, K, lin / nbx * 256,
+                                              lin % nbx * 256 + (hw % 2) * 128);
+    }
+}
+
 template <bool HAS_Z, bool Y_BF16, int GB_M, int BN = GB_N>
 static void launch_gemm_t(const GemmArgs &a, const uint16_t *Xh, int lda, hipStream_t s) {
     auto kern = q4_gemm_kernel<HAS_Z, Y_BF16, GB_M, BN>;
@@ -101,8 +126,17 @@ static void launch_gemm_t(const GemmArgs &a, const uint16_t *Xh, int lda, hipStr
 }
 
 // 256 x 256 tiles when they fill whole rounds of the chip (or many rounds);
-// else 256 tokens x 128 weight rows when those do (the same dequant work per
-// MFMA, e.g. 2048-token micro-batches); else 128 x 256.
+// past one round with at most half a round left over, whole rounds of them
+// plus the rest as 256 x 128 halves in the same launch (2048-token
+// micro-batches of 4096->12288); else 256 tokens x 128 weight rows when those
+// fill whole rounds (the same dequant work per MFMA); else 128 x 256.
+template <bool HAS_Z, bool Y_BF16>
+static void launch_gemm_mixed(const GemmArgs &a, const uint16_t *Xh, int lda, int nbig, int nhalf, hipStream_t s) {
+    const int nbx = (a.N + 255) / 256;
+    q4_gemm_mixed_kernel<HAS_Z, Y_BF16><<<unsigned(nbig + nhalf), G_THREADS, 0, s>>>(
+        a.W, a.S, a.Z, Xh, lda, a.T, a.Y, a.ldy, a.N, a.K, nbx, nbig, nhalf);
+}
+
 template <bool HAS_Z, bool Y_BF16>
 static void launch_gemm_m(const GemmArgs &a, const uint16_t *Xh, int lda, hipStream_t s) {
     int cus = 0, dev = 0;
@@ -113,8 +147,10 @@ static void launch_gemm_m(const GemmArgs &a, const uint16_t *Xh, int lda, hipStr
         const double rounds = double(nb) / cus;
         return rounds >= 4.0 || (rounds >= 1.0 && rounds - double(int64_t(rounds)) < 0.01);
     };
-    const int64_t t256 = (a.T + 255) / 256;
-    if (whole(int64_t((a.N + 255) / 256) * t256)) launch_gemm_t<HAS_Z, Y_BF16, 256>(a, Xh, lda, s);
+    const int64_t t256 = (a.T + 255) / 256, nb = int64_t((a.N + 255) / 256) * t256;
+    if (whole(nb)) launch_gemm_t<HAS_Z, Y_BF16, 256>(a, Xh, lda, s);
+    else if (nb > cus && 2 * (nb % cus) <= cus)  // e.g. 2048 tokens x 12288 rows: 256 whole tiles + 256 halves
+        launch_gemm_mixed<HAS_Z, Y_BF16>(a, Xh, lda, int(nb / cus * cus), int(2 * (nb % cus)), s);
     else if (whole(int64_t((a.N + 127) / 128) * t256)) launch_gemm_t<HAS_Z, Y_BF16, 256, 128>(a, Xh, lda, s);
     else launch_gemm_t<HAS_Z, Y_BF16, 128>(a, Xh, lda, s);
 }
