@@ -63,6 +63,7 @@ def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
 
 
 @pytest.mark.parametrize("T,E,H,F,k", [(1, 64, 1024, 256, 4), (2, 64, 1024, 256, 4), (2, 16, 1024, 256, 8),
+                                       (1, 4, 1024, 256, 2), (2, 4, 1024, 256, 3), (2, 8, 1024, 256, 8),
                                        (3, 64, 1024, 512, 4), (4, 64, 1024, 256, 4),
                                        (6, 64, 1024, 256, 4), (6, 64, 1024, 512, 4), (1, 256, 4096, 1536, 8),
                                        (2, 256, 4096, 1536, 8), (4, 256, 4096, 1536, 8)])
@@ -70,7 +71,8 @@ def test_moe_decode_matches_unfused_path(gpu, T, E, H, F, k):
     """The block against routing + experts + combine as separate calls: yp
     bit-identical, on both sides of the switch that folds the combine into
     the down projection (up to 4 tokens; batches 1 and 2 in one block per 16
-    output rows), with experts chosen by both tokens (E = 16, k = 8), and at
+    output rows), with experts chosen by both tokens (E = 16, k = 8; E = 8, k = 8:
+    every expert twice), fewer experts than the kernels' waves (E = 4), and at
     config 3's full size (down projection with 6 groups per wave)."""
     print(f"moe_decode vs unfused T={T} E={E} H={H} F={F}", flush=True)
     ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 77 + T, T, E, H, F, k, True)

@@ -241,8 +241,9 @@ __global__ __launch_bounds__(1024) void moe_down_t1_kernel(const uint32_t *dw, c
               n = lane % 16;
     const int y = wave / 2, kp = wave % 2;
     // n_active and active[y] requested together (one latency); the weight
-    // loads need only e
-    const int na = ld_uniform(n_active, 0), ea = ld_uniform(active, y);
+    // loads need only e (active holds E entries: the read stays inside them,
+    // the value is used only for y < n_active <= E)
+    const int na = ld_uniform(n_active, 0), ea = ld_uniform(active, min(y, E - 1));
     const int rows = min(na, topk);
     const bool live = y < rows;  // wave-uniform
     const int e = live ? min(max(ea, 0), E - 1) : 0;
@@ -306,7 +307,7 @@ __global__ __launch_bounds__(1024) void moe_down_t2_kernel(const uint32_t *dw, c
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, y = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
               n = lane % 16;
-    const int na = ld_uniform(n_active, 0), ea = ld_uniform(active, y);
+    const int na = ld_uniform(n_active, 0), ea = ld_uniform(active, min(y, E - 1));  // (as in the batch-1 kernel)
     const int P = 2 * topk;  // slots (pairs) of the two tokens
     const bool live = y < min(na, 16);  // wave-uniform
     const int e = live ? min(max(ea, 0), E - 1) : 0;
