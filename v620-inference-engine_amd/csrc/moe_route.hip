@@ -124,6 +124,29 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return readlane64(v, 63);
 }
 
+// Wave maximum of a 32-bit unsigned value (lane 63's result, read to every
+// lane): each step's DPP move fuses into the max instruction.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#define QW_UMAX_STEP(ctrl, rm) v = max(v, QW_DPP(v, ctrl, rm, 0xf, false));
+    QW_UMAX_STEP(DPP_XOR1, 0xf)
+    QW_UMAX_STEP(DPP_XOR2, 0xf)
+    QW_UMAX_STEP(DPP_HALF_MIRROR, 0xf)
+    QW_UMAX_STEP(DPP_MIRROR, 0xf)
+    QW_UMAX_STEP(DPP_BCAST15, 0xa)
+    QW_UMAX_STEP(DPP_BCAST31, 0xc)
+#undef QW_UMAX_STEP
+    return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
+}
+
+// The wave maximum of 64-bit keys as two 32-bit maxima: the high words',
+// then the low words' among the lanes whose high word is that maximum (the
+// same order as comparing whole keys).
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
+    const uint32_t hi = uint32_t(v >> 32), mh = wave_max_u32(hi);
+    const uint32_t ml = wave_max_u32(hi == mh ? uint32_t(v) : 0u);
+    return (uint64_t(mh) << 32) | ml;
+}
+
 __device__ __forceinline__ float wave_max_f32(float v) {
 #define QW_FMAX_STEP(ctrl) v = fmaxf(v, __builtin_bit_cast(float, QW_DPP(__builtin_bit_cast(uint32_t, v), ctrl, 0xf, 0xf, false)));
     QW_FMAX_STEP(DPP_XOR1)
@@ -180,17 +203,26 @@ __device__ __forceinline__ void topk_wave(const ExpfGlibc &ex, LogitFn logit, in
         const float p = ex(v[i] - mx);
         key[i] = idx < E ? (uint64_t(__builtin_bit_cast(uint32_t, p)) << 32) | uint32_t(~uint32_t(idx)) : 0ull;
     }
+    // the lane's keys in descending order (insertion network), so that its
+    // best untaken key is always key[0]
+#pragma unroll
+    for (int i = 1; i < PER; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j) {
+            const uint64_t a = key[j - 1], b = key[j];
+            key[j - 1] = a > b ? a : b;
+            key[j] = a > b ? b : a;
+        }
     double top = 0.0;
     int my_e = 0;
     float my_p = 0.f;
     for (int j = 0; j < k; ++j) {
-        uint64_t best = key[0];
+        const uint64_t w = wave_max_key(key[0]);
+        if (key[0] == w) {  // taken (keys are distinct: one lane): its next key moves up
 #pragma unroll
-        for (int i = 1; i < PER; ++i) best = key[i] > best ? key[i] : best;
-        const uint64_t w = wave_max_u64(best);
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (key[i] == w) key[i] = 0ull;  // taken
+            for (int i = 0; i + 1 < PER; ++i) key[i] = key[i + 1];
+            key[PER - 1] = 0ull;
+        }
         const float p = __builtin_bit_cast(float, uint32_t(w >> 32));
         top += double(p);
         if (lane == j) {
@@ -394,6 +426,25 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// The routing block's copy of every logit into LDS (agent-scope loads, eight
+// in flight per thread before their writes), then a barrier.
+__device__ __forceinline__ void load_logits_lds(const float *logits, int n, float *sl) {
+    const int bd = blockDim.x;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * bd) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = ld_agent(logits + min(i0 + j * bd, n - 1));
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (i0 + j * bd < n) sl[i0 + j * bd] = v[j];
+    }
+    __syncthreads();
+}
+
+// Whether the K-sliced router's last block routes from LDS: the T x E logits
+// fit beside the routing's static arrays.
+__host__ __device__ inline bool router_lds_route(int T, int E) { return size_t(T) * E * 4 <= 96 * 1024; }
+
 template <int PER>
 __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterArgs r) {
     extern __shared__ __align__(16) unsigned char smem[];  // x slice, [T][kl]
@@ -403,20 +454,34 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
     const int T = a.T, E = a.E, H = r.H, kc = r.kl / 8, k0 = blockIdx.y * r.kl;
     const int e = blockIdx.x * 16 + wave;
     // kl <= 512: each lane owns at most one run of 8 weights of its expert's
-    // slice; they are requested before the activations are staged
+    // slice; they are requested before the activations are staged. Lanes
+    // past the slice (and waves past E) read a valid run and zero it: the
+    // token loop below then has no branch around the weights, so the wait
+    // for them is not repeated per token. On this GPU stores count on the
+    // same counter as loads, so each repeated wait also waited for the
+    // previous token's logit store (one memory round trip per token).
     const bool mine = e < E && lane < kc;
-    float4 w0 = {0.f, 0.f, 0.f, 0.f}, w1 = w0;
-    if (mine) {
-        const float *w = r.w + int64_t(e) * H + k0 + lane * 8;
-        w0 = *reinterpret_cast<const float4 *>(w);
-        w1 = *reinterpret_cast<const float4 *>(w + 4);
-    }
+    const float *wp = r.w + int64_t(min(e, E - 1)) * H + k0 + min(lane, kc - 1) * 8;
+    float4 w0 = *reinterpret_cast<const float4 *>(wp), w1 = *reinterpret_cast<const float4 *>(wp + 4);
+    if (!mine) w0 = w1 = float4{0.f, 0.f, 0.f, 0.f};
     uint4 *xs = reinterpret_cast<uint4 *>(smem);
-    for (int i = tid; i < T * kc; i += blockDim.x) {
-        const int t = i / kc, c = i - t * kc;
-        xs[i] = *reinterpret_cast<const uint4 *>(r.x + int64_t(t) * H + k0 + c * 8);
+    // activation pieces: four loads in flight per thread before their writes
+    for (int i0 = tid; i0 < T * kc; i0 += 4 * int(blockDim.x)) {
+        uint4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = min(i0 + j * int(blockDim.x), T * kc - 1), t = i / kc, c = i - t * kc;
+            v[j] = *reinterpret_cast<const uint4 *>(r.x + int64_t(t) * H + k0 + c * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (i0 + j * int(blockDim.x) < T * kc) xs[i0 + j * blockDim.x] = v[j];
     }
     __syncthreads();
+    // the weights' one wait, here: every token below then finds them ready
+    // (each token's block is guarded by t < T, and the compiler would
+    // otherwise wait again in each)
+    asm volatile("" ::"v"(w0.x), "v"(w0.y), "v"(w0.z), "v"(w0.w), "v"(w1.x), "v"(w1.y), "v"(w1.z), "v"(w1.w));
     // x rows bf16 or fp16 (a block-uniform choice; both conversions are exact)
     auto dots = [&](auto cvt) {
         if (e >= E) return;
@@ -424,8 +489,8 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
         for (int t = 0; t < 64; ++t) {
             if (t < T) {
                 float s = 0.f;
-                if (mine) {
-                    const uint4 v = xs[t * kc + lane];
+                {
+                    const uint4 v = xs[t * kc + min(lane, kc - 1)];
                     s = fmaf(w0.x, cvt(uint16_t(v.x)), s);
                     s = fmaf(w0.y, cvt(uint16_t(v.x >> 16)), s);
                     s = fmaf(w0.z, cvt(uint16_t(v.y)), s);
@@ -455,21 +520,39 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
         }
         return v;
     };
+    // The routing block reads the logits from LDS (the activation slice's
+    // area, free by then) when they fit: one memory round trip for all of
+    // them instead of one per token and wave.
+    const bool lds_route = router_lds_route(T, E);
+    float *sl = reinterpret_cast<float *>(smem);
     auto route = [&]() {
-        route_small_body<PER>(a, ex, [&](int t) {
-            const float *l = r.logits + int64_t(t) * E;
-            return [l](int i) { return ld_agent(l + i); };
-        });
+        if (lds_route) {
+            route_small_body<PER>(a, ex, [&](int t) {
+                const float *l = sl + t * E;
+                return [l](int i) { return l[i]; };
+            });
+        } else {
+            route_small_body<PER>(a, ex, [&](int t) {
+                const float *l = r.logits + int64_t(t) * E;
+                return [l](int i) { return ld_agent(l + i); };
+            });
+        }
     };
     if (T * E <= 2 * int(blockDim.x)) {
         // few logits (decode batches): the last block of the whole grid sums
         // every logit's slices (the same additions in the same order as the
         // per-group sums below) and routes, one hand-off instead of two
         if (!count_last_block(r.counter, int(gridDim.x * gridDim.y))) return;
-        for (int o = tid; o < TE; o += blockDim.x) st_agent(r.logits + o, slice_sum(o));
-        __builtin_amdgcn_s_waitcnt(0);
+        for (int o = tid; o < TE; o += blockDim.x) {
+            const float v = slice_sum(o);
+            st_agent(r.logits + o, v);
+            sl[o] = v;  // (T * E fits: at most 2048 logits)
+        }
         __syncthreads();
-        route();
+        route_small_body<PER>(a, ex, [&](int t) {
+            const float *l = sl + t * E;
+            return [l](int i) { return l[i]; };
+        });
         return;
     }
     // the last slice block of each group of 16 experts adds the group's
@@ -482,6 +565,7 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
     }
     // and the last group to finish routes
     if (!count_last_block(r.counter, int(gridDim.x))) return;
+    if (lds_route) load_logits_lds(r.logits, TE, sl);
     route();
 }
 
@@ -552,8 +636,7 @@ __global__ __launch_bounds__(EPB *WPE *WAVE) void router_full_kernel(RouteArgs a
         if (ee < E) st_agent(r.logits + int64_t(t) * E + ee, v);
     }
     if (!count_last_block(r.counter, int(gridDim.x))) return;
-    for (int i = tid; i < T * E; i += blockDim.x) sl[i] = ld_agent(r.logits + i);
-    __syncthreads();
+    load_logits_lds(r.logits, T * E, sl);
     route_small_body<PER>(a, ex, [&](int t) {
         const float *l = sl + t * E;
         return [l](int i) { return l[i]; };
@@ -598,7 +681,10 @@ static void launch_router_full(const RouteArgs &a, const RouterArgs &r, hipStrea
     else pick(std::integral_constant<int, 8>());
 }
 
-size_t router_lds_bytes(int T, int kl) { return size_t(T) * kl * 2; }
+size_t router_lds_bytes(int T, int kl, int E) {
+    const size_t x = size_t(T) * kl * 2, l = router_lds_route(T, E) ? size_t(T) * E * 4 : 0;
+    return x > l ? x : l;
+}
 
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s) {
     if (router_full_ok(a.T, a.E, r.H)) {
@@ -608,7 +694,7 @@ void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s)
     // callers guarantee kl in {128, 512}, H % kl == 0 and T <= 64
     const int per = (a.E + WAVE - 1) / WAVE;
     const dim3 grid(unsigned((a.E + 15) / 16), unsigned(r.H / r.kl));
-    const size_t lds = router_lds_bytes(a.T, r.kl);
+    const size_t lds = router_lds_bytes(a.T, r.kl, a.E);
     auto go = [&](auto kern) {
         if (lds > 48 * 1024) raise_lds_limit(reinterpret_cast<const void *>(kern));
         kern<<<grid, 1024, lds, s>>>(a, r);

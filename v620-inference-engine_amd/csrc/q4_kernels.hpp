@@ -112,7 +112,7 @@ struct RouterArgs {
     int32_t *counter;   // [1 + ceil(E / 16)], zero between calls
     int x_f16 = 0;      // x rows are fp16 (else bf16)
 };
-size_t router_lds_bytes(int T, int kl);
+size_t router_lds_bytes(int T, int kl, int E);
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
 // LDS bytes the slot pass needs for (T, E); the C-ABI rejects larger inputs.
 void launch_route(const RouteArgs &a, hipStream_t s);
