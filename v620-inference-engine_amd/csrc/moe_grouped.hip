@@ -9,7 +9,7 @@
 // carries token pair_tok[p]. A tile's height follows from its start and the
 // expert's slot count (tile_rows). Each block runs the shared q4 MFMA GEMM
 // core (q4_gemm_core.cuh) at that height on one list entry and 256 weight
-// rows:
+// rows (64-slot tiles: its register-dequant form, gemm_tile_rd64):
 //   gate/up  A = the tile's gathered token rows of x (fp16 copy in the
 //            workspace), weight rows = 128 gate rows and the same 128 up rows,
 //            interleaved by 32 (32-row groups alternate gate, up); epilogue
@@ -51,19 +51,26 @@ __device__ __forceinline__ void gate_up_tile(const GateUpTile &a, int e, int bas
     const int tid = threadIdx.x, wave = tid / WAVE;
     // weight tile row r = b_tile_row(): 32-row group r / 32 is gate when even,
     // up when odd, for columns j0 + 32 (r / 64) + r % 32 (wave-uniform choice)
-    const int r = b_tile_row(), col = (r / 64) * 32 + r % 32;
+    // (64-row tiles: the row this lane multiplies, 32 wave + lane % 32, the
+    // tile row the register-dequant core gives it)
+    const int r = BM == 64 ? wave * 32 + tid % 32 : b_tile_row(), col = (r / 64) * 32 + r % 32;
     const bool up = (r % 64) >= 32;
     const int64_t wrow = int64_t(e) * a.F + min(j0 + col, a.F - 1);
     const BRow b = up ? BRow(a.uw, a.us, a.uz, wrow, a.H / QGROUP) : BRow(a.gw, a.gs, a.gz, wrow, a.H / QGROUP);
-    const uint16_t *ap[BM / 32];
-#pragma unroll
-    for (int j = 0; j < BM / 32; ++j) ap[j] = a.xh + int64_t(a.pair_tok[base + min(a_load_row(j), M - 1)]) * a.H;
     f32x16 acc[2][Sh::NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
-    gemm_tile<BM, HAS_Z>(ap, b, a.H, acc);
+    if constexpr (BM == 64) {
+        const uint16_t *arow = a.xh + int64_t(a.pair_tok[base + min(wave * 8 + (tid % WAVE) / 8, M - 1)]) * a.H;
+        gemm_tile_rd64<HAS_Z>(arow, b, a.H, acc);
+    } else {
+        const uint16_t *ap[BM / 32];
+#pragma unroll
+        for (int j = 0; j < BM / 32; ++j) ap[j] = a.xh + int64_t(a.pair_tok[base + min(a_load_row(j), M - 1)]) * a.H;
+        gemm_tile<BM, HAS_Z>(ap, b, a.H, acc);
+    }
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
     auto store = [&](int cbase) {
@@ -132,16 +139,21 @@ __device__ __forceinline__ void down_tile(const uint32_t *dw, const uint16_t *ds
     using Sh = GemmShape<BM>;
     const int tid = threadIdx.x, wave = tid / WAVE;
     const int n0 = blockIdx.x * GB_N;
-    const BRow b(dw, ds, dz, int64_t(e) * H + min(n0 + b_tile_row(), H - 1), F / QGROUP);
-    const uint16_t *ap[BM / 32];
-#pragma unroll
-    for (int j = 0; j < BM / 32; ++j) ap[j] = h + int64_t(base + min(a_load_row(j), M - 1)) * F;
+    const int r = BM == 64 ? wave * 32 + tid % 32 : b_tile_row();  // (as in gate_up_tile)
+    const BRow b(dw, ds, dz, int64_t(e) * H + min(n0 + r, H - 1), F / QGROUP);
     f32x16 acc[2][Sh::NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
-    gemm_tile<BM, HAS_Z>(ap, b, F, acc);
+    if constexpr (BM == 64) {
+        gemm_tile_rd64<HAS_Z>(h + int64_t(base + min(wave * 8 + (tid % WAVE) / 8, M - 1)) * F, b, F, acc);
+    } else {
+        const uint16_t *ap[BM / 32];
+#pragma unroll
+        for (int j = 0; j < BM / 32; ++j) ap[j] = h + int64_t(base + min(a_load_row(j), M - 1)) * F;
+        gemm_tile<BM, HAS_Z>(ap, b, F, acc);
+    }
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
     constexpr int YB = YP16 ? 2 : 4;

@@ -259,6 +259,82 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
     }
 }
 
+// A 64-row tile (GemmShape<64>: wave w computes 64 rows x weight rows
+// 32 w .. 32 w + 31) with the weights dequantised in registers instead of
+// through LDS. In a 64-row tile each weight row feeds one wave, so the wave
+// that multiplies a row can dequantise it itself: the dequant then runs in
+// all 8 waves (beside their MFMAs) rather than in 4, and the weight tile's LDS
+// writes, reads and barrier hand-off are gone. Lane (l32, lh) holds weight
+// row 32 w + l32 (b: that row) and K half lh of each 64-K stage: one tiled
+// entry (quarter 2 (ks % 2) + lh of group ks / 2) per stage, requested two
+// stages ahead, one word dequantised per 16-K step. The A fragments are
+// read with the same K mapping (chunk kk + 4 lh). Only A goes through LDS:
+// wave w moves rows 8 w .. 8 w + 7 (arow: this lane's row, lane / 8).
+template <bool HAS_Z>
+__device__ __forceinline__ void gemm_tile_rd64(const uint16_t *arow, const BRow &b, int K, f32x16 (&acc)[2][1]) {
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+    const int l32 = lane % 32, lh = lane / 32, nk = K / GB_K;
+    constexpr int NLD = HAS_Z ? 3 : 2;  // weight-side loads per stage and lane
+    auto bufA = [&](int i) { return i ? lds_a1 : lds_a0; };
+    auto issue_a = [&](int ks, unsigned char *dst) {
+        const int r = wave * 8 + lane / 8, c = (lane % 8) ^ swz_x(r);
+        __builtin_amdgcn_global_load_lds(arow + ks * GB_K + c * 8, dst + wave * 8 * 128, 16, 0, 0);
+    };
+    struct WR {
+        uint4 w;
+        uint16_t s;
+        uint32_t z;
+    };
+    auto issue_w = [&](int ks, WR &r) {
+        ks = min(ks, nk - 1);  // past the end: a valid (unused) load
+        const int g = ks / 2;
+        r.w = b.w[g * 64 + ((ks % 2) * 2 + lh) * 16];
+        r.s = b.s[(g >> 2) * 64 + (g & 3)];
+        if constexpr (HAS_Z) r.z = b.z[(g >> 2) * 8];
+    };
+    auto compute = [&](const unsigned char *a, const WR &r, int ks) {
+        uint32_t sw = r.s, zw = HAS_Z ? r.z : 0u;
+        asm volatile("" : "+v"(sw), "+v"(zw));  // taken here, not at their loads (see commit_b)
+        const int g = ks / 2;
+        const uint32_t zb = zero_bytes(HAS_Z ? (zw >> (b.zs + 4 * (g & 3))) & 0xfu : 8u);
+        const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(sw));
+        const h2 s2 = {sc, sc};
+        const uint32_t words[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
+        uint4 af[2], an[2];
+        auto rd = [&](int kk, uint4 (&f)[2]) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) f[i] = *reinterpret_cast<const uint4 *>(a + swz(i * 32 + l32, kk + 4 * lh));
+        };
+        rd(0, af);
+#pragma unroll
+        for (int kk = 0; kk < GB_K / 16; ++kk) {
+            if (kk + 1 < GB_K / 16) rd(kk + 1, an);
+            const uint4 bf = dequant8(words[kk], zb, s2);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i][0] = mfma32<F16>(af[i], bf, acc[i][0]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) af[i] = an[i];
+        }
+    };
+    WR w0, w1;
+    issue_a(0, bufA(0));
+    issue_w(0, w0);
+    issue_w(1, w1);
+    wait_vm_below<NLD>();  // A(0) and W(0) here; W(1) stays in flight
+    __builtin_amdgcn_s_barrier();
+    auto stage = [&](int ks, int p, WR &cur) {
+        issue_a(min(ks + 1, nk - 1), bufA(p ^ 1));
+        compute(bufA(p), cur, ks);
+        issue_w(ks + 2, cur);
+        wait_vm_below<NLD>();  // everything but W(ks + 2): A(ks + 1) and W(ks + 1) arrived
+        __builtin_amdgcn_s_barrier();
+    };
+    for (int ks = 0; ks < nk; ks += 2) {  // nk is even (K is a multiple of 128)
+        stage(ks, 0, w0);
+        stage(ks + 1, 1, w1);
+    }
+}
+
 // Wave-private LDS transpose for the epilogue: the wave's acc[i][j] (rows
 // 64 wm + 32 i + 8(r/4) + 4 lh + r%4, weight row 32 j + l32 of its slice) is
 // handed to emit(row, col, 16-byte piece) one 64 x 32 column slice at a
