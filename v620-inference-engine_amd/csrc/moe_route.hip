@@ -729,62 +729,94 @@ void launch_route(const RouteArgs &a, hipStream_t s) {
 
 // out[t][j] = shared[t][j] + sum_i w[t][i] * yp[slot[t][i]][j], i in selection
 // order (src/kernels/moe_route.hip:168-185, 201-224). 4 columns per thread.
-// yp rows fp32, or fp16 (YP16)
-template <bool YP16>
-__device__ __forceinline__ float4 yp_row4(const void *yp, int64_t row, int H, int j) {
+// C consecutive groups of 4 elements of a yp row (fp32, or fp16 with YP16):
+// one 16-byte load per 4 fp32 values or per 8 fp16 values.
+template <bool YP16, int C>
+__device__ __forceinline__ void yp_row(const void *yp, int64_t row, int H, int j, float4 (&v)[C]) {
     if constexpr (YP16) {
-        const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(yp) + row * H + j);
-        return make_float4(f16_bits_to_f32(uint16_t(u.x)), f16_bits_to_f32(uint16_t(u.x >> 16)),
-                           f16_bits_to_f32(uint16_t(u.y)), f16_bits_to_f32(uint16_t(u.y >> 16)));
+        const uint16_t *p = static_cast<const uint16_t *>(yp) + row * H + j;
+        uint32_t u[2 * C];
+        if constexpr (C == 2) {
+            const uint4 q = *reinterpret_cast<const uint4 *>(p);
+            u[0] = q.x, u[1] = q.y, u[2] = q.z, u[3] = q.w;
+        } else {
+            const uint2 q = *reinterpret_cast<const uint2 *>(p);
+            u[0] = q.x, u[1] = q.y;
+        }
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            v[c] = make_float4(f16_bits_to_f32(uint16_t(u[2 * c])), f16_bits_to_f32(uint16_t(u[2 * c] >> 16)),
+                               f16_bits_to_f32(uint16_t(u[2 * c + 1])), f16_bits_to_f32(uint16_t(u[2 * c + 1] >> 16)));
     } else {
-        return *reinterpret_cast<const float4 *>(static_cast<const float *>(yp) + row * H + j);
+#pragma unroll
+        for (int c = 0; c < C; ++c) v[c] = *reinterpret_cast<const float4 *>(static_cast<const float *>(yp) + row * H + j + 4 * c);
     }
 }
 
-template <bool YP16>
+// out[t][j] = shared[t][j] + sum_i w_i yp[slot_i][j], selections in order;
+// a thread takes 4 C consecutive elements (C = 2 where H allows: 16-byte
+// loads of fp16 rows).
+template <bool YP16, int C>
 __global__ __launch_bounds__(256) void combine_kernel(const void *__restrict__ yp, const int32_t *__restrict__ tok_slot,
                                                       const float *__restrict__ tok_w, const float *__restrict__ shared,
                                                       int k, int H, void *__restrict__ out, int out_bf16) {
-    const int t = blockIdx.x, j = (blockIdx.y * 256 + threadIdx.x) * 4;
+    const int t = blockIdx.x, j = (blockIdx.y * 256 + threadIdx.x) * 4 * C;
     if (j >= H) return;
-    float4 acc = shared ? *reinterpret_cast<const float4 *>(shared + int64_t(t) * H + j) : make_float4(0, 0, 0, 0);
+    float4 acc[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+        acc[c] = shared ? *reinterpret_cast<const float4 *>(shared + int64_t(t) * H + j + 4 * c) : make_float4(0, 0, 0, 0);
     // up to 8 selections' rows requested together, then added in selection
     // order (the same sums as one at a time)
     for (int i0 = 0; i0 < k; i0 += 8) {
-        float4 v[8];
+        float4 v[8][C];
         float w[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int i = min(i0 + u, k - 1);
             w[u] = tok_w[t * k + i];
-            v[u] = yp_row4<YP16>(yp, int64_t(tok_slot[t * k + i]), H, j);
+            yp_row<YP16, C>(yp, int64_t(tok_slot[t * k + i]), H, j, v[u]);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             if (i0 + u < k) {
-                acc.x += w[u] * v[u].x;
-                acc.y += w[u] * v[u].y;
-                acc.z += w[u] * v[u].z;
-                acc.w += w[u] * v[u].w;
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    acc[c].x += w[u] * v[u][c].x;
+                    acc[c].y += w[u] * v[u][c].y;
+                    acc[c].z += w[u] * v[u][c].z;
+                    acc[c].w += w[u] * v[u][c].w;
+                }
             }
         }
     }
-    if (out_bf16) {
-        uint16_t *o = static_cast<uint16_t *>(out) + int64_t(t) * H + j;
-        uint2 pk;
-        pk.x = uint32_t(f32_to_bf16_rne(acc.x)) | (uint32_t(f32_to_bf16_rne(acc.y)) << 16);
-        pk.y = uint32_t(f32_to_bf16_rne(acc.z)) | (uint32_t(f32_to_bf16_rne(acc.w)) << 16);
-        *reinterpret_cast<uint2 *>(o) = pk;
-    } else {
-        *reinterpret_cast<float4 *>(static_cast<float *>(out) + int64_t(t) * H + j) = acc;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        if (out_bf16) {
+            uint16_t *o = static_cast<uint16_t *>(out) + int64_t(t) * H + j + 4 * c;
+            uint2 pk;
+            pk.x = uint32_t(f32_to_bf16_rne(acc[c].x)) | (uint32_t(f32_to_bf16_rne(acc[c].y)) << 16);
+            pk.y = uint32_t(f32_to_bf16_rne(acc[c].z)) | (uint32_t(f32_to_bf16_rne(acc[c].w)) << 16);
+            *reinterpret_cast<uint2 *>(o) = pk;
+        } else {
+            *reinterpret_cast<float4 *>(static_cast<float *>(out) + int64_t(t) * H + j + 4 * c) = acc[c];
+        }
     }
 }
 
 void launch_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared,
                     int T, int topk, int H, void *out, int out_bf16, hipStream_t s) {
-    const dim3 grid(unsigned(T), unsigned((H / 4 + 255) / 256));
-    if (yp_f16) combine_kernel<true><<<grid, 256, 0, s>>>(yp, tok_slot, tok_w, shared, topk, H, out, out_bf16);
-    else combine_kernel<false><<<grid, 256, 0, s>>>(yp, tok_slot, tok_w, shared, topk, H, out, out_bf16);
+    auto go = [&](auto kern, int c) {
+        const dim3 grid(unsigned(T), unsigned((H / (4 * c) + 255) / 256));
+        kern<<<grid, 256, 0, s>>>(yp, tok_slot, tok_w, shared, topk, H, out, out_bf16);
+    };
+    if (H % 8 == 0) {
+        if (yp_f16) go(combine_kernel<true, 2>, 2);
+        else go(combine_kernel<false, 2>, 2);
+    } else {
+        if (yp_f16) go(combine_kernel<true, 1>, 1);
+        else go(combine_kernel<false, 1>, 1);
+    }
 }
 
 }  // namespace qwq4
