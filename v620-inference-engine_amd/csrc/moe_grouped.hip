@@ -9,7 +9,7 @@
 // carries token pair_tok[p]. A tile's height follows from its start and the
 // expert's slot count (tile_rows). Each block runs the shared q4 MFMA GEMM
 // core (q4_gemm_core.cuh) at that height on one list entry and 256 weight
-// rows (64-slot tiles: its register-dequant form, gemm_tile_rd64):
+// rows (64- and 128-slot tiles: its register-dequant form, gemm_tile_rd):
 //   gate/up  A = the tile's gathered token rows of x (fp16 copy in the
 //            workspace), weight rows = 128 gate rows and the same 128 up rows,
 //            interleaved by 32 (32-row groups alternate gate, up); epilogue
@@ -49,6 +49,49 @@ template <int BM, bool HAS_Z>
 __device__ __forceinline__ void gate_up_tile(const GateUpTile &a, int e, int base, int M, int j0) {
     using Sh = GemmShape<BM>;
     const int tid = threadIdx.x, wave = tid / WAVE;
+    if constexpr (BM == 128) {
+        // register-dequant core, wave w: all 128 rows x 32 weight rows (group
+        // w: gate when even, up when odd, columns j0 + 32 (w / 2) ..)
+        const int r = wave * 32 + tid % 32, col = (r / 64) * 32 + r % 32;
+        const bool up = (r % 64) >= 32;
+        const int64_t wrow = int64_t(e) * a.F + min(j0 + col, a.F - 1);
+        const BRow b = up ? BRow(a.uw, a.us, a.uz, wrow, a.H / QGROUP) : BRow(a.gw, a.gs, a.gz, wrow, a.H / QGROUP);
+        const int lr = wave * 8 + (tid % WAVE) / 8;
+        const uint16_t *const arow[2] = {a.xh + int64_t(a.pair_tok[base + min(lr, M - 1)]) * a.H,
+                                         a.xh + int64_t(a.pair_tok[base + min(64 + lr, M - 1)]) * a.H};
+        f32x16 acc[4][1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][0] = f32x16{};
+        gemm_tile_rd<128, HAS_Z, 3>(arow, b, a.H, acc);
+        // the up wave of each pair hands its accumulators over through LDS
+        // (lds_a1 for pairs 0-1, lds_b1 for 2-3: free after the core)
+        const int pr = wave / 2, lane = tid % WAVE;
+        float *xbuf = reinterpret_cast<float *>(pr < 2 ? lds_a1 : lds_b1) + (pr % 2) * (4 * 16 * WAVE);
+        if (wave & 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) xbuf[(i * 16 + q) * WAVE + lane] = acc[i][0][q];
+        }
+        __syncthreads();
+        if (!(wave & 1)) {
+            auto cvt = [](float v, int, int) { return f32_to_f16_sat(v); };
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                f32x16 hv[2][1];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        hv[i][0][q] = silu_mul(acc[2 * hh + i][0][q], xbuf[((2 * hh + i) * 16 + q) * WAVE + lane]);
+                emit_tile<1, 2>(epi_slot(wave), hv, cvt, [&](int tr, int c, uint4 v) {
+                    const int m = hh * 64 + tr, j = j0 + pr * 32 + c;
+                    if (m < M && j < a.F) *reinterpret_cast<uint4 *>(a.h + int64_t(base + m) * a.F + j) = v;
+                });
+            }
+        }
+        return;
+    }
     // weight tile row r = b_tile_row(): 32-row group r / 32 is gate when even,
     // up when odd, for columns j0 + 32 (r / 64) + r % 32 (wave-uniform choice)
     // (64-row tiles: the row this lane multiplies, 32 wave + lane % 32, the
@@ -63,8 +106,8 @@ __device__ __forceinline__ void gate_up_tile(const GateUpTile &a, int e, int bas
 #pragma unroll
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
     if constexpr (BM == 64) {
-        const uint16_t *arow = a.xh + int64_t(a.pair_tok[base + min(wave * 8 + (tid % WAVE) / 8, M - 1)]) * a.H;
-        gemm_tile_rd64<HAS_Z>(arow, b, a.H, acc);
+        const uint16_t *const arow[1] = {a.xh + int64_t(a.pair_tok[base + min(wave * 8 + (tid % WAVE) / 8, M - 1)]) * a.H};
+        gemm_tile_rd<64, HAS_Z, 0>(arow, b, a.H, acc);
     } else {
         const uint16_t *ap[BM / 32];
 #pragma unroll
@@ -139,6 +182,28 @@ __device__ __forceinline__ void down_tile(const uint32_t *dw, const uint16_t *ds
     using Sh = GemmShape<BM>;
     const int tid = threadIdx.x, wave = tid / WAVE;
     const int n0 = blockIdx.x * GB_N;
+    constexpr int YB = YP16 ? 2 : 4;
+    if constexpr (BM == 128) {
+        // register-dequant core, wave w: all 128 rows x down rows n0 + 32 w ..
+        const BRow b(dw, ds, dz, int64_t(e) * H + min(n0 + wave * 32 + tid % 32, H - 1), F / QGROUP);
+        const int lr = wave * 8 + (tid % WAVE) / 8;
+        const uint16_t *const arow[2] = {h + int64_t(base + min(lr, M - 1)) * F, h + int64_t(base + min(64 + lr, M - 1)) * F};
+        f32x16 acc[4][1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][0] = f32x16{};
+        gemm_tile_rd<128, HAS_Z, 5 + YP16>(arow, b, F, acc);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+            emit_tile<1, YB>(
+                epi_slot(wave), *reinterpret_cast<const f32x16(*)[2][1]>(&acc[2 * hh][0]),
+                [](float v, int, int) { return f32_to_f16_sat(v); },
+                [&](int tr, int c, uint4 v) {
+                    const int m = hh * 64 + tr, n = n0 + wave * 32 + c;
+                    if (m < M && n < H)
+                        *reinterpret_cast<uint4 *>(static_cast<unsigned char *>(yp) + (int64_t(base + m) * H + n) * YB) = v;
+                });
+        return;
+    }
     const int r = BM == 64 ? wave * 32 + tid % 32 : b_tile_row();  // (as in gate_up_tile)
     const BRow b(dw, ds, dz, int64_t(e) * H + min(n0 + r, H - 1), F / QGROUP);
     f32x16 acc[2][Sh::NJ];
@@ -147,7 +212,8 @@ __device__ __forceinline__ void down_tile(const uint32_t *dw, const uint16_t *ds
 #pragma unroll
         for (int j = 0; j < Sh::NJ; ++j) acc[i][j] = f32x16{};
     if constexpr (BM == 64) {
-        gemm_tile_rd64<HAS_Z>(h + int64_t(base + min(wave * 8 + (tid % WAVE) / 8, M - 1)) * F, b, F, acc);
+        const uint16_t *const arow[1] = {h + int64_t(base + min(wave * 8 + (tid % WAVE) / 8, M - 1)) * F};
+        gemm_tile_rd<64, HAS_Z, 1 + YP16>(arow, b, F, acc);
     } else {
         const uint16_t *ap[BM / 32];
 #pragma unroll
@@ -156,7 +222,6 @@ __device__ __forceinline__ void down_tile(const uint32_t *dw, const uint16_t *ds
     }
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
-    constexpr int YB = YP16 ? 2 : 4;
     emit_tile<Sh::NJ, YB>(
         epi_slot(wave), acc, [](float v, int, int) { return f32_to_f16_sat(v); },
         [&](int tr, int c, uint4 v) {

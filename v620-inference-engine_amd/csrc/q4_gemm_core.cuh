@@ -259,26 +259,36 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
     }
 }
 
-// A 64-row tile (GemmShape<64>: wave w computes 64 rows x weight rows
-// 32 w .. 32 w + 31) with the weights dequantised in registers instead of
-// through LDS. In a 64-row tile each weight row feeds one wave, so the wave
-// that multiplies a row can dequantise it itself: the dequant then runs in
-// all 8 waves (beside their MFMAs) rather than in 4, and the weight tile's LDS
-// writes, reads and barrier hand-off are gone. Lane (l32, lh) holds weight
-// row 32 w + l32 (b: that row) and K half lh of each 64-K stage: one tiled
-// entry (quarter 2 (ks % 2) + lh of group ks / 2) per stage, requested two
-// stages ahead, one word dequantised per 16-K step. The A fragments are
-// read with the same K mapping (chunk kk + 4 lh). Only A goes through LDS:
-// wave w moves rows 8 w .. 8 w + 7 (arow: this lane's row, lane / 8).
-template <bool HAS_Z>
-__device__ __forceinline__ void gemm_tile_rd64(const uint16_t *arow, const BRow &b, int K, f32x16 (&acc)[2][1]) {
+// A BM-row tile (BM = 64 or 128) whose 256 weight rows are split over the
+// 8 waves, 32 each: wave w computes all BM rows x weight rows 32 w .. 32 w +
+// 31 (acc[BM / 32][1]), with the weights dequantised in registers instead of
+// through LDS. Each weight row then feeds one wave, so the wave that
+// multiplies a row dequantises it itself: the dequant runs in all 8 waves
+// (beside their MFMAs) rather than in 4, and the weight tile's LDS writes,
+// reads and barrier hand-off are gone. Lane (l32, lh) holds weight row
+// 32 w + l32 (b: that row) and K half lh of each 64-K stage: one tiled entry
+// (quarter 2 (ks % 2) + lh of group ks / 2) per stage, requested two stages
+// ahead, one word dequantised per 16-K step. The A fragments are read with
+// the same K mapping (chunk kk + 4 lh). Only A goes through LDS: wave w moves
+// rows 64 j + 8 w .. + 7 (arow[j]: this lane's row, 64 j + 8 w + lane / 8).
+// With 64 rows this is GemmShape<64>'s layout (wm = 0, wn2 = w).
+// (USE: a tag per call site; the host pass rejects one specialization
+// called from two kernels' device code)
+template <int BM, bool HAS_Z, int USE>
+__device__ __forceinline__ void gemm_tile_rd(const uint16_t *const (&arow)[BM / 64], const BRow &b, int K,
+                                             f32x16 (&acc)[BM / 32][1]) {
+    static_assert(BM == 64 || BM == 128, "64- or 128-row tiles");
+    constexpr int NI = BM / 32;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
     const int l32 = lane % 32, lh = lane / 32, nk = K / GB_K;
     constexpr int NLD = HAS_Z ? 3 : 2;  // weight-side loads per stage and lane
     auto bufA = [&](int i) { return i ? lds_a1 : lds_a0; };
     auto issue_a = [&](int ks, unsigned char *dst) {
-        const int r = wave * 8 + lane / 8, c = (lane % 8) ^ swz_x(r);
-        __builtin_amdgcn_global_load_lds(arow + ks * GB_K + c * 8, dst + wave * 8 * 128, 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < BM / 64; ++j) {
+            const int rb = 64 * j + wave * 8, r = rb + lane / 8, c = (lane % 8) ^ swz_x(r);
+            __builtin_amdgcn_global_load_lds(arow[j] + ks * GB_K + c * 8, dst + rb * 128, 16, 0, 0);
+        }
     };
     struct WR {
         uint4 w;
@@ -300,10 +310,10 @@ __device__ __forceinline__ void gemm_tile_rd64(const uint16_t *arow, const BRow 
         const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(sw));
         const h2 s2 = {sc, sc};
         const uint32_t words[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
-        uint4 af[2], an[2];
-        auto rd = [&](int kk, uint4 (&f)[2]) {
+        uint4 af[NI], an[NI];
+        auto rd = [&](int kk, uint4 (&f)[NI]) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) f[i] = *reinterpret_cast<const uint4 *>(a + swz(i * 32 + l32, kk + 4 * lh));
+            for (int i = 0; i < NI; ++i) f[i] = *reinterpret_cast<const uint4 *>(a + swz(i * 32 + l32, kk + 4 * lh));
         };
         rd(0, af);
 #pragma unroll
@@ -311,11 +321,12 @@ __device__ __forceinline__ void gemm_tile_rd64(const uint16_t *arow, const BRow 
             if (kk + 1 < GB_K / 16) rd(kk + 1, an);
             const uint4 bf = dequant8(words[kk], zb, s2);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) acc[i][0] = mfma32<F16>(af[i], bf, acc[i][0]);
+            for (int i = 0; i < NI; ++i) acc[i][0] = mfma32<F16>(af[i], bf, acc[i][0]);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) af[i] = an[i];
+            for (int i = 0; i < NI; ++i) af[i] = an[i];
         }
     };
+    constexpr int NA = BM / 64;  // direct A loads per stage and lane
     WR w0, w1;
     issue_a(0, bufA(0));
     issue_w(0, w0);
@@ -329,6 +340,7 @@ __device__ __forceinline__ void gemm_tile_rd64(const uint16_t *arow, const BRow 
         wait_vm_below<NLD>();  // everything but W(ks + 2): A(ks + 1) and W(ks + 1) arrived
         __builtin_amdgcn_s_barrier();
     };
+    (void)NA;
     for (int ks = 0; ks < nk; ks += 2) {  // nk is even (K is a multiple of 128)
         stage(ks, 0, w0);
         stage(ks + 1, 1, w1);
