@@ -15,14 +15,19 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("f16", [True, False])
-def test_quant_rows_bit_exact(gpu, oracle, f16):
+@pytest.mark.parametrize("pad", [0, 2])
+def test_quant_rows_bit_exact(gpu, oracle, f16, pad):
+    """Rows of stride K (16-byte loads, four groups per wave; 444 groups: a partly
+    used last block) and of stride K + 2 (the two-elements-per-lane kernel)."""
     r = np.random.default_rng(21)
     R, K = 37, 1536
     v = (r.standard_normal((R, K)) * 4).astype(np.float32)
     v[3, :128] = 0.0
     v[5, 128:256] = 1e-4
     bits = v.astype(np.float16).view(np.uint16) if f16 else synth.bf16_bits(v)
-    q, sc = qwq4.quant_rows_i8(to_dev(bits, gpu), x_f16=f16)
+    wide = np.zeros((R, K + pad), np.uint16)
+    wide[:, :K] = bits
+    q, sc = qwq4.quant_rows_i8(to_dev(wide, gpu)[:, :K], x_f16=f16)
     qr, sr = oracle.quant_rows_i8(bits, f16)
     assert np.array_equal(host(q), qr)
     assert np.array_equal(host(sc).view(np.uint32), sr.view(np.uint32))

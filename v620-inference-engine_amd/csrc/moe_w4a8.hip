@@ -44,9 +44,48 @@ int moe_w4a8_tile_m() { return W8_TILE_M; }
 
 // ------------------------------------------------------------ quantiser
 // One wave per (row, group of 128): two elements per lane.
+// One (row, 128-group) per 16-lane row of a wave (four per wave): lane i of
+// the row holds elements 8 i .. 8 i + 7 (one 16-byte load), the group's
+// amax is a maximum over the 16 lanes, and each element is quantised as
+// rint(x * (1 / sc)) with sc = amax / 127 (1 for an all-zero group).
 template <bool F16>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int rows,
                                                          int K, int8_t *__restrict__ q, float *__restrict__ scale) {
+    const int G = K / QGROUP, li = threadIdx.x % 16;
+    const int64_t item = int64_t(blockIdx.x) * (blockDim.x / 16) + threadIdx.x / 16;
+    const bool live = item < int64_t(rows) * G;
+    const int64_t it = live ? item : int64_t(rows) * G - 1;  // (every lane takes part in the shuffles)
+    const int64_t r = it / G;
+    const int g = int(it % G);
+    const uint4 u = *reinterpret_cast<const uint4 *>(x + r * ldx + g * QGROUP + 8 * li);
+    auto cvt = [](uint16_t b) { return F16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b); };
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[2 * j] = cvt(uint16_t(w[j]));
+        v[2 * j + 1] = cvt(uint16_t(w[j] >> 16));
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));  // within the 16-lane row
+    const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
+    uint32_t pk[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pk[j / 4] |= uint32_t(int(__builtin_rintf(v[j] * inv)) & 0xff) << (8 * (j % 4));
+    if (live) {
+        *reinterpret_cast<uint2 *>(q + r * K + g * QGROUP + 8 * li) = make_uint2(pk[0], pk[1]);
+        if (li == 0) scale[r * G + g] = sc;
+    }
+}
+
+// The same quantisation, one (row, group) per wave and two elements per lane:
+// for rows whose stride or base do not allow 16-byte loads.
+template <bool F16>
+__global__ __launch_bounds__(256) void quant_rows_pair_kernel(const uint16_t *__restrict__ x, int64_t ldx, int rows,
+                                                              int K, int8_t *__restrict__ q, float *__restrict__ scale) {
     const int G = K / QGROUP, lane = threadIdx.x % WAVE;
     const int64_t item = int64_t(blockIdx.x) * (blockDim.x / WAVE) + threadIdx.x / WAVE;
     if (item >= int64_t(rows) * G) return;
@@ -67,9 +106,15 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restr
 void launch_quant_rows(const uint16_t *x, int x_f16, int64_t ldx, int rows, int K, int8_t *q, float *scale,
                        hipStream_t s) {
     const int64_t items = int64_t(rows) * (K / QGROUP);
-    const unsigned blocks = unsigned((items + 3) / 4);
-    if (x_f16) quant_rows_kernel<true><<<blocks, 256, 0, s>>>(x, ldx, rows, K, q, scale);
-    else quant_rows_kernel<false><<<blocks, 256, 0, s>>>(x, ldx, rows, K, q, scale);
+    if (ldx % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0) {
+        const unsigned blocks = unsigned((items + 15) / 16);
+        if (x_f16) quant_rows_kernel<true><<<blocks, 256, 0, s>>>(x, ldx, rows, K, q, scale);
+        else quant_rows_kernel<false><<<blocks, 256, 0, s>>>(x, ldx, rows, K, q, scale);
+    } else {
+        const unsigned blocks = unsigned((items + 3) / 4);
+        if (x_f16) quant_rows_pair_kernel<true><<<blocks, 256, 0, s>>>(x, ldx, rows, K, q, scale);
+        else quant_rows_pair_kernel<false><<<blocks, 256, 0, s>>>(x, ldx, rows, K, q, scale);
+    }
 }
 
 // ------------------------------------------------------------ GEMM pieces
