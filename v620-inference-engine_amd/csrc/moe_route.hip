@@ -90,39 +90,6 @@ constexpr int DPP_MIRROR = 0x140;       // lane i <-> 15 - i within 16
 constexpr int DPP_BCAST15 = 0x142;      // lane 15 of each row into the next row
 constexpr int DPP_BCAST31 = 0x143;      // lane 31 into rows 2 and 3
 
-__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
-    const uint32_t lo = __builtin_amdgcn_readlane(int(uint32_t(v)), l);
-    const uint32_t hi = __builtin_amdgcn_readlane(int(uint32_t(v >> 32)), l);
-    return (uint64_t(hi) << 32) | lo;
-}
-
-// Maximum of a 64-bit key over the wave (every lane gets it).
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#define QW_MAX_STEP_RM(ctrl, rm)                                                       \
-    {                                                                                  \
-        const uint64_t o = (uint64_t(QW_DPP(uint32_t(v >> 32), ctrl, rm, 0xf, false)) << 32) | \
-                           QW_DPP(uint32_t(v), ctrl, rm, 0xf, false);                  \
-        v = o > v ? o : v;                                                             \
-    }
-#define QW_MAX_STEP(ctrl)                                                              \
-    {                                                                                  \
-        const uint64_t o = (uint64_t(QW_DPP(uint32_t(v >> 32), ctrl, 0xf, 0xf, false)) << 32) | \
-                           QW_DPP(uint32_t(v), ctrl, 0xf, 0xf, false);                 \
-        v = o > v ? o : v;                                                             \
-    }
-    QW_MAX_STEP(DPP_XOR1)
-    QW_MAX_STEP(DPP_XOR2)
-    QW_MAX_STEP(DPP_HALF_MIRROR)
-    QW_MAX_STEP(DPP_MIRROR)
-    // rows combined by broadcasts: lane 15 of rows 0, 2 into rows 1, 3, then
-    // lane 31 into rows 2, 3; lane 63 ends with the wave's maximum (other
-    // lanes may hold partial values)
-    QW_MAX_STEP_RM(DPP_BCAST15, 0xa)
-    QW_MAX_STEP_RM(DPP_BCAST31, 0xc)
-#undef QW_MAX_STEP
-#undef QW_MAX_STEP_RM
-    return readlane64(v, 63);
-}
 
 // Wave maximum of a 32-bit unsigned value (lane 63's result, read to every
 // lane): each step's DPP move fuses into the max instruction.
@@ -154,7 +121,7 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     QW_FMAX_STEP(DPP_HALF_MIRROR)
     QW_FMAX_STEP(DPP_MIRROR)
 #undef QW_FMAX_STEP
-    // as in wave_max_u64 (masked-off lanes read 0 and may end wrong; only
+    // as in wave_max_u32 (masked-off lanes read 0 and may end wrong; only
     // lane 63, in both masks, is read)
 #define QW_FMAX_STEP_RM(ctrl, rm) \
     v = fmaxf(v, __builtin_bit_cast(float, QW_DPP(__builtin_bit_cast(uint32_t, v), ctrl, rm, 0xf, false)));
