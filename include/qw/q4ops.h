@@ -68,6 +68,12 @@ extern "C" {
 #define QW_Q4_EINVAL (-1)
 #define QW_Q4_ELAUNCH (-2)
 
+/* Element types of outputs and intermediates that take more than one
+ * (arguments named *_type). */
+#define QW_T_F32 0
+#define QW_T_BF16 1
+#define QW_T_F16 2
+
 /* Version of this ABI (bumped on any signature change). */
 int qw_q4_abi_version(void);
 
@@ -85,26 +91,32 @@ int qw_q4_untile(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt, int
 
 /* Decode GEMV (replaces gpu::gemv_rows, src/kernels/gemv.hpp:13-14), tiled
  * weights (Wt, St, Zt or NULL):
- *   y[m*ys + n] (+)= sum_k W[n][k] * x[m*xs + k],   m < M, n < N
- * x rows of stride xs (elements, a multiple of 8, x 16-byte aligned): bf16
- * (x_f16 = 0) or fp16 (x_f16 = 1, the engine's decode rows,
- * src/kernels/gemv.hpp:11-14); y fp32 (y_bf16 = 0) or bf16 (y_bf16 = 1,
- * round to nearest even) rows of stride ys; accumulate != 0 adds to y.
- * 1 <= M <= 32. Every product is exact, sums in fp32. */
+ *   y[m*ys + n] (+)= sum_k W[n][k] * x[m*xs + off(n) + k],   m < M, n < N
+ * off(n) = (n / rpg) * K when rpg > 0 (row n reads activation slice n / rpg:
+ * the engine's hyper-connection down projection, src/engine/decode.hip:55-59),
+ * else 0. rpg 0 or >= 16, at most 64 slices (each runs as one launch; rpg need
+ * not be a multiple of 16).
+ * x rows of stride xs (elements, a multiple of 8, x 16-byte aligned; with
+ * M > 1 and rpg > 0, xs covers every slice): bf16 (x_f16 = 0) or fp16
+ * (x_f16 = 1, the engine's decode rows, src/kernels/gemv.hpp:11-14); y fp32
+ * (y_bf16 = 0) or bf16 (y_bf16 = 1, round to nearest even) rows of stride ys;
+ * accumulate != 0 adds to y. 1 <= M <= 32. Every product is exact, sums in
+ * fp32. */
 int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *x, int x_f16, int xs, void *y,
-               int ys, int y_bf16, int N, int K, int M, int accumulate, void *stream);
+               int ys, int y_bf16, int N, int K, int M, int rpg, int accumulate, void *stream);
 
 /* Dense GEMV on 16-bit weights (the role of gpu::gemv_rows with fp16
  * weights, src/kernels/gemv.hpp:13-14, which the engine runs the shared
  * expert's projections through, src/engine/decode.hip:99-101; and of
  * ref::Model::linear on bf16 weights, src/ref/ref_model.cpp:86-97):
- *   y[m*ys + n] (+)= sum_k W[n*ldw + k] * x[m*xs + k],   m < M, n < N
+ *   y[m*ys + n] (+)= sum_k W[n*ldw + k] * x[m*xs + off(n) + k],   m < M, n < N
  * f16 = 1: W and x fp16; f16 = 0: W and x bf16 (the MFMA takes matching
  * types; every product is exact, sums in fp32). W row-major, ldw >= K a
  * multiple of 8, 16-byte aligned; K a multiple of 32; any N >= 1; x rows of
- * stride xs as in qw_q4_gemv; y fp32 or bf16 (y_bf16). 1 <= M <= 32. */
+ * stride xs and row slices (rpg, off(n)) as in qw_q4_gemv; y fp32 or bf16
+ * (y_bf16). 1 <= M <= 32. */
 int qw_w16_gemv(const uint16_t *W, int ldw, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N,
-                int K, int M, int accumulate, void *stream);
+                int K, int M, int rpg, int accumulate, void *stream);
 
 /* Bytes of the tiled layout of a 16-bit [N][K] matrix (N padded to a
  * multiple of 16 rows). */
@@ -124,7 +136,7 @@ int qw_w16_tile(const uint16_t *W, int ldw, int N, int K, void *Wt, void *stream
 /* qw_w16_gemv on weights in the tiled layout (qw_w16_tile); the same
  * arguments and results, bit for bit, without ldw. */
 int qw_w16_gemv_tiled(const void *Wt, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N, int K,
-                      int M, int accumulate, void *stream);
+                      int M, int rpg, int accumulate, void *stream);
 
 /* The shared expert's SwiGLU x gate folded into its down projection: the
  * result of qw_swiglu_gate(v, ldv, n, M, h) followed by
@@ -177,7 +189,10 @@ int qw_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, void *str
 /* Prefill GEMM (replaces gpu::gemm, src/kernels/gemm.hpp:14-15, with tiled
  * q4 weights): Y[t][n] = sum_k X[t][k] * W[n][k], t < T. X rows of stride
  * ldx, bf16 (x_f16 = 0) or fp16 (x_f16 = 1, the reference's prefill rows);
- * Y fp32 or bf16 rows of stride ldy. For bf16 rows, `workspace` (device
+ * Y rows of stride ldy, y_type QW_T_F32, QW_T_BF16 (round to nearest even)
+ * or QW_T_F16 (the reference's f16_out, which the engine passes for most
+ * prefill projections, src/engine/prefill.hip:218-334: round to nearest
+ * even, finite values beyond +-65504 saturate). For bf16 rows, `workspace` (device
  * memory of at least qw_q4_gemm_workspace_size(T, K) bytes, 256-byte
  * aligned) is scratch for the fp16 pre-pass; it holds nothing between calls.
  * fp16 rows need none (workspace may be NULL).
@@ -188,7 +203,7 @@ int qw_swiglu_gate(const float *v, int ldv, int n, int T, uint16_t *h, void *str
  * sums in fp32. */
 size_t qw_q4_gemm_workspace_size(int T, int K);
 int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *X, int x_f16, int ldx, int T,
-               void *Y, int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream);
+               void *Y, int ldy, int y_type, int N, int K, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Routing of T tokens over E experts (replaces gpu::moe_route_B for decode
  * rows and gpu::moe_route_T + moe_scatter_T for prefill, moe.hpp:17-27; math
@@ -217,7 +232,10 @@ int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_
 /* Gathered per-expert GEMVs for decode batches (replaces gpu::moe_experts_P,
  * moe.hpp:35-37). For every slot p of expert e (from qw_moe_route):
  *   h[p]  = silu(G_e x[pair_tok[p]]) * (U_e x[pair_tok[p]])     fp16 [T*k][F]
- *   yp[p] = D_e h[p]                                            fp32 [T*k][H]
+ *   yp[p] = D_e h[p]                             fp32 or fp16 [T*k][H]
+ * yp fp32 (yp_f16 = 0) or fp16 (yp_f16 = 1: the reference's moe_experts_P
+ * output, src/kernels/moe.hpp:35-37, and the engine's b.yp buffer; round to
+ * nearest even, finite values beyond +-65504 saturate), 4-byte aligned.
  * Weights are tiled (qw_q4_tile) over the stacked experts: gate and up as one
  * [E*F][H] matrix each, down as [E*H][F]; zeros may be NULL. x [T][H], bf16
  * (x_f16 = 0) or fp16 (x_f16 = 1).
@@ -227,7 +245,7 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
                         const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                         const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
                         const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int x_f16, int T,
-                        int topk, uint16_t *h, float *yp, void *stream);
+                        int topk, uint16_t *h, void *yp, int yp_f16, void *stream);
 
 /* Grouped per-expert GEMMs for prefill chunks (replaces gpu::moe_experts_T,
  * moe.hpp:29-32): the same outputs as qw_moe_experts_gemv for any T, over
@@ -286,11 +304,16 @@ int qw_moe_experts_w4a8(const uint32_t *gw, const uint16_t *gs, const uint16_t *
 int qw_quant_rows_i8(const uint16_t *x, int x_f16, int rows, int K, int ldx, int8_t *q, float *scale, void *stream);
 
 /* Weighted combine (replaces gpu::moe_combine_B/T, moe.hpp:42-46):
- *   out[t][j] = shared[t][j] + sum_{i<k} tok_w[t][i] * yp[tok_slot[t][i]][j]
- * yp fp32 (yp_f16 = 0) or fp16 (yp_f16 = 1); shared fp32 [T][H] or NULL;
- * out fp32 or bf16 (out_bf16). H % 4 == 0. Sums in fp32, selection order. */
-int qw_moe_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared, int T,
-                   int topk, int H, void *out, int out_bf16, void *stream);
+ *   out[t][j] = shared[t][j] + sum_{i<k, slot >= 0} tok_w[t][i] * yp[tok_slot[t][i]][j]
+ * yp fp32 (yp_f16 = 0) or fp16 (yp_f16 = 1); shared [T][H] fp32
+ * (shared_f16 = 0, moe_combine_B) or fp16 (shared_f16 = 1, moe_combine_T),
+ * or NULL; out of out_type QW_T_F32 (moe_combine_B), QW_T_F16 (moe_combine_T;
+ * round to nearest even, finite values beyond +-65504 saturate) or QW_T_BF16.
+ * A negative slot (a selection another rank holds, in the reference's
+ * expert-parallel layout) adds nothing, as in the reference. H % 4 == 0.
+ * Sums in fp32: the shared value, then the selections in order. */
+int qw_moe_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const void *shared,
+                   int shared_f16, int T, int topk, int H, void *out, int out_type, void *stream);
 
 /* Format surface (bit-exact): nibbles as bytes [N][K]; dequantised fp32
  * weights [N][K]; reference-engine word order -> checkpoint word order. */
@@ -304,10 +327,12 @@ int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, 
  * math of ref::Model::moe, src/ref/ref_model.cpp:406-463):
  *   logits = x . router_w^T (fp32 weights [E][H], the reference's fp32 router);
  *   routing as qw_moe_route; experts as qw_moe_experts_gemv;
- *   out[t] = shared[t] + sum_i top_w[t][i] * yp[tok_slot[t][i]]   (fp32 or bf16)
+ *   out[t] = shared[t] + sum_i top_w[t][i] * yp[tok_slot[t][i]]   (out_type)
  * The router GEMV and routing share a launch; up to T = 4 the combine runs
- * inside the down projection, above that in a launch of its own. Outputs: out, logits [T][E], top_e, top_w, tok_slot [T][k],
- * h, yp (as qw_moe_experts_gemv). shared fp32 [T][H] or NULL (e.g. the shared
+ * inside the down projection, above that in a launch of its own. Outputs: out
+ * (QW_T_F32, the engine's moe_combine_B rows, QW_T_BF16 or QW_T_F16), logits
+ * [T][E], top_e, top_w, tok_slot [T][k], h, yp (fp32 or fp16 with yp_f16, as
+ * qw_moe_experts_gemv; the combine adds the values yp holds). shared fp32 [T][H] or NULL (e.g. the shared
  * expert's output). x [T][H] bf16 (x_f16 = 0) or fp16 (x_f16 = 1). 1 <= T <= 32.
  * workspace: qw_moe_decode_workspace_size(...) bytes, 256-byte aligned, filled
  * with zeros once before its first use (it holds completion counters that
@@ -316,28 +341,35 @@ size_t qw_moe_decode_workspace_size(int T, int E, int topk, int H, int F);
 int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
                   const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
                   const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
-                  void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
-                  uint16_t *h, float *yp, void *workspace, size_t workspace_bytes, void *stream);
+                  void *out, int out_type, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
+                  uint16_t *h, void *yp, int yp_f16, void *workspace, size_t workspace_bytes, void *stream);
 
 /* qw_moe_decode without a workspace argument: it allocates nothing and
  * needs no caller scratch. No counterpart in the reference; it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops). The scratch (completion counters, partial router
  * logits, routing arrays) is one library-held device array per GPU of
- * qw_moe_decode_static_max_bytes() = 4 MiB, kept until the process ends;
- * shapes needing more (about T * E * ceil(H / 512) * 4 bytes plus a few
- * E-sized arrays) are rejected with QW_Q4_EINVAL. The counters start at zero
- * (the array is zero when the library loads) and every call leaves them at
- * zero. All calls on one GPU share the array: calls that overlap on one GPU
- * (on different streams, or from different threads) race and must not be
+ * qw_moe_decode_static_max_bytes() = 4 MiB, kept until the process ends.
+ * Every shape qw_moe_decode accepts fits (T <= 32, E <= 1024, k <= 64 and
+ * the supported H, F: at most about 3.97 MB). The completion counters start
+ * at zero (the array is zero when the library loads) and every completed call
+ * leaves them at zero. A call that returns QW_Q4_ELAUNCH after some of its
+ * kernels were enqueued enqueues a clearing kernel behind them; after any
+ * other failure of the device work (a kernel fault, a capture that was
+ * abandoned mid-call), call qw_moe_decode_static_reset before the next call.
+ * All calls on one GPU share the array: calls that overlap on one GPU (on
+ * different streams, or from different threads) race and must not be
  * issued. */
 size_t qw_moe_decode_static_max_bytes(void);
 int qw_moe_decode_static(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk,
                          const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
                          const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
-                         const uint16_t *dz, int H, int F, const float *shared, void *out, int out_bf16,
-                         float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot, uint16_t *h, float *yp,
-                         void *stream);
+                         const uint16_t *dz, int H, int F, const float *shared, void *out, int out_type,
+                         float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot, uint16_t *h, void *yp,
+                         int yp_f16, void *stream);
+/* Clears the completion counters of the current GPU's static scratch (one
+ * small kernel on `stream`; no allocation, no memset node). */
+int qw_moe_decode_static_reset(void *stream);
 
 /* Scale conversion as the reference does it at load (weight_convert.cpp:19-26):
  * bf16 -> fp16 bits, magnitudes above 65504 saturated, round to nearest even. */

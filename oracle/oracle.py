@@ -119,8 +119,27 @@ def q4_dequant(W, S, Z, N, K):
     return out
 
 
-def q4_linear(W, S, Z, N, K, x, threads=None):
-    """y[t][n] = sum_k deq(W)[n][k] x[t][k]; x fp32 [T][K] -> y fp32 [T][N]."""
+def _row_slices(N, K, x, rpg):
+    """Rows grouped over activation slices as gpu::gemv_rows groups them
+    (src/kernels/gemv.hip:16-17: row n reads x + (n / rpg) * K): yields
+    (r0, r1, x slice [T][K]) per slice of x [T][slices * K]."""
+    T = x.shape[0]
+    for s, r0 in enumerate(range(0, N, rpg)):
+        yield r0, min(N, r0 + rpg), np.ascontiguousarray(x[:, s * K:(s + 1) * K]).reshape(T, K)
+
+
+def q4_linear(W, S, Z, N, K, x, threads=None, rpg=0):
+    """y[t][n] = sum_k deq(W)[n][k] x[t][off(n) + k]; x fp32 [T][K] (or [T][slices * K] with
+    rpg > 0, off(n) = (n // rpg) * K) -> y fp32 [T][N]."""
+    if rpg:
+        x = _c(x, np.float32)
+        x = x.reshape(x.shape[0] if x.ndim > 1 else 1, -1)
+        y = np.empty((x.shape[0], N), np.float32)
+        W, S = np.asarray(W).reshape(N, -1), np.asarray(S).reshape(N, -1)
+        Z = None if Z is None else np.asarray(Z).reshape(N, -1)
+        for r0, r1, xs in _row_slices(N, K, x, rpg):
+            y[:, r0:r1] = q4_linear(W[r0:r1], S[r0:r1], None if Z is None else Z[r0:r1], r1 - r0, K, xs, threads)
+        return y
     x = _c(x, np.float32).reshape(-1, K)
     T = x.shape[0]
     y = np.empty((T, N), np.float32)
@@ -210,11 +229,19 @@ def moe(x, logits, topk, gate, up, down, threads=None, want_parts=False):
     return out
 
 
-def linear_w16(W, x, f16=False, threads=None):
-    """y[t][o] = sum_i W[o][i] x[t][i], W 16-bit bits [N][K] (bf16, or fp16 with f16) widened
-    to fp32 (ref::Model::linear, src/ref/ref_model.cpp:86-97)."""
+def linear_w16(W, x, f16=False, threads=None, rpg=0):
+    """y[t][o] = sum_i W[o][i] x[t][off(o) + i], W 16-bit bits [N][K] (bf16, or fp16 with f16)
+    widened to fp32 (ref::Model::linear, src/ref/ref_model.cpp:86-97); rows grouped over
+    activation slices with rpg > 0 as gpu::gemv_rows does (off(o) = (o // rpg) * K)."""
     W = _c(W, np.uint16)
     N, K = W.shape
+    if rpg:
+        x = _c(x, np.float32)
+        x = x.reshape(x.shape[0] if x.ndim > 1 else 1, -1)
+        y = np.empty((x.shape[0], N), np.float32)
+        for r0, r1, xs in _row_slices(N, K, x, rpg):
+            y[:, r0:r1] = linear_w16(W[r0:r1], xs, f16, threads)
+        return y
     x = _c(x, np.float32).reshape(-1, K)
     T = x.shape[0]
     y = np.empty((T, N), np.float32)

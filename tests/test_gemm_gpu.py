@@ -71,6 +71,55 @@ def test_gemm_microbatch_fp32_out(gpu, oracle):
     assert rel_err(Y[np.ix_(toks, rows)], ref) <= TOL
 
 
+def _f16_sat(y32):
+    """fp32 -> fp16 round to nearest even, finite values beyond +-65504 saturated."""
+    y = np.asarray(y32, np.float32)
+    fin = np.isfinite(y)
+    return np.where(fin, np.clip(y, -65504.0, 65504.0), y).astype(np.float16)
+
+
+@pytest.mark.parametrize("N,K,T", [(12288, 4096, 4096), (4096, 6144, 2048), (384, 1024, 200)])
+def test_gemm_f16_out(gpu, oracle, N, K, T):
+    """fp16 Y (the reference's gemm(..., f16_out = true), which the engine's
+    prefill passes for most projections): the fp16 rows are the fp32 results
+    rounded to nearest even, bit for bit, on fp16 activation rows (the
+    engine's) at config-4 sizes, and within the tolerance of the oracle
+    (plus fp16's half ulp) on sampled tokens and rows."""
+    import torch
+    print(f"gemm f16 out T={T} N={N} K={K}", flush=True)
+    W, S, Z = synth.q4_weights(54, f"h{N}x{K}", N, K)
+    xb, xf = synth.acts(54, f"hx{K}", T, K)
+    x16 = xf.astype(np.float16)
+    dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
+    X = torch.from_numpy(x16).to(gpu)
+    Y32 = host(qwq4.gemm(dW, dS, dZ, X, N, K))
+    Y16 = host(qwq4.gemm(dW, dS, dZ, X, N, K, y_dtype=torch.float16))
+    assert Y16.dtype == np.float16
+    assert np.array_equal(Y16.view(np.uint16), _f16_sat(Y32).view(np.uint16))
+    r = np.random.default_rng(2)
+    toks = np.sort(np.unique(np.r_[0, T - 1, r.choice(T, min(T, 32), replace=False)]))
+    rows = np.sort(np.unique(np.r_[0, N - 1, r.choice(N, min(N, 512), replace=False)]))
+    ref = oracle.q4_linear(W[rows], S[rows], Z[rows], len(rows), K, x16.astype(np.float32)[toks])
+    got = Y16[np.ix_(toks, rows)].astype(np.float64)
+    bound = TOL * np.max(np.abs(ref)) + 2.0**-11 * np.abs(ref)
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+def test_gemm_f16_out_saturates(gpu):
+    """fp16 Y beyond the fp16 range saturates to +-65504 (no infinities)."""
+    import torch
+    N, K, T = 256, 512, 64
+    W, S, Z = synth.q4_weights(55, "sat", N, K)
+    S = np.full_like(S, np.float16(60.0).view(np.uint16))
+    dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
+    X = torch.full((T, K), 100.0, dtype=torch.float16, device=gpu)
+    Y32 = host(qwq4.gemm(dW, dS, dZ, X, N, K))
+    Y16 = host(qwq4.gemm(dW, dS, dZ, X, N, K, y_dtype=torch.float16))
+    assert np.max(np.abs(Y32)) > 65504.0
+    assert np.all(np.isfinite(Y16.astype(np.float32)))
+    assert np.array_equal(Y16.view(np.uint16), _f16_sat(Y32).view(np.uint16))
+
+
 # (E, H, F, k, T, zeros, bias): few tokens per expert (one partial tile each,
 # some experts empty); many per expert (several tiles, ragged last tile, F
 # not a multiple of 256); symmetric weights (no zero tensor).

@@ -72,6 +72,39 @@ def test_gemv_lm_head(gpu, oracle, M):
     assert bf16_err_ok(y, r)
 
 
+@pytest.mark.parametrize("N,K,rpg,M", [(1296, 1024, 324, 1), (1296, 1024, 324, 8), (12288, 4096, 3076, 1),
+                                        (12288, 4096, 3076, 8), (4096, 6144, 2048, 4), (2000, 512, 130, 3),
+                                        (4096, 4096, 64, 32)])
+def test_gemv_row_slices(gpu, oracle, N, K, rpg, M):
+    """gemv_rows' row grouping (rpg: row n reads activation slice n // rpg,
+    src/kernels/gemv.hip:16-17) on q4 weights: the engine's hyper-connection
+    shape (4 slices of 324 rows: tiles straddle two slices), config 2's
+    4096->12288 in 4 slices of 3076 rows (not a multiple of 16) at batches 1
+    and 8, slices of whole tiles, and 64 slices at batch 32 (two launches
+    per slice). Rows strided over every slice, accumulated into y; against
+    the oracle; rows past N untouched; each row equal, bit for bit, to the
+    ungrouped GEMV of its own slice."""
+    import torch
+    print(f"gemv rpg N={N} K={K} rpg={rpg} M={M}", flush=True)
+    ns = (N + rpg - 1) // rpg
+    W, S, Z = synth.q4_weights(15, f"r{N}x{K}", N, K)
+    xs = ns * K + 8
+    xb, xf = synth.acts(15, f"rx{M}x{xs}", M, xs)
+    dW, dS, dZ = qwq4.tile(to_dev(W, gpu), to_dev(S, gpu), to_dev(Z, gpu), N, K)
+    dx = to_dev(xb, gpu)
+    y = torch.full((M, N + 16), 0.5, dtype=torch.float32, device=gpu)
+    qwq4.gemv(dW, dS, dZ, dx, N, K, M, y=y, accumulate=True, xs=xs, ys=N + 16, rpg=rpg)
+    yh = host(y)
+    assert np.all(yh[:, N:] == 0.5)
+    ref = oracle.q4_linear(W, S, Z, N, K, xf[:, :ns * K], rpg=rpg) + 0.5
+    assert rel_err(yh[:, :N], ref) <= TOL
+    # each slice's rows equal the plain GEMV of that slice (same arithmetic)
+    for sl in sorted({0, ns - 1, ns // 2}):
+        y1 = host(qwq4.gemv(dW, dS, dZ, dx[:, sl * K:].contiguous(), N, K, M))
+        r0, r1 = sl * rpg, min(N, (sl + 1) * rpg)
+        assert np.array_equal((y1[:, r0:r1] + np.float32(0.5)).view(np.uint32), yh[:, r0:r1].view(np.uint32))
+
+
 def test_gemv_rows_independent_bit_exact(gpu):
     N, K, M = 2048, 4096, 8
     (W, S, Z, xb, xf), (dW, dS, dZ, dx) = _setup(gpu, N, K, M)

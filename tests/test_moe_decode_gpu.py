@@ -35,6 +35,7 @@ def _case(gpu, seed, T, E, H, F, k, with_shared):
                                                    (1, 256, 4096, 1536, 8, True, True),
                                                    (2, 256, 4096, 1536, 8, True, False),
                                                    (4, 256, 4096, 1536, 8, False, False),
+                                                   (16, 256, 4096, 1536, 8, True, True),
                                                    (32, 256, 4096, 1536, 8, True, True)])
 def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
     print(f"moe_decode T={T} E={E} H={H} F={F} k={k}", flush=True)
@@ -66,24 +67,42 @@ def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
                                        (1, 4, 1024, 256, 2), (2, 4, 1024, 256, 3), (2, 8, 1024, 256, 8),
                                        (3, 64, 1024, 512, 4), (4, 64, 1024, 256, 4),
                                        (6, 64, 1024, 256, 4), (6, 64, 1024, 512, 4), (1, 256, 4096, 1536, 8),
-                                       (2, 256, 4096, 1536, 8), (4, 256, 4096, 1536, 8)])
-def test_moe_decode_matches_unfused_path(gpu, T, E, H, F, k):
-    """The block against routing + experts + combine as separate calls: yp
+                                       (2, 256, 4096, 1536, 8), (4, 256, 4096, 1536, 8), (16, 256, 4096, 1536, 8)])
+@pytest.mark.parametrize("yp16", [False, True])
+def test_moe_decode_matches_unfused_path(gpu, T, E, H, F, k, yp16):
+    """The block against routing + experts + combine as separate calls, with
+    fp32 and fp16 yp (the combine then adds the fp16 values): yp and out
     bit-identical, on both sides of the switch that folds the combine into
     the down projection (up to 4 tokens; batches 1 and 2 in one block per 16
     output rows), with experts chosen by both tokens (E = 16, k = 8; E = 8, k = 8:
     every expert twice), fewer experts than the kernels' waves (E = 4), and at
     config 3's full size (down projection with 6 groups per wave)."""
-    print(f"moe_decode vs unfused T={T} E={E} H={H} F={F}", flush=True)
+    print(f"moe_decode vs unfused T={T} E={E} H={H} F={F} yp16={yp16}", flush=True)
     ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 77 + T, T, E, H, F, k, True)
     out, buf = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
-                               out_bf16=False)
+                               out_bf16=False, yp_f16=yp16)
     r = qwq4.moe_route(buf.logits, k)
-    h, yp = qwq4.moe_experts_gemv(g, u, d, r, to_dev(xb, gpu), E, F)
+    h, yp = qwq4.moe_experts_gemv(g, u, d, r, to_dev(xb, gpu), E, F, yp_f16=yp16)
     o2 = qwq4.moe_combine(yp, r, H, shared=to_dev(sh, gpu), out_bf16=False)
     assert np.array_equal(host(r.top_e), host(buf.top_e))
-    assert np.array_equal(host(yp), host(buf.yp))
+    assert np.array_equal(host(yp).view(np.uint8), host(buf.yp).view(np.uint8))
     assert np.array_equal(host(out).view(np.uint32), host(o2).view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 2, 4, 8])
+def test_moe_decode_f16_out(gpu, T):
+    """fp16 output rows (QW_T_F16): the fp32 output of the same call rounded
+    to nearest even, bit for bit, with the combine folded into the down
+    projection (T <= 4) and as its own launch (T = 8)."""
+    import torch
+    E, H, F, k = 64, 1024, 256, 4
+    ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 130 + T, T, E, H, F, k, True)
+    o32, _ = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
+                             out_bf16=False, yp_f16=True)
+    o16, _ = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
+                             out_dtype=torch.float16, yp_f16=True)
+    want = np.clip(host(o32), -65504, 65504).astype(np.float16)
+    assert np.array_equal(host(o16).view(np.uint16), want.view(np.uint16))
 
 
 @pytest.mark.parametrize("T,E", [(6, 64), (8, 64), (8, 256)])

@@ -178,6 +178,71 @@ def test_combine_with_shared(gpu):
     assert np.allclose(o, want, rtol=1e-6)
 
 
+def _f16_sat(y32):
+    y = np.asarray(y32, np.float32)
+    return np.where(np.isfinite(y), np.clip(y, -65504.0, 65504.0), y).astype(np.float16)
+
+
+@pytest.mark.parametrize("T,E,H,F", [(1, 64, 1024, 512), (2, 64, 1024, 512), (8, 64, 1024, 512), (32, 64, 1024, 512),
+                                     (8, 256, 4096, 1536)])
+def test_experts_gemv_yp_f16(gpu, oracle, T, E, H, F):
+    """fp16 yp (the reference's moe_experts_P output, moe.hpp:35-37): the
+    fp32 sums rounded to nearest even, bit for bit against the fp32 yp of the
+    same kernels, h unchanged; the combine of the fp16 rows within the
+    tolerance of the oracle's MoE."""
+    k = 8
+    print(f"moe gemv yp16 T={T} E={E} H={H} F={F}", flush=True)
+    ex = synth.experts(44, E, H, F)
+    xb, xf = synth.acts(44, f"x{T}", T, H)
+    l = synth.router_logits(44, f"l{T}", T, E)
+    out = oracle.moe(xf, l, k, *ex)
+    (dg, du, dd), E, F = _experts_dev(gpu, ex)
+    dx = to_dev(xb, gpu)
+    r = qwq4.moe_route(to_dev(l, gpu), k)
+    h32, yp32 = qwq4.moe_experts_gemv(dg, du, dd, r, dx, E, F)
+    h16, yp16 = qwq4.moe_experts_gemv(dg, du, dd, r, dx, E, F, yp_f16=True)
+    assert host(yp16).dtype == np.float16
+    assert np.array_equal(host(h16).view(np.uint16), host(h32).view(np.uint16))
+    assert np.array_equal(host(yp16).view(np.uint16), _f16_sat(host(yp32)).view(np.uint16))
+    o = host(qwq4.moe_combine(yp16, r, H, out_bf16=False))
+    assert rel_err(o, out) <= TOL
+
+
+@pytest.mark.parametrize("H", [64, 4096, 100])
+def test_combine_fp16_rows_and_foreign_slots(gpu, H):
+    """moe_combine_T's types (fp16 yp, fp16 shared, fp16 out, moe.hpp:42-43)
+    and moe_combine_B's (fp16 yp, fp32 shared and out): out = shared + the
+    weighted rows in selection order, against an fp64 sum of the same fp16
+    values; a negative slot (a selection another rank holds) adds nothing,
+    as in the reference (moe_route.hip:174-175)."""
+    import torch
+    T, k = 5, 4
+    rng = np.random.default_rng(H)
+    yp = torch.from_numpy(rng.standard_normal((T * k, H)).astype(np.float16)).to(gpu)
+    r = qwq4.Route(T, 8, k, gpu)
+    slots = rng.permutation(T * k).reshape(T, k).astype(np.int32)
+    slots[1, 2] = -1
+    slots[3, 0] = -1
+    w = rng.random((T, k)).astype(np.float32)
+    r.tok_slot.copy_(torch.from_numpy(slots))
+    r.top_w.copy_(torch.from_numpy(w))
+    sh16 = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16)).to(gpu)
+    y = host(yp).astype(np.float64)
+    want = host(sh16).astype(np.float64)
+    for t in range(T):
+        for i in range(k):
+            if slots[t, i] >= 0:
+                want[t] += float(w[t, i]) * y[slots[t, i]]
+    o32 = host(qwq4.moe_combine(yp, r, H, shared=sh16, out_dtype=torch.float32))
+    assert np.max(np.abs(o32 - want)) <= 1e-5 * np.max(np.abs(want))
+    o16 = host(qwq4.moe_combine(yp, r, H, shared=sh16, out_dtype=torch.float16))
+    assert o16.dtype == np.float16
+    assert np.array_equal(o16.view(np.uint16), _f16_sat(o32).view(np.uint16))
+    sh32 = sh16.float()
+    ob = host(qwq4.moe_combine(yp, r, H, shared=sh32, out_bf16=False))
+    assert np.array_equal(ob.view(np.uint32), o32.view(np.uint32))
+
+
 @pytest.mark.parametrize("T", [8, 32])
 def test_decode_and_prefill_experts_agree(gpu, oracle, T):
     """The decode path (gathered GEMVs, bf16 operands) and the prefill path

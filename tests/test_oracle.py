@@ -128,6 +128,32 @@ def test_linear_exact_cases(oracle):
     assert np.all(oracle.q4_linear(W, S, Z, N, K, np.zeros((1, K), np.float32)) == 0)
 
 
+@pytest.mark.parametrize("rpg", [20, 32, 324])
+def test_linear_row_slices_one_hot(oracle, rpg):
+    """Rows grouped over activation slices (gpu::gemv_rows' rpg,
+    src/kernels/gemv.hip:16-17: row n reads slice n // rpg): with x one-hot
+    at column k of slice s, row n gives deq[n][k] exactly when n // rpg == s
+    and 0 otherwise, for the q4 and the 16-bit linear; the one-hot sum over
+    all slices gives every row's column k."""
+    N, K = 48 if rpg < 64 else 660, 256
+    W, S, Z = synth.q4_weights(9, "rs", N, K)
+    deq = oracle.q4_dequant(W, S, Z, N, K)
+    ns = (N + rpg - 1) // rpg
+    r = np.random.default_rng(rpg)
+    W16 = (r.standard_normal((N, K)) * 0.05).astype(np.float16)
+    for sl in range(ns):
+        x = np.zeros((1, ns * K), np.float32)
+        x[0, sl * K + 77] = 1.0
+        y = oracle.q4_linear(W, S, Z, N, K, x, rpg=rpg)
+        yw = oracle.linear_w16(W16.view(np.uint16), x, True, rpg=rpg)
+        rows = (np.arange(N) // rpg) == sl
+        assert np.array_equal(y[0][rows], deq[rows, 77]) and np.all(y[0][~rows] == 0)
+        assert np.array_equal(yw[0][rows], W16[rows, 77].astype(np.float32)) and np.all(yw[0][~rows] == 0)
+    x = np.zeros((1, ns * K), np.float32)
+    x[0, [s * K + 5 for s in range(ns)]] = 1.0
+    assert np.array_equal(oracle.q4_linear(W, S, Z, N, K, x, rpg=rpg)[0], deq[:, 5])
+
+
 # ------------------------------------------------------------- routing
 def test_route_order_and_weights(oracle):
     T, E, k = 64, 256, 8
@@ -235,12 +261,12 @@ def test_expf_tie_pairs_are_rounding_conflicts():
 
 
 def test_device_expf_table_is_nearest_powers_of_two():
-    """The 32-entry table of the device's expf (csrc/moe_route.hip) holds the
+    """The 32-entry table of the device's expf (csrc/route_core.cuh) holds the
     doubles nearest 2^(i/32), i << 47 subtracted from their bits."""
     import re
     import struct
     from decimal import Decimal, getcontext
-    src = open(os.path.join(ROOT, "v620-inference-engine_amd", "csrc", "moe_route.hip")).read()
+    src = open(os.path.join(ROOT, "v620-inference-engine_amd", "csrc", "route_core.cuh")).read()
     body = src[src.index("kExp2Tab32[32] = {"):]
     vals = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{16})ull", body[:body.index("};")])]
     assert len(vals) == 32

@@ -43,6 +43,35 @@ def test_w16_gemv(gpu, oracle, f16, N, K, M):
     assert rel_err(y, oracle.linear_w16(Wb, xf, f16)) <= TOL
 
 
+@pytest.mark.parametrize("N,K,rpg,M", [(1296, 1024, 324, 1), (1296, 1024, 324, 4), (1296, 1024, 324, 8),
+                                        (4096, 2048, 1024, 2), (1000, 512, 130, 3)])
+def test_w16_gemv_row_slices(gpu, oracle, N, K, rpg, M):
+    """gemv_rows' row grouping (rpg: row n reads activation slice n // rpg,
+    src/kernels/gemv.hip:16-17) on fp16 weights, row-major and tiled at
+    load: the engine's hyper-connection down projection (4 streams of 324
+    rows, decode.hip:55-59; 324 is not a multiple of 16, so tiles straddle
+    two slices) and others, strided rows covering every slice, accumulating
+    into y. Against the oracle; the two layouts bit for bit; rows past N
+    untouched."""
+    import torch
+    print(f"w16 gemv rpg N={N} K={K} rpg={rpg} M={M}", flush=True)
+    ns = (N + rpg - 1) // rpg
+    Wb, _ = w16(84, f"r{N}x{K}", N, K, True)
+    xs = ns * K + 8
+    xb, xf = rows(84, f"rx{M}", M, xs, True)
+    dW, dx = to_dev(Wb, gpu), to_dev(xb, gpu)
+    ref = oracle.linear_w16(Wb, xf[:, :ns * K], True, rpg=rpg) + 0.25
+    y = torch.full((M, N + 16), 0.25, dtype=torch.float32, device=gpu)
+    qwq4.gemv_w16(dW, dx, M, y=y, accumulate=True, f16=True, xs=xs, ys=N + 16, rpg=rpg)
+    yh = host(y)
+    assert np.all(yh[:, N:] == 0.25)
+    assert rel_err(yh[:, :N], ref) <= TOL
+    Wt = qwq4.w16_tile(dW)
+    yt = torch.full((M, N + 16), 0.25, dtype=torch.float32, device=gpu)
+    qwq4.gemv_w16_tiled(Wt, N, K, dx, M, y=yt, accumulate=True, f16=True, xs=xs, ys=N + 16, rpg=rpg)
+    assert np.array_equal(host(yt).view(np.uint32), yh.view(np.uint32))
+
+
 def test_w16_gemv_strides_bf16_out_and_accumulate(gpu, oracle):
     import torch
     N, K, M = 500, 1024, 5

@@ -76,39 +76,56 @@ int check_ckpt(const char *fn, const uint32_t *W, const uint16_t *S, int64_t N, 
     return 0;
 }
 
+// Activation rows and row grouping of the dense GEMVs: rpg = 0 (every row
+// reads x[m * xs ...]) or rpg >= 16 rows per slice (row n reads slice n / rpg
+// at x + m * xs + (n / rpg) * K, gpu::gemv_rows, src/kernels/gemv.hpp:11-14);
+// at most 64 slices (one launch each). With more than one row, the stride
+// covers every slice.
+int check_rpg(const char *fn, int rpg, int N, int K, int M, const void *x, int xs) {
+    REQUIRE(rpg == 0 || rpg >= 16, "%s: rpg = %d (need 0 or >= 16)", fn, rpg);
+    const int64_t slices = rpg > 0 ? (int64_t(N) + rpg - 1) / rpg : 1;
+    REQUIRE(slices <= 64, "%s: rpg = %d gives %lld slices of N = %d (at most 64)", fn, rpg, (long long)slices, N);
+    REQUIRE(xs >= K && xs % 8 == 0 && aligned(x, 16) && (M == 1 || int64_t(xs) >= slices * K),
+            "%s: x stride %d must be >= K, a multiple of 8 and cover %lld slices of K = %d, x 16-byte aligned", fn, xs,
+            (long long)slices, K);
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
 
-int qw_q4_abi_version(void) { return 3; }
+int qw_q4_abi_version(void) { return 4; }
 
 const char *qw_q4_last_error(void) { return g_err.c_str(); }
 
 int qw_q4_gemv(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *x, int x_f16, int xs, void *y,
-               int ys, int y_bf16, int N, int K, int M, int accumulate, void *stream) {
+               int ys, int y_bf16, int N, int K, int M, int rpg, int accumulate, void *stream) {
     if (int r = check_q4("qw_q4_gemv", W, S, N, K)) return r;
     REQUIRE(x && y, "qw_q4_gemv: null x or y");
     REQUIRE(M >= 1 && M <= 32, "qw_q4_gemv: M = %d outside 1..32", M);
-    REQUIRE(xs >= K && xs % 8 == 0 && aligned(x, 16), "qw_q4_gemv: x stride %d must be >= K, a multiple of 8, x 16-byte aligned", xs);
+    if (int r = check_rpg("qw_q4_gemv", rpg, N, K, M, x, xs)) return r;
     REQUIRE(ys >= N || M == 1, "qw_q4_gemv: y stride %d < N", ys);
     REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_q4_gemv: y misaligned");
     qwq4::GemvArgs a{W, S, Z, x, xs, y, ys, y_bf16 != 0, N, K, M, accumulate != 0};
     a.x_f16 = x_f16 != 0;
+    a.rpg = rpg;
     qwq4::launch_gemv(a, st(stream));
     return launched("qw_q4_gemv");
 }
 
 int qw_w16_gemv(const uint16_t *W, int ldw, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N,
-                int K, int M, int accumulate, void *stream) {
+                int K, int M, int rpg, int accumulate, void *stream) {
     REQUIRE(W && x && y, "qw_w16_gemv: null W, x or y");
     REQUIRE(N >= 1 && K >= 32 && K % 32 == 0, "qw_w16_gemv: N = %d, K = %d (need N >= 1, K a positive multiple of 32)",
             N, K);
     REQUIRE(ldw >= K && ldw % 8 == 0 && aligned(W, 16), "qw_w16_gemv: ldw %d must be >= K, a multiple of 8, W 16-byte aligned", ldw);
     REQUIRE(M >= 1 && M <= 32, "qw_w16_gemv: M = %d outside 1..32", M);
-    REQUIRE(xs >= K && xs % 8 == 0 && aligned(x, 16), "qw_w16_gemv: x stride %d must be >= K, a multiple of 8, x 16-byte aligned", xs);
+    if (int r = check_rpg("qw_w16_gemv", rpg, N, K, M, x, xs)) return r;
     REQUIRE(ys >= N || M == 1, "qw_w16_gemv: y stride %d < N", ys);
     REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_w16_gemv: y misaligned");
     qwq4::W16Args a{W, ldw, x, xs, y, ys, y_bf16 != 0, N, K, M, accumulate != 0, f16 != 0, 0};
+    a.rpg = rpg;
     qwq4::launch_w16_gemv(a, st(stream));
     return launched("qw_w16_gemv");
 }
@@ -128,18 +145,18 @@ int qw_w16_tile(const uint16_t *W, int ldw, int N, int K, void *Wt, void *stream
 }
 
 int qw_w16_gemv_tiled(const void *Wt, const uint16_t *x, int xs, int f16, void *y, int ys, int y_bf16, int N, int K,
-                      int M, int accumulate, void *stream) {
+                      int M, int rpg, int accumulate, void *stream) {
     REQUIRE(Wt && x && y, "qw_w16_gemv_tiled: null Wt, x or y");
     REQUIRE(N >= 1 && K >= 32 && K % 32 == 0,
             "qw_w16_gemv_tiled: N = %d, K = %d (need N >= 1, K a positive multiple of 32)", N, K);
     REQUIRE(aligned(Wt, 16), "qw_w16_gemv_tiled: Wt must be 16-byte aligned");
     REQUIRE(M >= 1 && M <= 32, "qw_w16_gemv_tiled: M = %d outside 1..32", M);
-    REQUIRE(xs >= K && xs % 8 == 0 && aligned(x, 16),
-            "qw_w16_gemv_tiled: x stride %d must be >= K, a multiple of 8, x 16-byte aligned", xs);
+    if (int r = check_rpg("qw_w16_gemv_tiled", rpg, N, K, M, x, xs)) return r;
     REQUIRE(ys >= N || M == 1, "qw_w16_gemv_tiled: y stride %d < N", ys);
     REQUIRE(aligned(y, y_bf16 ? 2 : 4), "qw_w16_gemv_tiled: y misaligned");
     qwq4::W16Args a{static_cast<const uint16_t *>(Wt), K, x, xs, y, ys, y_bf16 != 0, N, K, M, accumulate != 0,
                     f16 != 0, 1};
+    a.rpg = rpg;
     qwq4::launch_w16_gemv(a, st(stream));
     return launched("qw_w16_gemv_tiled");
 }
@@ -215,18 +232,20 @@ size_t qw_q4_gemm_workspace_size(int T, int K) {
 }
 
 int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const uint16_t *X, int x_f16, int ldx, int T,
-               void *Y, int ldy, int y_bf16, int N, int K, void *workspace, size_t workspace_bytes, void *stream) {
+               void *Y, int ldy, int y_type, int N, int K, void *workspace, size_t workspace_bytes, void *stream) {
     if (int r = check_q4("qw_q4_gemm", W, S, N, K)) return r;
     REQUIRE(X && Y, "qw_q4_gemm: null X or Y");
     REQUIRE(T >= 1, "qw_q4_gemm: T = %d must be >= 1", T);
     REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(X, 16), "qw_q4_gemm: ldx %d must be >= K, a multiple of 8, X 16-byte aligned", ldx);
     REQUIRE(ldy >= N, "qw_q4_gemm: ldy %d < N", ldy);
-    REQUIRE(aligned(Y, 16) && ldy % (y_bf16 ? 8 : 4) == 0,
+    REQUIRE(y_type == QW_T_F32 || y_type == QW_T_BF16 || y_type == QW_T_F16, "qw_q4_gemm: y_type = %d (0 fp32, 1 bf16, 2 fp16)",
+            y_type);
+    REQUIRE(aligned(Y, 16) && ldy % (y_type == QW_T_F32 ? 4 : 8) == 0,
             "qw_q4_gemm: Y must be 16-byte aligned with rows of a multiple of 16 bytes (ldy %d)", ldy);
     const size_t need = x_f16 ? 0 : qwq4::gemm_workspace_bytes(T, K);
     REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
             "qw_q4_gemm: workspace needs %zu bytes, 256-byte aligned (got %zu)", need, workspace_bytes);
-    qwq4::GemmArgs a{W, S, Z, X, ldx, T, Y, ldy, y_bf16 != 0, N, K, workspace};
+    qwq4::GemmArgs a{W, S, Z, X, ldx, T, Y, ldy, y_type, N, K, workspace};
     a.x_f16 = x_f16 != 0;
     qwq4::launch_gemm(a, st(stream));
     return launched("qw_q4_gemm");
@@ -252,7 +271,7 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
                         const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                         const uint16_t *dz, int E, int H, int F, const int32_t *offsets, const int32_t *active,
                         const int32_t *n_active, const int32_t *pair_tok, const uint16_t *x, int x_f16, int T,
-                        int topk, uint16_t *h, float *yp, void *stream) {
+                        int topk, uint16_t *h, void *yp, int yp_f16, void *stream) {
     if (int r = check_q4("qw_moe_experts_gemv(gate)", gw, gs, int64_t(E) * F, H)) return r;
     if (int r = check_q4("qw_moe_experts_gemv(up)", uw, us, int64_t(E) * F, H)) return r;
     if (int r = check_q4("qw_moe_experts_gemv(down)", dw, ds, int64_t(E) * H, F)) return r;
@@ -260,10 +279,11 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
     REQUIRE(T >= 1 && T <= 32, "qw_moe_experts_gemv: T = %d outside 1..32", T);
     REQUIRE(qwq4::moe_gemv_supported(H, F), "qw_moe_experts_gemv: H = %d, F = %d too large", H, F);
     REQUIRE(topk >= 1 && topk <= E, "qw_moe_experts_gemv: topk = %d outside 1..E", topk);
-    REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(yp, 4), "qw_moe_experts_gemv: x/h must be 16-byte aligned");
+    REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(yp, 4), "qw_moe_experts_gemv: x/h must be 16-byte aligned, yp 4");
     qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, offsets, active, n_active, pair_tok,
                         x, T, topk, h, yp};
     a.x_f16 = x_f16 != 0;
+    a.yp_f16 = yp_f16 != 0;
     qwq4::launch_moe_gemv(a, st(stream));
     return launched("qw_moe_experts_gemv");
 }
@@ -340,14 +360,18 @@ int qw_moe_experts_w4a8(const uint32_t *gw, const uint16_t *gs, const uint16_t *
     return launched("qw_moe_experts_w4a8");
 }
 
-int qw_moe_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared, int T,
-                   int topk, int H, void *out, int out_bf16, void *stream) {
+int qw_moe_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const void *shared,
+                   int shared_f16, int T, int topk, int H, void *out, int out_type, void *stream) {
     REQUIRE(yp && tok_slot && tok_w && out, "qw_moe_combine: null pointer");
     REQUIRE(T >= 1 && topk >= 1 && H >= 4 && H % 4 == 0, "qw_moe_combine: T = %d, topk = %d, H = %d (need H %% 4 == 0)", T,
             topk, H);
-    REQUIRE(aligned(yp, yp_f16 ? 8 : 16) && (!shared || aligned(shared, 16)) && aligned(out, out_bf16 ? 8 : 16),
+    REQUIRE(out_type == QW_T_F32 || out_type == QW_T_BF16 || out_type == QW_T_F16,
+            "qw_moe_combine: out_type = %d (0 fp32, 1 bf16, 2 fp16)", out_type);
+    REQUIRE(aligned(yp, yp_f16 ? 8 : 16) && (!shared || aligned(shared, shared_f16 ? 8 : 16)) &&
+                aligned(out, out_type == QW_T_F32 ? 16 : 8),
             "qw_moe_combine: misaligned yp/shared/out");
-    qwq4::launch_combine(yp, yp_f16 != 0, tok_slot, tok_w, shared, T, topk, H, out, out_bf16 != 0, st(stream));
+    qwq4::launch_combine(yp, yp_f16 != 0, tok_slot, tok_w, shared, shared_f16 != 0, T, topk, H, out, out_type,
+                         st(stream));
     return launched("qw_moe_combine");
 }
 
@@ -552,7 +576,7 @@ int moe_decode_check(const char *fn, const float *router_w, const uint16_t *x, i
                      const uint32_t *gw, const uint16_t *gs, const uint32_t *uw, const uint16_t *us,
                      const uint32_t *dw, const uint16_t *ds, int H, int F, const void *out, const float *logits,
                      const int32_t *top_e, const float *top_w, const int32_t *tok_slot, const uint16_t *h,
-                     const float *yp) {
+                     const void *yp, int out_type) {
     if (int r = check_q4(fn, gw, gs, int64_t(E) * F, H)) return r;
     if (int r = check_q4(fn, uw, us, int64_t(E) * F, H)) return r;
     if (int r = check_q4(fn, dw, ds, int64_t(E) * H, F)) return r;
@@ -560,8 +584,11 @@ int moe_decode_check(const char *fn, const float *router_w, const uint16_t *x, i
     REQUIRE(T >= 1 && T <= 32, "%s: T = %d outside 1..32", fn, T);
     REQUIRE(E >= 1 && E <= 1024 && topk >= 1 && topk <= E && topk <= 64, "%s: E = %d, topk = %d", fn, E, topk);
     REQUIRE(qwq4::moe_gemv_supported(H, F), "%s: H = %d, F = %d too large", fn, H, F);
-    REQUIRE(aligned(router_w, 16) && aligned(x, 16) && aligned(h, 16), "%s: router_w, x, h must be 16-byte aligned",
-            fn);
+    REQUIRE(aligned(router_w, 16) && aligned(x, 16) && aligned(h, 16) && aligned(yp, 4),
+            "%s: router_w, x, h must be 16-byte aligned, yp 4-byte", fn);
+    REQUIRE(out_type == QW_T_F32 || out_type == QW_T_BF16 || out_type == QW_T_F16,
+            "%s: out_type = %d (0 fp32, 1 bf16, 2 fp16)", fn, out_type);
+    REQUIRE(aligned(out, out_type == QW_T_F32 ? 16 : 8), "%s: out misaligned", fn);
     return 0;
 }
 
@@ -570,8 +597,8 @@ int moe_decode_check(const char *fn, const float *router_w, const uint16_t *x, i
 void moe_decode_launch(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
                        const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
                        const uint16_t *uz, const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F,
-                       const float *shared, void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w,
-                       int32_t *tok_slot, uint16_t *h, float *yp, unsigned char *w, const DecodeLayout &L,
+                       const float *shared, void *out, int out_type, float *logits, int32_t *top_e, float *top_w,
+                       int32_t *tok_slot, uint16_t *h, void *yp, int yp_f16, unsigned char *w, const DecodeLayout &L,
                        hipStream_t s) {
     auto at = [&](size_t off) { return reinterpret_cast<int32_t *>(w + off); };
     qwq4::RouteArgs ra{logits, T, E, topk, 0, top_e, top_w, at(L.counts), at(L.offsets), tok_slot, at(L.pair_tok),
@@ -583,12 +610,13 @@ void moe_decode_launch(const float *router_w, const uint16_t *x, int x_f16, int 
     // (one launch less); from there on its own launch is faster than the
     // serial tail it adds to those blocks
     const bool fold = T <= 4;
-    const qwq4::CombineArgs cmb{at(L.dcounters), tok_slot, top_w, shared, out, out_bf16};
+    const qwq4::CombineArgs cmb{at(L.dcounters), tok_slot, top_w, shared, out, out_type};
     qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, at(L.offsets), at(L.active), at(L.n_active),
                         at(L.pair_tok), x, T, topk, h, yp, fold ? &cmb : nullptr};
     a.x_f16 = x_f16 != 0;
+    a.yp_f16 = yp_f16 != 0;
     qwq4::launch_moe_gemv(a, s);
-    if (!fold) qwq4::launch_combine(yp, 0, tok_slot, top_w, shared, T, topk, H, out, out_bf16, s);
+    if (!fold) qwq4::launch_combine(yp, yp_f16 != 0, tok_slot, top_w, shared, 0, T, topk, H, out, out_type, s);
 }
 
 // ---- the allocation-free variant's scratch: one array per GPU, held until
@@ -623,6 +651,18 @@ int static_scratch(void **ptr) {
     return 0;
 }
 
+// Zeroes the completion counters at the start of the scratch (a fill
+// kernel rather than a memset node, so it is also safe inside graph capture).
+__global__ void zero_counters_kernel(uint32_t *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+void reset_static_counters(void *scratch_ptr, hipStream_t s) {
+    constexpr int n = int(kStaticCounterBytes / 4);
+    zero_counters_kernel<<<(n + 255) / 256, 256, 0, s>>>(static_cast<uint32_t *>(scratch_ptr), n);
+}
+
 // The workspace layout with the counters moved to the fixed region.
 DecodeLayout static_layout(int T, int E, int topk, int H, int F) {
     DecodeLayout L = decode_layout(T, E, topk, H, F);
@@ -640,16 +680,16 @@ extern "C" {
 int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
                   const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
                   const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
-                  void *out, int out_bf16, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
-                  uint16_t *h, float *yp, void *workspace, size_t workspace_bytes, void *stream) {
+                  void *out, int out_type, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
+                  uint16_t *h, void *yp, int yp_f16, void *workspace, size_t workspace_bytes, void *stream) {
     if (int r = moe_decode_check("qw_moe_decode", router_w, x, T, E, topk, gw, gs, uw, us, dw, ds, H, F, out, logits,
-                                 top_e, top_w, tok_slot, h, yp))
+                                 top_e, top_w, tok_slot, h, yp, out_type))
         return r;
     REQUIRE(workspace && aligned(workspace, 256), "qw_moe_decode: workspace null or not 256-byte aligned");
     const DecodeLayout L = decode_layout(T, E, topk, H, F);
     REQUIRE(workspace_bytes >= L.total, "qw_moe_decode: workspace needs %zu bytes", L.total);
-    moe_decode_launch(router_w, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_bf16,
-                      logits, top_e, top_w, tok_slot, h, yp, static_cast<unsigned char *>(workspace), L, st(stream));
+    moe_decode_launch(router_w, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_type,
+                      logits, top_e, top_w, tok_slot, h, yp, yp_f16, static_cast<unsigned char *>(workspace), L, st(stream));
     return launched("qw_moe_decode");
 }
 
@@ -658,13 +698,16 @@ size_t qw_moe_decode_static_max_bytes(void) { return kStaticScratchBytes; }
 int qw_moe_decode_static(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk,
                          const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
                          const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
-                         const uint16_t *dz, int H, int F, const float *shared, void *out, int out_bf16,
-                         float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot, uint16_t *h, float *yp,
-                         void *stream) {
+                         const uint16_t *dz, int H, int F, const float *shared, void *out, int out_type,
+                         float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot, uint16_t *h, void *yp,
+                         int yp_f16, void *stream) {
     if (int r = moe_decode_check("qw_moe_decode_static", router_w, x, T, E, topk, gw, gs, uw, us, dw, ds, H, F, out,
-                                 logits, top_e, top_w, tok_slot, h, yp))
+                                 logits, top_e, top_w, tok_slot, h, yp, out_type))
         return r;
     const DecodeLayout L = static_layout(T, E, topk, H, F);
+    // Every shape moe_decode_check accepts fits (the largest, T = 32,
+    // E = 1024, H = 3840, k = 64, needs about 3.97 MB of the 4 MiB); these
+    // checks guard that bound should the limits above change.
     REQUIRE(L.total <= kStaticScratchBytes,
             "qw_moe_decode_static: T = %d, E = %d, k = %d, H = %d needs %zu bytes of scratch, more than the %zu "
             "the library holds (use qw_moe_decode with a workspace)",
@@ -673,9 +716,25 @@ int qw_moe_decode_static(const float *router_w, const uint16_t *x, int x_f16, in
             "qw_moe_decode_static: E = %d or H = %d needs more completion counters than the scratch holds", E, H);
     void *w = nullptr;
     if (int r = static_scratch(&w)) return r;
-    moe_decode_launch(router_w, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_bf16,
-                      logits, top_e, top_w, tok_slot, h, yp, static_cast<unsigned char *>(w), L, st(stream));
-    return launched("qw_moe_decode_static");
+    moe_decode_launch(router_w, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_type,
+                      logits, top_e, top_w, tok_slot, h, yp, yp_f16, static_cast<unsigned char *>(w), L, st(stream));
+    const int rc = launched("qw_moe_decode_static");
+    if (rc != QW_Q4_OK) {
+        // a launch failed after others were enqueued: the counters those
+        // left behind would misplace the next call's last block, so they are
+        // cleared behind them on the same stream
+        reset_static_counters(w, st(stream));
+        if (hipGetLastError() != hipSuccess)
+            g_err += "; clearing the completion counters failed too (call qw_moe_decode_static_reset)";
+    }
+    return rc;
+}
+
+int qw_moe_decode_static_reset(void *stream) {
+    void *w = nullptr;
+    if (int r = static_scratch(&w)) return r;
+    reset_static_counters(w, st(stream));
+    return launched("qw_moe_decode_static_reset");
 }
 
 }  // extern "C"

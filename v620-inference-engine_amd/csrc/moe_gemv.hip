@@ -18,7 +18,9 @@
 //   gate/up  waves = subtiles x {gate, up} x KS; the reducing wave also
 //            forms h = silu(g) * u (fp16, saturated, the reference's fp16
 //            intermediate) from the two sums it holds.
-//   down     waves = subtiles x KS; yp fp32.
+//   down     waves = subtiles x KS; yp fp32, or fp16 (YP16: rounded to
+//            nearest even, finite values beyond +-65504 saturated; the
+//            reference's moe_experts_P output).
 #include "q4_gemv_core.cuh"
 #include "q4_kernels.hpp"
 
@@ -29,7 +31,29 @@ __host__ __device__ inline size_t moe_lds_bytes(int R, int K) {
 }
 
 __device__ __forceinline__ uint16_t silu_mul_f16(float g, float u) {
-    return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(g / (1.f + __expf(-g)) * u));
+    return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(silu_ref(g) * u));
+}
+
+// yp element as stored: the fp32 sum, or its fp16 rounding (YP16) as a
+// float, so a fused combine adds exactly what the unfused one reads back.
+template <bool YP16>
+__device__ __forceinline__ float yp_value(float v) {
+    if constexpr (YP16) return float(f32_to_f16_satfinite(v));
+    else return v;
+}
+
+template <bool YP16>
+__device__ __forceinline__ void store_yp(void *yp, int64_t i, float v) {
+    if constexpr (YP16) static_cast<uint16_t *>(yp)[i] = __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(v));
+    else static_cast<float *>(yp)[i] = v;
+}
+
+// The fused combine's output element (type c.out_type: 0 fp32, 1 bf16,
+// 2 fp16 saturated).
+__device__ __forceinline__ void store_out(const CombineArgs &c, int64_t i, float v) {
+    if (c.out_type == 1) static_cast<uint16_t *>(c.out)[i] = f32_to_bf16_rne(v);
+    else if (c.out_type == 2) static_cast<uint16_t *>(c.out)[i] = __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(v));
+    else static_cast<float *>(c.out)[i] = v;
 }
 
 // A wave-uniform read of routing data through the scalar cache (the
@@ -129,13 +153,13 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
 // CMB: the last block of each row block (over the active experts, counted
 // on a device-scope counter) also forms the combined output of those rows
 // for every token, in the fixed selection order, then clears the counter.
-template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB, bool MULTI>
+template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB, bool MULTI, bool YP16>
 __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz,
                                                             const int32_t *__restrict__ offsets,
                                                             const int32_t *__restrict__ active,
                                                             const int32_t *__restrict__ n_active,
                                                             const uint16_t *__restrict__ h, int E, int H, int F, int R,
-                                                            float *__restrict__ yp, CombineArgs c, int T, int topk) {
+                                                            void *__restrict__ yp, CombineArgs c, int T, int topk) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int e = block_expert(n_active, active, E);
     if (e < 0) return;
@@ -170,10 +194,17 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = 4 * q + r;
-                if (m < mc) {
-                    float *dst = yp + int64_t(base + m0 + m) * H + lsub * 16 + n;
-                    if constexpr (CMB) st_agent(dst, acc[0][r]);
-                    else *dst = acc[0][r];
+                const int64_t i = int64_t(base + m0 + m) * H + lsub * 16 + n;
+                if constexpr (CMB && YP16) {
+                    // fp16 pairs of adjacent rows (lanes n, n ^ 1) as one
+                    // agent-coherent 32-bit store by the even lane
+                    const uint32_t hv = __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(acc[0][r]));
+                    const uint32_t pv = uint32_t(__shfl_xor(int(hv), 1));
+                    if (m < mc && (n & 1) == 0)
+                        st_agent_u32(reinterpret_cast<uint32_t *>(static_cast<uint16_t *>(yp) + i), hv | (pv << 16));
+                } else if (m < mc) {
+                    if constexpr (CMB) st_agent(static_cast<float *>(yp) + i, acc[0][r]);
+                    else store_yp<YP16>(yp, i, acc[0][r]);
                 }
             }
         }
@@ -207,17 +238,21 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
                 const int qn = min(c.qc, topk - q0);
                 for (int p = tid; p < ne * qn; p += nt) {
                     const int qq = p / ne, ee = e0 + (p - qq * ne), tk2 = ee / nr, j2 = r0 + (ee - tk2 * nr);
-                    ybuf[p] = ld_agent(yp + int64_t(c.tok_slot[tk2 * topk + q0 + qq]) * H + j2);
+                    const int64_t yi = int64_t(c.tok_slot[tk2 * topk + q0 + qq]) * H + j2;
+                    if constexpr (YP16) {
+                        const uint32_t w = ld_agent_u32(
+                            reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(yp) + (yi & ~int64_t(1))));
+                        ybuf[p] = f16_bits_to_f32(uint16_t(w >> ((yi & 1) * 16)));
+                    } else {
+                        ybuf[p] = ld_agent(static_cast<const float *>(yp) + yi);
+                    }
                 }
                 __syncthreads();
                 if (tid < ne)
                     for (int qq = 0; qq < qn; ++qq) v += c.tok_w[tk * topk + q0 + qq] * ybuf[qq * ne + tid];
                 __syncthreads();
             }
-            if (tid < ne) {
-                if (c.out_bf16) static_cast<uint16_t *>(c.out)[int64_t(tk) * H + j] = f32_to_bf16_rne(v);
-                else static_cast<float *>(c.out)[int64_t(tk) * H + j] = v;
-            }
+            if (tid < ne) store_out(c, int64_t(tk) * H + j, v);
         }
     }
 }
@@ -230,12 +265,12 @@ __global__ __launch_bounds__(512) void moe_down_gemv_kernel(const uint32_t *dw, 
 // combine's order (shared row, then the selections in order): no yp round
 // trip through memory and no cross-block count before the combine. yp is
 // still written (an output of the decode block).
-template <int GW, bool HAS_Z, bool CH4>
+template <int GW, bool HAS_Z, bool CH4, bool YP16>
 __global__ __launch_bounds__(1024) void moe_down_t1_kernel(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz,
                                                            const int32_t *__restrict__ active,
                                                            const int32_t *__restrict__ n_active,
                                                            const uint16_t *__restrict__ h, int E, int H, int F,
-                                                           float *__restrict__ yp, CombineArgs c, int topk) {
+                                                           void *__restrict__ yp, CombineArgs c, int topk) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
               n = lane % 16;
@@ -274,8 +309,8 @@ __global__ __launch_bounds__(1024) void moe_down_t1_kernel(const uint32_t *dw, c
     if (kp == 0 && live) {
         acc += red[y * WAVE + lane];
         if (q == 0) {
-            yb[y * 16 + n] = acc[0];
-            yp[int64_t(y) * H + blockIdx.x * 16 + n] = acc[0];
+            yb[y * 16 + n] = yp_value<YP16>(acc[0]);
+            store_yp<YP16>(yp, int64_t(y) * H + blockIdx.x * 16 + n, acc[0]);
         }
     }
     __syncthreads();
@@ -286,8 +321,7 @@ __global__ __launch_bounds__(1024) void moe_down_t1_kernel(const uint32_t *dw, c
 #pragma unroll
         for (int qq = 0; qq < 8; ++qq)
             if (qq < topk) v += w_q[qq] * yb[slot_q[qq] * 16 + tid];
-        if (c.out_bf16) static_cast<uint16_t *>(c.out)[j] = f32_to_bf16_rne(v);
-        else static_cast<float *>(c.out)[j] = v;
+        store_out(c, j, v);
     }
 }
 
@@ -297,13 +331,13 @@ __global__ __launch_bounds__(1024) void moe_down_t1_kernel(const uint32_t *dw, c
 // K halves of the general kernel's split into two accumulators and adds them
 // as its reduction does (same values, bit for bit); the block then forms both
 // tokens' outputs in the combine's order. yp is still written.
-template <int GW, bool HAS_Z, bool CH4>
+template <int GW, bool HAS_Z, bool CH4, bool YP16>
 __global__ __launch_bounds__(1024) void moe_down_t2_kernel(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz,
                                                            const int32_t *__restrict__ offsets,
                                                            const int32_t *__restrict__ active,
                                                            const int32_t *__restrict__ n_active,
                                                            const uint16_t *__restrict__ h, int E, int H, int F,
-                                                           float *__restrict__ yp, CombineArgs c, int topk) {
+                                                           void *__restrict__ yp, CombineArgs c, int topk) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, y = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
               n = lane % 16;
@@ -339,8 +373,8 @@ __global__ __launch_bounds__(1024) void moe_down_t2_kernel(const uint32_t *dw, c
         for (int r = 0; r < 4; ++r) {
             const int m = 4 * q + r;
             if (m < M) {
-                yb[(base + m) * 16 + n] = a0[r];
-                yp[int64_t(base + m) * H + blockIdx.x * 16 + n] = a0[r];
+                yb[(base + m) * 16 + n] = yp_value<YP16>(a0[r]);
+                store_yp<YP16>(yp, int64_t(base + m) * H + blockIdx.x * 16 + n, a0[r]);
             }
         }
     }
@@ -352,8 +386,7 @@ __global__ __launch_bounds__(1024) void moe_down_t2_kernel(const uint32_t *dw, c
 #pragma unroll
         for (int qq = 0; qq < 8; ++qq)
             if (qq < topk) v += w_q[tk * topk + qq] * yb[slot_q[tk * topk + qq] * 16 + row];
-        if (c.out_bf16) static_cast<uint16_t *>(c.out)[int64_t(tk) * H + j] = f32_to_bf16_rne(v);
-        else static_cast<float *>(c.out)[int64_t(tk) * H + j] = v;
+        store_out(c, int64_t(tk) * H + j, v);
     }
 }
 
@@ -389,18 +422,18 @@ static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStrea
                                 a.E, a.H, a.F, R, a.h);
 }
 
-template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB>
+template <int KS, int GW, bool HAS_Z, bool CH4, bool CMB, bool YP16>
 static void launch_down_c(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
     if constexpr (CMB && KS == 2 && GW <= 8) {  // GW 16 would spill at 1024 threads
         if (a.T == 1 && a.topk <= 8) {
             const size_t lds = size_t(x_pieces(8, a.F)) * 16 + size_t(8) * WAVE * 16 + 8 * 16 * 4;
-            moe_down_t1_kernel<GW, HAS_Z, CH4><<<unsigned(a.H / 16), 1024, lds, s>>>(
+            moe_down_t1_kernel<GW, HAS_Z, CH4, YP16><<<unsigned(a.H / 16), 1024, lds, s>>>(
                 a.dw, a.ds, a.dz, a.active, a.n_active, a.h, a.E, a.H, a.F, a.yp, *a.cmb, a.topk);
             return;
         }
         if constexpr (GW <= 6) {  // two ranges of 8 groups would spill at 1024 threads
             if (a.T == 2 && a.topk <= 8) {
-                auto kern = moe_down_t2_kernel<GW, HAS_Z, CH4>;
+                auto kern = moe_down_t2_kernel<GW, HAS_Z, CH4, YP16>;
                 const size_t lds = size_t(x_pieces(16, a.F)) * 16 + 16 * 16 * 4;
                 if (lds > 64 * 1024) raise_lds_limit(reinterpret_cast<const void *>(kern));
                 kern<<<unsigned(a.H / 16), 1024, lds, s>>>(a.dw, a.ds, a.dz, a.offsets, a.active, a.n_active, a.h,
@@ -409,7 +442,8 @@ static void launch_down_c(const MoeGemvArgs &a, int max_active, int R, hipStream
             }
         }
     }
-    auto kern = a.T <= R ? moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB, false> : moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB, true>;
+    auto kern = a.T <= R ? moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB, false, YP16>
+                         : moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB, true, YP16>;
     const size_t lds = moe_lds_bytes(R, a.F);
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
     constexpr int SUB = 8 / KS;
@@ -424,8 +458,13 @@ static void launch_down_c(const MoeGemvArgs &a, int max_active, int R, hipStream
 
 template <int KS, int GW, bool HAS_Z, bool CH4>
 static void launch_down(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
-    if (a.cmb) launch_down_c<KS, GW, HAS_Z, CH4, true>(a, max_active, R, s);
-    else launch_down_c<KS, GW, HAS_Z, CH4, false>(a, max_active, R, s);
+    if (a.yp_f16) {
+        if (a.cmb) launch_down_c<KS, GW, HAS_Z, CH4, true, true>(a, max_active, R, s);
+        else launch_down_c<KS, GW, HAS_Z, CH4, false, true>(a, max_active, R, s);
+    } else {
+        if (a.cmb) launch_down_c<KS, GW, HAS_Z, CH4, true, false>(a, max_active, R, s);
+        else launch_down_c<KS, GW, HAS_Z, CH4, false, false>(a, max_active, R, s);
+    }
 }
 
 template <bool DOWN, int KS, int GW, bool HAS_Z, bool CH4>

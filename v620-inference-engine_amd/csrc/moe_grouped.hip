@@ -33,7 +33,7 @@ static __device__ __forceinline__ uint16_t f32_to_f16_sat(float v) {
     return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(v));
 }
 
-static __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + __expf(-g)) * u; }
+static __device__ __forceinline__ float silu_mul(float g, float u) { return silu_ref(g) * u; }
 
 struct GateUpTile {
     const uint32_t *gw, *uw;

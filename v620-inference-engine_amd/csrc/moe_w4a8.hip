@@ -136,8 +136,6 @@ static __device__ __forceinline__ uint16_t f16_sat(float v) {
     return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(v));
 }
 
-// the reference's silu: x * (1 / (1 + exp(-x))) (src/kernels/common.cuh:94-99)
-static __device__ __forceinline__ float silu_ref(float g) { return g * (1.f / (1.f + __expf(-g))); }
 
 constexpr int W8_BN = 128;  // weight rows per block
 constexpr int W8_K = 128;   // K per stage (one scale group)

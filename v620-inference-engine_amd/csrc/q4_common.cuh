@@ -157,6 +157,13 @@ __device__ __forceinline__ _Float16 f32_to_f16_satfinite(float v) {
     return _Float16(finite ? fminf(fmaxf(v, -65504.f), 65504.f) : v);
 }
 
+// The reference's activation functions (src/kernels/common.cuh:94-99):
+// sigmoid(x) = 1 / (1 + exp(-x)) with the fast exp, silu(x) = x * sigmoid(x)
+// (a multiply by the reciprocal, not a division: the two can differ in the
+// last bit). Every SwiGLU of this library uses these two.
+__device__ __forceinline__ float sigmoid_ref(float x) { return 1.f / (1.f + __expf(-x)); }
+__device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __builtin_bit_cast(float, uint32_t(b) << 16); }
 
 __device__ __forceinline__ int group_zero(const uint32_t *Z, int64_t row, int zw, int g) {
@@ -205,6 +212,12 @@ __device__ __forceinline__ void st_agent(float *p, float v) {
 }
 __device__ __forceinline__ float ld_agent(const float *p) {
     return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent_u32(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_agent_u32(const uint32_t *p) {
+    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Counts the calling block on *counter; true in every thread of the block
 // that counted total-th. Every thread's earlier st_agent stores are complete

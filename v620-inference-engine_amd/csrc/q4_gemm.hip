@@ -51,7 +51,7 @@ void launch_x_to_f16(const uint16_t *X, int ldx, int T, int K, uint16_t *Xh, hip
 }
 
 // One GB_M x BN output tile at tokens t0.., weight rows n0..
-template <bool HAS_Z, bool Y_BF16, int GB_M, int BN>
+template <bool HAS_Z, int YT, int GB_M, int BN>
 __device__ __forceinline__ void gemm_tile_at(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt,
                                              const uint16_t *__restrict__ Xh, int lda, int T, void *__restrict__ Y,
                                              int ldy, int N, int K, int t0, int n0) {
@@ -69,9 +69,13 @@ __device__ __forceinline__ void gemm_tile_at(const uint32_t *Wt, const uint16_t 
     gemm_tile<GB_M, HAS_Z, BN>(ap, b, K, acc);
 
     const int wm = wave / Sh::NWN, wn2 = wave % Sh::NWN;
-    constexpr int YB = Y_BF16 ? 2 : 4;
+    constexpr int YB = YT == 0 ? 4 : 2;
     emit_tile<Sh::NJ, YB>(
-        epi_slot(wave), acc, [](float v, int, int) { return f32_to_bf16_rne(v); },
+        epi_slot(wave), acc,
+        [](float v, int, int) {
+            if constexpr (YT == 1) return f32_to_bf16_rne(v);
+            else return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(v));
+        },
         [&](int tr, int col, uint4 v) {
             const int t = t0 + wm * 64 + tr, n = n0 + wn2 * Sh::WNR + col;
             if (t < T && n < N)
@@ -84,7 +88,7 @@ __device__ __forceinline__ void gemm_tile_at(const uint32_t *Wt, const uint16_t 
 // run together and hit the same L2
 __device__ __forceinline__ int xcd_item(int w, int nb) { return nb % 8 == 0 ? (w % 8) * (nb / 8) + w / 8 : w; }
 
-template <bool HAS_Z, bool Y_BF16, int GB_M, int BN = GB_N>
+template <bool HAS_Z, int YT, int GB_M, int BN = GB_N>
 __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
                                                             const uint16_t *St,
                                                             const uint16_t *Zt,
@@ -93,7 +97,7 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
     // token-major tile order (consecutive items share their X rows)
     const int lin = xcd_item(int(blockIdx.y * gridDim.x + blockIdx.x), int(gridDim.x * gridDim.y));
     const int by = lin / gridDim.x, bx = lin % gridDim.x;
-    gemm_tile_at<HAS_Z, Y_BF16, GB_M, BN>(Wt, St, Zt, Xh, lda, T, Y, ldy, N, K, by * GB_M, bx * BN);
+    gemm_tile_at<HAS_Z, YT, GB_M, BN>(Wt, St, Zt, Xh, lda, T, Y, ldy, N, K, by * GB_M, bx * BN);
 }
 
 // 256 x 256 tiles that do not fill whole rounds of the chip: the first nbig
@@ -101,7 +105,7 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_kernel(const uint32_t *Wt,
 // halves, so the last round has twice the blocks at half the work each
 // instead of a partly idle round of whole tiles. Tiles are numbered
 // token-major over the 256 x 256 grid of nbx tiles per row.
-template <bool HAS_Z, bool Y_BF16>
+template <bool HAS_Z, int YT>
 __global__ __launch_bounds__(G_THREADS) void q4_gemm_mixed_kernel(const uint32_t *Wt, const uint16_t *St,
                                                                   const uint16_t *Zt,
                                                                   const uint16_t *__restrict__ Xh, int lda, int T,
@@ -110,17 +114,17 @@ __global__ __launch_bounds__(G_THREADS) void q4_gemm_mixed_kernel(const uint32_t
     const int w = blockIdx.x;
     if (w < nbig) {
         const int lin = xcd_item(w, nbig);
-        gemm_tile_at<HAS_Z, Y_BF16, 256, 256>(Wt, St, Zt, Xh, lda, T, Y, ldy, N, K, lin / nbx * 256, lin % nbx * 256);
+        gemm_tile_at<HAS_Z, YT, 256, 256>(Wt, St, Zt, Xh, lda, T, Y, ldy, N, K, lin / nbx * 256, lin % nbx * 256);
     } else {
         const int hw = xcd_item(w - nbig, nhalf), lin = nbig + hw / 2;
-        gemm_tile_at<HAS_Z, Y_BF16, 256, 128>(Wt, St, Zt, Xh, lda, T, Y, ldy, N, K, lin / nbx * 256,
+        gemm_tile_at<HAS_Z, YT, 256, 128>(Wt, St, Zt, Xh, lda, T, Y, ldy, N, K, lin / nbx * 256,
                                               lin % nbx * 256 + (hw % 2) * 128);
     }
 }
 
-template <bool HAS_Z, bool Y_BF16, int GB_M, int BN = GB_N>
+template <bool HAS_Z, int YT, int GB_M, int BN = GB_N>
 static void launch_gemm_t(const GemmArgs &a, const uint16_t *Xh, int lda, hipStream_t s) {
-    auto kern = q4_gemm_kernel<HAS_Z, Y_BF16, GB_M, BN>;
+    auto kern = q4_gemm_kernel<HAS_Z, YT, GB_M, BN>;
     const dim3 grid(unsigned((a.N + BN - 1) / BN), unsigned((a.T + GB_M - 1) / GB_M));
     kern<<<grid, G_THREADS, 0, s>>>(a.W, a.S, a.Z, Xh, lda, a.T, a.Y, a.ldy, a.N, a.K);
 }
@@ -130,14 +134,14 @@ static void launch_gemm_t(const GemmArgs &a, const uint16_t *Xh, int lda, hipStr
 // plus the rest as 256 x 128 halves in the same launch (2048-token
 // micro-batches of 4096->12288); else 256 tokens x 128 weight rows when those
 // fill whole rounds (the same dequant work per MFMA); else 128 x 256.
-template <bool HAS_Z, bool Y_BF16>
+template <bool HAS_Z, int YT>
 static void launch_gemm_mixed(const GemmArgs &a, const uint16_t *Xh, int lda, int nbig, int nhalf, hipStream_t s) {
     const int nbx = (a.N + 255) / 256;
-    q4_gemm_mixed_kernel<HAS_Z, Y_BF16><<<unsigned(nbig + nhalf), G_THREADS, 0, s>>>(
+    q4_gemm_mixed_kernel<HAS_Z, YT><<<unsigned(nbig + nhalf), G_THREADS, 0, s>>>(
         a.W, a.S, a.Z, Xh, lda, a.T, a.Y, a.ldy, a.N, a.K, nbx, nbig, nhalf);
 }
 
-template <bool HAS_Z, bool Y_BF16>
+template <bool HAS_Z, int YT>
 static void launch_gemm_m(const GemmArgs &a, const uint16_t *Xh, int lda, hipStream_t s) {
     int cus = 0, dev = 0;
     (void)hipGetDevice(&dev);
@@ -148,11 +152,11 @@ static void launch_gemm_m(const GemmArgs &a, const uint16_t *Xh, int lda, hipStr
         return rounds >= 4.0 || (rounds >= 1.0 && rounds - double(int64_t(rounds)) < 0.01);
     };
     const int64_t t256 = (a.T + 255) / 256, nb = int64_t((a.N + 255) / 256) * t256;
-    if (whole(nb)) launch_gemm_t<HAS_Z, Y_BF16, 256>(a, Xh, lda, s);
+    if (whole(nb)) launch_gemm_t<HAS_Z, YT, 256>(a, Xh, lda, s);
     else if (nb > cus && 2 * (nb % cus) <= cus)  // e.g. 2048 tokens x 12288 rows: 256 whole tiles + 256 halves
-        launch_gemm_mixed<HAS_Z, Y_BF16>(a, Xh, lda, int(nb / cus * cus), int(2 * (nb % cus)), s);
-    else if (whole(int64_t((a.N + 127) / 128) * t256)) launch_gemm_t<HAS_Z, Y_BF16, 256, 128>(a, Xh, lda, s);
-    else launch_gemm_t<HAS_Z, Y_BF16, 128>(a, Xh, lda, s);
+        launch_gemm_mixed<HAS_Z, YT>(a, Xh, lda, int(nb / cus * cus), int(2 * (nb % cus)), s);
+    else if (whole(int64_t((a.N + 127) / 128) * t256)) launch_gemm_t<HAS_Z, YT, 256, 128>(a, Xh, lda, s);
+    else launch_gemm_t<HAS_Z, YT, 128>(a, Xh, lda, s);
 }
 
 // bf16 rows go through the fp16 pre-pass into the workspace; fp16 rows
@@ -167,11 +171,13 @@ void launch_gemm(const GemmArgs &a, hipStream_t s) {
         lda = a.K;
     }
     if (a.Z) {
-        if (a.y_bf16) launch_gemm_m<true, true>(a, Xh, lda, s);
-        else launch_gemm_m<true, false>(a, Xh, lda, s);
+        if (a.y_type == 1) launch_gemm_m<true, 1>(a, Xh, lda, s);
+        else if (a.y_type == 2) launch_gemm_m<true, 2>(a, Xh, lda, s);
+        else launch_gemm_m<true, 0>(a, Xh, lda, s);
     } else {
-        if (a.y_bf16) launch_gemm_m<false, true>(a, Xh, lda, s);
-        else launch_gemm_m<false, false>(a, Xh, lda, s);
+        if (a.y_type == 1) launch_gemm_m<false, 1>(a, Xh, lda, s);
+        else if (a.y_type == 2) launch_gemm_m<false, 2>(a, Xh, lda, s);
+        else launch_gemm_m<false, 0>(a, Xh, lda, s);
     }
 }
 

@@ -337,16 +337,18 @@ __device__ __forceinline__ void stage_x_issue(const uint16_t *__restrict__ x, in
 template <int MB, int MR>
 constexpr int acc_elems() { return (MB - 1) * 4 + MR; }
 
+// Rows n_lo <= row < N of the subtile are stored (n_lo > 0: a launch whose
+// first rows belong to another activation slice, see launch_gemv).
 template <int MB, int MR>
 __device__ __forceinline__ void store_rows(const f32x4 (&acc)[MB], void *y, int ys, int y_bf16, int accumulate,
-                                           int M, int N, int sub, int lane) {
-    const int q = lane / 16, n = lane % 16;
+                                           int M, int N, int sub, int lane, int n_lo = 0) {
+    const int q = lane / 16, n = lane % 16, row = sub * 16 + n;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int r = 0; r < (mb == MB - 1 ? MR : 4); ++r) {
             const int m = mb * 16 + 4 * q + r;
-            if (m < M && sub * 16 + n < N) store_y(y, int64_t(m) * ys + sub * 16 + n, acc[mb][r], y_bf16, accumulate);
+            if (m < M && row < N && row >= n_lo) store_y(y, int64_t(m) * ys + row, acc[mb][r], y_bf16, accumulate);
         }
 }
 

@@ -39,13 +39,13 @@ template <typename XT, int NW, int MB, bool HAS_Z, bool CH4, bool PF, bool KSNW,
 __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t *Wt, const uint16_t *St, const uint16_t *Zt,
                                                              const uint16_t *x, int xs, int M, int K, int N, int KS_,
                                                              int SUB_, void *__restrict__ y, int ys, int y_bf16,
-                                                             int accumulate) {
+                                                             int accumulate, int n_lo) {
     // KSNW: one subtile per item, split over all NW waves, each wave exactly
     // GW groups (all compile-time)
     const int KS = KSNW ? NW : KS_, SUB = KSNW ? 1 : SUB_;
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int GW = DENSE_GW;
-    const int G = KSNW ? NW * GW : K / QGROUP, kc = x_row_stride(K), nsub = N / 16, gpk = KSNW ? GW : G / KS,
+    const int G = KSNW ? NW * GW : K / QGROUP, kc = x_row_stride(K), nsub = (N + 15) / 16, gpk = KSNW ? GW : G / KS,
               items = (nsub + SUB - 1) / SUB;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE,
               q = lane / 16, n = lane % 16, waves = KSNW ? NW : int(blockDim.x) / WAVE;
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t
         }
         ksplit_sum<MB, MR>(acc[0], red, KS, wave, kp, lane);
         const int sub = blockIdx.x * SUB + sl;
-        if (kp == 0 && sub < nsub) store_rows<MB, MR>(acc[0], y, ys, y_bf16, accumulate, M, N, sub, lane);
+        if (kp == 0 && sub < nsub) store_rows<MB, MR>(acc[0], y, ys, y_bf16, accumulate, M, N, sub, lane, n_lo);
     } else {
         // gpk <= GW here
         WaveRange<GW, HAS_Z, CH4> wn[1];
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(NW * WAVE) void q4_gemv_block_kernel(const uint32_t
                                lane);
             par ^= 1;
             const int sub = item * SUB + sl;
-            if (kp == 0 && sub < nsub) store_rows<MB, MR>(acc[0], y, ys, y_bf16, accumulate, M, N, sub, lane);
+            if (kp == 0 && sub < nsub) store_rows<MB, MR>(acc[0], y, ys, y_bf16, accumulate, M, N, sub, lane, n_lo);
             wr[0] = wn[0];
         }
     }
@@ -149,7 +149,7 @@ static void launch_dense_one(const GemvArgs &a, int KS, int SUB, int items, size
     const int threads = KS * SUB * WAVE;
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), threads, lds);  // LDS limit
     kern<<<items, threads, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.M, a.K, a.N, KS, SUB, a.y, a.ys,
-                                     a.y_bf16, a.accumulate);
+                                     a.y_bf16, a.accumulate, a.n_lo);
 }
 
 // Small batches (at most 4 activation pieces per thread) stage through
@@ -160,7 +160,7 @@ static void launch_dense_one(const GemvArgs &a, int KS, int SUB, int items, size
 template <typename XT, int NW, int MB, bool HAS_Z, bool CH4, bool KSNW, bool P4, int MR>
 static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
     const int waves = KS * SUB, threads = waves * WAVE, gpk = a.K / QGROUP / KS;
-    const int nsub = a.N / 16, items = (nsub + SUB - 1) / SUB;
+    const int nsub = (a.N + 15) / 16, items = (nsub + SUB - 1) / SUB;
     const int xpt = (a.M * (a.K / 8) + threads - 1) / threads;
     if constexpr (MB == 1) {
         // batches of 4 rows over more items than one round of resident
@@ -196,7 +196,7 @@ static void launch_dense_t(const GemvArgs &a, int KS, int SUB, hipStream_t s) {
     // keeps weight loads in flight
     const int blocks = items < lp.max_blocks ? items : lp.max_blocks;
     pf<<<blocks, threads, lds, s>>>(a.W, a.S, a.Z, a.x, a.xs, a.M, a.K, a.N, KS, SUB, a.y, a.ys,
-                                    a.y_bf16, a.accumulate);
+                                    a.y_bf16, a.accumulate, a.n_lo);
 }
 
 template <typename XT, int MB, bool HAS_Z, bool CH4, bool P4, int MR>

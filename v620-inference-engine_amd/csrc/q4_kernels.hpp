@@ -29,6 +29,8 @@ struct GemvArgs {
     void *y;
     int ys, y_bf16, N, K, M, accumulate;
     int x_f16 = 0;  // x rows are fp16 (else bf16)
+    int rpg = 0;    // rows per activation slice (0: one slice), as in gpu::gemv_rows
+    int n_lo = 0;   // rows below n_lo are computed but not stored (internal)
 };
 void launch_gemv(const GemvArgs &a, hipStream_t s);
 
@@ -40,7 +42,7 @@ struct CombineArgs {
     const float *tok_w;
     const float *shared;  // fp32 [T][H] or null
     void *out;
-    int out_bf16;
+    int out_type;  // 0 fp32, 1 bf16, 2 fp16
     int qc;  // selections staged per pass of the combine (set by the launcher)
 };
 // Down row blocks of the decode experts for H (the counters combine needs).
@@ -61,9 +63,10 @@ struct MoeGemvArgs {
     const uint16_t *x;
     int T, topk;
     uint16_t *h;
-    float *yp;
+    void *yp;                // fp32, or fp16 with yp_f16
     const CombineArgs *cmb;  // null: yp only
     int x_f16 = 0;           // x rows are fp16 (else bf16)
+    int yp_f16 = 0;
 };
 void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s);
 // Whether the expert GEMVs take these sizes (a wave holds <= 16 groups of its K range).
@@ -117,8 +120,9 @@ void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s)
 // LDS bytes the slot pass needs for (T, E); the C-ABI rejects larger inputs.
 void launch_route(const RouteArgs &a, hipStream_t s);
 
-void launch_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const float *shared,
-                    int T, int topk, int H, void *out, int out_bf16, hipStream_t s);
+// out_type: 0 fp32, 1 bf16, 2 fp16; shared fp32, or fp16 with shared_f16.
+void launch_combine(const void *yp, int yp_f16, const int32_t *tok_slot, const float *tok_w, const void *shared,
+                    int shared_f16, int T, int topk, int H, void *out, int out_type, hipStream_t s);
 
 // checkpoint order <-> tiled device format (q4_common.cuh)
 void launch_tile(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64_t N, int64_t K, uint32_t *Wt,
@@ -142,7 +146,9 @@ struct W16Args {
     int xs;
     void *y;
     int ys, y_bf16, N, K, M, accumulate, f16;
-    int tiled;  // W in the layout of launch_w16_tile (ldw unused)
+    int tiled;     // W in the layout of launch_w16_tile (ldw unused)
+    int rpg = 0;   // rows per activation slice (0: one slice), as in gpu::gemv_rows
+    int n_lo = 0;  // rows below n_lo are computed but not stored (internal)
 };
 bool w16_fits(int M, int K, int N);
 void launch_w16_gemv(const W16Args &a, hipStream_t s);
@@ -203,7 +209,7 @@ struct GemmArgs {
     const uint16_t *X;
     int ldx, T;
     void *Y;
-    int ldy, y_bf16, N, K;
+    int ldy, y_type, N, K;  // y_type: 0 fp32, 1 bf16, 2 fp16
     void *ws;  // workspace: fp16 copy of X (bf16 rows only)
     int x_f16 = 0;  // X rows are fp16 (else bf16)
 };

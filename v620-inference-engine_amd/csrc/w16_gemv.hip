@@ -31,7 +31,7 @@ constexpr int W16_MAX_KS = 8;  // waves per block
 template <typename XT, int MB, int MR, int XPT, int WS, bool TILED>
 __global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16_t *W, int ldw, const uint16_t *x,
                                                                     int xs, int M, int K, int N, void *__restrict__ y,
-                                                                    int ys, int y_bf16, int accumulate) {
+                                                                    int ys, int y_bf16, int accumulate, int n_lo) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int KS = blockDim.x / WAVE;
     const int tid = threadIdx.x, kp = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(W16_MAX_KS *WAVE) void w16_gemv_kernel(const uint16
             }
     }
     ksplit_sum<MB, MR>(acc, red, KS, kp, kp, lane);
-    if (kp == 0) store_rows<MB, MR>(acc, y, ys, y_bf16, accumulate, M, N, blockIdx.x, lane);
+    if (kp == 0) store_rows<MB, MR>(acc, y, ys, y_bf16, accumulate, M, N, blockIdx.x, lane, n_lo);
 }
 
 template <typename XT, int MB, int MR, bool TILED>
@@ -97,7 +97,8 @@ static void launch_w16_t(const W16Args &a, int KS, hipStream_t s) {
     const unsigned blocks = unsigned((a.N + 15) / 16);
     auto go = [&](auto kern) {
         if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), threads, lds);
-        kern<<<blocks, threads, lds, s>>>(a.W, a.ldw, a.x, a.xs, a.M, a.K, a.N, a.y, a.ys, a.y_bf16, a.accumulate);
+        kern<<<blocks, threads, lds, s>>>(a.W, a.ldw, a.x, a.xs, a.M, a.K, a.N, a.y, a.ys, a.y_bf16, a.accumulate,
+                                          a.n_lo);
     };
     const int spw = (a.K / 32 + KS - 1) / KS;
     auto pick = [&](auto ws) {
@@ -140,8 +141,34 @@ static void launch_w16_fit(const W16Args &a, hipStream_t s) {
     }
 }
 
-// Batches whose activations exceed LDS run as several launches of fewer rows.
+static void launch_w16_rows(const W16Args &a, hipStream_t s);
+
+// Rows grouped over activation slices (rpg > 0; row n reads x + (n / rpg) * K,
+// as gpu::gemv_rows does, src/kernels/gemv.hip:17): one launch per slice.
+// Row-major weights start the launch at the slice's first row; tiled ones at
+// its first 16-row tile, storing only the slice's rows (a tile that straddles
+// two slices is computed in both launches).
 void launch_w16_gemv(const W16Args &a, hipStream_t s) {
+    if (a.rpg <= 0) {
+        launch_w16_rows(a, s);
+        return;
+    }
+    const size_t ysz = a.y_bf16 ? 2 : 4;
+    for (int r0 = 0, sl = 0; r0 < a.N; r0 += a.rpg, ++sl) {
+        const int r1 = r0 + a.rpg < a.N ? r0 + a.rpg : a.N, b0 = a.tiled ? r0 / 16 * 16 : r0;
+        W16Args b = a;
+        b.rpg = 0;
+        b.W = a.tiled ? a.W + int64_t(b0) * a.K : a.W + int64_t(b0) * a.ldw;
+        b.x = a.x + int64_t(sl) * a.K;
+        b.y = static_cast<char *>(a.y) + int64_t(b0) * ysz;
+        b.N = r1 - b0;
+        b.n_lo = r0 - b0;
+        launch_w16_rows(b, s);
+    }
+}
+
+// Batches whose activations exceed LDS run as several launches of fewer rows.
+static void launch_w16_rows(const W16Args &a, hipStream_t s) {
     if (w16_fits(a.M, a.K, a.N)) {
         launch_w16_fit(a, s);
         return;
@@ -182,11 +209,12 @@ void launch_w16_tile(const uint16_t *W, int64_t ldw, int N, int K, void *Wt, hip
 // expert's activation, v the output of its fused gate/up/gate-logit GEMV.
 // Finite values beyond the fp16 range saturate (f32_to_f16_satfinite). The
 // standalone kernel and the fused down projection below share these helpers,
-// so both produce the same bits.
-__device__ __forceinline__ float sigmoid_gate(float gl) { return 1.f / (1.f + expf(-gl)); }
+// so both produce the same bits. silu and sigmoid are the reference's forms
+// (silu_ref, sigmoid_ref), in the reference's order of the products
+// (src/kernels/moe_route.hip:187-193).
+__device__ __forceinline__ float sigmoid_gate(float gl) { return sigmoid_ref(gl); }
 __device__ __forceinline__ uint16_t swiglu_h(float g, float u, float gate) {
-    const float silu = g / (1.f + expf(-g));
-    return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(silu * u * gate));
+    return __builtin_bit_cast(uint16_t, f32_to_f16_satfinite(silu_ref(g) * u * gate));
 }
 
 __global__ __launch_bounds__(256) void swiglu_gate_kernel(const float *__restrict__ v, int ldv, int n, int T,

@@ -20,6 +20,7 @@ SYMBOLS = (
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
     "qw_moe_decode_workspace_size", "qw_moe_decode", "qw_moe_decode_static_max_bytes", "qw_moe_decode_static",
+    "qw_moe_decode_static_reset",
     "qw_w16_gemv", "qw_w16_tiled_size", "qw_w16_tile", "qw_w16_gemv_tiled", "qw_w16_swiglu_gemv_tiled", "qw_i8_gemv", "qw_i8_tiled_size", "qw_i8_tile",
     "qw_moe_w4a8_tile_m", "qw_moe_w4a8_workspace_size", "qw_moe_experts_w4a8", "qw_quant_rows_i8", "qw_swiglu_gate",
     "qw_wcache_open", "qw_wcache_put", "qw_wcache_get", "qw_wcache_finish", "qw_wcache_close",
@@ -33,15 +34,15 @@ _SZ = ctypes.c_size_t
 _SIGS = {
     "qw_q4_abi_version": ([], _I),
     "qw_q4_last_error": ([], ctypes.c_char_p),
-    "qw_q4_gemv": ([_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_q4_gemv": ([_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_q4_gemm_workspace_size": ([_I, _I], _SZ),
     "qw_q4_gemm": ([_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _P, _SZ, _P], _I),
     "qw_moe_route": ([_P, _I, _I, _I, _I] + [_P] * 11 + [_P], _I),
-    "qw_moe_experts_gemv": ([_P] * 9 + [_I, _I, _I] + [_P] * 5 + [_I, _I, _I, _P, _P, _P], _I),
+    "qw_moe_experts_gemv": ([_P] * 9 + [_I, _I, _I] + [_P] * 5 + [_I, _I, _I, _P, _P, _I, _P], _I),
     "qw_moe_grouped_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "qw_moe_experts_grouped": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _I, _P, _P, _I, _P, _SZ, _P], _I),
     "qw_moe_grouped_tile_m": ([], _I),
-    "qw_moe_combine": ([_P, _I, _P, _P, _P, _I, _I, _I, _P, _I, _P], _I),
+    "qw_moe_combine": ([_P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P], _I),
     "qw_q4_tiled_size": ([_I64, _I64, _P, _P, _P], None),
     "qw_q4_tile": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P], _I),
     "qw_q4_untile": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P], _I),
@@ -51,12 +52,12 @@ _SIGS = {
     "qw_bf16_to_f16": ([_P, _P, _I64, _P], _I),
     "qw_read_probe": ([_P, _I64, _P], _I),
     "qw_moe_decode_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
-    "qw_moe_decode": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P, _SZ, _P], _I),
+    "qw_moe_decode": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_I, _P, _SZ, _P], _I),
     "qw_moe_decode_static_max_bytes": ([], _SZ),
-    "qw_w16_gemv": ([_P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_w16_gemv": ([_P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_w16_tiled_size": ([_I, _I], _SZ),
     "qw_w16_tile": ([_P, _I, _I, _I, _P, _P], _I),
-    "qw_w16_gemv_tiled": ([_P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "qw_w16_gemv_tiled": ([_P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_w16_swiglu_gemv_tiled": ([_P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P], _I),
     "qw_i8_gemv": ([_P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_i8_tiled_size": ([_I, _I, _I, _P, _P], None),
@@ -66,7 +67,8 @@ _SIGS = {
     "qw_moe_experts_w4a8": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _I, _P, _P, _P, _SZ, _P], _I),
     "qw_quant_rows_i8": ([_P, _I, _I, _I, _I, _P, _P, _P], _I),
     "qw_swiglu_gate": ([_P, _I, _I, _I, _P, _P], _I),
-    "qw_moe_decode_static": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_P], _I),
+    "qw_moe_decode_static": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_I, _P], _I),
+    "qw_moe_decode_static_reset": ([_P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
     "qw_st_close": ([_P], None),
     "qw_wcache_open": ([ctypes.c_char_p, ctypes.c_uint64, _P, _P], _I),
@@ -159,6 +161,24 @@ def tile_experts(W, S, Z, rows, K):
 
 
 # ---------------------------------------------------------------- operators
+# element-type codes of the *_type arguments (QW_T_F32, QW_T_BF16, QW_T_F16)
+T_F32, T_BF16, T_F16 = 0, 1, 2
+
+
+def _tcode(t):
+    """QW_T_* code of a tensor's dtype (float32, bfloat16, float16)."""
+    import torch
+    codes = {torch.float32: T_F32, torch.bfloat16: T_BF16, torch.float16: T_F16}
+    if t.dtype not in codes:
+        raise TypeError(f"unsupported element type {t.dtype}")
+    return codes[t.dtype]
+
+
+def _tdtype(code):
+    import torch
+    return {T_F32: torch.float32, T_BF16: torch.bfloat16, T_F16: torch.float16}[code]
+
+
 def _is_f16(x, x_f16):
     """x_f16 given, else from the tensor: float16 -> fp16 rows, anything else
     (bfloat16, or int16 bit patterns) -> bf16 rows."""
@@ -166,9 +186,10 @@ def _is_f16(x, x_f16):
     return bool(x_f16) if x_f16 is not None else x.dtype == torch.float16
 
 
-def gemv(W, S, Z, x, N, K, M=None, y=None, y_bf16=False, accumulate=False, xs=None, ys=None, x_f16=None):
-    """y[m][n] (+)= sum_k deq(W)[n][k] x[m][k]. x: bf16 rows (bfloat16, or int16 bit patterns) or fp16
-    rows (float16, or x_f16=True with int16 bit patterns)."""
+def gemv(W, S, Z, x, N, K, M=None, y=None, y_bf16=False, accumulate=False, xs=None, ys=None, x_f16=None, rpg=0):
+    """y[m][n] (+)= sum_k deq(W)[n][k] x[m][off(n) + k], off(n) = (n // rpg) * K when rpg (row
+    slices, gpu::gemv_rows). x: bf16 rows (bfloat16, or int16 bit patterns) or fp16 rows (float16,
+    or x_f16=True with int16 bit patterns)."""
     import torch
     M = M if M is not None else x.shape[0]
     xs = xs if xs is not None else x.stride(0) if x.dim() == 2 else K
@@ -177,12 +198,12 @@ def gemv(W, S, Z, x, N, K, M=None, y=None, y_bf16=False, accumulate=False, xs=No
     ys = ys if ys is not None else (y.stride(0) if y.dim() == 2 else N)
     _dev(W, S, Z, x, y)
     rc = lib().qw_q4_gemv(_ptr(W), _ptr(S), _ptr(Z), _ptr(x), int(_is_f16(x, x_f16)), xs, _ptr(y), ys, int(y_bf16),
-                          N, K, M, int(accumulate), _stream())
+                          N, K, M, rpg, int(accumulate), _stream())
     _check(rc, "qw_q4_gemv")
     return y
 
 
-def gemv_w16(W, x, M=None, y=None, y_bf16=False, accumulate=False, f16=None, xs=None, ys=None):
+def gemv_w16(W, x, M=None, y=None, y_bf16=False, accumulate=False, f16=None, xs=None, ys=None, rpg=0):
     """y[m][n] (+)= sum_k W[n][k] x[m][k] for 16-bit W [N][K] (row-major, stride W.stride(0)):
     fp16 W with fp16 x (f16 True, the default for float16 tensors) or bf16 with bf16."""
     import torch
@@ -194,7 +215,7 @@ def gemv_w16(W, x, M=None, y=None, y_bf16=False, accumulate=False, f16=None, xs=
         y = torch.zeros((M, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=x.device)
     ys = ys if ys is not None else (y.stride(0) if y.dim() == 2 else N)
     _dev(W, x, y)
-    rc = lib().qw_w16_gemv(_ptr(W), W.stride(0), _ptr(x), xs, int(f16), _ptr(y), ys, int(y_bf16), N, K, M,
+    rc = lib().qw_w16_gemv(_ptr(W), W.stride(0), _ptr(x), xs, int(f16), _ptr(y), ys, int(y_bf16), N, K, M, rpg,
                            int(accumulate), _stream())
     _check(rc, "qw_w16_gemv")
     return y
@@ -211,7 +232,7 @@ def w16_tile(W):
     return Wt
 
 
-def gemv_w16_tiled(Wt, N, K, x, M=None, y=None, y_bf16=False, accumulate=False, f16=None, xs=None, ys=None):
+def gemv_w16_tiled(Wt, N, K, x, M=None, y=None, y_bf16=False, accumulate=False, f16=None, xs=None, ys=None, rpg=0):
     """gemv_w16 on the tiled layout (w16_tile) of a 16-bit [N][K] matrix."""
     import torch
     M = M if M is not None else x.shape[0]
@@ -221,7 +242,7 @@ def gemv_w16_tiled(Wt, N, K, x, M=None, y=None, y_bf16=False, accumulate=False, 
         y = torch.zeros((M, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=x.device)
     ys = ys if ys is not None else (y.stride(0) if y.dim() == 2 else N)
     _dev(Wt, x, y)
-    rc = lib().qw_w16_gemv_tiled(_ptr(Wt), _ptr(x), xs, int(f16), _ptr(y), ys, int(y_bf16), N, K, M,
+    rc = lib().qw_w16_gemv_tiled(_ptr(Wt), _ptr(x), xs, int(f16), _ptr(y), ys, int(y_bf16), N, K, M, rpg,
                                  int(accumulate), _stream())
     _check(rc, "qw_w16_gemv_tiled")
     return y
@@ -289,17 +310,20 @@ def gemm_workspace_size(T, K):
     return lib().qw_q4_gemm_workspace_size(T, K)
 
 
-def gemm(W, S, Z, X, N, K, Y=None, y_bf16=False, workspace=None, x_f16=None):
+def gemm(W, S, Z, X, N, K, Y=None, y_bf16=False, workspace=None, x_f16=None, y_dtype=None):
+    """Y[t][n] = sum_k X[t][k] deq(W)[n][k]; Y fp32, bf16 (y_bf16) or any of float32 / bfloat16 /
+    float16 (y_dtype, or the dtype of a given Y; float16 is the reference's f16_out)."""
     import torch
     T = X.shape[0]
     f16 = _is_f16(X, x_f16)
     if Y is None:
-        Y = torch.empty((T, N), dtype=torch.bfloat16 if y_bf16 else torch.float32, device=X.device)
+        dt = y_dtype if y_dtype is not None else torch.bfloat16 if y_bf16 else torch.float32
+        Y = torch.empty((T, N), dtype=dt, device=X.device)
     if workspace is None and not f16:
         workspace = torch.empty(gemm_workspace_size(T, K), dtype=torch.uint8, device=X.device)
     _dev(W, S, Z, X, Y, workspace)
     rc = lib().qw_q4_gemm(_ptr(W), _ptr(S), _ptr(Z), _ptr(X), int(f16), X.stride(0), T, _ptr(Y), Y.stride(0),
-                          int(y_bf16), N, K, _ptr(workspace), 0 if workspace is None else workspace.numel(), _stream())
+                          _tcode(Y), N, K, _ptr(workspace), 0 if workspace is None else workspace.numel(), _stream())
     _check(rc, "qw_q4_gemm")
     return Y
 
@@ -336,19 +360,21 @@ def moe_route(logits, topk, tile_m=0, out=None):
     return r
 
 
-def moe_experts_gemv(gate, up, down, route, x, E, F, h=None, yp=None, x_f16=None):
-    """gate/up/down: tiled (Wt, St, Zt) of the stacked experts; returns (h fp16, yp fp32)."""
+def moe_experts_gemv(gate, up, down, route, x, E, F, h=None, yp=None, x_f16=None, yp_f16=False):
+    """gate/up/down: tiled (Wt, St, Zt) of the stacked experts; returns (h fp16, yp fp32, or fp16
+    with yp_f16 or an fp16 yp tensor)."""
     import torch
     H = x.shape[1]
     T, topk = route.T, route.topk
     if h is None:
         h = torch.empty((T * topk, F), dtype=torch.float16, device=x.device)
     if yp is None:
-        yp = torch.empty((T * topk, H), dtype=torch.float32, device=x.device)
+        yp = torch.empty((T * topk, H), dtype=torch.float16 if yp_f16 else torch.float32, device=x.device)
     _dev(x, h, yp, *gate, *up, *down)
     rc = lib().qw_moe_experts_gemv(*[_ptr(t) for t in (*gate, *up, *down)], E, H, F, _ptr(route.offsets),
                                    _ptr(route.active), _ptr(route.n_active), _ptr(route.pair_tok), _ptr(x),
-                                   int(_is_f16(x, x_f16)), T, topk, _ptr(h), _ptr(yp), _stream())
+                                   int(_is_f16(x, x_f16)), T, topk, _ptr(h), _ptr(yp),
+                                   int(yp.dtype == torch.float16), _stream())
     _check(rc, "qw_moe_experts_gemv")
     return h, yp
 
@@ -421,14 +447,18 @@ def moe_experts_w4a8(gate, up, down, route, x, E, F, h=None, yp=None, workspace=
     return h, yp
 
 
-def moe_combine(yp, route, H, shared=None, out=None, out_bf16=True):
+def moe_combine(yp, route, H, shared=None, out=None, out_bf16=True, out_dtype=None):
+    """out = shared + sum_i w_i yp[slot_i]; yp and shared fp32 or float16 (by dtype), out bf16
+    (out_bf16), fp32, or the dtype given (out_dtype, or that of a given out)."""
     import torch
     T, topk = route.T, route.topk
     if out is None:
-        out = torch.empty((T, H), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=yp.device)
+        dt = out_dtype if out_dtype is not None else torch.bfloat16 if out_bf16 else torch.float32
+        out = torch.empty((T, H), dtype=dt, device=yp.device)
     _dev(yp, shared, out)
     rc = lib().qw_moe_combine(_ptr(yp), int(yp.dtype == torch.float16), _ptr(route.tok_slot), _ptr(route.top_w),
-                              _ptr(shared), T, topk, H, _ptr(out), int(out_bf16), _stream())
+                              _ptr(shared), int(shared is not None and shared.dtype == torch.float16), T, topk, H,
+                              _ptr(out), _tcode(out), _stream())
     _check(rc, "qw_moe_combine")
     return out
 
@@ -457,7 +487,7 @@ def from_engine_order(words):
 class MoeDecode:
     """Buffers of the fused decode block (qw_moe_decode) for T tokens."""
 
-    def __init__(self, T, E, topk, H, F, device):
+    def __init__(self, T, E, topk, H, F, device, yp_f16=False):
         import torch
         i32 = dict(dtype=torch.int32, device=device)
         self.T, self.E, self.topk, self.H, self.F = T, E, topk, H, F
@@ -466,23 +496,27 @@ class MoeDecode:
         self.top_w = torch.empty((T, topk), dtype=torch.float32, device=device)
         self.tok_slot = torch.empty((T, topk), **i32)
         self.h = torch.empty((T * topk, F), dtype=torch.float16, device=device)
-        self.yp = torch.empty((T * topk, H), dtype=torch.float32, device=device)
+        self.yp = torch.empty((T * topk, H), dtype=torch.float16 if yp_f16 else torch.float32, device=device)
         # zero once: holds completion counters every call leaves at zero
         self.ws = torch.zeros(lib().qw_moe_decode_workspace_size(T, E, topk, H, F), dtype=torch.uint8, device=device)
 
 
-def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, out=None, out_bf16=True, x_f16=None):
-    """Router GEMV + routing + experts + combine for a decode batch (3 launches; 4 above 4 tokens)."""
+def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, out=None, out_bf16=True, x_f16=None,
+               out_dtype=None, yp_f16=False):
+    """Router GEMV + routing + experts + combine for a decode batch (3 launches; 4 above 4 tokens).
+    out bf16 (out_bf16), fp32, or out_dtype / the dtype of a given out; yp fp32, or fp16 with yp_f16
+    (or a buf whose yp is float16)."""
     import torch
     T, H = x.shape
-    buf = buf if buf is not None else MoeDecode(T, E, topk, H, F, x.device)
+    buf = buf if buf is not None else MoeDecode(T, E, topk, H, F, x.device, yp_f16=yp_f16)
     if out is None:
-        out = torch.empty((T, H), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=x.device)
+        dt = out_dtype if out_dtype is not None else torch.bfloat16 if out_bf16 else torch.float32
+        out = torch.empty((T, H), dtype=dt, device=x.device)
     _dev(router_w, x, shared, out, *gate, *up, *down)
     rc = lib().qw_moe_decode(_ptr(router_w), _ptr(x), int(_is_f16(x, x_f16)), T, E, topk, *map(_ptr, gate), *map(_ptr, up), *map(_ptr, down),
-                             H, F, _ptr(shared), _ptr(out), int(out_bf16), _ptr(buf.logits), _ptr(buf.top_e),
-                             _ptr(buf.top_w), _ptr(buf.tok_slot), _ptr(buf.h), _ptr(buf.yp), _ptr(buf.ws),
-                             buf.ws.numel(), _stream())
+                             H, F, _ptr(shared), _ptr(out), _tcode(out), _ptr(buf.logits), _ptr(buf.top_e),
+                             _ptr(buf.top_w), _ptr(buf.tok_slot), _ptr(buf.h), _ptr(buf.yp),
+                             int(buf.yp.dtype == torch.float16), _ptr(buf.ws), buf.ws.numel(), _stream())
     _check(rc, "qw_moe_decode")
     return out, buf
 
