@@ -605,7 +605,11 @@ void moe_decode_launch(const float *router_w, const uint16_t *x, int x_f16, int 
                        at(L.active), at(L.n_active), nullptr, nullptr, nullptr};
     qwq4::RouterArgs rr{router_w, x, H, L.kl, reinterpret_cast<float *>(w + L.part), logits, at(L.rcounter)};
     rr.x_f16 = x_f16 != 0;
-    qwq4::launch_router_route(ra, rr, s);
+    // small batches: the router launch writes the logits only, and the
+    // gate/up blocks route the batch themselves (no cross-block hand-off)
+    const bool local = qwq4::moe_local_route_ok(T, E, topk) && qwq4::router_logits_ok(T, E, H);
+    if (local) qwq4::launch_router_logits(rr, T, E, s);
+    else qwq4::launch_router_route(ra, rr, s);
     // up to 4 tokens the combine runs in the down projection's last blocks
     // (one launch less); from there on its own launch is faster than the
     // serial tail it adds to those blocks
@@ -615,6 +619,12 @@ void moe_decode_launch(const float *router_w, const uint16_t *x, int x_f16, int 
                         at(L.pair_tok), x, T, topk, h, yp, fold ? &cmb : nullptr};
     a.x_f16 = x_f16 != 0;
     a.yp_f16 = yp_f16 != 0;
+    if (local) {
+        a.route_logits = logits;
+        a.top_e = top_e;
+        a.top_w = top_w;
+        a.tok_slot = tok_slot;
+    }
     qwq4::launch_moe_gemv(a, s);
     if (!fold) qwq4::launch_combine(yp, yp_f16 != 0, tok_slot, top_w, shared, 0, T, topk, H, out, out_type, s);
 }

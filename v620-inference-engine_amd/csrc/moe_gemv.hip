@@ -23,6 +23,7 @@
 //            reference's moe_experts_P output).
 #include "q4_gemv_core.cuh"
 #include "q4_kernels.hpp"
+#include "route_core.cuh"
 
 namespace qwq4 {
 
@@ -146,6 +147,148 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
             wr.fetch(t, kp * gpk, gpk, opaque_lane());
             lds_barrier();  // the previous chunk's rows and partials are consumed
             chunk(m0);
+        }
+    }
+}
+
+// ---- decode batches that route themselves (the kernel takes T <= 4, k <= 8:
+// at most 32 selections; moe_local_route_ok picks where it pays). The router
+// launch then only writes the logits, with no
+// cross-block hand-off (its counted last block, reload and routing took
+// about 4 us of the batch-1 block), and every gate/up block routes the batch
+// from the logits before its weight requests: wave t < T picks token t's
+// top k (topk_wave, the routing kernels' code: the C library's expf, order
+// (p desc, index asc), weights renormalised in double), then every wave
+// derives the slots from the selections in LDS. A selection (t, j) of
+// expert e gets the slot off(e) + #(earlier tokens of e), off(e) = the
+// selections of smaller experts: experts ascending, tokens ascending, the
+// order of the routing kernels. Block y serves the y-th active expert
+// (ascending); block (0, 0) writes the routing outputs for the down
+// projection, the combine and the caller.
+struct LocalRoute {
+    const float *logits;  // [T][E]
+    int32_t *top_e, *tok_slot, *pair_tok, *offsets, *active, *n_active;
+    float *top_w;
+};
+
+// One wave's view of the batch's routing: lane i < P holds selection i
+// (token i / k): its expert, slot, and whether it is its expert's first
+// selection (then act is the expert's rank among the active ones and cnt
+// its number of tokens).
+struct LaneRoute {
+    int e, slot, act, cnt;
+    bool first;
+};
+
+__device__ __forceinline__ LaneRoute lane_route(const int32_t *s_te, int P, int k, int lane) {
+    LaneRoute r;
+    const bool live = lane < P;
+    r.e = live ? s_te[lane] : 0x7fffffff;
+    const int t = lane / k;  // (one division; the loop reads the other lanes' tokens)
+    int off = 0, rank = 0, cnt = 0;
+    for (int l = 0; l < P; ++l) {
+        const int el = __builtin_amdgcn_readlane(r.e, l), tl = __builtin_amdgcn_readlane(t, l);
+        off += el < r.e;
+        rank += el == r.e && tl < t;
+        cnt += el == r.e;
+    }
+    r.first = live && rank == 0;
+    const uint64_t fm = __ballot(r.first);
+    int act = 0;
+    for (int l = 0; l < P; ++l) {
+        const int el = __builtin_amdgcn_readlane(r.e, l);
+        act += ((fm >> l) & 1ull) && el < r.e;
+    }
+    r.slot = off + rank;
+    r.act = act;
+    r.cnt = cnt;
+    return r;
+}
+
+template <typename XT, int KS, int GW, bool HAS_Z, bool CH4, int PER>
+__global__ __launch_bounds__(512) void moe_gate_up_routed_kernel(
+    const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
+    const uint16_t *uz, LocalRoute lr, const uint16_t *__restrict__ x, int E, int H, int F, int T, int k,
+    uint16_t *__restrict__ h) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int32_t s_te[64];
+    __shared__ float s_tw[64];
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
+              n = lane % 16;
+    const int P = T * k;
+    if (wave < T) {
+        ExpfGlibc ex;
+        ex.load(lane);
+        const float *l = lr.logits + int64_t(wave) * E;
+        topk_wave<PER>(ex, [&](int i) { return l[i]; }, E, k, lane, s_te + wave * k, s_tw + wave * k);
+    }
+    __syncthreads();
+    const LaneRoute rt = lane_route(s_te, P, k, lane);
+    const uint64_t mine = __ballot(rt.first && rt.act == int(blockIdx.y));
+    const int n_act = __popcll(__ballot(rt.first));  // (every lane takes part in the ballot)
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+        if (lane < P) {
+            lr.top_e[lane] = rt.e;
+            lr.top_w[lane] = s_tw[lane];
+            lr.tok_slot[lane] = rt.slot;
+            lr.pair_tok[rt.slot] = lane / k;
+            if (rt.first) {
+                lr.active[rt.act] = rt.e;
+                lr.offsets[rt.e] = rt.slot;
+                lr.offsets[rt.e + 1] = rt.slot + rt.cnt;
+            }
+        }
+        if (lane == 0) *lr.n_active = n_act;
+    }
+    if (mine == 0ull) return;  // fewer active experts than blocks
+    const int src = __builtin_ctzll(mine);
+    const int e = __builtin_amdgcn_readlane(rt.e, src), M = __builtin_amdgcn_readlane(rt.cnt, src);
+    constexpr int SUB = 8 / (2 * KS);
+    const int sl = wave / (2 * KS), mat = (wave / KS) % 2, kp = wave % KS;
+    const int G = H / QGROUP, gpk = G / KS, fsub = F / 16, kc = x_row_stride(H);
+    const int lsub = blockIdx.x * SUB + sl;
+    const int64_t sub = int64_t(e) * fsub + min(lsub, fsub - 1);
+    const Q4Tile tl = mat ? Q4Tile(uw, us, uz, sub, G) : Q4Tile(gw, gs, gz, sub, G);
+    WaveRange<GW, HAS_Z, CH4> wr;
+    wr.fetch(tl, kp * gpk, gpk, opaque_lane());
+    const int base = __builtin_amdgcn_readlane(rt.slot, src);
+    // the expert's tokens in slot order: its selections' lanes ascending
+    // (lane = t k + j, so ascending lanes are ascending tokens)
+    const uint64_t em = __ballot(lane < P && rt.e == e);
+    int tok[4];
+    {
+        uint64_t m = em;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            tok[i] = m ? __builtin_ctzll(m) / k : 0;
+            m &= m - 1;
+        }
+    }
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(M, H));
+    stage_rows_issue(
+        [&](int m) {
+            const int t = m == 0 ? tok[0] : m == 1 ? tok[1] : m == 2 ? tok[2] : tok[3];
+            return x + int64_t(t) * H;
+        },
+        M, H, xl);
+    __syncthreads();
+    const uint4 *xr = xl + min(n, M - 1) * kc + q * 4;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    compute_zq_inline<XT>(wr, xr, acc);
+    red[wave * WAVE + lane] = acc;
+    lds_barrier();
+    if (mat == 0 && kp == 0 && lsub < fsub) {
+        f32x4 g = red[wave * WAVE + lane], u = red[(wave + KS) * WAVE + lane];
+#pragma unroll
+        for (int j = 1; j < KS; ++j) {
+            g += red[(wave + j) * WAVE + lane];
+            u += red[(wave + KS + j) * WAVE + lane];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * q + r;
+            if (m < M) h[int64_t(base + m) * F + lsub * 16 + n] = silu_mul_f16(g[r], u[r]);
         }
     }
 }
@@ -408,7 +551,43 @@ static int down_ks(int G) {
 }
 
 template <int KS, int GW, bool HAS_Z, bool CH4>
+static void launch_gate_up_routed(const MoeGemvArgs &a, int max_active, hipStream_t s) {
+    const LocalRoute lr{a.route_logits, a.top_e, a.tok_slot, const_cast<int32_t *>(a.pair_tok),
+                        const_cast<int32_t *>(a.offsets), const_cast<int32_t *>(a.active),
+                        const_cast<int32_t *>(a.n_active), a.top_w};
+    const int per = (a.E + WAVE - 1) / WAVE;
+    const size_t lds = moe_lds_bytes(a.T, a.H);
+    constexpr int SUB = 8 / (2 * KS);
+    const dim3 grid(unsigned((a.F / 16 + SUB - 1) / SUB), unsigned(max_active));
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
+        kern<<<grid, 512, lds, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, lr, a.x, a.E, a.H, a.F, a.T, a.topk, a.h);
+    };
+    auto pick = [&](auto xt) {
+        using XT = decltype(xt);
+        if (per <= 1) go(moe_gate_up_routed_kernel<XT, KS, GW, HAS_Z, CH4, 1>);
+        else if (per <= 2) go(moe_gate_up_routed_kernel<XT, KS, GW, HAS_Z, CH4, 2>);
+        else if (per <= 4) go(moe_gate_up_routed_kernel<XT, KS, GW, HAS_Z, CH4, 4>);
+        else go(moe_gate_up_routed_kernel<XT, KS, GW, HAS_Z, CH4, 8>);
+    };
+    if (a.x_f16) pick(F16{});
+    else pick(BF16{});
+}
+
+// Batch 1 only. Routing in every block costs each block the top-k's
+// latency (about 1.3 us of its 8 serial wave-maximum rounds) before its
+// weight requests; at batch 1 (768 blocks, one round) that is less than the
+// router's hand-off it replaces (30.3 against 31.7 us per MoE block, same
+// box), at batch 2 (1536 blocks, two rounds, each paying it) it is more
+// (52.5 against 47.2 us), and at batch 4 more again.
+bool moe_local_route_ok(int T, int E, int topk) { return T == 1 && topk <= 8 && E <= 512; }
+
+template <int KS, int GW, bool HAS_Z, bool CH4>
 static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStream_t s) {
+    if (a.route_logits) {
+        launch_gate_up_routed<KS, GW, HAS_Z, CH4>(a, max_active, s);
+        return;
+    }
     // an expert has at most T tokens: one chunk of R rows holds them when R >= T
     auto kern = a.T <= R ? (a.x_f16 ? moe_gate_up_gemv_kernel<F16, KS, GW, HAS_Z, CH4, false>
                                     : moe_gate_up_gemv_kernel<BF16, KS, GW, HAS_Z, CH4, false>)

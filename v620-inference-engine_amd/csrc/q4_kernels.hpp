@@ -67,7 +67,16 @@ struct MoeGemvArgs {
     const CombineArgs *cmb;  // null: yp only
     int x_f16 = 0;           // x rows are fp16 (else bf16)
     int yp_f16 = 0;
+    // Non-null: the gate/up blocks route the batch themselves from these
+    // logits [T][E] (moe_local_route_ok), and block (0, 0) writes the
+    // routing outputs: top_e, top_w, tok_slot and the offsets, active,
+    // n_active and pair_tok above (which are then outputs, not inputs).
+    const float *route_logits = nullptr;
+    int32_t *top_e = nullptr, *tok_slot = nullptr;
+    float *top_w = nullptr;
 };
+// Whether the gate/up decode GEMV can route a batch of T tokens itself.
+bool moe_local_route_ok(int T, int E, int topk);
 void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s);
 // Whether the expert GEMVs take these sizes (a wave holds <= 16 groups of its K range).
 bool moe_gemv_supported(int H, int F);
@@ -117,6 +126,11 @@ struct RouterArgs {
 };
 size_t router_lds_bytes(int T, int kl, int E);
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
+// The fp32 router GEMV alone (logits, no routing and no hand-off), for the
+// batches whose expert GEMVs route themselves; false if the full-K router
+// does not take the shape.
+bool router_logits_ok(int T, int E, int H);
+void launch_router_logits(const RouterArgs &r, int T, int E, hipStream_t s);
 // LDS bytes the slot pass needs for (T, E); the C-ABI rejects larger inputs.
 void launch_route(const RouteArgs &a, hipStream_t s);
 

@@ -92,6 +92,10 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // same order as comparing whole keys).
 __device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
     const uint32_t hi = uint32_t(v >> 32), mh = wave_max_u32(hi);
+    const uint64_t at = __ballot(hi == mh);
+    // one lane holds the largest high word (the usual case: no two equal
+    // probabilities): its key is the maximum, no second reduction
+    if ((at & (at - 1)) == 0ull) return (uint64_t(mh) << 32) | uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v)), __builtin_ctzll(at)));
     const uint32_t ml = wave_max_u32(hi == mh ? uint32_t(v) : 0u);
     return (uint64_t(mh) << 32) | ml;
 }
