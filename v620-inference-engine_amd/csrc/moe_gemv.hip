@@ -216,6 +216,11 @@ __global__ __launch_bounds__(512) void moe_gate_up_routed_kernel(
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
               n = lane % 16;
     const int P = T * k;
+    // every token row goes to LDS first (direct loads, row t at t * kc), in
+    // flight while the batch is routed: the weights then are the only loads
+    // the compute waits for, group by group as they arrive
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    stage_rows_issue([&](int m) { return x + int64_t(m) * H; }, T, H, xl);
     if (wave < T) {
         ExpfGlibc ex;
         ex.load(lane);
@@ -264,16 +269,11 @@ __global__ __launch_bounds__(512) void moe_gate_up_routed_kernel(
             m &= m - 1;
         }
     }
-    uint4 *xl = reinterpret_cast<uint4 *>(smem);
-    f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(M, H));
-    stage_rows_issue(
-        [&](int m) {
-            const int t = m == 0 ? tok[0] : m == 1 ? tok[1] : m == 2 ? tok[2] : tok[3];
-            return x + int64_t(t) * H;
-        },
-        M, H, xl);
-    __syncthreads();
-    const uint4 *xr = xl + min(n, M - 1) * kc + q * 4;
+    f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(T, H));
+    // the lane's token row: the expert's (min(n, M - 1))-th token
+    const int mr = min(n, M - 1);
+    const int trow = mr == 0 ? tok[0] : mr == 1 ? tok[1] : mr == 2 ? tok[2] : tok[3];
+    const uint4 *xr = xl + trow * kc + q * 4;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
     compute_zq_inline<XT>(wr, xr, acc);
     red[wave * WAVE + lane] = acc;
@@ -418,6 +418,14 @@ __global__ __launch_bounds__(1024) void moe_down_t1_kernel(const uint32_t *dw, c
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
               n = lane % 16;
     const int y = wave / 2, kp = wave % 2;
+    // the h rows of the k slots (at T = 1 every slot is one active expert's)
+    // and the shared row go out first, beside the routing reads: by the time
+    // the weights are requested they are in flight, and the compute then
+    // waits for the weights group by group as they arrive
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    stage_rows_issue([&](int m) { return h + int64_t(m) * F; }, topk, F, xl);
+    const float shv = c.shared && tid < 16 ? c.shared[blockIdx.x * 16 + tid] : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
     // n_active and active[y] requested together (one latency); the weight
     // loads need only e (active holds E entries: the read stays inside them,
     // the value is used only for y < n_active <= E)
@@ -439,12 +447,12 @@ __global__ __launch_bounds__(1024) void moe_down_t1_kernel(const uint32_t *dw, c
         slot_q[qq] = qq < topk ? ld_uniform(c.tok_slot, qq) : 0;
         w_q[qq] = qq < topk ? ld_uniform_f32(c.tok_w, qq) : 0.f;
     }
-    const float shv = c.shared && tid < 16 ? c.shared[blockIdx.x * 16 + tid] : 0.f;
-    uint4 *xl = reinterpret_cast<uint4 *>(smem);
     f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(8, F));
     float *yb = reinterpret_cast<float *>(red + 8 * WAVE);  // [8][16]
-    stage_rows_issue([&](int m) { return h + int64_t(m) * F; }, max(rows, 1), F, xl);
-    __syncthreads();
+    // the h rows (this wave's oldest loads) of every wave, not the weights
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_below<WaveRange<GW, HAS_Z, CH4>::LOADS>();
+    __builtin_amdgcn_s_barrier();
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
     if (live) compute_zq_inline<F16>(wr, xl + y * kc + q * 4, acc);
     if (kp == 1) red[y * WAVE + lane] = acc;
