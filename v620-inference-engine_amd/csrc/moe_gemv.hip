@@ -151,6 +151,67 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
     }
 }
 
+// Batches of up to 4 tokens: every token row goes to LDS first (row t at
+// t * kc, direct loads, issued before anything waits), then the expert's
+// weights; the compute then waits only for the weights, group by group as
+// they arrive, instead of for all of them behind the rows of the expert's
+// tokens. The MFMA's token row n reads row pair_tok[base + n].
+template <typename XT, int KS, int GW, bool HAS_Z, bool CH4>
+__global__ __launch_bounds__(512) void moe_gate_up_small_kernel(
+    const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
+    const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
+    const int32_t *__restrict__ n_active, const int32_t *__restrict__ pair_tok, const uint16_t *__restrict__ x, int E,
+    int H, int F, int T, uint16_t *__restrict__ h) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    stage_rows_issue([&](int m) { return x + int64_t(m) * H; }, T, H, xl);
+    __builtin_amdgcn_sched_barrier(0);
+    const int e = block_expert(n_active, active, E);
+    if (e < 0) {
+        wait_vm_below<0>();  // the rows' direct loads land before the block's LDS is released
+        return;
+    }
+    constexpr int SUB = 8 / (2 * KS);
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
+              n = lane % 16;
+    const int sl = wave / (2 * KS), mat = (wave / KS) % 2, kp = wave % KS;
+    const int G = H / QGROUP, gpk = G / KS, fsub = F / 16, kc = x_row_stride(H);
+    const int lsub = blockIdx.x * SUB + sl;
+    const int64_t sub = int64_t(e) * fsub + min(lsub, fsub - 1);
+    const Q4Tile tl = mat ? Q4Tile(uw, us, uz, sub, G) : Q4Tile(gw, gs, gz, sub, G);
+    WaveRange<GW, HAS_Z, CH4> wr;
+    wr.fetch(tl, kp * gpk, gpk, opaque_lane());
+    const int base = ld_uniform(offsets, e), M = ld_uniform(offsets, e + 1) - base;
+    int tok[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tok[i] = ld_uniform(pair_tok, base + min(i, M - 1));
+    f32x4 *red = reinterpret_cast<f32x4 *>(xl + x_pieces(T, H));
+    const int mr = min(n, M - 1);
+    const int trow = mr == 0 ? tok[0] : mr == 1 ? tok[1] : mr == 2 ? tok[2] : tok[3];
+    const uint4 *xr = xl + trow * kc + q * 4;
+    // the rows (this wave's oldest loads) of every wave, not the weights
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_below<WaveRange<GW, HAS_Z, CH4>::LOADS>();
+    __builtin_amdgcn_s_barrier();
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    compute_zq_inline<XT>(wr, xr, acc);
+    red[wave * WAVE + lane] = acc;
+    lds_barrier();
+    if (mat == 0 && kp == 0 && lsub < fsub) {
+        f32x4 g = red[wave * WAVE + lane], u = red[(wave + KS) * WAVE + lane];
+#pragma unroll
+        for (int j = 1; j < KS; ++j) {
+            g += red[(wave + j) * WAVE + lane];
+            u += red[(wave + KS + j) * WAVE + lane];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * q + r;
+            if (m < M) h[int64_t(base + m) * F + lsub * 16 + n] = silu_mul_f16(g[r], u[r]);
+        }
+    }
+}
+
 // ---- decode batches that route themselves (the kernel takes T <= 4, k <= 8:
 // at most 32 selections; moe_local_route_ok picks where it pays). The router
 // launch then only writes the logits, with no
@@ -492,8 +553,13 @@ __global__ __launch_bounds__(1024) void moe_down_t2_kernel(const uint32_t *dw, c
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, y = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
               n = lane % 16;
-    const int na = ld_uniform(n_active, 0), ea = ld_uniform(active, min(y, E - 1));  // (as in the batch-1 kernel)
     const int P = 2 * topk;  // slots (pairs) of the two tokens
+    // h rows of every slot and the shared rows first (as in the batch-1 kernel)
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    stage_rows_issue([&](int m) { return h + int64_t(m) * F; }, P, F, xl);
+    const float shv = c.shared && tid < 32 ? c.shared[int64_t(tid / 16) * H + blockIdx.x * 16 + tid % 16] : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+    const int na = ld_uniform(n_active, 0), ea = ld_uniform(active, min(y, E - 1));  // (as in the batch-1 kernel)
     const bool live = y < min(na, 16);  // wave-uniform
     const int e = live ? min(max(ea, 0), E - 1) : 0;
     const int G = F / QGROUP, gpk = G / 2, hsub = H / 16, kc = x_row_stride(F);
@@ -509,11 +575,10 @@ __global__ __launch_bounds__(1024) void moe_down_t2_kernel(const uint32_t *dw, c
         slot_q[i] = i < P ? ld_uniform(c.tok_slot, i) : 0;
         w_q[i] = i < P ? ld_uniform_f32(c.tok_w, i) : 0.f;
     }
-    const float shv = c.shared && tid < 32 ? c.shared[int64_t(tid / 16) * H + blockIdx.x * 16 + tid % 16] : 0.f;
-    uint4 *xl = reinterpret_cast<uint4 *>(smem);
     float *yb = reinterpret_cast<float *>(xl + x_pieces(16, F));  // [16 slots][16 rows]
-    stage_rows_issue([&](int m) { return h + int64_t(m) * F; }, P, F, xl);
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_below<2 * WaveRange<GW, HAS_Z, CH4>::LOADS>();
+    __builtin_amdgcn_s_barrier();
     if (live) {
         const uint4 *xr = xl + (base + min(n, max(M, 1) - 1)) * kc + q * 4;
         f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
@@ -596,6 +661,17 @@ static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStrea
         launch_gate_up_routed<KS, GW, HAS_Z, CH4>(a, max_active, s);
         return;
     }
+    constexpr int SUB = 8 / (2 * KS);
+    const dim3 grid(unsigned((a.F / 16 + SUB - 1) / SUB), unsigned(max_active));
+    if (a.T <= 4) {
+        auto kern = a.x_f16 ? moe_gate_up_small_kernel<F16, KS, GW, HAS_Z, CH4>
+                            : moe_gate_up_small_kernel<BF16, KS, GW, HAS_Z, CH4>;
+        const size_t lds = moe_lds_bytes(a.T, a.H);
+        if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
+        kern<<<grid, 512, lds, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets, a.active, a.n_active, a.pair_tok,
+                                    a.x, a.E, a.H, a.F, a.T, a.h);
+        return;
+    }
     // an expert has at most T tokens: one chunk of R rows holds them when R >= T
     auto kern = a.T <= R ? (a.x_f16 ? moe_gate_up_gemv_kernel<F16, KS, GW, HAS_Z, CH4, false>
                                     : moe_gate_up_gemv_kernel<BF16, KS, GW, HAS_Z, CH4, false>)
@@ -603,8 +679,6 @@ static void launch_gate_up(const MoeGemvArgs &a, int max_active, int R, hipStrea
                                     : moe_gate_up_gemv_kernel<BF16, KS, GW, HAS_Z, CH4, true>);
     const size_t lds = moe_lds_bytes(R, a.H);
     if (lds > 64 * 1024) (void)persistent_shape(reinterpret_cast<const void *>(kern), 512, lds);
-    constexpr int SUB = 8 / (2 * KS);
-    const dim3 grid(unsigned((a.F / 16 + SUB - 1) / SUB), unsigned(max_active));
     kern<<<grid, 512, lds, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets, a.active, a.n_active, a.pair_tok, a.x,
                                 a.E, a.H, a.F, R, a.h);
 }
