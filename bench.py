@@ -403,6 +403,97 @@ def bench_gemm(torch, qwq4, dev, steps, warmup):
     return res
 
 
+class SmiSampler:
+    """Samples the GPU's own telemetry (amdsmi gpu_metrics) from a thread while
+    kernels run: the graphics clock of every XCD, the socket power, and the
+    residency counters of the package power limit (PPT)."""
+
+    def __init__(self, period_s=0.01):
+        import amdsmi
+        self.smi = amdsmi
+        amdsmi.amdsmi_init()
+        self.h = amdsmi.amdsmi_get_processor_handles()[0]
+        self.period = period_s
+        self.samples = []
+
+    def read(self):
+        m = self.smi.amdsmi_get_gpu_metrics_info(self.h)
+        clk = [c for c in m.get("current_gfxclks", []) if isinstance(c, (int, float))]
+        return {"clk": sum(clk) / len(clk) if clk else float("nan"), "power": m.get("current_socket_power"),
+                "ppt": m.get("ppt_residency_acc"), "acc": m.get("accumulation_counter")}
+
+    def __enter__(self):
+        import threading
+        self.samples = []
+        self.stop = threading.Event()
+        self.first = self.read()
+
+        def loop():
+            while not self.stop.is_set():
+                self.samples.append(self.read())
+                time.sleep(self.period)
+        self.t = threading.Thread(target=loop, daemon=True)
+        self.t.start()
+        return self
+
+    def __exit__(self, *exc):
+        self.stop.set()
+        self.t.join()
+        self.last = self.read()
+
+    def summary(self):
+        import statistics
+        clk = [s["clk"] for s in self.samples]
+        pw = [s["power"] for s in self.samples if isinstance(s["power"], (int, float))]
+        out = {"samples": len(self.samples), "gfxclk_mhz_median": statistics.median(clk),
+               "gfxclk_mhz_min": min(clk), "gfxclk_mhz_max": max(clk),
+               "socket_power_w_median": statistics.median(pw) if pw else None}
+        try:
+            out["ppt_limit_residency"] = (self.last["ppt"] - self.first["ppt"]) / (self.last["acc"] - self.first["acc"])
+        except (TypeError, ZeroDivisionError):
+            out["ppt_limit_residency"] = None
+        return out
+
+
+def bench_gemm_power(torch, qwq4, dev, seconds=1.5):
+    """Clock and power of the q4 prefill GEMM beside hipBLASLt (torch.matmul)
+    on the same contraction with plain fp16 weights (the dequantised q4
+    weights), one process, interleaved: 4096 tokens x 4096 -> 12288, fp16
+    rows, fp16 out. Each leg replays its HIP graph for `seconds` after a 1 s
+    warm-up while SmiSampler reads the GPU's telemetry."""
+    T, N, K = 4096, QKV, H
+    W = gen_q4(torch, dev, N, K, seed=300 + N)
+    X = gen_x(torch, dev, T, K, seed=301).view(torch.bfloat16).float().half()
+    Wc = qwq4.untile(*W, N, K)
+    Wf = qwq4.dequant(*Wc, N, K).half()
+    del Wc
+    Y = torch.empty((T, N), dtype=torch.float16, device=dev)
+    legs = {"q4_gemm": graphed(torch, lambda: qwq4.gemm(*W, X, N, K, Y=Y)),
+            "hipblaslt_fp16": graphed(torch, lambda: torch.matmul(X, Wf.t(), out=Y))}
+    flops = 2.0 * T * N * K
+    res = {}
+    for rep in range(2):
+        for name, fn in legs.items():
+            t_end = time.perf_counter() + 1.0
+            while time.perf_counter() < t_end:
+                for _ in range(50):
+                    fn()
+                torch.cuda.synchronize()
+            n = 0
+            with SmiSampler() as smi, Timer(torch) as t:
+                t_end = time.perf_counter() + seconds
+                while time.perf_counter() < t_end:
+                    for _ in range(20):
+                        fn()
+                    n += 20
+                    torch.cuda.synchronize()
+            r = {"TFLOP_s": flops * n / (t.ms * 1e-3) / 1e12, "us": t.ms * 1e3 / n}
+            r.update(smi.summary())
+            res[f"{name}#{rep}"] = r
+            print(f"# {name} rep {rep}: {json.dumps(r)}", file=sys.stderr, flush=True)
+    return res
+
+
 # ---------------------------------------------------------------- config 5
 def bench_moe_prefill(torch, qwq4, dev, steps, warmup):
     E, F, k, T = 256, 1536, 8, 4096
@@ -607,7 +698,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, shared, i8, gemm, moe_prefill; or traffic (launches for PMC runs), or dominant (the roofline kernel's launches alone)")
+    ap.add_argument("--workload", default="all", help="all, or a comma list of gemv, moe, shared, i8, gemm, moe_prefill; or traffic (launches for PMC runs), or dominant (the roofline kernel's launches alone), or gemm_power (clock and power of the prefill GEMM beside hipBLASLt)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--moe-batches", default="1,2,4,8,16,32",
                     help="decode batches of the moe workload (comma list), e.g. one batch for a per-launch trace")
@@ -627,6 +718,9 @@ def main():
     qwq4.lib()
     if a.workload == "traffic":
         traffic_probe(torch, qwq4, dev)
+        return
+    if a.workload == "gemm_power":
+        print(json.dumps(bench_gemm_power(torch, qwq4, dev)))
         return
     if a.workload == "dominant":
         print(json.dumps(bench_dominant(torch, qwq4, dev, a.steps, a.warmup)))
