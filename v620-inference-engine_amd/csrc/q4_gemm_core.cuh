@@ -259,57 +259,65 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
     }
 }
 
-// A BM-row tile (BM = 64 or 128) whose 256 weight rows are split over the
-// 8 waves, 32 each: wave w computes all BM rows x weight rows 32 w .. 32 w +
-// 31 (acc[BM / 32][1]), with the weights dequantised in registers instead of
-// through LDS. Each weight row then feeds one wave, so the wave that
-// multiplies a row dequantises it itself: the dequant runs in all 8 waves
-// (beside their MFMAs) rather than in 4, and the weight tile's LDS writes,
-// reads and barrier hand-off are gone. Lane (l32, lh) holds weight row
-// 32 w + l32 (b: that row) and K half lh of each 64-K stage: one tiled entry
-// (quarter 2 (ks % 2) + lh of group ks / 2) per stage, requested two stages
-// ahead, one word dequantised per 16-K step. The A fragments are read with
-// the same K mapping (chunk kk + 4 lh). Only A goes through LDS: wave w moves
-// rows 64 j + 8 w .. + 7 (arow[j]: this lane's row, 64 j + 8 w + lane / 8).
-// With 64 rows this is GemmShape<64>'s layout (wm = 0, wn2 = w).
+// A BM-row tile (BM = 32, 64 or 128) by 512 weight rows, weights dequantised
+// in registers: wave w owns weight rows 64 w .. 64 w + 63 as two 32-row
+// groups (b0: 64 w + lane % 32, b1: 64 w + 32 + lane % 32) and computes all
+// BM rows of A against both (acc[i][j]: A rows 32 i .., group j). Every
+// weight row feeds one wave, which dequantises it itself (one tiled entry
+// per row, stage and lane, requested two stages ahead, one word per 16-K
+// step), so each dequantised word serves 2 BM / 32 MFMAs, and each A
+// fragment read from LDS serves two MFMAs (half the LDS reads per MFMA of a
+// one-group-per-wave form, 32 weight rows per wave, which the grouped GEMMs
+// used before: 1.96 against 1.82-1.86 ms per config-5 chunk). Only A goes
+// through LDS: wave w moves rows 64 j + 8 w .. + 7 (arow[j]: this lane's
+// row, 64 j + 8 w + lane / 8; rows past BM none). Four-wave blocks of 256
+// weight rows (two blocks per CU) measured slower (down GEMM 835 against
+// 661 us).
 // (USE: a tag per call site; the host pass rejects one specialization
 // called from two kernels' device code)
 template <int BM, bool HAS_Z, int USE>
-__device__ __forceinline__ void gemm_tile_rd(const uint16_t *const (&arow)[BM / 64], const BRow &b, int K,
-                                             f32x16 (&acc)[BM / 32][1]) {
-    static_assert(BM == 64 || BM == 128, "64- or 128-row tiles");
-    constexpr int NI = BM / 32;
+__device__ __forceinline__ void gemm_tile_rd2(const uint16_t *const (&arow)[(BM + 63) / 64], const BRow &b0,
+                                              const BRow &b1, int K, f32x16 (&acc)[BM / 32][2]) {
+    static_assert(BM == 32 || BM == 64 || BM == 128, "32-, 64- or 128-row tiles");
+    constexpr int NI = BM / 32, NA = (BM + 63) / 64;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
     const int l32 = lane % 32, lh = lane / 32, nk = K / GB_K;
-    constexpr int NLD = HAS_Z ? 3 : 2;  // weight-side loads per stage and lane
+    constexpr int NLD = HAS_Z ? 6 : 4;  // weight-side loads per stage and lane
     auto bufA = [&](int i) { return i ? lds_a1 : lds_a0; };
     auto issue_a = [&](int ks, unsigned char *dst) {
 #pragma unroll
-        for (int j = 0; j < BM / 64; ++j) {
+        for (int j = 0; j < NA; ++j) {
             const int rb = 64 * j + wave * 8, r = rb + lane / 8, c = (lane % 8) ^ swz_x(r);
-            __builtin_amdgcn_global_load_lds(arow[j] + ks * GB_K + c * 8, dst + rb * 128, 16, 0, 0);
+            if (rb < BM)  // (wave-uniform)
+                __builtin_amdgcn_global_load_lds(arow[j] + ks * GB_K + c * 8, dst + rb * 128, 16, 0, 0);
         }
     };
     struct WR {
-        uint4 w;
-        uint16_t s;
-        uint32_t z;
+        uint4 w0, w1;
+        uint16_t s0, s1;
+        uint32_t z0, z1;
     };
     auto issue_w = [&](int ks, WR &r) {
         ks = min(ks, nk - 1);  // past the end: a valid (unused) load
-        const int g = ks / 2;
-        r.w = b.w[g * 64 + ((ks % 2) * 2 + lh) * 16];
-        r.s = b.s[(g >> 2) * 64 + (g & 3)];
-        if constexpr (HAS_Z) r.z = b.z[(g >> 2) * 8];
+        const int g = ks / 2, e = g * 64 + ((ks % 2) * 2 + lh) * 16, so = (g >> 2) * 64 + (g & 3);
+        r.w0 = b0.w[e];
+        r.w1 = b1.w[e];
+        r.s0 = b0.s[so];
+        r.s1 = b1.s[so];
+        if constexpr (HAS_Z) {
+            r.z0 = b0.z[(g >> 2) * 8];
+            r.z1 = b1.z[(g >> 2) * 8];
+        }
     };
     auto compute = [&](const unsigned char *a, const WR &r, int ks) {
-        uint32_t sw = r.s, zw = HAS_Z ? r.z : 0u;
-        asm volatile("" : "+v"(sw), "+v"(zw));  // taken here, not at their loads (see commit_b)
+        uint32_t s0 = r.s0, s1 = r.s1, z0 = HAS_Z ? r.z0 : 0u, z1 = HAS_Z ? r.z1 : 0u;
+        asm volatile("" : "+v"(s0), "+v"(s1), "+v"(z0), "+v"(z1));  // taken here, not at their loads (see commit_b)
         const int g = ks / 2;
-        const uint32_t zb = zero_bytes(HAS_Z ? (zw >> (b.zs + 4 * (g & 3))) & 0xfu : 8u);
-        const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(sw));
-        const h2 s2 = {sc, sc};
-        const uint32_t words[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
+        const uint32_t zb0 = zero_bytes(HAS_Z ? (z0 >> (b0.zs + 4 * (g & 3))) & 0xfu : 8u);
+        const uint32_t zb1 = zero_bytes(HAS_Z ? (z1 >> (b1.zs + 4 * (g & 3))) & 0xfu : 8u);
+        const _Float16 c0 = __builtin_bit_cast(_Float16, uint16_t(s0)), c1 = __builtin_bit_cast(_Float16, uint16_t(s1));
+        const h2 sa = {c0, c0}, sb = {c1, c1};
+        const uint32_t wa[4] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w}, wb[4] = {r.w1.x, r.w1.y, r.w1.z, r.w1.w};
         uint4 af[NI], an[NI];
         auto rd = [&](int kk, uint4 (&f)[NI]) {
 #pragma unroll
@@ -319,14 +327,16 @@ __device__ __forceinline__ void gemm_tile_rd(const uint16_t *const (&arow)[BM / 
 #pragma unroll
         for (int kk = 0; kk < GB_K / 16; ++kk) {
             if (kk + 1 < GB_K / 16) rd(kk + 1, an);
-            const uint4 bf = dequant8(words[kk], zb, s2);
+            const uint4 f0 = dequant8(wa[kk], zb0, sa), f1 = dequant8(wb[kk], zb1, sb);
 #pragma unroll
-            for (int i = 0; i < NI; ++i) acc[i][0] = mfma32<F16>(af[i], bf, acc[i][0]);
+            for (int i = 0; i < NI; ++i) {
+                acc[i][0] = mfma32<F16>(af[i], f0, acc[i][0]);
+                acc[i][1] = mfma32<F16>(af[i], f1, acc[i][1]);
+            }
 #pragma unroll
             for (int i = 0; i < NI; ++i) af[i] = an[i];
         }
     };
-    constexpr int NA = BM / 64;  // direct A loads per stage and lane
     WR w0, w1;
     issue_a(0, bufA(0));
     issue_w(0, w0);
@@ -340,7 +350,6 @@ __device__ __forceinline__ void gemm_tile_rd(const uint16_t *const (&arow)[BM / 
         wait_vm_below<NLD>();  // everything but W(ks + 2): A(ks + 1) and W(ks + 1) arrived
         __builtin_amdgcn_s_barrier();
     };
-    (void)NA;
     for (int ks = 0; ks < nk; ks += 2) {  // nk is even (K is a multiple of 128)
         stage(ks, 0, w0);
         stage(ks + 1, 1, w1);
