@@ -42,16 +42,23 @@ __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_x(
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-// 8 packed nibbles (tiled word) -> 8 fp16 weights (q - z) * s
-__device__ __forceinline__ uint4 dequant8(uint32_t w, uint32_t zb, h2 s2) {
-    const uint4 u = unpack8<F16>(w, zb);  // 1040 + (q - z), exact
-    const h2 bias = {(_Float16)1040.f, (_Float16)1040.f};
+// 8 packed nibbles (tiled word) -> 8 fp16 weights (q - z) * s: the nibbles
+// become fp16 1024 + q (unpack8 with no byte offset), 1024 + z is subtracted
+// (exact), then one rounding multiply by s
+__device__ __forceinline__ uint4 dequant8(uint32_t w, h2 bias, h2 s2) {
+    const uint4 u = unpack8<F16>(w, 0u);  // 1024 + q, exact
     uint4 r;
     r.x = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, u.x) - bias) * s2);
     r.y = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, u.y) - bias) * s2);
     r.z = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, u.z) - bias) * s2);
     r.w = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, u.w) - bias) * s2);
     return r;
+}
+
+// the packed fp16 1024 + z of a zero point z (0..15)
+__device__ __forceinline__ h2 zero_bias(uint32_t z) {
+    const _Float16 b = __builtin_bit_cast(_Float16, uint16_t(0x6400u | z));
+    return h2{b, b};
 }
 
 // GB_M rows of A by BN weight rows (BN = 256, or 128 where a 256 x 256
@@ -166,7 +173,7 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
         // for them a stage early, and with them for everything issued since)
         uint32_t zw = HAS_Z ? r.z : 0u, sw = r.s;
         asm volatile("" : "+v"(zw), "+v"(sw));
-        const uint32_t zb = zero_bytes(HAS_Z ? (zw >> (b.zs + 4 * (g & 3))) & 0xfu : 8u);
+        const h2 zb = zero_bias(HAS_Z ? (zw >> (b.zs + 4 * (g & 3))) & 0xfu : 8u);
         const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(sw));
         const h2 s2 = {sc, sc};
         const uint4 w = (NH == 1 || !h) ? r.w0 : r.w1;
@@ -313,8 +320,8 @@ __device__ __forceinline__ void gemm_tile_rd2(const uint16_t *const (&arow)[(BM 
         uint32_t s0 = r.s0, s1 = r.s1, z0 = HAS_Z ? r.z0 : 0u, z1 = HAS_Z ? r.z1 : 0u;
         asm volatile("" : "+v"(s0), "+v"(s1), "+v"(z0), "+v"(z1));  // taken here, not at their loads (see commit_b)
         const int g = ks / 2;
-        const uint32_t zb0 = zero_bytes(HAS_Z ? (z0 >> (b0.zs + 4 * (g & 3))) & 0xfu : 8u);
-        const uint32_t zb1 = zero_bytes(HAS_Z ? (z1 >> (b1.zs + 4 * (g & 3))) & 0xfu : 8u);
+        const h2 zb0 = zero_bias(HAS_Z ? (z0 >> (b0.zs + 4 * (g & 3))) & 0xfu : 8u);
+        const h2 zb1 = zero_bias(HAS_Z ? (z1 >> (b1.zs + 4 * (g & 3))) & 0xfu : 8u);
         const _Float16 c0 = __builtin_bit_cast(_Float16, uint16_t(s0)), c1 = __builtin_bit_cast(_Float16, uint16_t(s1));
         const h2 sa = {c0, c0}, sb = {c1, c1};
         const uint32_t wa[4] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w}, wb[4] = {r.w1.x, r.w1.y, r.w1.z, r.w1.w};
