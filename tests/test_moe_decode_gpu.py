@@ -67,7 +67,8 @@ def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
                                        (1, 4, 1024, 256, 2), (2, 4, 1024, 256, 3), (2, 8, 1024, 256, 8),
                                        (3, 64, 1024, 512, 4), (4, 64, 1024, 256, 4),
                                        (6, 64, 1024, 256, 4), (6, 64, 1024, 512, 4), (1, 256, 4096, 1536, 8),
-                                       (2, 256, 4096, 1536, 8), (4, 256, 4096, 1536, 8), (16, 256, 4096, 1536, 8)])
+                                       (2, 256, 4096, 1536, 8), (4, 256, 4096, 1536, 8), (16, 256, 4096, 1536, 8),
+                                       (1, 64, 2048, 512, 6), (1, 32, 4096, 2048, 8), (1, 512, 2048, 256, 8)])
 @pytest.mark.parametrize("yp16", [False, True])
 def test_moe_decode_matches_unfused_path(gpu, T, E, H, F, k, yp16):
     """The block against routing + experts + combine as separate calls, with
@@ -76,7 +77,9 @@ def test_moe_decode_matches_unfused_path(gpu, T, E, H, F, k, yp16):
     the down projection (up to 4 tokens; batches 1 and 2 in one block per 16
     output rows), with experts chosen by both tokens (E = 16, k = 8; E = 8, k = 8:
     every expert twice), fewer experts than the kernels' waves (E = 4), and at
-    config 3's full size (down projection with 6 groups per wave)."""
+    config 3's full size (down projection with 6 groups per wave), and batch 1
+    at H 2048 / 4096 with down K halves of 2 to 8 groups and E up to 512 (the
+    gate/up blocks' own routing over 1 to 8 logits per lane)."""
     print(f"moe_decode vs unfused T={T} E={E} H={H} F={F} yp16={yp16}", flush=True)
     ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 77 + T, T, E, H, F, k, True)
     out, buf = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
