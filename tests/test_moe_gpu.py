@@ -107,7 +107,7 @@ def _mixed_tiles(counts, g):
         while m0 < c:
             out.append((e, m0))
             rem = c - m0
-            m0 += 4 * g if rem > 3 * g else 2 * g if rem > g else g
+            m0 += 4 * g if rem > 3 * g else 3 * g if rem > 2 * g else 2 * g if rem > g else g
     return out
 
 
@@ -125,7 +125,8 @@ def test_route_mixed_tiles(gpu, T, E, k):
     assert got == want
     # the heights cover every remainder class at these sizes
     rems = {min(4 * g, int(counts[e]) - m0) for e, m0 in want}
-    assert any(x > 2 * g for x in rems) and any(g < x <= 2 * g for x in rems) and any(x <= g for x in rems)
+    assert any(x > 3 * g for x in rems) and any(2 * g < x <= 3 * g for x in rems)
+    assert any(g < x <= 2 * g for x in rems) and any(x <= g for x in rems)
 
 
 @pytest.mark.parametrize("T,zeros", [(1, True), (2, True), (4, False), (8, True), (16, True), (17, False),

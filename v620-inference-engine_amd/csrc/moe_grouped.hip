@@ -4,8 +4,8 @@
 // token rows).
 //
 // Work is the (expert, tile) list written by the routing kernel
-// (qw_moe_route with tile_m = GROUPED_TILE_M = -32: mixed tiles of 128, 64
-// and 32 slots); slots of one expert are contiguous (offsets[e] ..), slot p
+// (qw_moe_route with tile_m = GROUPED_TILE_M = -32: mixed tiles of 128, 96,
+// 64 and 32 slots); slots of one expert are contiguous (offsets[e] ..), slot p
 // carries token pair_tok[p]. A tile's height follows from its start and the
 // expert's slot count (tile_rows). Each block runs the register-dequant MFMA
 // core (gemm_tile_rd2, q4_gemm_core.cuh) at that height on one list entry
@@ -126,6 +126,7 @@ __global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(GateUpTile 
     const int base = offsets[e] + m0, rows = tile_rows(rem, GROUPED_TILE_M), M = min(rows, rem);
     const int j0 = blockIdx.x * 256;
     if (rows == 128) gate_up_tile<128, HAS_Z>(a, e, base, M, j0);
+    else if (rows == 96) gate_up_tile<96, HAS_Z>(a, e, base, M, j0);
     else if (rows == 64) gate_up_tile<64, HAS_Z>(a, e, base, M, j0);
     else gate_up_tile<32, HAS_Z>(a, e, base, M, j0);
 }
@@ -140,6 +141,7 @@ __global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
     const int e = tile_e[tile], m0 = tile_m0[tile], rem = offsets[e + 1] - offsets[e] - m0;
     const int base = offsets[e] + m0, rows = tile_rows(rem, GROUPED_TILE_M), M = min(rows, rem);
     if (rows == 128) down_tile<128, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
+    else if (rows == 96) down_tile<96, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
     else if (rows == 64) down_tile<64, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
     else down_tile<32, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
 }

@@ -15,7 +15,7 @@
 // down projection, which writes yp in fp16.
 //
 // Schedule (the fp16 core's, q4_gemm_core.cuh, in int8): work is the routing
-// tile list (mixed 256 / 128 / 64-slot tiles, as for the fp16 grouped path);
+// tile list (mixed 128 / 96 / 64 / 32-slot tiles, run as 128- and 64-slot blocks);
 // a block of 8 waves takes one entry and 128 weight rows (gate/up: 64 gate
 // and the same 64 up rows, interleaved by 32). K runs in stages of 128 (one
 // scale group) through a double-buffered LDS; an int8 row of a stage is 128
@@ -38,7 +38,7 @@ namespace qwq4 {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int W8_TILE_M = -64;  // the routing's mixed 256 / 128 / 64-slot tiles
+constexpr int W8_TILE_M = -32;  // the routing's mixed 128 / 96 / 64 / 32-slot tiles (the grouped path's list)
 
 int moe_w4a8_tile_m() { return W8_TILE_M; }
 
@@ -143,8 +143,8 @@ constexpr int W8_K = 128;   // K per stage (one scale group)
 // activation scales of a stage's tile rows (waves 0-3 fill them), two stages
 static __shared__ __align__(16) float w8_lsx[2][256];
 
-// Block shapes: BM = 128 or 64 slot rows (a 256-slot list entry runs as two
-// 128-slot halves, blockIdx.z); waves 2 (slots) x 4 (weight rows), each MT
+// Block shapes: BM = 128 or 64 slot rows (list entries of 96 and 32 slots
+// run at the next height); waves 2 (slots) x 4 (weight rows), each MT
 // 32-row slot tiles by one 32-row weight tile.
 template <int BM>
 struct W8Shape {
@@ -290,8 +290,10 @@ __device__ __forceinline__ void w8_tile(const ApT &ap, const float *sxr, const B
     }
 }
 
-// The block's slots: list entry blockIdx.y (expert, first slot), half
-// blockIdx.z of a 256-slot entry; real slots M of a block of `rows`.
+// The block's slots: list entry blockIdx.y (expert, first slot); real slots
+// M of a block of `rows` (128 for entries of 96 and 128 slots, 64 for 32 and
+// 64: the same blocks as a list of 256 / 128 / 64-slot entries with the 256s
+// split in two, all in list order).
 struct W8Entry {
     int e, base, M, rows;
 };
@@ -300,11 +302,10 @@ static __device__ __forceinline__ bool w8_entry(const W8Args &a, W8Entry &t) {
     if (tile >= *a.n_tiles) return false;
     t.e = a.tile_e[tile];
     const int m0 = a.tile_m0[tile], rem = a.offsets[t.e + 1] - a.offsets[t.e] - m0;
-    const int rows = tile_rows(rem, W8_TILE_M), half = int(blockIdx.z);
-    if (rows <= 128 && half > 0) return false;
-    t.rows = rows > 128 ? 128 : rows;
-    t.base = a.offsets[t.e] + m0 + half * 128;
-    t.M = min(t.rows, rem - half * 128);
+    const int rows = tile_rows(rem, W8_TILE_M);
+    t.rows = rows > 64 ? 128 : 64;
+    t.base = a.offsets[t.e] + m0;
+    t.M = min(rows, rem);
     return true;
 }
 
@@ -442,11 +443,11 @@ void launch_moe_w4a8(W8Args a, const uint16_t *x, int x_f16, int T, int topk, hi
     a.sh = reinterpret_cast<float *>(w);
     launch_quant_rows(x, x_f16, a.H, T, a.H, const_cast<int8_t *>(a.qx), const_cast<float *>(a.sx), s);
     const int max_tiles = int(P / -W8_TILE_M) + a.E;
-    if (a.gz) moe_gate_up_w4a8_kernel<true><<<dim3(unsigned(a.F / 64), unsigned(max_tiles), 2), G_THREADS, 0, s>>>(a);
-    else moe_gate_up_w4a8_kernel<false><<<dim3(unsigned(a.F / 64), unsigned(max_tiles), 2), G_THREADS, 0, s>>>(a);
+    if (a.gz) moe_gate_up_w4a8_kernel<true><<<dim3(unsigned(a.F / 64), unsigned(max_tiles)), G_THREADS, 0, s>>>(a);
+    else moe_gate_up_w4a8_kernel<false><<<dim3(unsigned(a.F / 64), unsigned(max_tiles)), G_THREADS, 0, s>>>(a);
     launch_quant_rows(a.h, 1, a.F, int(P), a.F, const_cast<int8_t *>(a.qh), const_cast<float *>(a.sh), s);
-    if (a.dz) moe_down_w4a8_kernel<true><<<dim3(unsigned(a.H / W8_BN), unsigned(max_tiles), 2), G_THREADS, 0, s>>>(a);
-    else moe_down_w4a8_kernel<false><<<dim3(unsigned(a.H / W8_BN), unsigned(max_tiles), 2), G_THREADS, 0, s>>>(a);
+    if (a.dz) moe_down_w4a8_kernel<true><<<dim3(unsigned(a.H / W8_BN), unsigned(max_tiles)), G_THREADS, 0, s>>>(a);
+    else moe_down_w4a8_kernel<false><<<dim3(unsigned(a.H / W8_BN), unsigned(max_tiles)), G_THREADS, 0, s>>>(a);
 }
 
 }  // namespace qwq4
