@@ -221,9 +221,9 @@ int qw_q4_gemm(const uint32_t *W, const uint16_t *S, const uint16_t *Z, const ui
  * expert ascending, tiles over its slots offsets[e] + m0 ..:
  *   tile_e, tile_m0 [T*k/|tile_m| + E], n_tiles [1]  (tile_m 0: may be NULL).
  *   tile_m > 0: tiles of tile_m slots. tile_m = -g (mixed): the tile starting
- *   rem slots before the end of the expert's range has 4g slots when rem > 3g,
- *   3g when rem > 2g, 2g when rem > g, else g (whole 4g tiles, then one tile
- *   for the rest).
+ *   rem slots before the end of the expert's range has 4g slots when rem > 5g,
+ *   else rem rounded up to a multiple of g (whole 4g tiles, then one tile for
+ *   the rest, a rest of at most g joining the last whole tile).
  * Limits: 1 <= k <= min(E, 64), E <= 1024, T * k < 2^30. Above 16 tokens the
  * slots are assigned by one block per 64 tokens. */
 int qw_moe_route(const float *logits, int T, int E, int topk, int tile_m, int32_t *top_e, float *top_w,
@@ -251,8 +251,7 @@ int qw_moe_experts_gemv(const uint32_t *gw, const uint16_t *gs, const uint16_t *
 /* Grouped per-expert GEMMs for prefill chunks (replaces gpu::moe_experts_T,
  * moe.hpp:29-32): the same outputs as qw_moe_experts_gemv for any T, over
  * the (expert, tile) list qw_moe_route writes when called with
- * tile_m = qw_moe_grouped_tile_m() (mixed tiles, -32: 128, 96, 64 and 32
- * slots). x [T][H] bf16 (x_f16 = 0) or fp16 (x_f16 = 1). For bf16 x,
+ * tile_m = qw_moe_grouped_tile_m() (mixed tiles, -32: 32 to 160 slots). x [T][H] bf16 (x_f16 = 0) or fp16 (x_f16 = 1). For bf16 x,
  * workspace: at least qw_moe_grouped_workspace_size(...) bytes (an fp16
  * copy of x), 256-byte aligned; fp16 x needs none. x and h pass through fp16 as in qw_q4_gemm (finite
  * values beyond +-65504 saturate, infinities and NaN pass through). yp
@@ -280,8 +279,8 @@ int qw_moe_experts_grouped(const uint32_t *gw, const uint16_t *gs, const uint16_
  *   yp[p] = fp16(D_e . h[p])                     fp16 [T*k][H]
  * (finite values beyond +-65504 saturate). Weights tiled as for
  * qw_moe_experts_grouped; tile list from qw_moe_route with
- * tile_m = qw_moe_w4a8_tile_m() (the grouped path's list: -32, mixed 128,
- * 96, 64 and 32-slot tiles). The int32 sums run per 128-wide group (the reference:
+ * tile_m = qw_moe_w4a8_tile_m() (the grouped path's list: -32, mixed tiles
+ * of 32 to 160 slots). The int32 sums run per 128-wide group (the reference:
  * per 64-wide step; the fp32 rescale roundings differ by about 1e-7 of the
  * result). x [T][H] fp16 (x_f16 = 1,
  * the reference's rows) or bf16. H and F multiples of 128. workspace: at

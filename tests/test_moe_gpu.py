@@ -107,7 +107,7 @@ def _mixed_tiles(counts, g):
         while m0 < c:
             out.append((e, m0))
             rem = c - m0
-            m0 += 4 * g if rem > 3 * g else 3 * g if rem > 2 * g else 2 * g if rem > g else g
+            m0 += 4 * g if rem > 5 * g else -(-rem // g) * g
     return out
 
 
@@ -124,9 +124,9 @@ def test_route_mixed_tiles(gpu, T, E, k):
     got = list(zip(host(r.tile_e)[:nt].tolist(), host(r.tile_m0)[:nt].tolist()))
     assert got == want
     # the heights cover every remainder class at these sizes
-    rems = {min(4 * g, int(counts[e]) - m0) for e, m0 in want}
-    assert any(x > 3 * g for x in rems) and any(2 * g < x <= 3 * g for x in rems)
-    assert any(g < x <= 2 * g for x in rems) and any(x <= g for x in rems)
+    rems = {int(counts[e]) - m0 for e, m0 in want}
+    classes = (0, g, 2 * g, 3 * g, 4 * g) if T >= 4096 else (0, g, 2 * g)  # every height at full size
+    assert all(any(lo < x <= lo + g for x in rems) for lo in classes)
 
 
 @pytest.mark.parametrize("T,zeros", [(1, True), (2, True), (4, False), (8, True), (16, True), (17, False),

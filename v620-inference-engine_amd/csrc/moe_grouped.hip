@@ -4,8 +4,8 @@
 // token rows).
 //
 // Work is the (expert, tile) list written by the routing kernel
-// (qw_moe_route with tile_m = GROUPED_TILE_M = -32: mixed tiles of 128, 96,
-// 64 and 32 slots); slots of one expert are contiguous (offsets[e] ..), slot p
+// (qw_moe_route with tile_m = GROUPED_TILE_M = -32: mixed tiles of 32 to 160
+// slots); slots of one expert are contiguous (offsets[e] ..), slot p
 // carries token pair_tok[p]. A tile's height follows from its start and the
 // expert's slot count (tile_rows). Each block runs the register-dequant MFMA
 // core (gemm_tile_rd2, q4_gemm_core.cuh) at that height on one list entry
@@ -24,7 +24,8 @@
 
 namespace qwq4 {
 
-// 128, 64 or 32 slots: same box, config 5, 1.82-1.86 ms per chunk against
+// 32 to 160 slots. Before the 96- and 160-slot tiles (128, 64 or 32 slots):
+// same box, config 5, 1.82-1.86 ms per chunk against
 // 1.96 with tiles of 256 (role-split core), 128 and 64 (one 32-row weight
 // group per wave); the finer remainders cut the padded rows from 1.25 to 1.12
 // of the real ones, and each A fragment feeds two MFMAs.
@@ -49,7 +50,7 @@ struct GateUpTile {
     uint16_t *h;
 };
 
-// ---- a tile of 32, 64 or 128 slots by 512 weight rows (gemm_tile_rd2)
+// ---- a tile of 32 to 160 slots by 512 weight rows (gemm_tile_rd2)
 // gate/up: wave w holds gate and up rows of the same 32 columns j0 + 32 w ..
 // (group 0 gate, group 1 up), so h = silu(g) * u is formed in the wave.
 template <int BM, bool HAS_Z>
@@ -125,7 +126,8 @@ __global__ __launch_bounds__(G_THREADS) void moe_gate_up_gemm_kernel(GateUpTile 
     const int e = tile_e[tile], m0 = tile_m0[tile], rem = offsets[e + 1] - offsets[e] - m0;
     const int base = offsets[e] + m0, rows = tile_rows(rem, GROUPED_TILE_M), M = min(rows, rem);
     const int j0 = blockIdx.x * 256;
-    if (rows == 128) gate_up_tile<128, HAS_Z>(a, e, base, M, j0);
+    if (rows == 160) gate_up_tile<160, HAS_Z>(a, e, base, M, j0);
+    else if (rows == 128) gate_up_tile<128, HAS_Z>(a, e, base, M, j0);
     else if (rows == 96) gate_up_tile<96, HAS_Z>(a, e, base, M, j0);
     else if (rows == 64) gate_up_tile<64, HAS_Z>(a, e, base, M, j0);
     else gate_up_tile<32, HAS_Z>(a, e, base, M, j0);
@@ -140,7 +142,8 @@ __global__ __launch_bounds__(G_THREADS) void moe_down_gemm_kernel(
     if (tile >= *n_tiles) return;
     const int e = tile_e[tile], m0 = tile_m0[tile], rem = offsets[e + 1] - offsets[e] - m0;
     const int base = offsets[e] + m0, rows = tile_rows(rem, GROUPED_TILE_M), M = min(rows, rem);
-    if (rows == 128) down_tile<128, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
+    if (rows == 160) down_tile<160, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
+    else if (rows == 128) down_tile<128, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
     else if (rows == 96) down_tile<96, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
     else if (rows == 64) down_tile<64, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);
     else down_tile<32, HAS_Z, YP16>(dw, ds, dz, e, base, M, h, H, F, yp);

@@ -15,7 +15,7 @@
 // down projection, which writes yp in fp16.
 //
 // Schedule (the fp16 core's, q4_gemm_core.cuh, in int8): work is the routing
-// tile list (mixed 128 / 96 / 64 / 32-slot tiles, run as 128- and 64-slot blocks);
+// tile list (mixed tiles of 32 to 160 slots, run as 128- and 64-slot blocks);
 // a block of 8 waves takes one entry and 128 weight rows (gate/up: 64 gate
 // and the same 64 up rows, interleaved by 32). K runs in stages of 128 (one
 // scale group) through a double-buffered LDS; an int8 row of a stage is 128
@@ -38,7 +38,7 @@ namespace qwq4 {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int W8_TILE_M = -32;  // the routing's mixed 128 / 96 / 64 / 32-slot tiles (the grouped path's list)
+constexpr int W8_TILE_M = -32;  // the routing's mixed tiles of 32 to 160 slots (the grouped path's list)
 
 int moe_w4a8_tile_m() { return W8_TILE_M; }
 
@@ -144,7 +144,7 @@ constexpr int W8_K = 128;   // K per stage (one scale group)
 static __shared__ __align__(16) float w8_lsx[2][256];
 
 // Block shapes: BM = 128 or 64 slot rows (list entries of 96 and 32 slots
-// run at the next height); waves 2 (slots) x 4 (weight rows), each MT
+// run at the next height, 160 as 128 + 64); waves 2 (slots) x 4 (weight rows), each MT
 // 32-row slot tiles by one 32-row weight tile.
 template <int BM>
 struct W8Shape {
@@ -291,11 +291,12 @@ __device__ __forceinline__ void w8_tile(const ApT &ap, const float *sxr, const B
 }
 
 // The block's slots: list entry blockIdx.y (expert, first slot); real slots
-// M of a block of `rows` (128 for entries of 96 and 128 slots, 64 for 32 and
-// 64: the same blocks as a list of 256 / 128 / 64-slot entries with the 256s
-// split in two, all in list order).
+// M of a block of `rows` (128 for entries of 96 to 160 slots, 64 for 32 and
+// 64; a 160-slot entry's last 32 in a second 64-slot pass of the same block),
+// all in list order.
 struct W8Entry {
     int e, base, M, rows;
+    int rest;  // slots past the first 128 of a 160-slot entry, run as a second 64-slot pass
 };
 static __device__ __forceinline__ bool w8_entry(const W8Args &a, W8Entry &t) {
     const int tile = blockIdx.y;
@@ -303,9 +304,11 @@ static __device__ __forceinline__ bool w8_entry(const W8Args &a, W8Entry &t) {
     t.e = a.tile_e[tile];
     const int m0 = a.tile_m0[tile], rem = a.offsets[t.e + 1] - a.offsets[t.e] - m0;
     const int rows = tile_rows(rem, W8_TILE_M);
+    const int real = min(rows, rem);
     t.rows = rows > 64 ? 128 : 64;
     t.base = a.offsets[t.e] + m0;
-    t.M = min(rows, rem);
+    t.M = min(t.rows, real);
+    t.rest = real - t.M;
     return true;
 }
 
@@ -377,6 +380,10 @@ __global__ __launch_bounds__(G_THREADS) void moe_gate_up_w4a8_kernel(W8Args a) {
     if (!w8_entry(a, t)) return;
     if (t.rows == 128) gate_up_w8<128, HAS_Z>(a, t);
     else gate_up_w8<64, HAS_Z>(a, t);
+    if (t.rest > 0) {
+        __syncthreads();  // the first pass's LDS is consumed
+        gate_up_w8<64, HAS_Z>(a, W8Entry{t.e, t.base + 128, t.rest, 64, 0});
+    }
 }
 
 // down tile: block rows are down rows n0 .. n0 + 127 of expert e
@@ -421,6 +428,10 @@ __global__ __launch_bounds__(G_THREADS) void moe_down_w4a8_kernel(W8Args a) {
     if (!w8_entry(a, t)) return;
     if (t.rows == 128) down_w8<128, HAS_Z>(a, t);
     else down_w8<64, HAS_Z>(a, t);
+    if (t.rest > 0) {
+        __syncthreads();  // the first pass's LDS is consumed
+        down_w8<64, HAS_Z>(a, W8Entry{t.e, t.base + 128, t.rest, 64, 0});
+    }
 }
 
 size_t moe_w4a8_workspace_bytes(int T, int topk, int H, int F) {

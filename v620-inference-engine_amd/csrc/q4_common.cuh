@@ -237,14 +237,14 @@ __device__ __forceinline__ bool count_last_block(int *counter, int total) {
 // Tile lists over an expert's contiguous slots (routing with tile_m != 0).
 // tile_m > 0: tiles of tile_m rows. tile_m = -g: mixed tiles; the tile that
 // starts rem slots before the end of the expert's range has 4g rows when
-// rem > 3g, 3g when rem > 2g, 2g when rem > g, else g: whole 4g tiles, then
-// one tile for the rest rounded up to g (each tile of an expert's range
-// dequantises the expert's weights once, so the fewest tiles at the least
-// padding).
+// rem > 5g, else rem rounded up to a multiple of g (g to 5g): whole 4g tiles,
+// then one tile for the rest, a rest of at most g joining the last whole
+// tile. Each tile of an expert's range dequantises the expert's weights once:
+// the fewest tiles at the least padding.
 __device__ __forceinline__ int tile_rows(int rem, int tile_m) {
     if (tile_m > 0) return tile_m;
     const int g = -tile_m;
-    return rem > 3 * g ? 4 * g : rem > 2 * g ? 3 * g : rem > g ? 2 * g : g;
+    return rem > 5 * g ? 4 * g : (rem + g - 1) / g * g;
 }
 
 // Number of tiles over c slots.

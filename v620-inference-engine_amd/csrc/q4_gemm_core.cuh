@@ -285,7 +285,7 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
 template <int BM, bool HAS_Z, int USE>
 __device__ __forceinline__ void gemm_tile_rd2(const uint16_t *const (&arow)[(BM + 63) / 64], const BRow &b0,
                                               const BRow &b1, int K, f32x16 (&acc)[BM / 32][2]) {
-    static_assert(BM == 32 || BM == 64 || BM == 96 || BM == 128, "32-, 64-, 96- or 128-row tiles");
+    static_assert(BM % 32 == 0 && BM <= 160, "tiles of 32 to 160 rows");
     constexpr int NI = BM / 32, NA = (BM + 63) / 64;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
     const int l32 = lane % 32, lh = lane / 32, nk = K / GB_K;
