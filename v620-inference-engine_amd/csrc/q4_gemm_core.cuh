@@ -266,7 +266,7 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *const *ap, const BRow 
     }
 }
 
-// A BM-row tile (BM = 32, 64 or 128) by 512 weight rows, weights dequantised
+// A BM-row tile (BM a multiple of 32 up to 160) by 512 weight rows, weights dequantised
 // in registers: wave w owns weight rows 64 w .. 64 w + 63 as two 32-row
 // groups (b0: 64 w + lane % 32, b1: 64 w + 32 + lane % 32) and computes all
 // BM rows of A against both (acc[i][j]: A rows 32 i .., group j). Every
