@@ -325,7 +325,11 @@ int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, 
 /* A routed-MoE decode block in three or four launches (the engine's decode step calls
  * router GEMV -> route -> experts -> combine back to back, src/engine/decode.hip:99-111;
  * math of ref::Model::moe, src/ref/ref_model.cpp:406-463):
- *   logits = x . router_w^T (fp32 weights [E][H], the reference's fp32 router);
+ *   logits = x . router_w^T, router_w [E][H] fp32 (router_f16 = 0, the reference
+ *   model's fp32 router) or fp16 (router_f16 = 1, the engine's w.router, which
+ *   decode.hip:101 runs through gemv_rows); fp16 weights are widened exactly, so
+ *   fp16 weights and fp32 weights holding the same values give the same bits;
+ *   sums in fp32;
  *   routing as qw_moe_route; experts as qw_moe_experts_gemv;
  *   out[t] = shared[t] + sum_i top_w[t][i] * yp[tok_slot[t][i]]   (out_type)
  * The router GEMV and routing share a launch; up to T = 4 the combine runs
@@ -338,8 +342,9 @@ int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, 
  * with zeros once before its first use (it holds completion counters that
  * every call leaves at zero); calls that share a workspace must not overlap. */
 size_t qw_moe_decode_workspace_size(int T, int E, int topk, int H, int F);
-int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
-                  const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
+int qw_moe_decode(const void *router_w, int router_f16, const uint16_t *x, int x_f16, int T, int E, int topk,
+                  const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
+                  const uint16_t *uz,
                   const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
                   void *out, int out_type, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
                   uint16_t *h, void *yp, int yp_f16, void *workspace, size_t workspace_bytes, void *stream);
@@ -361,7 +366,7 @@ int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, in
  * different streams, or from different threads) race and must not be
  * issued. */
 size_t qw_moe_decode_static_max_bytes(void);
-int qw_moe_decode_static(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk,
+int qw_moe_decode_static(const void *router_w, int router_f16, const uint16_t *x, int x_f16, int T, int E, int topk,
                          const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
                          const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                          const uint16_t *dz, int H, int F, const float *shared, void *out, int out_type,

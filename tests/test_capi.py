@@ -27,7 +27,7 @@ def test_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert qwq4.lib().qw_q4_abi_version() == 4
+    assert qwq4.lib().qw_q4_abi_version() == 5
 
 
 @pytest.mark.parametrize("call", [
@@ -49,7 +49,7 @@ def test_abi_version():
     lambda L: L.qw_moe_experts_grouped(*([ctypes.c_void_p(256)] * 9), 256, 4096, 1536,
                                        *([ctypes.c_void_p(256)] * 6), 0, 4096, 8, ctypes.c_void_p(256),
                                        ctypes.c_void_p(256), 0, ctypes.c_void_p(256), 0, None),  # workspace too small
-    lambda L: L.qw_moe_decode(ctypes.c_void_p(256), ctypes.c_void_p(256), 0, 33, 256, 8,
+    lambda L: L.qw_moe_decode(ctypes.c_void_p(256), 0, ctypes.c_void_p(256), 0, 33, 256, 8,
                               *([ctypes.c_void_p(256)] * 9), 4096, 1536, None, ctypes.c_void_p(256), 1,
                               *([ctypes.c_void_p(256)] * 6), 0, ctypes.c_void_p(256), 1 << 30, None),  # T > 32
     lambda L: L.qw_i8_gemv(ctypes.c_void_p(256), ctypes.c_void_p(256), 32, ctypes.c_void_p(256), 96,
@@ -88,9 +88,12 @@ def test_abi_version():
                                4096, ctypes.c_void_p(256), 5, None),  # out_type 5
     lambda L: L.qw_moe_combine(ctypes.c_void_p(256), 1, ctypes.c_void_p(256), ctypes.c_void_p(256),
                                ctypes.c_void_p(260), 0, 1, 8, 4096, ctypes.c_void_p(256), 2, None),  # fp32 shared at 4 B
-    lambda L: L.qw_moe_decode(ctypes.c_void_p(256), ctypes.c_void_p(256), 0, 4, 256, 8,
+    lambda L: L.qw_moe_decode(ctypes.c_void_p(256), 0, ctypes.c_void_p(256), 0, 4, 256, 8,
                               *([ctypes.c_void_p(256)] * 9), 4096, 1536, None, ctypes.c_void_p(256), 7,
                               *([ctypes.c_void_p(256)] * 6), 1, ctypes.c_void_p(256), 1 << 30, None),  # out_type 7
+    lambda L: L.qw_moe_decode(ctypes.c_void_p(256), 2, ctypes.c_void_p(256), 0, 4, 256, 8,
+                              *([ctypes.c_void_p(256)] * 9), 4096, 1536, None, ctypes.c_void_p(256), 0,
+                              *([ctypes.c_void_p(256)] * 6), 1, ctypes.c_void_p(256), 1 << 30, None),  # router_f16 2
 ])
 def test_bad_arguments_are_rejected(call):
     L = qwq4.lib()

@@ -38,7 +38,7 @@ struct PrefillBuf {
 void engine_calls(Batch &b, PrefillBuf &p, rocblas_handle blas, hipStream_t s, const uint16_t *w16,
                   const qw::gpu::W16t &sh_gu, const qw::gpu::W16t &sh_down, const qw::gpu::Q4 &wq,
                   const qw::gpu::Q4 &g, const qw::gpu::Q4 &u, const qw::gpu::Q4 &d, const qw::gpu::Q8t &w8,
-                  const qw::gpu::MoeShape &sh, const float *router_w, void *ws, size_t ws_bytes) {
+                  const qw::gpu::MoeShape &sh, const uint16_t *router_w, void *ws, size_t ws_bytes) {
     const int M = 4, T = 4096, HC = 4, SH = 1024, HC_DOWN = 324, HC_SEND = 1300;
     bool accumulate = false, f16_out = true;
     int rpg = HC_DOWN;

@@ -108,6 +108,27 @@ def test_moe_decode_f16_out(gpu, T):
     assert np.array_equal(host(o16).view(np.uint16), want.view(np.uint16))
 
 
+@pytest.mark.parametrize("T", [1, 4, 16])
+def test_moe_decode_fp16_router(gpu, T):
+    """The engine's fp16 router weights (router_f16 = 1, decode.hip:101's w.router)
+    against fp32 weights holding the same values: logits, routing and output bit
+    for bit, through all three router kernels (logits only at batch 1, GEMV and
+    routing in one launch up to 8 tokens, the K-sliced router above)."""
+    import torch
+    E, H, F, k = 64, 2048, 256, 6
+    print(f"moe_decode fp16 router T={T}", flush=True)
+    ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 150 + T, T, E, H, F, k, True)
+    w16 = to_dev(Wr.astype(np.float16), gpu)
+    w32 = w16.float()
+    o16, b16 = qwq4.moe_decode(w16, to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu), out_bf16=False)
+    o32, b32 = qwq4.moe_decode(w32, to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu), out_bf16=False)
+    assert np.array_equal(host(b16.logits).view(np.uint32), host(b32.logits).view(np.uint32))
+    assert np.array_equal(host(b16.top_e), host(b32.top_e))
+    assert np.array_equal(host(o16).view(np.uint32), host(o32).view(np.uint32))
+    with pytest.raises(TypeError):
+        qwq4.moe_decode(w32.to(torch.bfloat16), to_dev(xb, gpu), k, g, u, d, E, F)
+
+
 @pytest.mark.parametrize("T,E", [(6, 64), (8, 64), (8, 256)])
 def test_moe_decode_router_lds_limit(gpu, oracle, T, E):
     """H = 8192: the full-K router stages the token rows (T x 16 KB) in LDS

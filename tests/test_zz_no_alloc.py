@@ -22,7 +22,7 @@ def _static_call(L, Wr, x, T, E, k, g, u, d, H, F, shared, outs):
     out, logits, top_e, top_w, tok_slot, h, yp = outs
     import torch
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    return L.qw_moe_decode_static(_ptr(Wr), _ptr(x), 0, T, E, k, *map(_ptr, g), *map(_ptr, u), *map(_ptr, d), H, F,
+    return L.qw_moe_decode_static(_ptr(Wr), 0, _ptr(x), 0, T, E, k, *map(_ptr, g), *map(_ptr, u), *map(_ptr, d), H, F,
                                   _ptr(shared), _ptr(out), 0, _ptr(logits), _ptr(top_e), _ptr(top_w), _ptr(tok_slot),
                                   _ptr(h), _ptr(yp), int(yp.dtype == torch.float16), s)
 
@@ -63,9 +63,9 @@ def test_static_rejects_unsupported_shapes(gpu):
     array, so no accepted shape is refused for its scratch.)"""
     L = qwq4.lib()
     p = ctypes.c_void_p(1 << 20)
-    rc = L.qw_moe_decode_static(p, p, 0, 33, 256, 8, *([p] * 9), 4096, 1536, None, p, 0, *([p] * 6), 0, None)
+    rc = L.qw_moe_decode_static(p, 0, p, 0, 33, 256, 8, *([p] * 9), 4096, 1536, None, p, 0, *([p] * 6), 0, None)
     assert rc == -1 and b"outside 1..32" in L.qw_q4_last_error()
-    rc = L.qw_moe_decode_static(p, p, 0, 32, 1024, 8, *([p] * 9), 65536, 1536, None, p, 0, *([p] * 6), 0, None)
+    rc = L.qw_moe_decode_static(p, 0, p, 0, 32, 1024, 8, *([p] * 9), 65536, 1536, None, p, 0, *([p] * 6), 0, None)
     assert rc == -1 and b"too large" in L.qw_q4_last_error()
 
 

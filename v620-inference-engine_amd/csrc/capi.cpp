@@ -95,7 +95,7 @@ int check_rpg(const char *fn, int rpg, int N, int K, int M, const void *x, int x
 
 extern "C" {
 
-int qw_q4_abi_version(void) { return 4; }
+int qw_q4_abi_version(void) { return 5; }
 
 const char *qw_q4_last_error(void) { return g_err.c_str(); }
 
@@ -572,7 +572,7 @@ size_t qw_moe_decode_workspace_size(int T, int E, int topk, int H, int F) {
 
 namespace {
 
-int moe_decode_check(const char *fn, const float *router_w, const uint16_t *x, int T, int E, int topk,
+int moe_decode_check(const char *fn, const void *router_w, const uint16_t *x, int T, int E, int topk,
                      const uint32_t *gw, const uint16_t *gs, const uint32_t *uw, const uint16_t *us,
                      const uint32_t *dw, const uint16_t *ds, int H, int F, const void *out, const float *logits,
                      const int32_t *top_e, const float *top_w, const int32_t *tok_slot, const uint16_t *h,
@@ -594,7 +594,7 @@ int moe_decode_check(const char *fn, const float *router_w, const uint16_t *x, i
 
 // Router GEMV + routing, the expert GEMVs, and the combine (folded into the
 // down projection up to 4 tokens), on the scratch w laid out as L.
-void moe_decode_launch(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
+void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
                        const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
                        const uint16_t *uz, const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F,
                        const float *shared, void *out, int out_type, float *logits, int32_t *top_e, float *top_w,
@@ -605,6 +605,7 @@ void moe_decode_launch(const float *router_w, const uint16_t *x, int x_f16, int 
                        at(L.active), at(L.n_active), nullptr, nullptr, nullptr};
     qwq4::RouterArgs rr{router_w, x, H, L.kl, reinterpret_cast<float *>(w + L.part), logits, at(L.rcounter)};
     rr.x_f16 = x_f16 != 0;
+    rr.w_f16 = router_f16 != 0;
     // small batches: the router launch writes the logits only, and the
     // gate/up blocks route the batch themselves (no cross-block hand-off)
     const bool local = qwq4::moe_local_route_ok(T, E, topk) && qwq4::router_logits_ok(T, E, H);
@@ -687,30 +688,32 @@ DecodeLayout static_layout(int T, int E, int topk, int H, int F) {
 
 extern "C" {
 
-int qw_moe_decode(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
+int qw_moe_decode(const void *router_w, int router_f16, const uint16_t *x, int x_f16, int T, int E, int topk, const uint32_t *gw,
                   const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
                   const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F, const float *shared,
                   void *out, int out_type, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
                   uint16_t *h, void *yp, int yp_f16, void *workspace, size_t workspace_bytes, void *stream) {
+    REQUIRE(router_f16 == 0 || router_f16 == 1, "qw_moe_decode: router_f16 = %d (0: fp32 weights, 1: fp16)", router_f16);
     if (int r = moe_decode_check("qw_moe_decode", router_w, x, T, E, topk, gw, gs, uw, us, dw, ds, H, F, out, logits,
                                  top_e, top_w, tok_slot, h, yp, out_type))
         return r;
     REQUIRE(workspace && aligned(workspace, 256), "qw_moe_decode: workspace null or not 256-byte aligned");
     const DecodeLayout L = decode_layout(T, E, topk, H, F);
     REQUIRE(workspace_bytes >= L.total, "qw_moe_decode: workspace needs %zu bytes", L.total);
-    moe_decode_launch(router_w, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_type,
+    moe_decode_launch(router_w, router_f16, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_type,
                       logits, top_e, top_w, tok_slot, h, yp, yp_f16, static_cast<unsigned char *>(workspace), L, st(stream));
     return launched("qw_moe_decode");
 }
 
 size_t qw_moe_decode_static_max_bytes(void) { return kStaticScratchBytes; }
 
-int qw_moe_decode_static(const float *router_w, const uint16_t *x, int x_f16, int T, int E, int topk,
+int qw_moe_decode_static(const void *router_w, int router_f16, const uint16_t *x, int x_f16, int T, int E, int topk,
                          const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
                          const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
                          const uint16_t *dz, int H, int F, const float *shared, void *out, int out_type,
                          float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot, uint16_t *h, void *yp,
                          int yp_f16, void *stream) {
+    REQUIRE(router_f16 == 0 || router_f16 == 1, "qw_moe_decode_static: router_f16 = %d (0: fp32 weights, 1: fp16)", router_f16);
     if (int r = moe_decode_check("qw_moe_decode_static", router_w, x, T, E, topk, gw, gs, uw, us, dw, ds, H, F, out,
                                  logits, top_e, top_w, tok_slot, h, yp, out_type))
         return r;
@@ -726,7 +729,7 @@ int qw_moe_decode_static(const float *router_w, const uint16_t *x, int x_f16, in
             "qw_moe_decode_static: E = %d or H = %d needs more completion counters than the scratch holds", E, H);
     void *w = nullptr;
     if (int r = static_scratch(&w)) return r;
-    moe_decode_launch(router_w, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_type,
+    moe_decode_launch(router_w, router_f16, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_type,
                       logits, top_e, top_w, tok_slot, h, yp, yp_f16, static_cast<unsigned char *>(w), L, st(stream));
     const int rc = launched("qw_moe_decode_static");
     if (rc != QW_Q4_OK) {

@@ -248,6 +248,20 @@ __device__ __forceinline__ void load_logits_lds(const float *logits, int n, floa
 // fit beside the routing's static arrays.
 __host__ __device__ inline bool router_lds_route(int T, int E) { return size_t(T) * E * 4 <= 96 * 1024; }
 
+// A run of 8 router weights as loaded -> fp32: fp32 bits in raw0 / raw1, or
+// 8 fp16 in raw0 (w_f16, exact widening).
+__device__ __forceinline__ void widen_run(const uint4 &raw0, const uint4 &raw1, int w_f16, float4 &w0, float4 &w1) {
+    if (w_f16) {
+        w0 = float4{f16_bits_to_f32(uint16_t(raw0.x)), f16_bits_to_f32(uint16_t(raw0.x >> 16)),
+                    f16_bits_to_f32(uint16_t(raw0.y)), f16_bits_to_f32(uint16_t(raw0.y >> 16))};
+        w1 = float4{f16_bits_to_f32(uint16_t(raw0.z)), f16_bits_to_f32(uint16_t(raw0.z >> 16)),
+                    f16_bits_to_f32(uint16_t(raw0.w)), f16_bits_to_f32(uint16_t(raw0.w >> 16))};
+    } else {
+        w0 = __builtin_bit_cast(float4, raw0);
+        w1 = __builtin_bit_cast(float4, raw1);
+    }
+}
+
 template <int PER>
 __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterArgs r) {
     extern __shared__ __align__(16) unsigned char smem[];  // x slice, [T][kl]
@@ -264,9 +278,18 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
     // same counter as loads, so each repeated wait also waited for the
     // previous token's logit store (one memory round trip per token).
     const bool mine = e < E && lane < kc;
-    const float *wp = r.w + int64_t(min(e, E - 1)) * H + k0 + min(lane, kc - 1) * 8;
-    float4 w0 = *reinterpret_cast<const float4 *>(wp), w1 = *reinterpret_cast<const float4 *>(wp + 4);
-    if (!mine) w0 = w1 = float4{0.f, 0.f, 0.f, 0.f};
+    const int64_t wo = int64_t(min(e, E - 1)) * H + k0 + min(lane, kc - 1) * 8;
+    // as loaded (fp32 bits, or 8 fp16 in raw0), widened after the activations
+    // are staged (fp16 -> fp32 is exact: the same products as fp32 weights
+    // holding the same values)
+    uint4 raw0, raw1 = make_uint4(0u, 0u, 0u, 0u);
+    if (r.w_f16) {
+        raw0 = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(r.w) + wo);
+    } else {
+        const float *wp = static_cast<const float *>(r.w) + wo;
+        raw0 = *reinterpret_cast<const uint4 *>(wp);
+        raw1 = *reinterpret_cast<const uint4 *>(wp + 4);
+    }
     uint4 *xs = reinterpret_cast<uint4 *>(smem);
     // activation pieces: four loads in flight per thread before their writes
     for (int i0 = tid; i0 < T * kc; i0 += 4 * int(blockDim.x)) {
@@ -284,6 +307,9 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
     // the weights' one wait, here: every token below then finds them ready
     // (each token's block is guarded by t < T, and the compiler would
     // otherwise wait again in each)
+    float4 w0, w1;
+    widen_run(raw0, raw1, r.w_f16, w0, w1);
+    if (!mine) w0 = w1 = float4{0.f, 0.f, 0.f, 0.f};
     asm volatile("" ::"v"(w0.x), "v"(w0.y), "v"(w0.z), "v"(w0.w), "v"(w1.x), "v"(w1.y), "v"(w1.z), "v"(w1.w));
     // x rows bf16 or fp16 (a block-uniform choice; both conversions are exact)
     auto dots = [&](auto cvt) {
@@ -392,13 +418,24 @@ __global__ __launch_bounds__(EPB *WPE *WAVE) void router_full_kernel(RouteArgs a
     ExpfGlibc ex;
     ex.load(lane);
     // the lane's runs of 8 weights: chunks lane, lane + 64, .. of its part
-    float4 w[NCH][2];
-    const float *wr = r.w + int64_t(e) * H + wp * kw;
+    // (as loaded; widened to fp32 once the activations are staged)
+    uint4 wraw[NCH][2];
+    const int64_t wo = int64_t(e) * H + wp * kw;
+    if (r.w_f16) {
+        const uint16_t *wr = static_cast<const uint16_t *>(r.w) + wo;
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-        const int c = min(lane + j * WAVE, nch - 1);
-        w[j][0] = *reinterpret_cast<const float4 *>(wr + c * 8);
-        w[j][1] = *reinterpret_cast<const float4 *>(wr + c * 8 + 4);
+        for (int j = 0; j < NCH; ++j) {
+            wraw[j][0] = *reinterpret_cast<const uint4 *>(wr + min(lane + j * WAVE, nch - 1) * 8);
+            wraw[j][1] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    } else {
+        const float *wr = static_cast<const float *>(r.w) + wo;
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+            const int c = min(lane + j * WAVE, nch - 1);
+            wraw[j][0] = *reinterpret_cast<const uint4 *>(wr + c * 8);
+            wraw[j][1] = *reinterpret_cast<const uint4 *>(wr + c * 8 + 4);
+        }
     }
     uint4 *xs = reinterpret_cast<uint4 *>(smem);
     const int xc = H / 8;
@@ -409,6 +446,9 @@ __global__ __launch_bounds__(EPB *WPE *WAVE) void router_full_kernel(RouteArgs a
     float *part = reinterpret_cast<float *>(xs + T * xc);  // [T][EPB][WPE]
     float *sl = part + T * EPB * WPE;                     // [T][E] (last block)
     __syncthreads();
+    float4 w[NCH][2];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) widen_run(wraw[j][0], wraw[j][1], r.w_f16, w[j][0], w[j][1]);
     auto dots = [&](auto cvt) {
         for (int t = 0; t < T; ++t) {
             float s = 0.f;

@@ -116,13 +116,14 @@ struct RouteArgs {
 };
 // fp32 router GEMV fused with the decode routing (T <= 64).
 struct RouterArgs {
-    const float *w;     // [E][H]
+    const void *w;      // [E][H] fp32, or fp16 (w_f16)
     const uint16_t *x;  // bf16 or fp16 [T][H]
     int H, kl;          // K slice per block (a multiple of 8 dividing H)
     float *part;        // [H / kl][T][E] partial logits
     float *logits;      // [T][E]
     int32_t *counter;   // [1 + ceil(E / 16)], zero between calls
     int x_f16 = 0;      // x rows are fp16 (else bf16)
+    int w_f16 = 0;      // router weights are fp16 (the engine's w.router), else fp32
 };
 size_t router_lds_bytes(int T, int kl, int E);
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);

@@ -52,7 +52,7 @@ _SIGS = {
     "qw_bf16_to_f16": ([_P, _P, _I64, _P], _I),
     "qw_read_probe": ([_P, _I64, _P], _I),
     "qw_moe_decode_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
-    "qw_moe_decode": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_I, _P, _SZ, _P], _I),
+    "qw_moe_decode": ([_P, _I, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_I, _P, _SZ, _P], _I),
     "qw_moe_decode_static_max_bytes": ([], _SZ),
     "qw_w16_gemv": ([_P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "qw_w16_tiled_size": ([_I, _I], _SZ),
@@ -67,7 +67,7 @@ _SIGS = {
     "qw_moe_experts_w4a8": ([_P] * 9 + [_I, _I, _I] + [_P] * 6 + [_I, _I, _I, _P, _P, _P, _SZ, _P], _I),
     "qw_quant_rows_i8": ([_P, _I, _I, _I, _I, _P, _P, _P], _I),
     "qw_swiglu_gate": ([_P, _I, _I, _I, _P, _P], _I),
-    "qw_moe_decode_static": ([_P, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_I, _P], _I),
+    "qw_moe_decode_static": ([_P, _I, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_I, _P], _I),
     "qw_moe_decode_static_reset": ([_P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
     "qw_st_close": ([_P], None),
@@ -504,8 +504,8 @@ class MoeDecode:
 def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, out=None, out_bf16=True, x_f16=None,
                out_dtype=None, yp_f16=False):
     """Router GEMV + routing + experts + combine for a decode batch (3 launches; 4 above 4 tokens).
-    out bf16 (out_bf16), fp32, or out_dtype / the dtype of a given out; yp fp32, or fp16 with yp_f16
-    (or a buf whose yp is float16)."""
+    router_w [E][H] float32, or float16 (the engine's router weights). out bf16 (out_bf16), fp32, or
+    out_dtype / the dtype of a given out; yp fp32, or fp16 with yp_f16 (or a buf whose yp is float16)."""
     import torch
     T, H = x.shape
     buf = buf if buf is not None else MoeDecode(T, E, topk, H, F, x.device, yp_f16=yp_f16)
@@ -513,7 +513,9 @@ def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, o
         dt = out_dtype if out_dtype is not None else torch.bfloat16 if out_bf16 else torch.float32
         out = torch.empty((T, H), dtype=dt, device=x.device)
     _dev(router_w, x, shared, out, *gate, *up, *down)
-    rc = lib().qw_moe_decode(_ptr(router_w), _ptr(x), int(_is_f16(x, x_f16)), T, E, topk, *map(_ptr, gate), *map(_ptr, up), *map(_ptr, down),
+    if router_w.dtype not in (torch.float32, torch.float16):
+        raise TypeError(f"moe_decode: router_w must be float32 or float16, not {router_w.dtype}")
+    rc = lib().qw_moe_decode(_ptr(router_w), int(router_w.dtype == torch.float16), _ptr(x), int(_is_f16(x, x_f16)), T, E, topk, *map(_ptr, gate), *map(_ptr, up), *map(_ptr, down),
                              H, F, _ptr(shared), _ptr(out), _tcode(out), _ptr(buf.logits), _ptr(buf.top_e),
                              _ptr(buf.top_w), _ptr(buf.tok_slot), _ptr(buf.h), _ptr(buf.yp),
                              int(buf.yp.dtype == torch.float16), _ptr(buf.ws), buf.ws.numel(), _stream())
