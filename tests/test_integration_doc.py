@@ -25,12 +25,12 @@ def blocks(lang):
 # rocblas_handle). A wrapper that took another buffer type (an fp32 yp, a
 # bf16 flag) fails to compile here.
 ENGINE_CALLS = r"""
-struct Batch {
+struct Batch {  // Rank::Batch's fields used here; top_e, active, n_active are the integration's additions
     float *X, *hc_send, *router, *tok_w, *sh_out, *out_moe, *proj, *logits;
     uint16_t *y, *bin, *moe_h, *yp, *sh_h;
     int32_t *counts, *offsets, *tok_slot, *pair_tok, *top_e, *active, *n_active;
 };
-struct PrefillBuf {
+struct PrefillBuf {  // PrefillBuf's fields used here; top_e, active, n_active, tile_e, tile_m0, n_tiles added
     float *logits, *tok_w, *d;
     uint16_t *xn, *bin, *part16, *moe_h, *yp, *sh_h, *sh_out;
     int32_t *counts, *offsets, *tok_slot, *pair_tok, *top_e, *active, *n_active, *tile_e, *tile_m0, *n_tiles;
