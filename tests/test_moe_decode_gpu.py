@@ -15,8 +15,8 @@ from _gpu_util import TOL, bf16_err_ok, host, rel_err, to_dev
 pytestmark = pytest.mark.gpu
 
 
-def _case(gpu, seed, T, E, H, F, k, with_shared):
-    ex = synth.experts(seed, E, H, F)
+def _case(gpu, seed, T, E, H, F, k, with_shared, zeros=True):
+    ex = synth.experts(seed, E, H, F, zeros=zeros)
     xb, xf = synth.acts(seed, "dx", T, H)
     r = np.random.default_rng(seed)
     Wr = (r.standard_normal((E, H)) * 0.05).astype(np.float32)
@@ -106,6 +106,27 @@ def test_moe_decode_f16_out(gpu, T):
                              out_dtype=torch.float16, yp_f16=True)
     want = np.clip(host(o32), -65504, 65504).astype(np.float16)
     assert np.array_equal(host(o16).view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("T", [1, 2, 4, 8])
+def test_moe_decode_symmetric_experts(gpu, oracle, T):
+    """Symmetric experts (no zero points: zero 8 for every group, the
+    reference's format, ref_model.cpp:114) through the fused block at config
+    3's full size: against the oracle, and bit for bit against the unfused
+    calls (the batch-1 routed gate/up and the batch-1 / batch-2 down kernels
+    without zeros)."""
+    E, H, F, k = 256, 4096, 1536, 8
+    print(f"moe_decode symmetric T={T}", flush=True)
+    ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 170 + T, T, E, H, F, k, True, zeros=False)
+    assert g[2] is None and d[2] is None
+    out, buf = qwq4.moe_decode(to_dev(Wr, gpu), to_dev(xb, gpu), k, g, u, d, E, F, shared=to_dev(sh, gpu),
+                               out_bf16=False, yp_f16=True)
+    r = qwq4.moe_route(buf.logits, k)
+    h, yp = qwq4.moe_experts_gemv(g, u, d, r, to_dev(xb, gpu), E, F, yp_f16=True)
+    o2 = qwq4.moe_combine(yp, r, H, shared=to_dev(sh, gpu), out_bf16=False)
+    assert np.array_equal(host(out).view(np.uint32), host(o2).view(np.uint32))
+    ref = oracle.moe(xf, host(buf.logits), k, *ex) + sh
+    assert rel_err(host(out), ref) <= TOL
 
 
 @pytest.mark.parametrize("T", [1, 4, 16])
