@@ -38,8 +38,8 @@ DOM_KERNEL = "q4_gemv_block_kernel<qwq4::BF16, 8, 1, true, true"
 H, QKV, FFN_DOWN_K, VOCAB = 4096, 12288, 6144, 151936
 
 
-def q4_bytes(N, K):
-    return N * K // 2 + N * (K // 128) * 2 + N * (K // 128) // 2
+def q4_bytes(N, K, zeros=True):
+    return N * K // 2 + N * (K // 128) * 2 + (N * (K // 128) // 2 if zeros else 0)
 
 
 def gen_q4(torch, dev, N, K, zeros=True, lead=(), seed=0):
@@ -212,12 +212,15 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
     fused block) and so its own experts; bytes are the distinct experts each
     block reads. Between two reads of one expert the step streams the other
     blocks' experts (>= 8 x 9.4 MB at batch 1, past the 256 MB Infinity
-    Cache), so the weights come from HBM."""
+    Cache), so the weights come from HBM. The experts are symmetric (group-128
+    fp16 scales, no zero points: config 3's format and the reference's,
+    ref_model.cpp:114); the fused block is also timed at batch 1 on experts
+    with zero points (block_zero_points)."""
     E, F, k, L = 256, 1536, 8, MOE_LAYERS
-    gate = gen_q4(torch, dev, F, H, lead=(E,), seed=10)
-    up = gen_q4(torch, dev, F, H, lead=(E,), seed=11)
-    down = gen_q4(torch, dev, H, F, lead=(E,), seed=12)
-    per_expert = q4_bytes(F, H) * 2 + q4_bytes(H, F)
+    gate = gen_q4(torch, dev, F, H, zeros=False, lead=(E,), seed=10)
+    up = gen_q4(torch, dev, F, H, zeros=False, lead=(E,), seed=11)
+    down = gen_q4(torch, dev, H, F, zeros=False, lead=(E,), seed=12)
+    per_expert = q4_bytes(F, H, False) * 2 + q4_bytes(H, F, False)
     gr = torch.Generator(device=dev)
     gr.manual_seed(13)
     router_w = [torch.randn((E, H), generator=gr, device=dev) * 0.02 for _ in range(L)]
@@ -275,6 +278,26 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
         bf = Uf * per_expert + L * E * H * 4
         out[B]["block"] = {"distinct_experts": Uf / L, "GB_s": bf * steps / (tf.ms * 1e-3) / 1e9,
                            "us_per_block": tf.ms * 1e3 / (steps * L)}
+        if B == 1:
+            # the same block on experts with a 4-bit zero point per group
+            zg = gen_q4(torch, dev, F, H, lead=(E,), seed=20)
+            zu = gen_q4(torch, dev, F, H, lead=(E,), seed=21)
+            zd = gen_q4(torch, dev, H, F, lead=(E,), seed=22)
+
+            def fused_z():
+                for l in range(L):
+                    qwq4.moe_decode(router_w[l], xs[l], k, zg, zu, zd, E, F, buf=buf, out=ob)
+
+            zstep = graphed(torch, fused_z)
+            for _ in range(warmup):
+                zstep()
+            with Timer(torch) as tz:
+                for _ in range(steps):
+                    zstep()
+            bz = Uf * (q4_bytes(F, H) * 2 + q4_bytes(H, F)) + L * E * H * 4
+            out[B]["block_zero_points"] = {"GB_s": bz * steps / (tz.ms * 1e-3) / 1e9,
+                                           "us_per_block": tz.ms * 1e3 / (steps * L)}
+            del zg, zu, zd
     return out
 
 
@@ -496,10 +519,13 @@ def bench_gemm_power(torch, qwq4, dev, seconds=1.5):
 
 # ---------------------------------------------------------------- config 5
 def bench_moe_prefill(torch, qwq4, dev, steps, warmup):
+    """Config 5: one 4096-token chunk through the config-3 experts (symmetric:
+    group-128 fp16 scales, no zero points); also timed on experts with zero
+    points (zero_points) and through the opt-in W4A8 path."""
     E, F, k, T = 256, 1536, 8, 4096
-    gate = gen_q4(torch, dev, F, H, lead=(E,), seed=10)
-    up = gen_q4(torch, dev, F, H, lead=(E,), seed=11)
-    down = gen_q4(torch, dev, H, F, lead=(E,), seed=12)
+    gate = gen_q4(torch, dev, F, H, zeros=False, lead=(E,), seed=10)
+    up = gen_q4(torch, dev, F, H, zeros=False, lead=(E,), seed=11)
+    down = gen_q4(torch, dev, H, F, zeros=False, lead=(E,), seed=12)
     x = gen_x(torch, dev, T, H, seed=400)
     g = torch.Generator(device=dev)
     g.manual_seed(401)
@@ -511,23 +537,33 @@ def bench_moe_prefill(torch, qwq4, dev, steps, warmup):
     o = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
     ws = torch.empty(max(qwq4.moe_grouped_workspace_size(T, k, E, H, F), 1), dtype=torch.uint8, device=dev)
 
-    def step():
-        qwq4.moe_route(logits, k, tile_m=tm, out=r)
-        qwq4.moe_experts_grouped(gate, up, down, r, x, E, F, h=h, yp=yp, workspace=ws)
-        qwq4.moe_combine(yp, r, H, out=o)
+    def timed(g_, u_, d_, warm):
+        def step():
+            qwq4.moe_route(logits, k, tile_m=tm, out=r)
+            qwq4.moe_experts_grouped(g_, u_, d_, r, x, E, F, h=h, yp=yp, workspace=ws)
+            qwq4.moe_combine(yp, r, H, out=o)
 
-    gstep = graphed(torch, step)  # one HIP graph per step, warmed for >= 1 s (steady clocks)
-    t_end = time.perf_counter() + 1.0
-    while time.perf_counter() < t_end or warmup > 0:
-        gstep()
-        torch.cuda.synchronize()
-        warmup -= 1
-    with Timer(torch) as t:
-        for _ in range(steps):
+        gstep = graphed(torch, step)  # one HIP graph per step, warmed for >= 1 s (steady clocks)
+        t_end = time.perf_counter() + 1.0
+        while time.perf_counter() < t_end or warm > 0:
             gstep()
+            torch.cuda.synchronize()
+            warm -= 1
+        with Timer(torch) as t:
+            for _ in range(steps):
+                gstep()
+        return t.ms
+
     flops = 2.0 * (k * T) * (2 * F * H + H * F)
-    res = {"TFLOP_s": flops * steps / (t.ms * 1e-3) / 1e12, "us_per_step": t.ms * 1e3 / steps,
-           "tokens_s": T * steps / (t.ms * 1e-3)}
+    ms = timed(gate, up, down, warmup)
+    res = {"TFLOP_s": flops * steps / (ms * 1e-3) / 1e12, "us_per_step": ms * 1e3 / steps,
+           "tokens_s": T * steps / (ms * 1e-3)}
+    zg = gen_q4(torch, dev, F, H, lead=(E,), seed=20)
+    zu = gen_q4(torch, dev, F, H, lead=(E,), seed=21)
+    zd = gen_q4(torch, dev, H, F, lead=(E,), seed=22)
+    msz = timed(zg, zu, zd, warmup)
+    res["zero_points"] = {"TFLOP_s": flops * steps / (msz * 1e-3) / 1e12, "us_per_step": msz * 1e3 / steps}
+    del zg, zu, zd
 
     # the reference's opt-in W4A8 path (int8 activations, lossy) on the same
     # experts and routing: 64-slot tiles, fp16 rows as the engine passes them
