@@ -322,7 +322,7 @@ int qw_q4_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64
                   void *stream);
 int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream);
 
-/* A routed-MoE decode block in three or four launches (the engine's decode step calls
+/* A routed-MoE decode block in three to five launches (the engine's decode step calls
  * router GEMV -> route -> experts -> combine back to back, src/engine/decode.hip:99-111;
  * math of ref::Model::moe, src/ref/ref_model.cpp:406-463):
  *   logits = x . router_w^T, router_w [E][H] fp32 (router_f16 = 0, the reference
@@ -332,8 +332,10 @@ int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, 
  *   sums in fp32;
  *   routing as qw_moe_route; experts as qw_moe_experts_gemv;
  *   out[t] = shared[t] + sum_i top_w[t][i] * yp[tok_slot[t][i]]   (out_type)
- * The router GEMV and routing share a launch; up to T = 4 the combine runs
- * inside the down projection, above that in a launch of its own. Outputs: out
+ * Launches: at T = 1 the router writes the logits and the gate/up blocks
+ * route; at T = 2..8 the logits launch is followed by the routing launch;
+ * above 8 tokens the router GEMV and routing share a launch. Up to T = 4 the
+ * combine runs inside the down projection, above that in a launch of its own. Outputs: out
  * (QW_T_F32, the engine's moe_combine_B rows, QW_T_BF16 or QW_T_F16), logits
  * [T][E], top_e, top_w, tok_slot [T][k], h, yp (fp32 or fp16 with yp_f16, as
  * qw_moe_experts_gemv; the combine adds the values yp holds). shared fp32 [T][H] or NULL (e.g. the shared

@@ -609,8 +609,15 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
     // small batches: the router launch writes the logits only, and the
     // gate/up blocks route the batch themselves (no cross-block hand-off)
     const bool local = qwq4::moe_local_route_ok(T, E, topk) && qwq4::router_logits_ok(T, E, H);
-    if (local) qwq4::launch_router_logits(rr, T, E, s);
-    else qwq4::launch_router_route(ra, rr, s);
+    if (local) {
+        qwq4::launch_router_logits(rr, T, E, s);
+    } else if (qwq4::router_split_ok(T, E, H)) {
+        // the logits over one block per expert, then the routing launch
+        qwq4::launch_router_logits(rr, T, E, s);
+        qwq4::launch_route(ra, s);
+    } else {
+        qwq4::launch_router_route(ra, rr, s);
+    }
     // up to 4 tokens the combine runs in the down projection's last blocks
     // (one launch less); from there on its own launch is faster than the
     // serial tail it adds to those blocks

@@ -533,6 +533,8 @@ static void launch_router_full(const RouteArgs &a, const RouterArgs &r, hipStrea
 
 bool router_logits_ok(int T, int E, int H) { return router_full_ok(T, E, H); }
 
+bool router_split_ok(int T, int E, int H) { return T >= 2 && T <= 8 && router_logits_ok(T, E, H); }
+
 template <int EPB, int WPE>
 static void launch_router_logits_t(const RouterArgs &r, int T, int E, hipStream_t s) {
     RouteArgs a{};

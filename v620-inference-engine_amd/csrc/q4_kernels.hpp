@@ -132,6 +132,10 @@ void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s)
 // does not take the shape.
 bool router_logits_ok(int T, int E, int H);
 void launch_router_logits(const RouterArgs &r, int T, int E, hipStream_t s);
+// Decode batches whose router runs as the logits launch (one block per
+// expert) followed by the routing launch instead of one launch of E / 8
+// blocks with the routing in its last block.
+bool router_split_ok(int T, int E, int H);
 // LDS bytes the slot pass needs for (T, E); the C-ABI rejects larger inputs.
 void launch_route(const RouteArgs &a, hipStream_t s);
 

@@ -503,7 +503,7 @@ class MoeDecode:
 
 def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, out=None, out_bf16=True, x_f16=None,
                out_dtype=None, yp_f16=False):
-    """Router GEMV + routing + experts + combine for a decode batch (3 launches; 4 above 4 tokens).
+    """Router GEMV + routing + experts + combine for a decode batch (3 to 5 launches).
     router_w [E][H] float32, or float16 (the engine's router weights). out bf16 (out_bf16), fp32, or
     out_dtype / the dtype of a given out; yp fp32, or fp16 with yp_f16 (or a buf whose yp is float16)."""
     import torch
