@@ -129,15 +129,17 @@ def test_moe_decode_symmetric_experts(gpu, oracle, T):
     assert rel_err(host(out), ref) <= TOL
 
 
-@pytest.mark.parametrize("T", [1, 4, 16])
-def test_moe_decode_fp16_router(gpu, T):
+@pytest.mark.parametrize("T,k", [(1, 6), (4, 6), (16, 6), (1, 10)])
+def test_moe_decode_fp16_router(gpu, T, k):
     """The engine's fp16 router weights (router_f16 = 1, decode.hip:101's w.router)
     against fp32 weights holding the same values: logits, routing and output bit
-    for bit, through all three router kernels (logits only at batch 1, GEMV and
-    routing in one launch up to 8 tokens, the K-sliced router above)."""
+    for bit, through every router path: the logits launch (batch 1, routed in the
+    gate/up blocks; batch 4, then a routing launch), the K-sliced router with the
+    routing in its last block (batch 16), and the full-K router with the routing in
+    its last block (batch 1 with k > 8)."""
     import torch
-    E, H, F, k = 64, 2048, 256, 6
-    print(f"moe_decode fp16 router T={T}", flush=True)
+    E, H, F = 64, 2048, 256
+    print(f"moe_decode fp16 router T={T} k={k}", flush=True)
     ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 150 + T, T, E, H, F, k, True)
     w16 = to_dev(Wr.astype(np.float16), gpu)
     w32 = w16.float()
