@@ -154,9 +154,10 @@ def test_moe_decode_fp16_router(gpu, T, k):
 
 @pytest.mark.parametrize("T,E", [(6, 64), (8, 64), (8, 256)])
 def test_moe_decode_router_lds_limit(gpu, oracle, T, E):
-    """H = 8192: the full-K router stages the token rows (T x 16 KB) in LDS
-    beside the routing's static arrays. T = 6 and 8 at E = 64 fit the CU's
-    160 KiB (the second within 2 KB); T = 8 at E = 256 does not and takes the
+    """H = 8192: the full-K router kernels stage the token rows (T x 16 KB) in
+    LDS (the routing variant beside its static arrays). T = 6 and 8 at E = 64
+    fit the CU's 160 KiB (the second within 2 KB) and take the logits launch
+    then the routing launch; T = 8 at E = 256 does not fit and takes the
     K-sliced router. Logits against the fp64 product, routing bit-exact with
     the oracle, output bit-identical to the unfused calls."""
     H, F, k = 8192, 128, 8
