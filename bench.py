@@ -215,7 +215,9 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
     Cache), so the weights come from HBM. The experts are symmetric (group-128
     fp16 scales, no zero points: config 3's format and the reference's,
     ref_model.cpp:114); the fused block is also timed at batch 1 on experts
-    with zero points (block_zero_points)."""
+    with zero points (block_zero_points) and, at batches 1-8, with a 16-bit shared expert, merged
+    into its launches (qw_moe_decode_with_shared) and as separate launches
+    (block_with_shared_expert; bytes add the shared expert's weights)."""
     E, F, k, L = 256, 1536, 8, MOE_LAYERS
     gate = gen_q4(torch, dev, F, H, zeros=False, lead=(E,), seed=10)
     up = gen_q4(torch, dev, F, H, zeros=False, lead=(E,), seed=11)
@@ -298,6 +300,51 @@ def bench_moe(torch, qwq4, dev, steps, warmup, batches=(1, 2, 4, 8, 16, 32)):
             out[B]["block_zero_points"] = {"GB_s": bz * steps / (tz.ms * 1e-3) / 1e9,
                                            "us_per_block": tz.ms * 1e3 / (steps * L)}
             del zg, zu, zd
+
+        if B <= 8:
+            # the block with the shared expert (16-bit, SH_FFN wide, weights of its own per
+            # block): qw_moe_decode_with_shared against the shared expert's own launches
+            # (two up to 4 rows, three above, as bench_shared picks them) followed by
+            # qw_moe_decode (the form the engine runs, src/engine/decode.hip:99-105)
+            gs = torch.Generator(device=dev)
+            gs.manual_seed(23)
+            sgu = [qwq4.w16_tile((torch.randn((2 * SH_FFN + 1, H), generator=gs, device=dev) * 0.05).half())
+                   for _ in range(L)]
+            sdn = [qwq4.w16_tile((torch.randn((H, SH_FFN), generator=gs, device=dev) * 0.05).half())
+                   for _ in range(L)]
+            sbuf = qwq4.MoeDecode(B, E, k, H, F, dev, Fs=SH_FFN)
+            xh = [x.half() if x.dtype != torch.float16 else x for x in xs]
+            sv = torch.empty((B, 2 * SH_FFN + 1), dtype=torch.float32, device=dev)
+            so = torch.empty((B, H), dtype=torch.float32, device=dev)
+            sh16 = torch.empty((B, SH_FFN), dtype=torch.float16, device=dev)
+
+            def with_shared():
+                for l in range(L):
+                    qwq4.moe_decode_with_shared(router_w[l], xh[l], k, gate, up, down, E, F, sgu[l], sdn[l],
+                                                SH_FFN, buf=sbuf, out=ob)
+
+            def separate():
+                for l in range(L):
+                    qwq4.gemv_w16_tiled(sgu[l], 2 * SH_FFN + 1, H, xh[l], B, y=sv, f16=True)
+                    if B <= 4:
+                        qwq4.swiglu_gemv_w16_tiled(sdn[l], H, sv, SH_FFN, B, y=so)
+                    else:
+                        qwq4.swiglu_gate(sv, SH_FFN, h=sh16)
+                        qwq4.gemv_w16_tiled(sdn[l], H, SH_FFN, sh16, B, y=so)
+                    qwq4.moe_decode(router_w[l], xh[l], k, gate, up, down, E, F, buf=sbuf, shared=so, out=ob)
+
+            sb = Uf * per_expert + L * E * H * 4 + L * ((2 * SH_FFN + 1) * H + H * SH_FFN) * 2
+            rs = {}
+            for name, fn in (("merged", with_shared), ("separate", separate)):
+                st = graphed(torch, fn)
+                for _ in range(warmup):
+                    st()
+                with Timer(torch) as ts:
+                    for _ in range(steps):
+                        st()
+                rs[name] = {"GB_s": sb * steps / (ts.ms * 1e-3) / 1e9, "us_per_block": ts.ms * 1e3 / (steps * L)}
+            out[B]["block_with_shared_expert"] = rs
+            del sgu, sdn
     return out
 
 

@@ -351,6 +351,29 @@ int qw_moe_decode(const void *router_w, int router_f16, const uint16_t *x, int x
                   void *out, int out_type, float *logits, int32_t *top_e, float *top_w, int32_t *tok_slot,
                   uint16_t *h, void *yp, int yp_f16, void *workspace, size_t workspace_bytes, void *stream);
 
+/* qw_moe_decode with the shared expert (the engine's decode.hip:98-101 before
+ * the routed block): sh_v = sh_gu x ([T][2 Fs + 1] fp32: gate, up and gate
+ * logit rows, the engine's b.shp), sh_out = sh_down swiglu_gate(sh_v) ([T][H]
+ * fp32, the engine's b.sh_out), and out = sh_out + the routed experts'
+ * combine. sh_gu [2 Fs + 1][H] is tiled 16-bit (qw_w16_tile) of x's type
+ * (fp16 with x_f16 = 1, bf16 else); sh_down [H][Fs] is tiled fp16; the
+ * arithmetic is that of qw_w16_gemv_tiled and qw_w16_swiglu_gemv_tiled (up
+ * to T = 4; qw_swiglu_gate + qw_w16_gemv_tiled above, the same values)
+ * followed by qw_moe_decode with shared = sh_out, bit for bit. Up
+ * to T = 8 the shared expert's gate/up GEMV runs in the router-logits launch
+ * and, at T = 1, its down GEMV in the routed gate/up launch, instead of
+ * launches of their own. Fs a multiple of 32. workspace:
+ * qw_moe_decode_with_shared_workspace_size(...) bytes (that of qw_moe_decode
+ * plus T * Fs * 2), zeroed once as for qw_moe_decode. */
+size_t qw_moe_decode_with_shared_workspace_size(int T, int E, int topk, int H, int F, int Fs);
+int qw_moe_decode_with_shared(const void *router_w, int router_f16, const uint16_t *x, int x_f16, int T, int E,
+                              int topk, const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                              const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                              const uint16_t *dz, int H, int F, const void *sh_gu, const void *sh_down, int Fs,
+                              float *sh_v, float *sh_out, void *out, int out_type, float *logits, int32_t *top_e,
+                              float *top_w, int32_t *tok_slot, uint16_t *h, void *yp, int yp_f16, void *workspace,
+                              size_t workspace_bytes, void *stream);
+
 /* qw_moe_decode without a workspace argument: it allocates nothing and
  * needs no caller scratch. No counterpart in the reference; it is for
  * callers that cannot allocate device memory (code under HIP graph capture,

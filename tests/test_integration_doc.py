@@ -61,6 +61,8 @@ void engine_calls(Batch &b, PrefillBuf &p, rocblas_handle blas, hipStream_t s, c
     qw::gpu::moe_combine_B(b.yp, b.tok_slot, b.tok_w, b.proj, M, sh, b.out_moe, s);
     qw::gpu::moe_block_B(router_w, b.bin, M, g, u, d, sh, b.proj, b.out_moe, b.logits, b.top_e, b.tok_w, b.tok_slot,
                          b.moe_h, b.yp, ws, ws_bytes, s);
+    qw::gpu::moe_block_shared_B(router_w, b.bin, M, g, u, d, sh, sh_gu, sh_down, b.router, b.sh_out, b.out_moe,
+                                b.logits, b.top_e, b.tok_w, b.tok_slot, b.moe_h, b.yp, ws, ws_bytes, s);
     // prefill.hip:324-339: router GEMM (fp32 out), experts, shared expert (fp16 out), combine
     qw::gpu::gemm(blas, wq, p.bin, sh.H, T, p.logits, sh.E, false);
     qw::gpu::gemm(blas, wq, p.bin, sh.H, T, p.part16, wq.N, f16_out);

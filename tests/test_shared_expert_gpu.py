@@ -263,3 +263,40 @@ def test_w16_swiglu_gemv_tiled_random_shapes(gpu, N, n, M):
         assert "staging LDS" in str(err) and M * n * 2 > 96 * 1024
         return
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("T,E,H,F,k,SF,f16", [(1, 256, 4096, 1536, 8, 1536, True), (1, 64, 2048, 512, 6, 512, False),
+                                              (1, 64, 1024, 256, 4, 320, True), (2, 256, 4096, 1536, 8, 1536, True),
+                                              (4, 64, 1024, 256, 4, 512, False), (8, 64, 2048, 512, 6, 1536, True),
+                                              (3, 256, 4096, 1536, 8, 1536, False),
+                                              (8, 256, 4096, 1536, 8, 1536, False)])
+def test_moe_decode_with_shared(gpu, oracle, T, E, H, F, k, SF, f16):
+    """qw_moe_decode_with_shared against its parts as separate calls (the
+    shared expert's tiled gate/up/gate-logit GEMV and SwiGLU-down GEMV, then
+    qw_moe_decode with their output as the shared rows): the shared rows, the
+    gate/up rows and the block's output bit for bit, and against the oracle.
+    With Fs a multiple of 256 the gate/up GEMV runs inside the router-logits
+    launch (batches 1-8: one, two and four rows per MFMA pass, every staging
+    width up to the looped one at 8 rows of 4096) and at batch 1 the down GEMV
+    inside the routed gate/up launch (fp16 rows and weights at config 3's size,
+    bf16 at H 2048 and at batches 3 and 8); Fs = 320 takes their own launches."""
+    print(f"moe decode with shared T={T} E={E} H={H} F={F} k={k} Fs={SF} f16={f16}", flush=True)
+    ex = synth.experts(95 + T, E, H, F, zeros=False)
+    xb, xf = rows(96, f"sx{T}x{H}", T, H, f16)
+    Wr = (np.random.default_rng(97 + T).standard_normal((E, H)) * 0.05).astype(np.float32)
+    gu_b, _ = w16(98, f"sgu{SF}x{H}", 2 * SF + 1, H, f16)
+    dn_b, _ = w16(99, f"sdn{H}x{SF}", H, SF, True)
+    from test_moe_gpu import _experts_dev
+    (g, u, d), _, _ = _experts_dev(gpu, ex)
+    gut, dnt = qwq4.w16_tile(to_dev(gu_b, gpu)), qwq4.w16_tile(to_dev(dn_b, gpu))
+    dx, dr = to_dev(xb, gpu), to_dev(Wr, gpu)
+    out, buf, sv, so = qwq4.moe_decode_with_shared(dr, dx, k, g, u, d, E, F, gut, dnt, SF, out_bf16=False,
+                                                   x_f16=f16, yp_f16=True)
+    v = qwq4.gemv_w16_tiled(gut, 2 * SF + 1, H, dx, T, f16=f16)
+    sh = qwq4.swiglu_gemv_w16_tiled(dnt, H, v, SF, T)
+    o2, _ = qwq4.moe_decode(dr, dx, k, g, u, d, E, F, shared=sh, out_bf16=False, x_f16=f16, yp_f16=True)
+    assert np.array_equal(host(sv).view(np.uint32), host(v).view(np.uint32))
+    assert np.array_equal(host(so).view(np.uint32), host(sh).view(np.uint32))
+    assert np.array_equal(host(out).view(np.uint32), host(o2).view(np.uint32))
+    ref = oracle.moe(xf, host(buf.logits), k, *ex) + oracle.shared_expert(xf, gu_b, dn_b, f16_gu=f16, f16_down=True)
+    assert rel_err(host(out), ref) <= TOL

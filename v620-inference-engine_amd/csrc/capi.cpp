@@ -599,7 +599,7 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
                        const uint16_t *uz, const uint32_t *dw, const uint16_t *ds, const uint16_t *dz, int H, int F,
                        const float *shared, void *out, int out_type, float *logits, int32_t *top_e, float *top_w,
                        int32_t *tok_slot, uint16_t *h, void *yp, int yp_f16, unsigned char *w, const DecodeLayout &L,
-                       hipStream_t s) {
+                       hipStream_t s, const qwq4::ShExpertArgs *sh = nullptr, uint16_t *sh_h = nullptr) {
     auto at = [&](size_t off) { return reinterpret_cast<int32_t *>(w + off); };
     qwq4::RouteArgs ra{logits, T, E, topk, 0, top_e, top_w, at(L.counts), at(L.offsets), tok_slot, at(L.pair_tok),
                        at(L.active), at(L.n_active), nullptr, nullptr, nullptr};
@@ -609,9 +609,35 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
     // small batches: the router launch writes the logits only, and the
     // gate/up blocks route the batch themselves (no cross-block hand-off)
     const bool local = qwq4::moe_local_route_ok(T, E, topk) && qwq4::router_logits_ok(T, E, H);
-    if (local) {
+    const bool split = !local && qwq4::router_split_ok(T, E, H);
+    // the shared expert: up to 8 tokens its gate/up GEMV shares the router
+    // logits launch, and at batch 1 its down GEMV the routed gate/up launch;
+    // otherwise its GEMVs run first, as launches of their own
+    const bool shl = sh && (local || split) && qwq4::shared_logits_ok(T, H, sh->Fs);
+    const bool sh1 = shl && local && T == 1;
+    const int nv = sh ? 2 * sh->Fs + 1 : 0;
+    // the SwiGLU folded into the down GEMV up to 4 rows (every block forms all
+    // of h, which costs more than the separate launch from 8 rows on)
+    auto shared_down = [&] {
+        if (T <= 4 && qwq4::w16_swiglu_fits(T, sh->Fs, H)) {
+            qwq4::launch_w16_swiglu(qwq4::W16SwigluArgs{sh->down, sh->v, nv, sh->Fs, sh->out, H, 0, H, T, 0}, s);
+        } else {
+            qwq4::launch_swiglu_gate(sh->v, nv, sh->Fs, T, sh_h, s);
+            qwq4::launch_w16_gemv(qwq4::W16Args{sh->down, sh->Fs, sh_h, sh->Fs, sh->out, H, 0, H, sh->Fs, T, 0, 1, 1}, s);
+        }
+    };
+    if (sh) {
+        if (!shl) qwq4::launch_w16_gemv(qwq4::W16Args{sh->gu, H, x, H, sh->v, nv, 0, nv, H, T, 0, x_f16 != 0, 1}, s);
+        if (!shl) shared_down();
+        shared = sh->out;
+    }
+    if (shl) {
+        qwq4::launch_router_logits_shgu(rr, T, E, *sh, s);
+        if (split) qwq4::launch_route(ra, s);
+        if (!sh1) shared_down();
+    } else if (local) {
         qwq4::launch_router_logits(rr, T, E, s);
-    } else if (qwq4::router_split_ok(T, E, H)) {
+    } else if (split) {
         // the logits over one block per expert, then the routing launch
         qwq4::launch_router_logits(rr, T, E, s);
         qwq4::launch_route(ra, s);
@@ -633,7 +659,16 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
         a.top_w = top_w;
         a.tok_slot = tok_slot;
     }
-    qwq4::launch_moe_gemv(a, s);
+    if (sh1) {
+        if (!qwq4::launch_gate_up_routed_shdown(a, *sh, s)) {
+            shared_down();
+            qwq4::launch_moe_gemv(a, s);
+        } else {
+            qwq4::launch_moe_down(a, s);
+        }
+    } else {
+        qwq4::launch_moe_gemv(a, s);
+    }
     if (!fold) qwq4::launch_combine(yp, yp_f16 != 0, tok_slot, top_w, shared, 0, T, topk, H, out, out_type, s);
 }
 
@@ -710,6 +745,41 @@ int qw_moe_decode(const void *router_w, int router_f16, const uint16_t *x, int x
     moe_decode_launch(router_w, router_f16, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, shared, out, out_type,
                       logits, top_e, top_w, tok_slot, h, yp, yp_f16, static_cast<unsigned char *>(workspace), L, st(stream));
     return launched("qw_moe_decode");
+}
+
+size_t qw_moe_decode_with_shared_workspace_size(int T, int E, int topk, int H, int F, int Fs) {
+    const size_t b = qw_moe_decode_workspace_size(T, E, topk, H, F);
+    if (b == 0 || Fs < 1) return 0;
+    return b + ((size_t(T) * Fs * 2 + 255) & ~size_t(255));
+}
+
+int qw_moe_decode_with_shared(const void *router_w, int router_f16, const uint16_t *x, int x_f16, int T, int E,
+                              int topk, const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw,
+                              const uint16_t *us, const uint16_t *uz, const uint32_t *dw, const uint16_t *ds,
+                              const uint16_t *dz, int H, int F, const void *sh_gu, const void *sh_down, int Fs,
+                              float *sh_v, float *sh_out, void *out, int out_type, float *logits, int32_t *top_e,
+                              float *top_w, int32_t *tok_slot, uint16_t *h, void *yp, int yp_f16, void *workspace,
+                              size_t workspace_bytes, void *stream) {
+    const char *fn = "qw_moe_decode_with_shared";
+    REQUIRE(router_f16 == 0 || router_f16 == 1, "%s: router_f16 = %d (0: fp32 weights, 1: fp16)", fn, router_f16);
+    if (int r = moe_decode_check(fn, router_w, x, T, E, topk, gw, gs, uw, us, dw, ds, H, F, out, logits, top_e, top_w,
+                                 tok_slot, h, yp, out_type))
+        return r;
+    REQUIRE(sh_gu && sh_down && sh_v && sh_out, "%s: null shared-expert pointer", fn);
+    REQUIRE(Fs >= 32 && Fs % 32 == 0 && H % 32 == 0, "%s: Fs = %d, H = %d (multiples of 32)", fn, Fs, H);
+    REQUIRE(aligned(sh_gu, 16) && aligned(sh_down, 16) && aligned(sh_v, 4) && aligned(sh_out, 4),
+            "%s: sh_gu, sh_down must be 16-byte aligned, sh_v, sh_out 4-byte", fn);
+    REQUIRE(workspace && aligned(workspace, 256), "%s: workspace null or not 256-byte aligned", fn);
+    const size_t need = qw_moe_decode_with_shared_workspace_size(T, E, topk, H, F, Fs);
+    REQUIRE(workspace_bytes >= need, "%s: workspace needs %zu bytes", fn, need);
+    const DecodeLayout L = decode_layout(T, E, topk, H, F);
+    unsigned char *w = static_cast<unsigned char *>(workspace);
+    const qwq4::ShExpertArgs sh{static_cast<const uint16_t *>(sh_gu), static_cast<const uint16_t *>(sh_down), Fs, sh_v,
+                                sh_out};
+    moe_decode_launch(router_w, router_f16, x, x_f16, T, E, topk, gw, gs, gz, uw, us, uz, dw, ds, dz, H, F, nullptr,
+                      out, out_type, logits, top_e, top_w, tok_slot, h, yp, yp_f16, w, L, st(stream), &sh,
+                      reinterpret_cast<uint16_t *>(w + L.total));
+    return launched(fn);
 }
 
 size_t qw_moe_decode_static_max_bytes(void) { return kStaticScratchBytes; }

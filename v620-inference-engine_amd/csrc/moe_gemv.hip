@@ -21,9 +21,12 @@
 //   down     waves = subtiles x KS; yp fp32, or fp16 (YP16: rounded to
 //            nearest even, finite values beyond +-65504 saturated; the
 //            reference's moe_experts_P output).
+#include <type_traits>
+
 #include "q4_gemv_core.cuh"
 #include "q4_kernels.hpp"
 #include "route_core.cuh"
+#include "w16_core.cuh"
 
 namespace qwq4 {
 
@@ -266,11 +269,14 @@ __device__ __forceinline__ LaneRoute lane_route(const int32_t *s_te, int P, int 
     return r;
 }
 
+// (bx, by): the block's column block and active-expert rank (arguments, so
+// that a kernel running other work in the same grid can call it)
 template <typename XT, int KS, int GW, bool HAS_Z, bool CH4, int PER>
-__global__ __launch_bounds__(512) void moe_gate_up_routed_kernel(
-    const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
-    const uint16_t *uz, LocalRoute lr, const uint16_t *__restrict__ x, int E, int H, int F, int T, int k,
-    uint16_t *__restrict__ h) {
+__device__ __forceinline__ void moe_gate_up_routed_block(const uint32_t *gw, const uint16_t *gs, const uint16_t *gz,
+                                                         const uint32_t *uw, const uint16_t *us, const uint16_t *uz,
+                                                         const LocalRoute &lr, const uint16_t *__restrict__ x, int E,
+                                                         int H, int F, int T, int k, uint16_t *__restrict__ h, int bx,
+                                                         int by) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int32_t s_te[64];
     __shared__ float s_tw[64];
@@ -290,9 +296,9 @@ __global__ __launch_bounds__(512) void moe_gate_up_routed_kernel(
     }
     __syncthreads();
     const LaneRoute rt = lane_route(s_te, P, k, lane);
-    const uint64_t mine = __ballot(rt.first && rt.act == int(blockIdx.y));
+    const uint64_t mine = __ballot(rt.first && rt.act == by);
     const int n_act = __popcll(__ballot(rt.first));  // (every lane takes part in the ballot)
-    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+    if (bx == 0 && by == 0 && wave == 0) {
         if (lane < P) {
             lr.top_e[lane] = rt.e;
             lr.top_w[lane] = s_tw[lane];
@@ -312,7 +318,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_routed_kernel(
     constexpr int SUB = 8 / (2 * KS);
     const int sl = wave / (2 * KS), mat = (wave / KS) % 2, kp = wave % KS;
     const int G = H / QGROUP, gpk = G / KS, fsub = F / 16, kc = x_row_stride(H);
-    const int lsub = blockIdx.x * SUB + sl;
+    const int lsub = bx * SUB + sl;
     const int64_t sub = int64_t(e) * fsub + min(lsub, fsub - 1);
     const Q4Tile tl = mat ? Q4Tile(uw, us, uz, sub, G) : Q4Tile(gw, gs, gz, sub, G);
     WaveRange<GW, HAS_Z, CH4> wr;
@@ -352,6 +358,15 @@ __global__ __launch_bounds__(512) void moe_gate_up_routed_kernel(
             if (m < M) h[int64_t(base + m) * F + lsub * 16 + n] = silu_mul_f16(g[r], u[r]);
         }
     }
+}
+
+template <typename XT, int KS, int GW, bool HAS_Z, bool CH4, int PER>
+__global__ __launch_bounds__(512) void moe_gate_up_routed_kernel(
+    const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
+    const uint16_t *uz, LocalRoute lr, const uint16_t *__restrict__ x, int E, int H, int F, int T, int k,
+    uint16_t *__restrict__ h) {
+    moe_gate_up_routed_block<XT, KS, GW, HAS_Z, CH4, PER>(gw, gs, gz, uw, us, uz, lr, x, E, H, F, T, k, h,
+                                                           int(blockIdx.x), int(blockIdx.y));
 }
 
 // CMB: the last block of each row block (over the active experts, counted
@@ -647,6 +662,66 @@ static void launch_gate_up_routed(const MoeGemvArgs &a, int max_active, hipStrea
     else pick(BF16{});
 }
 
+// ---- batch 1 with the shared expert: blocks 0 .. gx gy - 1 are the routed
+// gate/up blocks (column block b % gx, active expert b / gx, their launch
+// order), the blocks after them compute 16 rows each of the shared expert's
+// SwiGLU-down GEMV (as qw_w16_swiglu_gemv_tiled) from the gate/up/gate-logit
+// rows the block's first launch wrote.
+template <typename XT, int GW, bool HAS_Z, int PER, int SWS>
+__global__ __launch_bounds__(512) void gate_up_routed_shdown_kernel(
+    const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
+    const uint16_t *uz, LocalRoute lr, const uint16_t *__restrict__ x, int E, int H, int F, int k,
+    uint16_t *__restrict__ h, ShExpertArgs sh, int gx, int gy) {
+    const int b = blockIdx.x;
+    if (b < gx * gy)
+        moe_gate_up_routed_block<XT, 4, GW, HAS_Z, true, PER>(gw, gs, gz, uw, us, uz, lr, x, E, H, F, 1, k, h, b % gx,
+                                                             b / gx);
+    else
+        w16_swiglu_block<1, 1, 1, SWS>(sh.down, sh.v, 2 * sh.Fs + 1, 1, sh.Fs, H, sh.out, H, 0, 0, b - gx * gy);
+}
+
+bool launch_gate_up_routed_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, hipStream_t s) {
+    const int G = a.H / QGROUP;
+    // the routed launch's shape: K split in 4 over whole 4-group chunks
+    if (!a.route_logits || a.T != 1 || G % 16 != 0 || G / 4 > 8 || (a.gz != nullptr) != (a.uz != nullptr)) return false;
+    const int gx = a.F / 16, gy = a.topk < a.E ? a.topk : a.E, per = (a.E + WAVE - 1) / WAVE;
+    const LocalRoute lr{a.route_logits, a.top_e, a.tok_slot, const_cast<int32_t *>(a.pair_tok),
+                        const_cast<int32_t *>(a.offsets), const_cast<int32_t *>(a.active),
+                        const_cast<int32_t *>(a.n_active), a.top_w};
+    const size_t l1 = moe_lds_bytes(1, a.H), l2 = dense_lds_bytes(1, sh.Fs, 1, W16_MAX_KS, W16_MAX_KS);
+    const size_t lds = l1 > l2 ? l1 : l2;
+    const unsigned grid = unsigned(gx * gy + a.H / 16);
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024) raise_lds_limit(reinterpret_cast<const void *>(kern));
+        kern<<<grid, 512, lds, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, lr, a.x, a.E, a.H, a.F, a.topk, a.h, sh, gx,
+                                    gy);
+    };
+    auto by_ws = [&](auto xt, auto gw, auto hz, auto pr) {
+        using XT = decltype(xt);
+        constexpr int GW = decltype(gw)::value, PER = decltype(pr)::value;
+        constexpr bool HZ = decltype(hz)::value;
+        if (sh.Fs / 32 / W16_MAX_KS <= 8) go(gate_up_routed_shdown_kernel<XT, GW, HZ, PER, 8>);
+        else go(gate_up_routed_shdown_kernel<XT, GW, HZ, PER, 16>);
+    };
+    auto by_per = [&](auto xt, auto gw, auto hz) {
+        if (per <= 1) by_ws(xt, gw, hz, std::integral_constant<int, 1>());
+        else if (per <= 2) by_ws(xt, gw, hz, std::integral_constant<int, 2>());
+        else if (per <= 4) by_ws(xt, gw, hz, std::integral_constant<int, 4>());
+        else by_ws(xt, gw, hz, std::integral_constant<int, 8>());
+    };
+    auto by_z = [&](auto xt, auto gw) {
+        if (a.gz) by_per(xt, gw, std::true_type());
+        else by_per(xt, gw, std::false_type());
+    };
+    auto by_gw = [&](auto xt) {
+        if (G / 4 == 8) by_z(xt, std::integral_constant<int, 8>());
+        else by_z(xt, std::integral_constant<int, 4>());
+    };
+    if (a.x_f16) by_gw(F16{});
+    else by_gw(BF16{});
+    return true;
+}
+
 // Batch 1 only. Routing in every block costs each block the top-k's
 // latency (about 1.3 us of its 8 serial wave-maximum rounds) before its
 // weight requests; at batch 1 (768 blocks, one round) that is less than the
@@ -772,6 +847,12 @@ int moe_down_row_blocks(int H, int F) {
 bool moe_gemv_supported(int H, int F) {
     // each wave holds at most 16 groups of its K range
     return H / QGROUP / pick_ks(H / QGROUP, 4) <= 16 && F / QGROUP / down_ks(F / QGROUP) <= 16;
+}
+
+void launch_moe_down(const MoeGemvArgs &a, hipStream_t s) {
+    const int max_active = a.T * a.topk < a.E ? a.T * a.topk : a.E;
+    if (a.dz) launch_one<true, true>(a, max_active, s);
+    else launch_one<true, false>(a, max_active, s);
 }
 
 void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s) {

@@ -24,6 +24,7 @@
 
 #include "q4_common.cuh"
 #include "route_core.cuh"
+#include "w16_core.cuh"
 
 #include "q4_kernels.hpp"
 
@@ -409,12 +410,14 @@ __global__ __launch_bounds__(1024) void router_route_kernel(RouteArgs a, RouterA
 // every logit once into LDS and routes from there.
 // ROUTE false: the logits only, by plain stores (the kernel boundary makes
 // them visible to the next launch), no count and no routing.
-template <int PER, int EPB, int WPE, int NCH, bool ROUTE = true>
-__global__ __launch_bounds__(EPB *WPE *WAVE) void router_full_kernel(RouteArgs a, RouterArgs r) {
+// bx: the block's expert group (an argument, so that a kernel running other
+// work in the same grid can call it for a part of its blocks)
+template <int PER, int EPB, int WPE, int NCH, bool ROUTE>
+__device__ __forceinline__ void router_full_block(const RouteArgs &a, const RouterArgs &r, int bx) {
     extern __shared__ __align__(16) unsigned char smem[];  // x [T][H] | part sums [T][EPB][WPE] | logits [T][E]
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int T = a.T, E = a.E, H = r.H, kw = H / WPE, nch = kw / 8;
-    const int el = wave / WPE, wp = wave % WPE, e = min(int(blockIdx.x) * EPB + el, E - 1);
+    const int el = wave / WPE, wp = wave % WPE, e = min(bx * EPB + el, E - 1);
     ExpfGlibc ex;
     ex.load(lane);
     // the lane's runs of 8 weights: chunks lane, lane + 64, .. of its part
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(EPB *WPE *WAVE) void router_full_kernel(RouteArgs a
     else dots([](uint16_t b) { return bf16_bits_to_f32(b); });
     __syncthreads();
     for (int i = tid; i < T * EPB; i += blockDim.x) {
-        const int t = i / EPB, j = i - t * EPB, ee = int(blockIdx.x) * EPB + j;
+        const int t = i / EPB, j = i - t * EPB, ee = bx * EPB + j;
         float v = 0.f;
 #pragma unroll
         for (int q = 0; q < WPE; ++q) v += part[i * WPE + q];
@@ -491,6 +494,11 @@ __global__ __launch_bounds__(EPB *WPE *WAVE) void router_full_kernel(RouteArgs a
             return [l](int i) { return l[i]; };
         });
     }
+}
+
+template <int PER, int EPB, int WPE, int NCH, bool ROUTE = true>
+__global__ __launch_bounds__(EPB *WPE *WAVE) void router_full_kernel(RouteArgs a, RouterArgs r) {
+    router_full_block<PER, EPB, WPE, NCH, ROUTE>(a, r, int(blockIdx.x));
 }
 
 // The full-K router serves T <= 8 (activations staged whole) and H up to
@@ -559,6 +567,64 @@ static void launch_router_logits_t(const RouterArgs &r, int T, int E, hipStream_
 // against 30.3 with 4 experts per block and 30.4-31.2 with 8).
 void launch_router_logits(const RouterArgs &r, int T, int E, hipStream_t s) {
     launch_router_logits_t<1, 8>(r, T, E, s);
+}
+
+// ---- up to 8 tokens with the shared expert: blocks 0 .. E - 1 compute the
+// router logits (as launch_router_logits), blocks E .. compute 16 rows each
+// of the shared expert's gate/up/gate-logit GEMV (as qw_w16_gemv_tiled): two
+// independent GEMVs over the same activation rows in one launch, which also
+// gives the CUs the router leaves idle (E blocks) work.
+template <int NCH, typename SXT, int SMR, int SXPT, int SWS>
+__global__ __launch_bounds__(8 * WAVE) void router_logits_shgu_kernel(RouteArgs a, RouterArgs r, ShExpertArgs sh) {
+    const int b = blockIdx.x, N = 2 * sh.Fs + 1;
+    if (b < a.E) router_full_block<1, 1, 8, NCH, false>(a, r, b);
+    else w16_gemv_block<SXT, 1, SMR, SXPT, SWS, true>(sh.gu, 0, r.x, r.H, a.T, r.H, N, sh.v, N, 0, 0, 0, b - a.E);
+}
+
+bool shared_logits_ok(int T, int H, int Fs) {
+    return T >= 1 && T <= 8 && H % 256 == 0 && H <= 8192 && Fs % 256 == 0 && Fs <= 4096;
+}
+
+void launch_router_logits_shgu(const RouterArgs &r, int T, int E, const ShExpertArgs &sh, hipStream_t s) {
+    RouteArgs a{};
+    a.T = T;
+    a.E = E;
+    const int H = r.H, N = 2 * sh.Fs + 1;
+    // the router's LDS as launch_router_logits sizes it, the GEMV's as qw_w16_gemv's
+    const size_t lr = size_t(T) * H * 2 + size_t(T) * 8 * 4 + size_t(T) * E * 4,
+                 lw = dense_lds_bytes(T, H, 1, W16_MAX_KS, W16_MAX_KS);
+    const size_t lds = lr > lw ? lr : lw;
+    const unsigned grid = unsigned(E + (N + 15) / 16);
+    const int xpt = (T * (H / 8) + 8 * WAVE - 1) / (8 * WAVE);
+    auto go = [&](auto kern) {
+        if (lds > 48 * 1024) raise_lds_limit(reinterpret_cast<const void *>(kern));
+        kern<<<grid, 8 * WAVE, lds, s>>>(a, r, sh);
+    };
+    auto by_nch = [&](auto sxt, auto smr, auto sxpt, auto sws) {
+        using SXT = decltype(sxt);
+        constexpr int SMR = decltype(smr)::value, SXPT = decltype(sxpt)::value, SWS = decltype(sws)::value;
+        if (H / 64 <= WAVE) go(router_logits_shgu_kernel<1, SXT, SMR, SXPT, SWS>);
+        else go(router_logits_shgu_kernel<2, SXT, SMR, SXPT, SWS>);
+    };
+    auto by_ws = [&](auto sxt, auto smr, auto sxpt) {
+        if (H / 32 / W16_MAX_KS <= 8) by_nch(sxt, smr, sxpt, std::integral_constant<int, 8>());
+        else by_nch(sxt, smr, sxpt, std::integral_constant<int, 16>());
+    };
+    // loads per thread of the activation staging as launch_w16_t picks them
+    auto by_xpt = [&](auto sxt, auto smr) {
+        if (xpt <= 1) by_ws(sxt, smr, std::integral_constant<int, 1>());
+        else if (xpt <= 2) by_ws(sxt, smr, std::integral_constant<int, 2>());
+        else if (xpt <= 4) by_ws(sxt, smr, std::integral_constant<int, 4>());
+        else by_ws(sxt, smr, std::integral_constant<int, 0>());
+    };
+    // rows per MFMA pass as launch_w16_x picks them
+    auto by_mr = [&](auto sxt) {
+        if (T == 1) by_xpt(sxt, std::integral_constant<int, 1>());
+        else if (T == 2) by_xpt(sxt, std::integral_constant<int, 2>());
+        else by_xpt(sxt, std::integral_constant<int, 4>());
+    };
+    if (r.x_f16) by_mr(F16{});
+    else by_mr(BF16{});
 }
 
 size_t router_lds_bytes(int T, int kl, int E) {

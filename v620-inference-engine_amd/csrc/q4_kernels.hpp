@@ -48,6 +48,16 @@ struct CombineArgs {
 // Down row blocks of the decode experts for H (the counters combine needs).
 int moe_down_row_blocks(int H, int F);
 
+// The shared expert of a fused decode block (tiled 16-bit weights of x's
+// type, qw_w16_tile): v = gu x ([T][2 Fs + 1] fp32: gate, up, gate logit),
+// out = down swiglu_gate(v) ([T][H] fp32), the rows the combine adds.
+struct ShExpertArgs {
+    const uint16_t *gu;    // [2 Fs + 1][H]
+    const uint16_t *down;  // [H][Fs]
+    int Fs;
+    float *v;
+    float *out;
+};
 struct MoeGemvArgs {
     const uint32_t *gw;
     const uint16_t *gs;
@@ -78,6 +88,13 @@ struct MoeGemvArgs {
 // Whether the gate/up decode GEMV can route a batch of T tokens itself.
 bool moe_local_route_ok(int T, int E, int topk);
 void launch_moe_gemv(const MoeGemvArgs &a, hipStream_t s);
+// The down projection (with the folded combine where it applies) alone, after
+// a gate/up launch of the caller's.
+void launch_moe_down(const MoeGemvArgs &a, hipStream_t s);
+// Batch 1 gate/up routed in its blocks with the shared expert's SwiGLU-down
+// GEMV in the same launch; false (nothing launched) where the shapes do not
+// fit that launch.
+bool launch_gate_up_routed_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, hipStream_t s);
 // Whether the expert GEMVs take these sizes (a wave holds <= 16 groups of its K range).
 bool moe_gemv_supported(int H, int F);
 
@@ -125,6 +142,11 @@ struct RouterArgs {
     int x_f16 = 0;      // x rows are fp16 (else bf16)
     int w_f16 = 0;      // router weights are fp16 (the engine's w.router), else fp32
 };
+// Up to 8 tokens: the shared expert's gate/up GEMV in the router-logits launch
+// (and at batch 1 its down GEMV beside the routed gate/up) where the shapes
+// allow (T <= 8, H and Fs multiples of 256, H <= 8192, Fs <= 4096).
+bool shared_logits_ok(int T, int H, int Fs);
+void launch_router_logits_shgu(const RouterArgs &r, int T, int E, const ShExpertArgs &sh, hipStream_t s);
 size_t router_lds_bytes(int T, int kl, int E);
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
 // The fp32 router GEMV alone (logits, no routing and no hand-off), for the

@@ -20,7 +20,7 @@ SYMBOLS = (
     "qw_st_open", "qw_st_close", "qw_st_count", "qw_st_name", "qw_st_tensor",
     "qw_q4_load_staging_size", "qw_q4_load", "qw_q4_tiled_offset",
     "qw_moe_decode_workspace_size", "qw_moe_decode", "qw_moe_decode_static_max_bytes", "qw_moe_decode_static",
-    "qw_moe_decode_static_reset",
+    "qw_moe_decode_static_reset", "qw_moe_decode_with_shared_workspace_size", "qw_moe_decode_with_shared",
     "qw_w16_gemv", "qw_w16_tiled_size", "qw_w16_tile", "qw_w16_gemv_tiled", "qw_w16_swiglu_gemv_tiled", "qw_i8_gemv", "qw_i8_tiled_size", "qw_i8_tile",
     "qw_moe_w4a8_tile_m", "qw_moe_w4a8_workspace_size", "qw_moe_experts_w4a8", "qw_quant_rows_i8", "qw_swiglu_gate",
     "qw_wcache_open", "qw_wcache_put", "qw_wcache_get", "qw_wcache_finish", "qw_wcache_close",
@@ -68,6 +68,9 @@ _SIGS = {
     "qw_quant_rows_i8": ([_P, _I, _I, _I, _I, _P, _P, _P], _I),
     "qw_swiglu_gate": ([_P, _I, _I, _I, _P, _P], _I),
     "qw_moe_decode_static": ([_P, _I, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I] + [_P] * 6 + [_I, _P], _I),
+    "qw_moe_decode_with_shared_workspace_size": ([_I, _I, _I, _I, _I, _I], _SZ),
+    "qw_moe_decode_with_shared": ([_P, _I, _P, _I, _I, _I, _I] + [_P] * 9 + [_I, _I, _P, _P, _I, _P, _P, _P, _I]
+                                  + [_P] * 6 + [_I, _P, _SZ, _P], _I),
     "qw_moe_decode_static_reset": ([_P], _I),
     "qw_st_open": ([ctypes.c_char_p, _P], _I),
     "qw_st_close": ([_P], None),
@@ -487,10 +490,12 @@ def from_engine_order(words):
 class MoeDecode:
     """Buffers of the fused decode block (qw_moe_decode) for T tokens."""
 
-    def __init__(self, T, E, topk, H, F, device, yp_f16=False):
+    def __init__(self, T, E, topk, H, F, device, yp_f16=False, Fs=0):
+        """Fs > 0: also the shared expert's rows (sh_v [T][2 Fs + 1], sh_out [T][H], fp32) and the
+        workspace of qw_moe_decode_with_shared."""
         import torch
         i32 = dict(dtype=torch.int32, device=device)
-        self.T, self.E, self.topk, self.H, self.F = T, E, topk, H, F
+        self.T, self.E, self.topk, self.H, self.F, self.Fs = T, E, topk, H, F, Fs
         self.logits = torch.empty((T, E), dtype=torch.float32, device=device)
         self.top_e = torch.empty((T, topk), **i32)
         self.top_w = torch.empty((T, topk), dtype=torch.float32, device=device)
@@ -499,6 +504,11 @@ class MoeDecode:
         self.yp = torch.empty((T * topk, H), dtype=torch.float16 if yp_f16 else torch.float32, device=device)
         # zero once: holds completion counters every call leaves at zero
         self.ws = torch.zeros(lib().qw_moe_decode_workspace_size(T, E, topk, H, F), dtype=torch.uint8, device=device)
+        if Fs:
+            self.sh_v = torch.empty((T, 2 * Fs + 1), dtype=torch.float32, device=device)
+            self.sh_out = torch.empty((T, H), dtype=torch.float32, device=device)
+            self.ws_sh = torch.zeros(lib().qw_moe_decode_with_shared_workspace_size(T, E, topk, H, F, Fs),
+                                     dtype=torch.uint8, device=device)
 
 
 def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, out=None, out_bf16=True, x_f16=None,
@@ -521,6 +531,31 @@ def moe_decode(router_w, x, topk, gate, up, down, E, F, buf=None, shared=None, o
                              int(buf.yp.dtype == torch.float16), _ptr(buf.ws), buf.ws.numel(), _stream())
     _check(rc, "qw_moe_decode")
     return out, buf
+
+
+def moe_decode_with_shared(router_w, x, topk, gate, up, down, E, F, sh_gu, sh_down, Fs, buf=None, out=None,
+                           out_bf16=True, x_f16=None, yp_f16=False):
+    """moe_decode with the shared expert: sh_gu [2 Fs + 1][H] tiled 16-bit (w16_tile) of x's type,
+    sh_down [H][Fs] tiled fp16. Returns (out, buf, sh_v, sh_out): the shared expert's gate/up/gate-logit
+    rows and output rows (fp32) beside the block's output."""
+    import torch
+    T, H = x.shape
+    buf = buf if buf is not None else MoeDecode(T, E, topk, H, F, x.device, yp_f16=yp_f16, Fs=Fs)
+    if buf.Fs != Fs:
+        raise ValueError(f"moe_decode_with_shared: buf was made for Fs = {buf.Fs}, not {Fs}")
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=x.device)
+    if router_w.dtype not in (torch.float32, torch.float16):
+        raise TypeError(f"moe_decode_with_shared: router_w must be float32 or float16, not {router_w.dtype}")
+    sh_v, sh_out, ws = buf.sh_v, buf.sh_out, buf.ws_sh
+    _dev(router_w, x, out, sh_gu, sh_down, *gate, *up, *down)
+    rc = lib().qw_moe_decode_with_shared(
+        _ptr(router_w), int(router_w.dtype == torch.float16), _ptr(x), int(_is_f16(x, x_f16)), T, E, topk,
+        *map(_ptr, gate), *map(_ptr, up), *map(_ptr, down), H, F, _ptr(sh_gu), _ptr(sh_down), Fs, _ptr(sh_v),
+        _ptr(sh_out), _ptr(out), _tcode(out), _ptr(buf.logits), _ptr(buf.top_e), _ptr(buf.top_w), _ptr(buf.tok_slot),
+        _ptr(buf.h), _ptr(buf.yp), int(buf.yp.dtype == torch.float16), _ptr(ws), ws.numel(), _stream())
+    _check(rc, "qw_moe_decode_with_shared")
+    return out, buf, sh_v, sh_out
 
 
 # -------------------------------------------------------- checkpoint loading
