@@ -633,8 +633,12 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
     }
     if (shl) {
         qwq4::launch_router_logits_shgu(rr, T, E, *sh, s);
-        if (split) qwq4::launch_route(ra, s);
-        if (!sh1) shared_down();
+        if (split && !(T <= 4 && qwq4::launch_route_shdown(ra, *sh, H, s))) {
+            qwq4::launch_route(ra, s);
+            shared_down();
+        } else if (!split && !sh1) {
+            shared_down();
+        }
     } else if (local) {
         qwq4::launch_router_logits(rr, T, E, s);
     } else if (split) {

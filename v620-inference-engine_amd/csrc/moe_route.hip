@@ -673,6 +673,59 @@ void launch_route(const RouteArgs &a, hipStream_t s) {
     }
 }
 
+// ---- 2 to 4 tokens with the shared expert: block 0 routes the batch (as
+// route_small_kernel; 8 waves cover T <= 8 tokens and, one thread per expert,
+// E <= 512), blocks 1 .. run the shared expert's SwiGLU-gate + down GEMV (as
+// qw_w16_swiglu_gemv_tiled, 16 output rows each). Both read only what the
+// router-logits launch before them wrote.
+template <int PER, int SMR, int SXPT, int SWS>
+__global__ __launch_bounds__(8 * WAVE) void route_shdown_kernel(RouteArgs a, ShExpertArgs sh, int H) {
+    if (blockIdx.x == 0) {
+        ExpfGlibc ex;
+        ex.load(threadIdx.x % WAVE);
+        route_small_body<PER>(a, ex, [&](int t) {
+            const float *l = a.logits + int64_t(t) * a.E;
+            return [l](int i) { return l[i]; };
+        });
+    } else {
+        w16_swiglu_block<1, SMR, SXPT, SWS>(sh.down, sh.v, 2 * sh.Fs + 1, a.T, sh.Fs, H, sh.out, H, 0, 0,
+                                            int(blockIdx.x) - 1);
+    }
+}
+
+bool launch_route_shdown(const RouteArgs &a, const ShExpertArgs &sh, int H, hipStream_t s) {
+    const int T = a.T, Fs = sh.Fs;
+    if (T < 2 || T > 4 || a.E > 8 * WAVE || a.tile_m != 0 || Fs % 256 != 0 || !w16_swiglu_fits(T, Fs, H)) return false;
+    const size_t lds = dense_lds_bytes(T, Fs, 1, W16_MAX_KS, W16_MAX_KS);
+    if (lds + ROUTE_STATIC_LDS > 160 * 1024) return false;
+    const unsigned grid = unsigned(1 + (H + 15) / 16);
+    const int xpt = (T * (Fs / 8) + 8 * WAVE - 1) / (8 * WAVE), per = (a.E + WAVE - 1) / WAVE;
+    auto go = [&](auto kern) {
+        if (lds > 48 * 1024) raise_lds_limit(reinterpret_cast<const void *>(kern));
+        kern<<<grid, 8 * WAVE, lds, s>>>(a, sh, H);
+    };
+    auto by_per = [&](auto smr, auto sxpt, auto sws) {
+        constexpr int SMR = decltype(smr)::value, SXPT = decltype(sxpt)::value, SWS = decltype(sws)::value;
+        if (per <= 1) go(route_shdown_kernel<1, SMR, SXPT, SWS>);
+        else if (per <= 2) go(route_shdown_kernel<2, SMR, SXPT, SWS>);
+        else if (per <= 4) go(route_shdown_kernel<4, SMR, SXPT, SWS>);
+        else go(route_shdown_kernel<8, SMR, SXPT, SWS>);
+    };
+    // staging width and weight steps per wave as launch_w16_swiglu picks them
+    auto by_ws = [&](auto smr, auto sxpt) {
+        if ((Fs / 32 + W16_MAX_KS - 1) / W16_MAX_KS <= 8) by_per(smr, sxpt, std::integral_constant<int, 8>());
+        else by_per(smr, sxpt, std::integral_constant<int, 16>());
+    };
+    auto by_xpt = [&](auto smr) {
+        if (xpt <= 1) by_ws(smr, std::integral_constant<int, 1>());
+        else if (xpt <= 2) by_ws(smr, std::integral_constant<int, 2>());
+        else by_ws(smr, std::integral_constant<int, 4>());
+    };
+    if (T == 2) by_xpt(std::integral_constant<int, 2>());
+    else by_xpt(std::integral_constant<int, 4>());
+    return true;
+}
+
 // out[t][j] = shared[t][j] + sum_i w[t][i] * yp[slot[t][i]][j], i in selection
 // order (src/kernels/moe_route.hip:168-185, 201-224). 4 columns per thread.
 // C consecutive groups of 4 elements of a yp row (fp32, or fp16 with YP16):

@@ -147,6 +147,10 @@ struct RouterArgs {
 // allow (T <= 8, H and Fs multiples of 256, H <= 8192, Fs <= 4096).
 bool shared_logits_ok(int T, int H, int Fs);
 void launch_router_logits_shgu(const RouterArgs &r, int T, int E, const ShExpertArgs &sh, hipStream_t s);
+// 2 to 4 tokens: the routing (one block, as launch_route) and the shared
+// expert's SwiGLU-gate + down GEMV in one launch; false (nothing launched)
+// where the shapes do not allow it.
+bool launch_route_shdown(const RouteArgs &a, const ShExpertArgs &sh, int H, hipStream_t s);
 size_t router_lds_bytes(int T, int kl, int E);
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
 // The fp32 router GEMV alone (logits, no routing and no hand-off), for the
