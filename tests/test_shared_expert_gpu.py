@@ -278,8 +278,10 @@ def test_moe_decode_with_shared(gpu, oracle, T, E, H, F, k, SF, f16):
     With Fs a multiple of 256 the gate/up GEMV runs inside the router-logits
     launch (batches 1-8: one, two and four rows per MFMA pass, every staging
     width up to the looped one at 8 rows of 4096), the down GEMV at batch 1
-    inside the routed gate/up launch and at batches 2-4 inside the routing launch (fp16 rows and weights at config 3's size,
-    bf16 at H 2048 and at batches 3 and 8); Fs = 320 takes their own launches."""
+    inside the routed gate/up launch and at batches 2-4 inside the routing
+    launch, and at batch 8 the routing launch forms the SwiGLU rows (fp16 rows
+    and weights at config 3's size, bf16 at H 2048 and at batches 3 and 8);
+    Fs = 320 takes their own launches."""
     print(f"moe decode with shared T={T} E={E} H={H} F={F} k={k} Fs={SF} f16={f16}", flush=True)
     ex = synth.experts(95 + T, E, H, F, zeros=False)
     xb, xf = rows(96, f"sx{T}x{H}", T, H, f16)

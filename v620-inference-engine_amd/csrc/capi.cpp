@@ -618,12 +618,16 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
     const int nv = sh ? 2 * sh->Fs + 1 : 0;
     // the SwiGLU folded into the down GEMV up to 4 rows (every block forms all
     // of h, which costs more than the separate launch from 8 rows on)
+    const bool fold_sh = sh && T <= 4 && qwq4::w16_swiglu_fits(T, sh->Fs, H);
+    auto down_gemv = [&] {  // the down GEMV over the SwiGLU rows in sh_h
+        qwq4::launch_w16_gemv(qwq4::W16Args{sh->down, sh->Fs, sh_h, sh->Fs, sh->out, H, 0, H, sh->Fs, T, 0, 1, 1}, s);
+    };
     auto shared_down = [&] {
-        if (T <= 4 && qwq4::w16_swiglu_fits(T, sh->Fs, H)) {
+        if (fold_sh) {
             qwq4::launch_w16_swiglu(qwq4::W16SwigluArgs{sh->down, sh->v, nv, sh->Fs, sh->out, H, 0, H, T, 0}, s);
         } else {
             qwq4::launch_swiglu_gate(sh->v, nv, sh->Fs, T, sh_h, s);
-            qwq4::launch_w16_gemv(qwq4::W16Args{sh->down, sh->Fs, sh_h, sh->Fs, sh->out, H, 0, H, sh->Fs, T, 0, 1, 1}, s);
+            down_gemv();
         }
     };
     if (sh) {
@@ -633,10 +637,17 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
     }
     if (shl) {
         qwq4::launch_router_logits_shgu(rr, T, E, *sh, s);
-        if (split && !(T <= 4 && qwq4::launch_route_shdown(ra, *sh, H, s))) {
-            qwq4::launch_route(ra, s);
-            shared_down();
-        } else if (!split && !sh1) {
+        // the shared expert's SwiGLU-down (folded) or SwiGLU rows ride in the
+        // routing launch where the shapes allow
+        if (split) {
+            if (fold_sh && qwq4::launch_route_shdown(ra, *sh, H, s)) {
+            } else if (!fold_sh && qwq4::launch_route_shgate(ra, *sh, sh_h, s)) {
+                down_gemv();
+            } else {
+                qwq4::launch_route(ra, s);
+                shared_down();
+            }
+        } else if (!sh1) {
             shared_down();
         }
     } else if (local) {

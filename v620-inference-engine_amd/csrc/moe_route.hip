@@ -726,6 +726,39 @@ bool launch_route_shdown(const RouteArgs &a, const ShExpertArgs &sh, int H, hipS
     return true;
 }
 
+// ---- 5 to 8 tokens with the shared expert: block 0 routes the batch (as in
+// route_shdown_kernel), blocks 1 .. form the shared expert's SwiGLU-gate rows
+// h [T][Fs] (as swiglu_gate_kernel, 512 elements per block) for the down GEMV
+// launch that follows.
+template <int PER>
+__global__ __launch_bounds__(8 * WAVE) void route_shgate_kernel(RouteArgs a, const float *v, int n, uint16_t *h) {
+    if (blockIdx.x == 0) {
+        ExpfGlibc ex;
+        ex.load(threadIdx.x % WAVE);
+        route_small_body<PER>(a, ex, [&](int t) {
+            const float *l = a.logits + int64_t(t) * a.E;
+            return [l](int i) { return l[i]; };
+        });
+    } else {
+        const int i = (int(blockIdx.x) - 1) * int(blockDim.x) + int(threadIdx.x);
+        if (i >= a.T * n) return;
+        const int t = i / n, j = i - t * n;
+        const float *r = v + int64_t(t) * (2 * n + 1);
+        h[i] = swiglu_h(r[j], r[n + j], sigmoid_gate(r[2 * n]));
+    }
+}
+
+bool launch_route_shgate(const RouteArgs &a, const ShExpertArgs &sh, uint16_t *h, hipStream_t s) {
+    if (a.T < 1 || a.T > 8 || a.E > 8 * WAVE || a.tile_m != 0) return false;
+    const int n = sh.Fs, per = (a.E + WAVE - 1) / WAVE;
+    const unsigned grid = unsigned(1 + (a.T * n + 8 * WAVE - 1) / (8 * WAVE));
+    if (per <= 1) route_shgate_kernel<1><<<grid, 8 * WAVE, 0, s>>>(a, sh.v, n, h);
+    else if (per <= 2) route_shgate_kernel<2><<<grid, 8 * WAVE, 0, s>>>(a, sh.v, n, h);
+    else if (per <= 4) route_shgate_kernel<4><<<grid, 8 * WAVE, 0, s>>>(a, sh.v, n, h);
+    else route_shgate_kernel<8><<<grid, 8 * WAVE, 0, s>>>(a, sh.v, n, h);
+    return true;
+}
+
 // out[t][j] = shared[t][j] + sum_i w[t][i] * yp[slot[t][i]][j], i in selection
 // order (src/kernels/moe_route.hip:168-185, 201-224). 4 columns per thread.
 // C consecutive groups of 4 elements of a yp row (fp32, or fp16 with YP16):

@@ -151,6 +151,10 @@ void launch_router_logits_shgu(const RouterArgs &r, int T, int E, const ShExpert
 // expert's SwiGLU-gate + down GEMV in one launch; false (nothing launched)
 // where the shapes do not allow it.
 bool launch_route_shdown(const RouteArgs &a, const ShExpertArgs &sh, int H, hipStream_t s);
+// Up to 8 tokens: the routing and the shared expert's SwiGLU-gate rows h
+// [T][Fs] (sh.v's gate, up and gate-logit columns, as launch_swiglu_gate) in
+// one launch; false (nothing launched) where the shapes do not allow it.
+bool launch_route_shgate(const RouteArgs &a, const ShExpertArgs &sh, uint16_t *h, hipStream_t s);
 size_t router_lds_bytes(int T, int kl, int E);
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
 // The fp32 router GEMV alone (logits, no routing and no hand-off), for the
