@@ -5,7 +5,8 @@ One decode layer: QKV projection, routing, gathered experts, combine and the
 down projection, the fused MoE block (router GEMV, routing, experts and the
 combine, whose cross-block counters must be left at zero by every call) at
 batches 4 and 1, the shared expert on tiled fp16 weights (SwiGLU x gate folded
-into the down GEMV, and as two launches), plus a prefill GEMM, captured once and replayed several times with the program's own eager work and synchronisations in between.
+into the down GEMV, and as two launches), the fused block with the shared
+expert merged into its launches at batches 4 and 1, plus a prefill GEMM, captured once and replayed several times with the program's own eager work and synchronisations in between.
 Every replay must reproduce the eager results bit for bit (all kernels are
 deterministic), and the eager results must match the oracle.
 """
@@ -61,11 +62,17 @@ def test_decode_layer_graph_replays(gpu, oracle):
     gu16 = (torch.randn((2 * SF + 1, H), generator=torch.Generator(device=gpu).manual_seed(72), device=gpu) * 0.05).half()
     dn16 = (torch.randn((H, SF), generator=torch.Generator(device=gpu).manual_seed(73), device=gpu) * 0.05).half()
     gu16t, dn16t = qwq4.w16_tile(gu16), qwq4.w16_tile(dn16)
-    xh = x.float().half()
+    xh = to_dev(xf.astype(np.float16), gpu)  # x's values as fp16 rows (x holds bf16 bits)
     v = torch.empty((M, 2 * SF + 1), dtype=torch.float32, device=gpu)
     hs16 = torch.empty((M, SF), dtype=torch.float16, device=gpu)
     sh = torch.empty((M, H), dtype=torch.float32, device=gpu)
     sh3 = torch.empty((M, H), dtype=torch.float32, device=gpu)
+    # the fused block with the shared expert (its GEMVs inside the block's
+    # router, routing and gate/up launches) at batches 4 and 1, fp16 rows
+    msb, msb1 = qwq4.MoeDecode(M, E, k, H, F, gpu, Fs=SF), qwq4.MoeDecode(1, E, k, H, F, gpu, Fs=SF)
+    msout = torch.empty((M, H), dtype=torch.float32, device=gpu)
+    msout1 = torch.empty((1, H), dtype=torch.float32, device=gpu)
+    xh1 = xh[:1].contiguous()
 
     def layer():
         qwq4.gemv(*dq, x, QKV, H, M, y=yq, y_bf16=True)
@@ -80,8 +87,13 @@ def test_decode_layer_graph_replays(gpu, oracle):
         qwq4.swiglu_gemv_w16_tiled(dn16t, H, v, SF, M, y=sh)
         qwq4.swiglu_gate(v, SF, h=hs16)
         qwq4.gemv_w16_tiled(dn16t, H, SF, hs16, M, y=sh3)
+        qwq4.moe_decode_with_shared(router_w, xh, k, eg, eu, ed, E, F, gu16t, dn16t, SF, buf=msb, out=msout,
+                                    out_bf16=False)
+        qwq4.moe_decode_with_shared(router_w, xh1, k, eg, eu, ed, E, F, gu16t, dn16t, SF, buf=msb1, out=msout1,
+                                    out_bf16=False)
 
-    outs = (yq, yd, out, Y, r.top_e, r.pair_tok, h, mout, mdb.logits, mdb.top_e, mout1, mdb1.top_e, v, hs16, sh, sh3)
+    outs = (yq, yd, out, Y, r.top_e, r.pair_tok, h, mout, mdb.logits, mdb.top_e, mout1, mdb1.top_e, v, hs16, sh, sh3,
+            msout, msb.sh_out, msb.top_e, msout1, msb1.sh_out, msb1.top_e)
     layer()
     torch.cuda.synchronize()
     eager = [o.clone() for o in outs]
@@ -98,6 +110,12 @@ def test_decode_layer_graph_replays(gpu, oracle):
     hsb = host(hs16.view(torch.int16)).view(np.uint16)
     assert rel_err(host(sh), oracle.linear_w16(host(dn16.view(torch.int16)).view(np.uint16),
                                                hsb.view(np.float16).astype(np.float32), True)) <= TOL
+
+    xhf = xf.astype(np.float16).astype(np.float32)
+    assert torch.equal(msb.sh_out.view(torch.uint8), sh.view(torch.uint8))
+    assert rel_err(host(msout), oracle.moe(xhf, host(msb.logits), k, *ex) + host(sh)) <= TOL
+    assert rel_err(host(msb1.sh_out), host(sh)[:1]) <= TOL
+    assert rel_err(host(msout1), oracle.moe(xhf[:1], host(msb1.logits), k, *ex) + host(msb1.sh_out)) <= TOL
 
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
