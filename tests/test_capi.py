@@ -94,6 +94,15 @@ def test_abi_version():
     lambda L: L.qw_moe_decode(ctypes.c_void_p(256), 2, ctypes.c_void_p(256), 0, 4, 256, 8,
                               *([ctypes.c_void_p(256)] * 9), 4096, 1536, None, ctypes.c_void_p(256), 0,
                               *([ctypes.c_void_p(256)] * 6), 1, ctypes.c_void_p(256), 1 << 30, None),  # router_f16 2
+    lambda L: L.qw_moe_decode_with_shared(ctypes.c_void_p(256), 1, ctypes.c_void_p(256), 1, 1, 256, 8, *([ctypes.c_void_p(256)] * 9), 4096, 1536,
+                                          None, ctypes.c_void_p(256), 1536, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 2,
+                                          *([ctypes.c_void_p(256)] * 6), 1, ctypes.c_void_p(256), 1 << 30, None),  # null sh_gu
+    lambda L: L.qw_moe_decode_with_shared(ctypes.c_void_p(256), 1, ctypes.c_void_p(256), 1, 1, 256, 8, *([ctypes.c_void_p(256)] * 9), 4096, 1536,
+                                          ctypes.c_void_p(256), ctypes.c_void_p(256), 1544, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 2,
+                                          *([ctypes.c_void_p(256)] * 6), 1, ctypes.c_void_p(256), 1 << 30, None),  # Fs % 32
+    lambda L: L.qw_moe_decode_with_shared(ctypes.c_void_p(256), 1, ctypes.c_void_p(256), 1, 1, 256, 8, *([ctypes.c_void_p(256)] * 9), 4096, 1536,
+                                          ctypes.c_void_p(256), ctypes.c_void_p(256), 1536, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 2,
+                                          *([ctypes.c_void_p(256)] * 6), 1, ctypes.c_void_p(256), 4096, None),  # workspace too small
 ])
 def test_bad_arguments_are_rejected(call):
     L = qwq4.lib()
