@@ -302,3 +302,53 @@ def test_moe_decode_with_shared(gpu, oracle, T, E, H, F, k, SF, f16):
     assert np.array_equal(host(out).view(np.uint32), host(o2).view(np.uint32))
     ref = oracle.moe(xf, host(buf.logits), k, *ex) + oracle.shared_expert(xf, gu_b, dn_b, f16_gu=f16, f16_down=True)
     assert rel_err(host(out), ref) <= TOL
+
+
+def _random_block(n, seed):
+    """Seeded (T, E, H, F, k, Fs, f16, zeros) within the decode block's limits and a
+    few hundred MB of host experts: every router, routing and shared-expert path
+    (merged at T = 1, routing launch at 2-4 and 5-8, own launches above 8 or for Fs
+    not a multiple of 256)."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        T = int(r.choice([1, 1, 2, 3, 4, 5, 6, 8, 12, 16]))
+        E = int(r.choice([8, 16, 48, 64, 128, 256]))
+        H = int(r.choice([512, 768, 1024, 1536, 2048, 3072, 4096]))
+        F = int(r.choice([128, 256, 384, 512, 768, 1536]))
+        if E * F * H > 256 * 1536 * 1024:
+            continue
+        k = int(r.integers(1, min(8, E) + 1))
+        Fs = int(r.choice([256, 512, 1024, 1536, 32 * int(r.integers(1, 49))]))
+        out.append((T, E, H, F, k, Fs, bool(r.integers(0, 2)), bool(r.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("T,E,H,F,k,SF,f16,zeros", _random_block(12, 2036))
+def test_moe_decode_with_shared_random_shapes(gpu, T, E, H, F, k, SF, f16, zeros):
+    """qw_moe_decode_with_shared over seeded random shapes against its parts as
+    separate calls (shared gate/up GEMV, SwiGLU-down GEMV, then qw_moe_decode with
+    their output as the shared rows): routing, shared rows and output bit for bit."""
+    print(f"moe decode with shared random T={T} E={E} H={H} F={F} k={k} Fs={SF} f16={f16} zeros={zeros}", flush=True)
+    ex = synth.experts(3000 + T + E, E, H, F, zeros=zeros)
+    xb, _ = rows(3001, f"rx{T}x{H}", T, H, f16)
+    Wr = (np.random.default_rng(3002 + E).standard_normal((E, H)) * 0.05).astype(np.float32)
+    gu_b, _ = w16(3003, f"rgu{SF}x{H}", 2 * SF + 1, H, f16)
+    dn_b, _ = w16(3004, f"rdn{H}x{SF}", H, SF, True)
+    from test_moe_gpu import _experts_dev
+    (g, u, d), _, _ = _experts_dev(gpu, ex)
+    gut, dnt = qwq4.w16_tile(to_dev(gu_b, gpu)), qwq4.w16_tile(to_dev(dn_b, gpu))
+    dx, dr = to_dev(xb, gpu), to_dev(Wr, gpu)
+    out, buf, sv, so = qwq4.moe_decode_with_shared(dr, dx, k, g, u, d, E, F, gut, dnt, SF, out_bf16=False,
+                                                   x_f16=f16, yp_f16=True)
+    v = qwq4.gemv_w16_tiled(gut, 2 * SF + 1, H, dx, T, f16=f16)
+    if T <= 4:
+        sh = qwq4.swiglu_gemv_w16_tiled(dnt, H, v, SF, T)
+    else:
+        sh = qwq4.gemv_w16_tiled(dnt, H, SF, qwq4.swiglu_gate(v, SF), T)
+    o2, b2 = qwq4.moe_decode(dr, dx, k, g, u, d, E, F, shared=sh, out_bf16=False, x_f16=f16, yp_f16=True)
+    assert np.array_equal(host(buf.top_e), host(b2.top_e))
+    assert np.array_equal(host(buf.top_w).view(np.uint32), host(b2.top_w).view(np.uint32))
+    assert np.array_equal(host(sv).view(np.uint32), host(v).view(np.uint32))
+    assert np.array_equal(host(so).view(np.uint32), host(sh).view(np.uint32))
+    assert np.array_equal(host(out).view(np.uint32), host(o2).view(np.uint32))
