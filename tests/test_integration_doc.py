@@ -26,7 +26,7 @@ def blocks(lang):
 # bf16 flag) fails to compile here.
 ENGINE_CALLS = r"""
 struct Batch {  // Rank::Batch's fields used here; top_e, active, n_active are the integration's additions
-    float *X, *hc_send, *router, *tok_w, *sh_out, *out_moe, *proj, *logits;
+    float *X, *hc_send, *router, *tok_w, *shp, *sh_out, *out_moe, *proj, *logits;
     uint16_t *y, *bin, *moe_h, *yp, *sh_h;
     int32_t *counts, *offsets, *tok_slot, *pair_tok, *top_e, *active, *n_active;
 };
@@ -61,7 +61,7 @@ void engine_calls(Batch &b, PrefillBuf &p, rocblas_handle blas, hipStream_t s, c
     qw::gpu::moe_combine_B(b.yp, b.tok_slot, b.tok_w, b.proj, M, sh, b.out_moe, s);
     qw::gpu::moe_block_B(router_w, b.bin, M, g, u, d, sh, b.proj, b.out_moe, b.logits, b.top_e, b.tok_w, b.tok_slot,
                          b.moe_h, b.yp, ws, ws_bytes, s);
-    qw::gpu::moe_block_shared_B(router_w, b.bin, M, g, u, d, sh, sh_gu, sh_down, b.router, b.sh_out, b.out_moe,
+    qw::gpu::moe_block_shared_B(router_w, b.bin, M, g, u, d, sh, sh_gu, sh_down, b.shp, b.sh_out, b.out_moe,
                                 b.logits, b.top_e, b.tok_w, b.tok_slot, b.moe_h, b.yp, ws, ws_bytes, s);
     // prefill.hip:324-339: router GEMM (fp32 out), experts, shared expert (fp16 out), combine
     qw::gpu::gemm(blas, wq, p.bin, sh.H, T, p.logits, sh.E, false);
