@@ -640,12 +640,13 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
         // the shared expert's SwiGLU-down (folded) or SwiGLU rows ride in the
         // routing launch where the shapes allow
         if (split) {
-            if (fold_sh && qwq4::launch_route_shdown(ra, *sh, H, s)) {
-            } else if (!fold_sh && qwq4::launch_route_shgate(ra, *sh, sh_h, s)) {
-                down_gemv();
-            } else {
+            const bool rode = fold_sh ? qwq4::launch_route_shdown(ra, *sh, H, s)
+                                      : qwq4::launch_route_shgate(ra, *sh, sh_h, s);
+            if (!rode) {
                 qwq4::launch_route(ra, s);
                 shared_down();
+            } else if (!fold_sh) {
+                down_gemv();
             }
         } else if (!sh1) {
             shared_down();
