@@ -552,75 +552,6 @@ __global__ __launch_bounds__(1024) void moe_down_t1_kernel(const uint32_t *dw, c
     }
 }
 
-// Batch 2 with the combine (T = 2, k <= 8, the down K split in 2): at most
-// 16 experts are active, so block b holds output rows 16 b .. 16 b + 15 of all
-// of them, one wave per expert over its 1 or 2 slots. The wave computes both
-// K halves of the general kernel's split into two accumulators and adds them
-// as its reduction does (same values, bit for bit); the block then forms both
-// tokens' outputs in the combine's order. yp is still written.
-template <int GW, bool HAS_Z, bool CH4, bool YP16>
-__global__ __launch_bounds__(1024) void moe_down_t2_kernel(const uint32_t *dw, const uint16_t *ds, const uint16_t *dz,
-                                                           const int32_t *__restrict__ offsets,
-                                                           const int32_t *__restrict__ active,
-                                                           const int32_t *__restrict__ n_active,
-                                                           const uint16_t *__restrict__ h, int E, int H, int F,
-                                                           void *__restrict__ yp, CombineArgs c, int topk) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    const int tid = threadIdx.x, y = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
-              n = lane % 16;
-    const int P = 2 * topk;  // slots (pairs) of the two tokens
-    // h rows of every slot and the shared rows first (as in the batch-1 kernel)
-    uint4 *xl = reinterpret_cast<uint4 *>(smem);
-    stage_rows_issue([&](int m) { return h + int64_t(m) * F; }, P, F, xl);
-    const float shv = c.shared && tid < 32 ? c.shared[int64_t(tid / 16) * H + blockIdx.x * 16 + tid % 16] : 0.f;
-    __builtin_amdgcn_sched_barrier(0);
-    const int na = ld_uniform(n_active, 0), ea = ld_uniform(active, min(y, E - 1));  // (as in the batch-1 kernel)
-    const bool live = y < min(na, 16);  // wave-uniform
-    const int e = live ? min(max(ea, 0), E - 1) : 0;
-    const int G = F / QGROUP, gpk = G / 2, hsub = H / 16, kc = x_row_stride(F);
-    const Q4Tile t(dw, ds, dz, int64_t(e) * hsub + blockIdx.x, G);
-    WaveRange<GW, HAS_Z, CH4> wr0, wr1;
-    wr0.fetch(t, 0, gpk, opaque_lane());
-    wr1.fetch(t, gpk, gpk, opaque_lane());
-    const int base = ld_uniform(offsets, e), M = ld_uniform(offsets, e + 1) - base;
-    int slot_q[16];
-    float w_q[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        slot_q[i] = i < P ? ld_uniform(c.tok_slot, i) : 0;
-        w_q[i] = i < P ? ld_uniform_f32(c.tok_w, i) : 0.f;
-    }
-    float *yb = reinterpret_cast<float *>(xl + x_pieces(16, F));  // [16 slots][16 rows]
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vm_below<2 * WaveRange<GW, HAS_Z, CH4>::LOADS>();
-    __builtin_amdgcn_s_barrier();
-    if (live) {
-        const uint4 *xr = xl + (base + min(n, max(M, 1) - 1)) * kc + q * 4;
-        f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
-        compute_zq_inline<F16>(wr0, xr, a0);
-        compute_zq_inline<F16>(wr1, xr, a1);
-        a0 += a1;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 4 * q + r;
-            if (m < M) {
-                yb[(base + m) * 16 + n] = yp_value<YP16>(a0[r]);
-                store_yp<YP16>(yp, int64_t(base + m) * H + blockIdx.x * 16 + n, a0[r]);
-            }
-        }
-    }
-    __syncthreads();
-    if (tid < 32) {
-        const int tk = tid / 16, row = tid % 16, j = blockIdx.x * 16 + row;
-        float v = 0.f;
-        if (c.shared) v = shv;
-#pragma unroll
-        for (int qq = 0; qq < 8; ++qq)
-            if (qq < topk) v += w_q[tk * topk + qq] * yb[slot_q[tk * topk + qq] * 16 + row];
-        store_out(c, int64_t(tk) * H + j, v);
-    }
-}
-
 // K split: the largest power of two <= kmax dividing G with at most 16 groups
 // per wave; GW: the register budget for a wave's groups.
 static int pick_ks(int G, int kmax) {
@@ -766,16 +697,6 @@ static void launch_down_c(const MoeGemvArgs &a, int max_active, int R, hipStream
             moe_down_t1_kernel<GW, HAS_Z, CH4, YP16><<<unsigned(a.H / 16), 1024, lds, s>>>(
                 a.dw, a.ds, a.dz, a.active, a.n_active, a.h, a.E, a.H, a.F, a.yp, *a.cmb, a.topk);
             return;
-        }
-        if constexpr (GW <= 6) {  // two ranges of 8 groups would spill at 1024 threads
-            if (a.T == 2 && a.topk <= 8) {
-                auto kern = moe_down_t2_kernel<GW, HAS_Z, CH4, YP16>;
-                const size_t lds = size_t(x_pieces(16, a.F)) * 16 + 16 * 16 * 4;
-                if (lds > 64 * 1024) raise_lds_limit(reinterpret_cast<const void *>(kern));
-                kern<<<unsigned(a.H / 16), 1024, lds, s>>>(a.dw, a.ds, a.dz, a.offsets, a.active, a.n_active, a.h,
-                                                           a.E, a.H, a.F, a.yp, *a.cmb, a.topk);
-                return;
-            }
         }
     }
     auto kern = a.T <= R ? moe_down_gemv_kernel<KS, GW, HAS_Z, CH4, CMB, false, YP16>
