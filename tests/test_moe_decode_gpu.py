@@ -30,8 +30,8 @@ def _case(gpu, seed, T, E, H, F, k, with_shared, zeros=True):
                                                    (32, 32, 512, 384, 6, True, True), (8, 256, 4096, 1536, 8, True, True),
                                                    (3, 64, 1024, 512, 4, False, False),
                                                    (16, 64, 2048, 1536, 6, True, True),
-                                                   # config 3's full size at batches 1, 4 (combine folded
-                                                   # into the down projection) and 32 (separate combine)
+                                                   # config 3's full size at batches 1, 2 (combine folded
+                                                   # into the down projection), 4, 16 and 32 (separate combine)
                                                    (1, 256, 4096, 1536, 8, True, True),
                                                    (2, 256, 4096, 1536, 8, True, False),
                                                    (4, 256, 4096, 1536, 8, False, False),
@@ -74,8 +74,8 @@ def test_moe_decode_matches_unfused_path(gpu, T, E, H, F, k, yp16):
     """The block against routing + experts + combine as separate calls, with
     fp32 and fp16 yp (the combine then adds the fp16 values): yp and out
     bit-identical, on both sides of the switch that folds the combine into
-    the down projection (up to 4 tokens; batches 1 and 2 in one block per 16
-    output rows), with experts chosen by both tokens (E = 16, k = 8; E = 8, k = 8:
+    the down projection (up to 2 tokens; batch 1 in one block per 16 output
+    rows), with experts chosen by both tokens (E = 16, k = 8; E = 8, k = 8:
     every expert twice), fewer experts than the kernels' waves (E = 4), and at
     config 3's full size (down projection with 6 groups per wave), and batch 1
     at H 2048 / 4096 with down K halves of 2 to 8 groups and E up to 512 (the
@@ -96,7 +96,7 @@ def test_moe_decode_matches_unfused_path(gpu, T, E, H, F, k, yp16):
 def test_moe_decode_f16_out(gpu, T):
     """fp16 output rows (QW_T_F16): the fp32 output of the same call rounded
     to nearest even, bit for bit, with the combine folded into the down
-    projection (T <= 4) and as its own launch (T = 8)."""
+    projection (T <= 2) and as its own launch (T = 4, 8)."""
     import torch
     E, H, F, k = 64, 1024, 256, 4
     ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 130 + T, T, E, H, F, k, True)

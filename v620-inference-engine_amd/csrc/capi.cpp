@@ -660,10 +660,10 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
     } else {
         qwq4::launch_router_route(ra, rr, s);
     }
-    // up to 4 tokens the combine runs in the down projection's last blocks
-    // (one launch less); from there on its own launch is faster than the
+    // up to 2 tokens the combine runs in the down projection's last blocks
+    // (one launch less); from 3 tokens on its own launch is faster than the
     // serial tail it adds to those blocks
-    const bool fold = T <= 4;
+    const bool fold = T <= 2;
     const qwq4::CombineArgs cmb{at(L.dcounters), tok_slot, top_w, shared, out, out_type};
     qwq4::MoeGemvArgs a{gw, gs, gz, uw, us, uz, dw, ds, dz, E, H, F, at(L.offsets), at(L.active), at(L.n_active),
                         at(L.pair_tok), x, T, topk, h, yp, fold ? &cmb : nullptr};
