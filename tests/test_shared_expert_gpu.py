@@ -265,12 +265,18 @@ def test_w16_swiglu_gemv_tiled_random_shapes(gpu, N, n, M):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("T,E,H,F,k,SF,f16", [(1, 256, 4096, 1536, 8, 1536, True), (1, 64, 2048, 512, 6, 512, False),
-                                              (1, 64, 1024, 256, 4, 320, True), (2, 256, 4096, 1536, 8, 1536, True),
-                                              (4, 64, 1024, 256, 4, 512, False), (8, 64, 2048, 512, 6, 1536, True),
-                                              (3, 256, 4096, 1536, 8, 1536, False),
-                                              (8, 256, 4096, 1536, 8, 1536, False)])
-def test_moe_decode_with_shared(gpu, oracle, T, E, H, F, k, SF, f16):
+@pytest.mark.parametrize("T,E,H,F,k,SF,f16,zeros", [(1, 256, 4096, 1536, 8, 1536, True, False),
+                                                    (1, 64, 2048, 512, 6, 512, False, False),
+                                                    (1, 64, 1024, 256, 4, 320, True, False),
+                                                    (2, 256, 4096, 1536, 8, 1536, True, False),
+                                                    (4, 64, 1024, 256, 4, 512, False, False),
+                                                    (8, 64, 2048, 512, 6, 1536, True, False),
+                                                    (3, 256, 4096, 1536, 8, 1536, False, False),
+                                                    (8, 256, 4096, 1536, 8, 1536, False, False),
+                                                    (5, 128, 4096, 512, 6, 1024, True, True),
+                                                    (6, 64, 4096, 256, 8, 512, False, False),
+                                                    (7, 32, 4096, 256, 8, 1536, True, False)])
+def test_moe_decode_with_shared(gpu, oracle, T, E, H, F, k, SF, f16, zeros):
     """qw_moe_decode_with_shared against its parts as separate calls (the
     shared expert's tiled gate/up/gate-logit GEMV and SwiGLU-down GEMV, then
     qw_moe_decode with their output as the shared rows): the shared rows, the
@@ -279,11 +285,13 @@ def test_moe_decode_with_shared(gpu, oracle, T, E, H, F, k, SF, f16):
     launch (batches 1-8: one, two and four rows per MFMA pass, every staging
     width up to the looped one at 8 rows of 4096), the down GEMV at batch 1
     inside the routed gate/up launch and at batches 2-4 inside the routing
-    launch, and at batch 8 the routing launch forms the SwiGLU rows (fp16 rows
-    and weights at config 3's size, bf16 at H 2048 and at batches 3 and 8);
+    launch, and at batches 5-8 the routing launch forms the SwiGLU rows and, at
+    H 4096, the down GEMV over them rides in the gate/up launch (experts with
+    more than the 4 staged rows at batches 5-7; zero points at 5) (fp16 rows
+    and weights at config 3's size, bf16 at H 2048 and at batches 3, 6 and 8);
     Fs = 320 takes their own launches."""
-    print(f"moe decode with shared T={T} E={E} H={H} F={F} k={k} Fs={SF} f16={f16}", flush=True)
-    ex = synth.experts(95 + T, E, H, F, zeros=False)
+    print(f"moe decode with shared T={T} E={E} H={H} F={F} k={k} Fs={SF} f16={f16} zeros={zeros}", flush=True)
+    ex = synth.experts(95 + T, E, H, F, zeros=zeros)
     xb, xf = rows(96, f"sx{T}x{H}", T, H, f16)
     Wr = (np.random.default_rng(97 + T).standard_normal((E, H)) * 0.05).astype(np.float32)
     gu_b, _ = w16(98, f"sgu{SF}x{H}", 2 * SF + 1, H, f16)

@@ -635,10 +635,12 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
         if (!shl) shared_down();
         shared = sh->out;
     }
+    bool down_pending = false;  // the shared expert's down GEMV over sh_h still to launch
     if (shl) {
         qwq4::launch_router_logits_shgu(rr, T, E, *sh, s);
         // the shared expert's SwiGLU-down (folded) or SwiGLU rows ride in the
-        // routing launch where the shapes allow
+        // routing launch where the shapes allow (the down GEMV over the
+        // SwiGLU rows then rides in the gate/up launch below)
         if (split) {
             const bool rode = fold_sh ? qwq4::launch_route_shdown(ra, *sh, H, s)
                                       : qwq4::launch_route_shgate(ra, *sh, sh_h, s);
@@ -646,7 +648,7 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
                 qwq4::launch_route(ra, s);
                 shared_down();
             } else if (!fold_sh) {
-                down_gemv();
+                down_pending = true;
             }
         } else if (!sh1) {
             shared_down();
@@ -678,6 +680,13 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
     if (sh1) {
         if (!qwq4::launch_gate_up_routed_shdown(a, *sh, s)) {
             shared_down();
+            qwq4::launch_moe_gemv(a, s);
+        } else {
+            qwq4::launch_moe_down(a, s);
+        }
+    } else if (down_pending) {
+        if (!qwq4::launch_gate_up_shdown(a, *sh, sh_h, s)) {
+            down_gemv();
             qwq4::launch_moe_gemv(a, s);
         } else {
             qwq4::launch_moe_down(a, s);

@@ -78,26 +78,33 @@ __device__ __forceinline__ float ld_uniform_f32(const float *p, int i) {
 
 // Reads the block's expert: n_active and active[y] are requested together
 // (one latency), and the weight loads need only e.
-__device__ __forceinline__ int block_expert(const int32_t *n_active, const int32_t *active, int E) {
-    const int na = ld_uniform(n_active, 0), e = ld_uniform(active, blockIdx.y);
-    return int(blockIdx.y) < na ? min(max(e, 0), E - 1) : -1;
+// (by: the block's active-expert rank)
+__device__ __forceinline__ int block_expert_at(const int32_t *n_active, const int32_t *active, int E, int by) {
+    const int na = ld_uniform(n_active, 0), e = ld_uniform(active, by);
+    return by < na ? min(max(e, 0), E - 1) : -1;
 }
 
+__device__ __forceinline__ int block_expert(const int32_t *n_active, const int32_t *active, int E) {
+    return block_expert_at(n_active, active, E, int(blockIdx.y));
+}
+
+// (bx, by): the block's column block and active-expert rank (arguments, so
+// that a kernel running other work in the same grid can call it)
 template <typename XT, int KS, int GW, bool HAS_Z, bool CH4, bool MULTI>
-__global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
+__device__ __forceinline__ void moe_gate_up_gemv_block(
     const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
     const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
     const int32_t *__restrict__ n_active, const int32_t *__restrict__ pair_tok, const uint16_t *__restrict__ x, int E,
-    int H, int F, int R, uint16_t *__restrict__ h) {
+    int H, int F, int R, uint16_t *__restrict__ h, int bx, int by) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int e = block_expert(n_active, active, E);
+    const int e = block_expert_at(n_active, active, E, by);
     if (e < 0) return;
     constexpr int SUB = 8 / (2 * KS);
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE, q = lane / 16,
               n = lane % 16;
     const int sl = wave / (2 * KS), mat = (wave / KS) % 2, kp = wave % KS;
     const int G = H / QGROUP, gpk = G / KS, fsub = F / 16, kc = x_row_stride(H);
-    const int lsub = blockIdx.x * SUB + sl;
+    const int lsub = bx * SUB + sl;
     const int64_t sub = int64_t(e) * fsub + min(lsub, fsub - 1);
     const Q4Tile t = mat ? Q4Tile(uw, us, uz, sub, G) : Q4Tile(gw, gs, gz, sub, G);
     // the first chunk's weights go out before the slot range is known (an
@@ -152,6 +159,16 @@ __global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
             chunk(m0);
         }
     }
+}
+
+template <typename XT, int KS, int GW, bool HAS_Z, bool CH4, bool MULTI>
+__global__ __launch_bounds__(512) void moe_gate_up_gemv_kernel(
+    const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
+    const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
+    const int32_t *__restrict__ n_active, const int32_t *__restrict__ pair_tok, const uint16_t *__restrict__ x, int E,
+    int H, int F, int R, uint16_t *__restrict__ h) {
+    moe_gate_up_gemv_block<XT, KS, GW, HAS_Z, CH4, MULTI>(gw, gs, gz, uw, us, uz, offsets, active, n_active, pair_tok,
+                                                          x, E, H, F, R, h, int(blockIdx.x), int(blockIdx.y));
 }
 
 // Batches of up to 4 tokens: every token row goes to LDS first (row t at
@@ -650,6 +667,78 @@ bool launch_gate_up_routed_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, 
     };
     if (a.x_f16) by_gw(F16{});
     else by_gw(BF16{});
+    return true;
+}
+
+// ---- 5 to 8 tokens with the shared expert: grid rows y < max_active run the
+// gate/up GEMV of the y-th active expert (as moe_gate_up_gemv_kernel with
+// the K split in 4 over whole 4-group chunks, 8 groups per wave), the rows
+// after them the shared expert's down GEMV over its SwiGLU rows sh_h (as
+// qw_w16_gemv_tiled, 16 output rows per block). The two read different
+// inputs of earlier launches (the routing, sh_h) and write different outputs.
+template <typename XT, bool HAS_Z, bool MULTI, int SMR, int SXPT, int SWS>
+__global__ __launch_bounds__(512) void gate_up_shdown_gemv_kernel(
+    const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
+    const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
+    const int32_t *__restrict__ n_active, const int32_t *__restrict__ pair_tok, const uint16_t *__restrict__ x, int E,
+    int H, int F, int R, uint16_t *__restrict__ h, int max_active, ShExpertArgs sh, const uint16_t *sh_h, int T) {
+    const int by = int(blockIdx.y);
+    if (by < max_active) {
+        moe_gate_up_gemv_block<XT, 4, 8, HAS_Z, true, MULTI>(gw, gs, gz, uw, us, uz, offsets, active, n_active,
+                                                             pair_tok, x, E, H, F, R, h, int(blockIdx.x), by);
+    } else {
+        const int i = (by - max_active) * int(gridDim.x) + int(blockIdx.x);
+        if (i < (H + 15) / 16)
+            w16_gemv_block<F16, 1, SMR, SXPT, SWS, true>(sh.down, 0, sh_h, sh.Fs, T, sh.Fs, H, sh.out, H, 0, 0, 0, i);
+    }
+}
+
+bool launch_gate_up_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, const uint16_t *sh_h, hipStream_t s) {
+    const int G = a.H / QGROUP;
+    if (a.route_logits || a.T < 5 || a.T > 8 || G % 4 != 0 || pick_ks(G, 4) != 4 || G / 4 != 8 ||
+        sh.Fs % 256 != 0 || (a.gz != nullptr) != (a.uz != nullptr) || !w16_fits(a.T, sh.Fs, a.H))
+        return false;
+    // the gate/up launch's shape (launch_one, launch_gate_up): rows per chunk
+    // as many as keep the staged activations within 32 KB
+    int R = a.T < 16 ? a.T : 16;
+    while (R > 1 && size_t(R) * a.H * 2 > 32 * 1024) --R;
+    const int max_active = a.T * a.topk < a.E ? a.T * a.topk : a.E, gx = a.F / 16;
+    const int shb = (a.H + 15) / 16, rows = (shb + gx - 1) / gx;
+    const size_t l1 = moe_lds_bytes(R, a.H), l2 = dense_lds_bytes(a.T, sh.Fs, 1, W16_MAX_KS, W16_MAX_KS);
+    const size_t lds = l1 > l2 ? l1 : l2;
+    const dim3 grid(unsigned(gx), unsigned(max_active + rows));
+    // the down GEMV's template shape as qw_w16_gemv_tiled picks it for T rows
+    // of K = Fs (8 waves: Fs / 32 >= 8)
+    const int xpt = (a.T * (sh.Fs / 8) + 8 * WAVE - 1) / (8 * WAVE);
+    const bool ws16 = (sh.Fs / 32 + W16_MAX_KS - 1) / W16_MAX_KS > 8;
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024) raise_lds_limit(reinterpret_cast<const void *>(kern));
+        kern<<<grid, 512, lds, s>>>(a.gw, a.gs, a.gz, a.uw, a.us, a.uz, a.offsets, a.active, a.n_active, a.pair_tok,
+                                    a.x, a.E, a.H, a.F, R, a.h, max_active, sh, sh_h, a.T);
+    };
+    auto by_ws = [&](auto xt, auto hz, auto mu, auto sxpt) {
+        using XT = decltype(xt);
+        constexpr bool HZ = decltype(hz)::value, MU = decltype(mu)::value;
+        constexpr int SXPT = decltype(sxpt)::value;
+        if (ws16) go(gate_up_shdown_gemv_kernel<XT, HZ, MU, 4, SXPT, 16>);
+        else go(gate_up_shdown_gemv_kernel<XT, HZ, MU, 4, SXPT, 8>);
+    };
+    auto by_xpt = [&](auto xt, auto hz, auto mu) {
+        if (xpt <= 1) by_ws(xt, hz, mu, std::integral_constant<int, 1>());
+        else if (xpt <= 2) by_ws(xt, hz, mu, std::integral_constant<int, 2>());
+        else if (xpt <= 4) by_ws(xt, hz, mu, std::integral_constant<int, 4>());
+        else by_ws(xt, hz, mu, std::integral_constant<int, 0>());
+    };
+    auto by_multi = [&](auto xt, auto hz) {
+        if (a.T <= R) by_xpt(xt, hz, std::false_type());
+        else by_xpt(xt, hz, std::true_type());
+    };
+    auto by_z = [&](auto xt) {
+        if (a.gz) by_multi(xt, std::true_type());
+        else by_multi(xt, std::false_type());
+    };
+    if (a.x_f16) by_z(F16{});
+    else by_z(BF16{});
     return true;
 }
 

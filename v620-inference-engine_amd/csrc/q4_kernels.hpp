@@ -95,6 +95,10 @@ void launch_moe_down(const MoeGemvArgs &a, hipStream_t s);
 // GEMV in the same launch; false (nothing launched) where the shapes do not
 // fit that launch.
 bool launch_gate_up_routed_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, hipStream_t s);
+// 5 to 8 tokens: the gate/up GEMV (as launch_moe_gemv's) and the shared
+// expert's down GEMV over its SwiGLU rows sh_h [T][Fs] in one launch; false
+// (nothing launched) where the shapes do not allow it.
+bool launch_gate_up_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, const uint16_t *sh_h, hipStream_t s);
 // Whether the expert GEMVs take these sizes (a wave holds <= 16 groups of its K range).
 bool moe_gemv_supported(int H, int F);
 
