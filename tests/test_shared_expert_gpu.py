@@ -286,7 +286,7 @@ def test_moe_decode_with_shared(gpu, oracle, T, E, H, F, k, SF, f16, zeros):
     width up to the looped one at 8 rows of 4096), the down GEMV at batch 1
     inside the routed gate/up launch and at batches 2-4 inside the routing
     launch, and at batches 5-8 the routing launch forms the SwiGLU rows and, at
-    H 4096, the down GEMV over them rides in the gate/up launch (experts with
+    H 2048 and 4096, the down GEMV over them rides in the gate/up launch (experts with
     more than the 4 staged rows at batches 5-7; zero points at 5) (fp16 rows
     and weights at config 3's size, bf16 at H 2048 and at batches 3, 6 and 8);
     Fs = 320 takes their own launches."""

@@ -672,11 +672,11 @@ bool launch_gate_up_routed_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, 
 
 // ---- 5 to 8 tokens with the shared expert: grid rows y < max_active run the
 // gate/up GEMV of the y-th active expert (as moe_gate_up_gemv_kernel with
-// the K split in 4 over whole 4-group chunks, 8 groups per wave), the rows
+// the K split in 4 over whole 4-group chunks, GW = 4 or 8 groups per wave), the rows
 // after them the shared expert's down GEMV over its SwiGLU rows sh_h (as
 // qw_w16_gemv_tiled, 16 output rows per block). The two read different
 // inputs of earlier launches (the routing, sh_h) and write different outputs.
-template <typename XT, bool HAS_Z, bool MULTI, int SMR, int SXPT, int SWS>
+template <typename XT, int GW, bool HAS_Z, bool MULTI, int SMR, int SXPT, int SWS>
 __global__ __launch_bounds__(512) void gate_up_shdown_gemv_kernel(
     const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
     const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
@@ -684,8 +684,8 @@ __global__ __launch_bounds__(512) void gate_up_shdown_gemv_kernel(
     int H, int F, int R, uint16_t *__restrict__ h, int max_active, ShExpertArgs sh, const uint16_t *sh_h, int T) {
     const int by = int(blockIdx.y);
     if (by < max_active) {
-        moe_gate_up_gemv_block<XT, 4, 8, HAS_Z, true, MULTI>(gw, gs, gz, uw, us, uz, offsets, active, n_active,
-                                                             pair_tok, x, E, H, F, R, h, int(blockIdx.x), by);
+        moe_gate_up_gemv_block<XT, 4, GW, HAS_Z, true, MULTI>(gw, gs, gz, uw, us, uz, offsets, active, n_active,
+                                                              pair_tok, x, E, H, F, R, h, int(blockIdx.x), by);
     } else {
         const int i = (by - max_active) * int(gridDim.x) + int(blockIdx.x);
         if (i < (H + 15) / 16)
@@ -695,7 +695,9 @@ __global__ __launch_bounds__(512) void gate_up_shdown_gemv_kernel(
 
 bool launch_gate_up_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, const uint16_t *sh_h, hipStream_t s) {
     const int G = a.H / QGROUP;
-    if (a.route_logits || a.T < 5 || a.T > 8 || G % 4 != 0 || pick_ks(G, 4) != 4 || G / 4 != 8 ||
+    // the gate/up shapes of launch_gw with the K split in 4: 4 or 8 groups per
+    // wave, whole 4-group chunks (H 2048 and 4096)
+    if (a.route_logits || a.T < 5 || a.T > 8 || pick_ks(G, 4) != 4 || (G / 4 != 4 && G / 4 != 8) ||
         sh.Fs % 256 != 0 || (a.gz != nullptr) != (a.uz != nullptr) || !w16_fits(a.T, sh.Fs, a.H))
         return false;
     // the gate/up launch's shape (launch_one, launch_gate_up): rows per chunk
@@ -720,8 +722,13 @@ bool launch_gate_up_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, const u
         using XT = decltype(xt);
         constexpr bool HZ = decltype(hz)::value, MU = decltype(mu)::value;
         constexpr int SXPT = decltype(sxpt)::value;
-        if (ws16) go(gate_up_shdown_gemv_kernel<XT, HZ, MU, 4, SXPT, 16>);
-        else go(gate_up_shdown_gemv_kernel<XT, HZ, MU, 4, SXPT, 8>);
+        if (G / 4 == 4) {
+            if (ws16) go(gate_up_shdown_gemv_kernel<XT, 4, HZ, MU, 4, SXPT, 16>);
+            else go(gate_up_shdown_gemv_kernel<XT, 4, HZ, MU, 4, SXPT, 8>);
+        } else {
+            if (ws16) go(gate_up_shdown_gemv_kernel<XT, 8, HZ, MU, 4, SXPT, 16>);
+            else go(gate_up_shdown_gemv_kernel<XT, 8, HZ, MU, 4, SXPT, 8>);
+        }
     };
     auto by_xpt = [&](auto xt, auto hz, auto mu) {
         if (xpt <= 1) by_ws(xt, hz, mu, std::integral_constant<int, 1>());
