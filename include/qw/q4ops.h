@@ -334,7 +334,9 @@ int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, 
  *   out[t] = shared[t] + sum_i top_w[t][i] * yp[tok_slot[t][i]]   (out_type)
  * Launches: at T = 1 the router writes the logits and the gate/up blocks
  * route; at T = 2..8 the logits launch is followed by the routing launch;
- * above 8 tokens the router GEMV and routing share a launch. Up to T = 2 the
+ * at 9..32 partial logits per 512-wide K slice come from the fp32 MFMA and
+ * the routing launch adds them (slice order); elsewhere the router GEMV and
+ * routing share a launch. Up to T = 2 the
  * combine runs inside the down projection, above that in a launch of its own. Outputs: out
  * (QW_T_F32, the engine's moe_combine_B rows, QW_T_BF16 or QW_T_F16), logits
  * [T][E], top_e, top_w, tok_slot [T][k], h, yp (fp32 or fp16 with yp_f16, as

@@ -36,7 +36,13 @@ def _case(gpu, seed, T, E, H, F, k, with_shared, zeros=True):
                                                    (2, 256, 4096, 1536, 8, True, False),
                                                    (4, 256, 4096, 1536, 8, False, False),
                                                    (16, 256, 4096, 1536, 8, True, True),
-                                                   (32, 256, 4096, 1536, 8, True, True)])
+                                                   (32, 256, 4096, 1536, 8, True, True),
+                                                   # the MFMA router (9-32 tokens): experts not a multiple
+                                                   # of 16, 16 K slices (H 8192), one slice (H 512) with a
+                                                   # partial second token tile, 1024 experts
+                                                   (9, 40, 8192, 256, 4, True, False),
+                                                   (17, 48, 512, 128, 8, False, False),
+                                                   (24, 1024, 1024, 128, 8, True, False)])
 def test_moe_decode_matches_oracle(gpu, oracle, T, E, H, F, k, shared, bf16):
     print(f"moe_decode T={T} E={E} H={H} F={F} k={k}", flush=True)
     ex, xb, xf, Wr, sh, (g, u, d) = _case(gpu, 40 + T, T, E, H, F, k, shared)

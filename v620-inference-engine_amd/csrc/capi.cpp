@@ -659,6 +659,10 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
         // the logits over one block per expert, then the routing launch
         qwq4::launch_router_logits(rr, T, E, s);
         qwq4::launch_route(ra, s);
+    } else if (qwq4::router_mfma_ok(T, E, H, L.kl)) {
+        // partial logits per K slice on the MFMA, summed by the routing launch
+        qwq4::launch_router_mfma(rr, T, E, s);
+        qwq4::launch_route_part(ra, rr.part, L.ksplit, logits, s);
     } else {
         qwq4::launch_router_route(ra, rr, s);
     }

@@ -627,6 +627,183 @@ void launch_router_logits_shgu(const RouterArgs &r, int T, int E, const ShExpert
     else by_mr(BF16{});
 }
 
+// ---- router logits on the fp32 MFMA (9 to 32 tokens): block (g, s) forms
+// the partial logits of experts 16 g .. 16 g + 15 over K slice s (512 wide)
+// for every token, part[s][t][e]; the routing launch after it adds the
+// slices in slice order. No per-token wave reductions (the dot products'
+// cost in router_route_kernel) and no cross-block hand-off. Wave w takes
+// 64 K of the slice: per 16-K step lane (q, n) loads 4 consecutive weights
+// of expert 16 g + n and 4 activations of token 16 tt + n at K 4 q, and
+// v_mfma_f32_16x16x4f32 j adds the products of their j-th elements (tokens
+// as rows, experts as columns: the lane ends with expert 16 g + n, tokens
+// 16 tt + 4 q + r). Fp16 weights and 16-bit activations widen exactly. The
+// 8 waves' tiles are added in wave order through LDS.
+template <int TT>
+__global__ __launch_bounds__(8 * WAVE) void router_mfma_kernel(RouterArgs r, int T, int E) {
+    __shared__ f32x4 red[8][TT][WAVE];
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, q = lane / 16, n = lane % 16;
+    const int e0 = int(blockIdx.x) * 16, sl = int(blockIdx.y), H = r.H;
+    const int k0 = sl * 512 + wave * 64 + 4 * q;
+    const int e = min(e0 + n, E - 1);
+    constexpr int STEPS = 4;  // 64 K per wave in 16-K steps
+    uint4 wraw[STEPS];
+    uint2 xraw[TT][STEPS];
+#pragma unroll
+    for (int c = 0; c < STEPS; ++c) {
+        const int k = k0 + 16 * c;
+        if (r.w_f16) {
+            const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(r.w) + int64_t(e) * H + k);
+            wraw[c] = make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+            wraw[c] = *reinterpret_cast<const uint4 *>(static_cast<const float *>(r.w) + int64_t(e) * H + k);
+        }
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+            xraw[tt][c] = *reinterpret_cast<const uint2 *>(r.x + int64_t(min(16 * tt + n, T - 1)) * H + k);
+    }
+    const bool ev = e0 + n < E;
+    f32x4 acc[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < STEPS; ++c) {
+        float w[4];
+        if (r.w_f16) {
+            w[0] = f16_bits_to_f32(uint16_t(wraw[c].x));
+            w[1] = f16_bits_to_f32(uint16_t(wraw[c].x >> 16));
+            w[2] = f16_bits_to_f32(uint16_t(wraw[c].y));
+            w[3] = f16_bits_to_f32(uint16_t(wraw[c].y >> 16));
+        } else {
+            w[0] = __builtin_bit_cast(float, wraw[c].x);
+            w[1] = __builtin_bit_cast(float, wraw[c].y);
+            w[2] = __builtin_bit_cast(float, wraw[c].z);
+            w[3] = __builtin_bit_cast(float, wraw[c].w);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = ev ? w[j] : 0.f;
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+            const bool tv = 16 * tt + n < T;
+            const uint32_t lo = xraw[tt][c].x, hi = xraw[tt][c].y;
+            const uint16_t xs[4] = {uint16_t(lo), uint16_t(lo >> 16), uint16_t(hi), uint16_t(hi >> 16)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float xv = r.x_f16 ? f16_bits_to_f32(xs[j]) : bf16_bits_to_f32(xs[j]);
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(tv ? xv : 0.f, w[j], acc[tt], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) red[wave][tt][lane] = acc[tt];
+    __syncthreads();
+    if (tid < TT * WAVE) {
+        const int tt = tid / WAVE, l = tid % WAVE, qq = l / 16, nn = l % 16;
+        f32x4 v = red[0][tt][l];
+#pragma unroll
+        for (int w = 1; w < 8; ++w) v += red[w][tt][l];
+        const int ee = e0 + nn;
+        if (ee < E) {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int t = 16 * tt + 4 * qq + rr;
+                if (t < T) r.part[(int64_t(sl) * T + t) * E + ee] = v[rr];
+            }
+        }
+    }
+}
+
+bool router_mfma_ok(int T, int E, int H, int kl) {
+    // H / 512 slices: 1, 2, 4, 8 or 16 (launch_route_part's counts)
+    const int S = H / 512;
+    return T >= 9 && T <= 32 && E >= 1 && E <= 1024 && kl == 512 && H % 512 == 0 && (S & (S - 1)) == 0 && S <= 16;
+}
+
+void launch_router_mfma(const RouterArgs &r, int T, int E, hipStream_t s) {
+    const dim3 grid(unsigned((E + 15) / 16), unsigned(r.H / 512));
+    if (T <= 16) router_mfma_kernel<1><<<grid, 8 * WAVE, 0, s>>>(r, T, E);
+    else router_mfma_kernel<2><<<grid, 8 * WAVE, 0, s>>>(r, T, E);
+}
+
+// The routing launches over partial logits (part[s][t][e], S slices added
+// in slice order; the sums also go to logits, the rows a.logits names), as
+// launch_route. S is a compile-time count, so a lane's slice loads all go
+// out before the first add.
+template <int S>
+__device__ __forceinline__ float sum_slices(const float *p, int64_t plane, int i) {
+    float pv[S];
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) pv[sl] = p[sl * plane + i];
+    float v = pv[0];
+#pragma unroll
+    for (int sl = 1; sl < S; ++sl) v += pv[sl];
+    return v;
+}
+
+template <int PER, int S>
+__global__ __launch_bounds__(1024) void route_small_part_kernel(RouteArgs a, const float *part, float *logits) {
+    ExpfGlibc ex;
+    ex.load(threadIdx.x % WAVE);
+    const int64_t plane = int64_t(a.T) * a.E;
+    route_small_body<PER>(a, ex, [&](int t) {
+        const float *p = part + int64_t(t) * a.E;
+        float *lo = logits + int64_t(t) * a.E;
+        return [p, lo, plane](int i) {
+            const float v = sum_slices<S>(p, plane, i);
+            lo[i] = v;
+            return v;
+        };
+    });
+}
+
+template <int PER, int S>
+__global__ __launch_bounds__(256) void route_topk_part_kernel(const float *__restrict__ part, int T, int E, int k,
+                                                              float *__restrict__ logits, int32_t *__restrict__ top_e,
+                                                              float *__restrict__ top_w) {
+    const int t = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (t >= T) return;
+    ExpfGlibc ex;
+    ex.load(lane);
+    const int64_t plane = int64_t(T) * E;
+    const float *p = part + int64_t(t) * E;
+    float *lo = logits + int64_t(t) * E;
+    topk_wave<PER>(
+        ex,
+        [&](int i) {
+            const float v = sum_slices<S>(p, plane, i);
+            lo[i] = v;
+            return v;
+        },
+        E, k, lane, top_e + int64_t(t) * k, top_w + int64_t(t) * k);
+}
+
+template <int S>
+static void launch_route_part_s(const RouteArgs &a, const float *part, float *logits, hipStream_t s) {
+    const int per = (a.E + WAVE - 1) / WAVE;
+    if (a.T <= 16) {
+        if (per <= 1) route_small_part_kernel<1, S><<<1, 1024, 0, s>>>(a, part, logits);
+        else if (per <= 2) route_small_part_kernel<2, S><<<1, 1024, 0, s>>>(a, part, logits);
+        else if (per <= 4) route_small_part_kernel<4, S><<<1, 1024, 0, s>>>(a, part, logits);
+        else if (per <= 8) route_small_part_kernel<8, S><<<1, 1024, 0, s>>>(a, part, logits);
+        else route_small_part_kernel<16, S><<<1, 1024, 0, s>>>(a, part, logits);
+    } else {
+        const unsigned g = unsigned((a.T + 3) / 4);
+        if (per <= 4) route_topk_part_kernel<4, S><<<g, 256, 0, s>>>(part, a.T, a.E, a.topk, logits, a.top_e, a.top_w);
+        else if (per <= 8) route_topk_part_kernel<8, S><<<g, 256, 0, s>>>(part, a.T, a.E, a.topk, logits, a.top_e, a.top_w);
+        else route_topk_part_kernel<16, S><<<g, 256, 0, s>>>(part, a.T, a.E, a.topk, logits, a.top_e, a.top_w);
+        route_slots_kernel<<<unsigned((a.T + SLOT_CHUNK - 1) / SLOT_CHUNK), 1024, 0, s>>>(a);
+    }
+}
+
+void launch_route_part(const RouteArgs &a, const float *part, int S, float *logits, hipStream_t s) {
+    switch (S) {
+        case 1: launch_route_part_s<1>(a, part, logits, s); break;
+        case 2: launch_route_part_s<2>(a, part, logits, s); break;
+        case 4: launch_route_part_s<4>(a, part, logits, s); break;
+        case 8: launch_route_part_s<8>(a, part, logits, s); break;
+        default: launch_route_part_s<16>(a, part, logits, s); break;
+    }
+}
+
 size_t router_lds_bytes(int T, int kl, int E) {
     const size_t x = size_t(T) * kl * 2, l = router_lds_route(T, E) ? size_t(T) * E * 4 : 0;
     return x > l ? x : l;

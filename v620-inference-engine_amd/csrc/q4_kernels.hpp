@@ -159,6 +159,12 @@ bool launch_route_shdown(const RouteArgs &a, const ShExpertArgs &sh, int H, hipS
 // [T][Fs] (sh.v's gate, up and gate-logit columns, as launch_swiglu_gate) in
 // one launch; false (nothing launched) where the shapes do not allow it.
 bool launch_route_shgate(const RouteArgs &a, const ShExpertArgs &sh, uint16_t *h, hipStream_t s);
+// 9 to 32 tokens: partial router logits per 512-wide K slice on the fp32
+// MFMA (r.part [H / 512][T][E]), then routing launches that add the slices
+// in slice order (writing the sums to logits) and route as launch_route.
+bool router_mfma_ok(int T, int E, int H, int kl);
+void launch_router_mfma(const RouterArgs &r, int T, int E, hipStream_t s);
+void launch_route_part(const RouteArgs &a, const float *part, int S, float *logits, hipStream_t s);
 size_t router_lds_bytes(int T, int kl, int E);
 void launch_router_route(const RouteArgs &a, const RouterArgs &r, hipStream_t s);
 // The fp32 router GEMV alone (logits, no routing and no hand-off), for the
