@@ -322,7 +322,7 @@ int qw_q4_dequant(const uint32_t *W, const uint16_t *S, const uint32_t *Z, int64
                   void *stream);
 int qw_q4_from_engine_order(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream);
 
-/* A routed-MoE decode block in three to five launches (the engine's decode step calls
+/* A routed-MoE decode block in three to six launches (the engine's decode step calls
  * router GEMV -> route -> experts -> combine back to back, src/engine/decode.hip:99-111;
  * math of ref::Model::moe, src/ref/ref_model.cpp:406-463):
  *   logits = x . router_w^T, router_w [E][H] fp32 (router_f16 = 0, the reference
