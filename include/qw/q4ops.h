@@ -365,8 +365,8 @@ int qw_moe_decode(const void *router_w, int router_f16, const uint16_t *x, int x
  * to T = 8 the shared expert's gate/up GEMV runs in the router-logits launch
  * and its down GEMV in the routed gate/up launch (T = 1) or the routing
  * launch (T = 2 to 4; from 5 the routing launch forms the SwiGLU rows and
- * the down GEMV rides in the experts' gate/up launch), instead of launches of
- * their own. Fs a multiple of 32. workspace:
+ * the down GEMV rides in the experts' gate/up launch, as it does above 8
+ * tokens where the LDS allows), instead of launches of their own. Fs a multiple of 32. workspace:
  * qw_moe_decode_with_shared_workspace_size(...) bytes (that of qw_moe_decode
  * plus T * Fs * 2), zeroed once as for qw_moe_decode. */
 size_t qw_moe_decode_with_shared_workspace_size(int T, int E, int topk, int H, int F, int Fs);

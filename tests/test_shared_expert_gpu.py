@@ -275,7 +275,11 @@ def test_w16_swiglu_gemv_tiled_random_shapes(gpu, N, n, M):
                                                     (8, 256, 4096, 1536, 8, 1536, False, False),
                                                     (5, 128, 4096, 512, 6, 1024, True, True),
                                                     (6, 64, 4096, 256, 8, 512, False, False),
-                                                    (7, 32, 4096, 256, 8, 1536, True, False)])
+                                                    (7, 32, 4096, 256, 8, 1536, True, False),
+                                                    (12, 64, 2048, 256, 6, 512, True, False),
+                                                    (24, 128, 4096, 256, 8, 1024, False, True),
+                                                    (32, 256, 4096, 1536, 8, 1536, True, False),
+                                                    (20, 64, 4096, 256, 8, 256, True, True)])
 def test_moe_decode_with_shared(gpu, oracle, T, E, H, F, k, SF, f16, zeros):
     """qw_moe_decode_with_shared against its parts as separate calls (the
     shared expert's tiled gate/up/gate-logit GEMV and SwiGLU-down GEMV, then
@@ -288,8 +292,11 @@ def test_moe_decode_with_shared(gpu, oracle, T, E, H, F, k, SF, f16, zeros):
     launch, and at batches 5-8 the routing launch forms the SwiGLU rows and, at
     H 2048 and 4096, the down GEMV over them rides in the gate/up launch (experts with
     more than the 4 staged rows at batches 5-7; zero points at 5) (fp16 rows
-    and weights at config 3's size, bf16 at H 2048 and at batches 3, 6 and 8);
-    Fs = 320 takes their own launches."""
+    and weights at config 3's size, bf16 at H 2048 and at batches 3, 6 and 8).
+    Above 8 tokens the shared GEMVs take their own launches, except the down
+    GEMV, which rides in the gate/up launch where its LDS leaves the gate/up
+    blocks per CU unchanged (batch 12, and 20 with Fs 256: two row tiles;
+    batches 24 and 32 take its own launch); Fs = 320 takes their own launches."""
     print(f"moe decode with shared T={T} E={E} H={H} F={F} k={k} Fs={SF} f16={f16} zeros={zeros}", flush=True)
     ex = synth.experts(95 + T, E, H, F, zeros=zeros)
     xb, xf = rows(96, f"sx{T}x{H}", T, H, f16)

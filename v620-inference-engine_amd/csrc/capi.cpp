@@ -630,12 +630,21 @@ void moe_decode_launch(const void *router_w, int router_f16, const uint16_t *x, 
             down_gemv();
         }
     };
+    bool down_pending = false;  // the shared expert's down GEMV over sh_h still to launch
     if (sh) {
-        if (!shl) qwq4::launch_w16_gemv(qwq4::W16Args{sh->gu, H, x, H, sh->v, nv, 0, nv, H, T, 0, x_f16 != 0, 1}, s);
-        if (!shl) shared_down();
+        if (!shl) {
+            // its own launches; above 4 tokens the down GEMV over the SwiGLU
+            // rows rides in the experts' gate/up launch below where it can
+            qwq4::launch_w16_gemv(qwq4::W16Args{sh->gu, H, x, H, sh->v, nv, 0, nv, H, T, 0, x_f16 != 0, 1}, s);
+            if (fold_sh || local) {
+                shared_down();
+            } else {
+                qwq4::launch_swiglu_gate(sh->v, nv, sh->Fs, T, sh_h, s);
+                down_pending = true;
+            }
+        }
         shared = sh->out;
     }
-    bool down_pending = false;  // the shared expert's down GEMV over sh_h still to launch
     if (shl) {
         qwq4::launch_router_logits_shgu(rr, T, E, *sh, s);
         // the shared expert's SwiGLU-down (folded) or SwiGLU rows ride in the

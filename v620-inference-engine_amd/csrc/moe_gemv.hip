@@ -670,13 +670,13 @@ bool launch_gate_up_routed_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, 
     return true;
 }
 
-// ---- 5 to 8 tokens with the shared expert: grid rows y < max_active run the
+// ---- 5 to 32 tokens with the shared expert: grid rows y < max_active run the
 // gate/up GEMV of the y-th active expert (as moe_gate_up_gemv_kernel with
 // the K split in 4 over whole 4-group chunks, GW = 4 or 8 groups per wave), the rows
 // after them the shared expert's down GEMV over its SwiGLU rows sh_h (as
 // qw_w16_gemv_tiled, 16 output rows per block). The two read different
 // inputs of earlier launches (the routing, sh_h) and write different outputs.
-template <typename XT, int GW, bool HAS_Z, bool MULTI, int SMR, int SXPT, int SWS>
+template <typename XT, int GW, bool HAS_Z, bool MULTI, int SMB, int SXPT, int SWS>
 __global__ __launch_bounds__(512) void gate_up_shdown_gemv_kernel(
     const uint32_t *gw, const uint16_t *gs, const uint16_t *gz, const uint32_t *uw, const uint16_t *us,
     const uint16_t *uz, const int32_t *__restrict__ offsets, const int32_t *__restrict__ active,
@@ -689,7 +689,7 @@ __global__ __launch_bounds__(512) void gate_up_shdown_gemv_kernel(
     } else {
         const int i = (by - max_active) * int(gridDim.x) + int(blockIdx.x);
         if (i < (H + 15) / 16)
-            w16_gemv_block<F16, 1, SMR, SXPT, SWS, true>(sh.down, 0, sh_h, sh.Fs, T, sh.Fs, H, sh.out, H, 0, 0, 0, i);
+            w16_gemv_block<F16, SMB, 4, SXPT, SWS, true>(sh.down, 0, sh_h, sh.Fs, T, sh.Fs, H, sh.out, H, 0, 0, 0, i);
     }
 }
 
@@ -697,7 +697,7 @@ bool launch_gate_up_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, const u
     const int G = a.H / QGROUP;
     // the gate/up shapes of launch_gw with the K split in 4: 4 or 8 groups per
     // wave, whole 4-group chunks (H 2048 and 4096)
-    if (a.route_logits || a.T < 5 || a.T > 8 || pick_ks(G, 4) != 4 || (G / 4 != 4 && G / 4 != 8) ||
+    if (a.route_logits || a.T < 5 || a.T > 32 || pick_ks(G, 4) != 4 || (G / 4 != 4 && G / 4 != 8) ||
         sh.Fs % 256 != 0 || (a.gz != nullptr) != (a.uz != nullptr) || !w16_fits(a.T, sh.Fs, a.H))
         return false;
     // the gate/up launch's shape (launch_one, launch_gate_up): rows per chunk
@@ -706,11 +706,18 @@ bool launch_gate_up_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, const u
     while (R > 1 && size_t(R) * a.H * 2 > 32 * 1024) --R;
     const int max_active = a.T * a.topk < a.E ? a.T * a.topk : a.E, gx = a.F / 16;
     const int shb = (a.H + 15) / 16, rows = (shb + gx - 1) / gx;
-    const size_t l1 = moe_lds_bytes(R, a.H), l2 = dense_lds_bytes(a.T, sh.Fs, 1, W16_MAX_KS, W16_MAX_KS);
+    const int smb = a.T > 16 ? 2 : 1;
+    const size_t l1 = moe_lds_bytes(R, a.H), l2 = dense_lds_bytes(a.T, sh.Fs, smb, W16_MAX_KS, W16_MAX_KS);
+    // every block of the grid gets the larger LDS size: merge only where that
+    // leaves as many gate/up blocks per CU as the gate/up launch alone has
+    // (16 or more rows of the down GEMV stage more than the gate/up's chunk:
+    // 202 against 189-193 us per block at 16 tokens, 420 against 296 at 32)
+    if ((160 * 1024) / l2 < (160 * 1024) / l1) return false;
     const size_t lds = l1 > l2 ? l1 : l2;
     const dim3 grid(unsigned(gx), unsigned(max_active + rows));
     // the down GEMV's template shape as qw_w16_gemv_tiled picks it for T rows
-    // of K = Fs (8 waves: Fs / 32 >= 8)
+    // of K = Fs (8 waves: Fs / 32 >= 8; 4 rows per MFMA pass, two row tiles
+    // above 16 rows)
     const int xpt = (a.T * (sh.Fs / 8) + 8 * WAVE - 1) / (8 * WAVE);
     const bool ws16 = (sh.Fs / 32 + W16_MAX_KS - 1) / W16_MAX_KS > 8;
     auto go = [&](auto kern) {
@@ -722,13 +729,18 @@ bool launch_gate_up_shdown(const MoeGemvArgs &a, const ShExpertArgs &sh, const u
         using XT = decltype(xt);
         constexpr bool HZ = decltype(hz)::value, MU = decltype(mu)::value;
         constexpr int SXPT = decltype(sxpt)::value;
-        if (G / 4 == 4) {
-            if (ws16) go(gate_up_shdown_gemv_kernel<XT, 4, HZ, MU, 4, SXPT, 16>);
-            else go(gate_up_shdown_gemv_kernel<XT, 4, HZ, MU, 4, SXPT, 8>);
-        } else {
-            if (ws16) go(gate_up_shdown_gemv_kernel<XT, 8, HZ, MU, 4, SXPT, 16>);
-            else go(gate_up_shdown_gemv_kernel<XT, 8, HZ, MU, 4, SXPT, 8>);
-        }
+        auto by_mb = [&](auto mb) {
+            constexpr int MB = decltype(mb)::value;
+            if (G / 4 == 4) {
+                if (ws16) go(gate_up_shdown_gemv_kernel<XT, 4, HZ, MU, MB, SXPT, 16>);
+                else go(gate_up_shdown_gemv_kernel<XT, 4, HZ, MU, MB, SXPT, 8>);
+            } else {
+                if (ws16) go(gate_up_shdown_gemv_kernel<XT, 8, HZ, MU, MB, SXPT, 16>);
+                else go(gate_up_shdown_gemv_kernel<XT, 8, HZ, MU, MB, SXPT, 8>);
+            }
+        };
+        if (smb == 2) by_mb(std::integral_constant<int, 2>());
+        else by_mb(std::integral_constant<int, 1>());
     };
     auto by_xpt = [&](auto xt, auto hz, auto mu) {
         if (xpt <= 1) by_ws(xt, hz, mu, std::integral_constant<int, 1>());
